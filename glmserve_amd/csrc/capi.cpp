@@ -1,0 +1,262 @@
+// C-ABI of the MoE-layer hot path: argument checks, workspace carving and the
+// launch sequence. Declarations and contracts: include/glmmoe.h.
+#include <hip/hip_runtime.h>
+
+#include "../../include/glmmoe.h"
+#include "kernels.hpp"
+
+using namespace glmmoe;
+
+namespace {
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+int max_tiles_for(int n, int topk, int E, int with_shared) {
+    // sum_e ceil(c_e / T) <= (n*topk)/T + E, plus ceil(n/T) shared tiles.
+    return (n * topk) / kTileRows + E + (with_shared ? (n + kTileRows - 1) / kTileRows : 0) + 1;
+}
+
+int check_layer(const glmmoe_w4a16_layer* L, int n) {
+    if (!L || n <= 0) return GLMMOE_ERR_ARG;
+    if (L->hidden <= 0 || L->moe_inter <= 0 || L->n_experts <= 0 || L->topk <= 0)
+        return GLMMOE_ERR_ARG;
+    if (L->hidden % 128 || L->moe_inter % 128 || L->hidden > 8192) return GLMMOE_ERR_SHAPE;
+    if (L->n_experts > 512 || L->topk > 8 || L->topk > L->n_experts) return GLMMOE_ERR_SHAPE;
+    if (!L->gate_q || !L->gate_s || !L->up_q || !L->up_s || !L->down_q || !L->down_s)
+        return GLMMOE_ERR_ARG;
+    const bool any_sh = L->sh_gate_q || L->sh_up_q || L->sh_down_q;
+    const bool all_sh = L->sh_gate_q && L->sh_gate_s && L->sh_up_q && L->sh_up_s &&
+                        L->sh_down_q && L->sh_down_s;
+    if (any_sh && !all_sh) return GLMMOE_ERR_ARG;
+    return GLMMOE_OK;
+}
+
+inline bool has_shared(const glmmoe_w4a16_layer* L) { return L->sh_gate_q != nullptr; }
+
+ExpertPtrs ptrs(const glmmoe_w4a16_layer* L) {
+    return ExpertPtrs{L->gate_q, L->gate_s, L->up_q, L->up_s, L->down_q, L->down_s,
+                      L->sh_gate_q, L->sh_gate_s, L->sh_up_q, L->sh_up_s, L->sh_down_q,
+                      L->sh_down_s};
+}
+
+// Carves the workspace; with base == nullptr only computes the size.
+size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v) {
+    const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
+    const size_t nk = (size_t)n * k;
+    const size_t R = nk + (has_shared(L) ? (size_t)n : 0);
+    const size_t mt = (size_t)max_tiles_for(n, k, E, has_shared(L));
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> char* {
+        char* p = base ? base + off : nullptr;
+        off += align256(bytes);
+        return p;
+    };
+    glmmoe_layer_ws w{};
+    w.logits = reinterpret_cast<float*>(take((size_t)n * E * 4));
+    w.xsum = reinterpret_cast<float*>(take((size_t)n * (H / 128) * 4));
+    w.topk_ids = reinterpret_cast<int*>(take(nk * 4));
+    w.topk_w = reinterpret_cast<float*>(take(nk * 4));
+    w.expert_offsets = reinterpret_cast<int*>(take((size_t)(E + 2) * 4));
+    w.sorted_token_ids = reinterpret_cast<int*>(take(R * 4));
+    w.sorted_row = reinterpret_cast<int*>(take(R * 4));
+    w.inv = reinterpret_cast<int*>(take(nk * 4));
+    w.tiles = reinterpret_cast<int*>(take(mt * 16));
+    w.ntiles = reinterpret_cast<int*>(take(4));
+    w.h = reinterpret_cast<uint16_t*>(take(R * I * 2));
+    w.hsum = reinterpret_cast<float*>(take(R * (I / 16) * 4));
+    w.dpart = reinterpret_cast<float*>(take(R * H * 4));
+    w.bytes = off;
+    if (v) *v = w;
+    return off;
+}
+
+// ---- stage timing ring ------------------------------------------------------
+struct Prof {
+    bool on = false;
+    bool created = false;
+    int calls = 0;                       // calls recorded since the last read
+    hipEvent_t ev[GLMMOE_PROF_MAX_CALLS][GLMMOE_N_STAGES + 1];
+    bool has[GLMMOE_PROF_MAX_CALLS][GLMMOE_N_STAGES + 1];
+};
+Prof g_prof;
+
+// Records the boundary before stage `stage` (stage == N_STAGES: after the last).
+inline void mark(int stage, hipStream_t s) {
+    if (!g_prof.on || g_prof.calls >= GLMMOE_PROF_MAX_CALLS) return;
+    (void)hipEventRecord(g_prof.ev[g_prof.calls][stage], s);
+    g_prof.has[g_prof.calls][stage] = true;
+}
+inline void begin_call() {
+    if (!g_prof.on || g_prof.calls >= GLMMOE_PROF_MAX_CALLS) return;
+    for (int i = 0; i <= GLMMOE_N_STAGES; ++i) g_prof.has[g_prof.calls][i] = false;
+}
+inline void end_call(hipStream_t s) {
+    if (!g_prof.on || g_prof.calls >= GLMMOE_PROF_MAX_CALLS) return;
+    mark(GLMMOE_N_STAGES, s);
+    ++g_prof.calls;
+}
+
+// Dispatch onward, given ids/weights/xsum in the workspace view.
+int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int* ids,
+                const float* w, const float* xsum, float* out, const glmmoe_layer_ws& v,
+                hipStream_t s) {
+    const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
+    const int sh = has_shared(L) ? 1 : 0;
+    const int mt = max_tiles_for(n, k, E, sh);
+    mark(GLMMOE_STAGE_DISPATCH, s);
+    int rc = launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids, v.sorted_row,
+                             v.inv, v.tiles, v.ntiles, kTileRows, sh, 1, s);
+    if (rc) return rc;
+    const ExpertPtrs P = ptrs(L);
+    mark(GLMMOE_STAGE_GATE_UP, s);
+    rc = launch_gate_up(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.hsum, H,
+                        I, E, s);
+    if (rc) return rc;
+    mark(GLMMOE_STAGE_DOWN, s);
+    rc = launch_down(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
+    if (rc) return rc;
+    mark(GLMMOE_STAGE_COMBINE, s);
+    rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s);
+    if (rc) return rc;
+    end_call(s);
+    return GLMMOE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* glmmoe_version(void) { return "glmmoe 0.1 (gfx950)"; }
+
+int glmmoe_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
+                         float* logits, float* xsum, void* stream) {
+    if (!x || !wr || !logits || n <= 0 || H <= 0 || E <= 0) return GLMMOE_ERR_ARG;
+    if (H % 8 || H > 8192) return GLMMOE_ERR_SHAPE;
+    if (xsum && H % 128) return GLMMOE_ERR_SHAPE;
+    return launch_router_logits(x, wr, n, H, E, logits, xsum, S(stream));
+}
+
+int glmmoe_moe_router(const float* logits, const float* e_bias, int n, int E, int topk,
+                      int norm_topk, float routed_scale, int* topk_ids, float* topk_weights,
+                      void* stream) {
+    if (!logits || !topk_ids || !topk_weights || n <= 0 || E <= 0 || topk <= 0)
+        return GLMMOE_ERR_ARG;
+    if (topk > 8 || topk > E || E > 512) return GLMMOE_ERR_SHAPE;
+    return launch_router_topk(logits, e_bias, n, E, topk, norm_topk, routed_scale, topk_ids,
+                              topk_weights, S(stream));
+}
+
+int glmmoe_moe_dispatch(const int* topk_ids, int n, int topk, int E, int* expert_offsets,
+                        int* sorted_token_ids, int* sorted_row, void* stream) {
+    if (!topk_ids || !expert_offsets || !sorted_token_ids || !sorted_row || n <= 0 ||
+        topk <= 0 || E <= 0)
+        return GLMMOE_ERR_ARG;
+    if (E > 512 || (long)n * topk > (1L << 24)) return GLMMOE_ERR_SHAPE;
+    return launch_dispatch(topk_ids, n, topk, E, expert_offsets, sorted_token_ids, sorted_row,
+                           nullptr, nullptr, nullptr, kTileRows, 0, 0, S(stream));
+}
+
+size_t glmmoe_w4_packed_bytes(int rows, int K) { return (size_t)rows * K / 2; }
+size_t glmmoe_w4_packed_scale_bytes(int rows, int K) { return (size_t)rows * (K / 128) * 2; }
+
+int glmmoe_pack_w4a16(const uint8_t* qweight, const void* scales, int scales_dtype, int n_mats,
+                      int rows, int K, int group_size, uint8_t* packed_q,
+                      uint16_t* packed_scales, void* stream) {
+    if (!qweight || !scales || !packed_q || !packed_scales || n_mats <= 0 || rows <= 0 ||
+        K <= 0)
+        return GLMMOE_ERR_ARG;
+    if (rows % 16 || K % 128 || group_size != 128) return GLMMOE_ERR_SHAPE;
+    if (scales_dtype != 0 && scales_dtype != 1) return GLMMOE_ERR_ARG;
+    return launch_pack_w4(qweight, scales, scales_dtype, n_mats, rows, K, packed_q,
+                          packed_scales, S(stream));
+}
+
+size_t glmmoe_layer_workspace_bytes(const glmmoe_w4a16_layer* L, int n) {
+    if (check_layer(L, n)) return 0;
+    return carve(L, n, nullptr, nullptr);
+}
+
+int glmmoe_layer_workspace_view(const glmmoe_w4a16_layer* L, int n, void* workspace,
+                                glmmoe_layer_ws* view) {
+    const int rc = check_layer(L, n);
+    if (rc) return rc;
+    if (!workspace || !view) return GLMMOE_ERR_ARG;
+    carve(L, n, static_cast<char*>(workspace), view);
+    return GLMMOE_OK;
+}
+
+int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, float* out,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_layer(L, n);
+    if (rc) return rc;
+    if (!x || !out || !workspace || !L->router_w) return GLMMOE_ERR_ARG;
+    glmmoe_layer_ws v;
+    if (carve(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)
+        return GLMMOE_ERR_WORKSPACE;
+    hipStream_t s = S(stream);
+    const int H = L->hidden, E = L->n_experts, k = L->topk;
+    begin_call();
+    mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
+    rc = launch_router_logits(x, L->router_w, n, H, E, v.logits, v.xsum, s);
+    if (rc) return rc;
+    mark(GLMMOE_STAGE_ROUTER_TOPK, s);
+    rc = launch_router_topk(v.logits, L->e_bias, n, E, k, L->norm_topk, L->routed_scale,
+                            v.topk_ids, v.topk_w, s);
+    if (rc) return rc;
+    return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s);
+}
+
+int glmmoe_expert_ffn_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n,
+                            const int* topk_ids, const float* topk_w, float* out,
+                            void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_layer(L, n);
+    if (rc) return rc;
+    if (!x || !out || !workspace || !topk_ids || !topk_w) return GLMMOE_ERR_ARG;
+    glmmoe_layer_ws v;
+    if (carve(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)
+        return GLMMOE_ERR_WORKSPACE;
+    hipStream_t s = S(stream);
+    begin_call();
+    mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
+    rc = launch_xsum(x, n, L->hidden, v.xsum, s);
+    if (rc) return rc;
+    return run_experts(L, x, n, topk_ids, topk_w, v.xsum, out, v, s);
+}
+
+int glmmoe_profile_enable(int on) {
+    if (on && !g_prof.created) {
+        for (int c = 0; c < GLMMOE_PROF_MAX_CALLS; ++c)
+            for (int i = 0; i <= GLMMOE_N_STAGES; ++i)
+                if (hipEventCreate(&g_prof.ev[c][i]) != hipSuccess) return GLMMOE_ERR_LAUNCH;
+        g_prof.created = true;
+    }
+    g_prof.on = on != 0;
+    g_prof.calls = 0;
+    return GLMMOE_OK;
+}
+
+int glmmoe_profile_read(float* stage_ms, int* n_calls) {
+    if (!stage_ms || !n_calls) return GLMMOE_ERR_ARG;
+    for (int i = 0; i < GLMMOE_N_STAGES; ++i) { stage_ms[i] = 0.0f; n_calls[i] = 0; }
+    for (int c = 0; c < g_prof.calls; ++c) {
+        if (hipEventSynchronize(g_prof.ev[c][GLMMOE_N_STAGES]) != hipSuccess)
+            return GLMMOE_ERR_LAUNCH;
+        // Each recorded stage runs from its mark to the next recorded mark.
+        for (int i = 0; i < GLMMOE_N_STAGES; ++i) {
+            if (!g_prof.has[c][i]) continue;
+            int j = i + 1;
+            while (j <= GLMMOE_N_STAGES && !g_prof.has[c][j]) ++j;
+            float ms = 0.0f;
+            if (hipEventElapsedTime(&ms, g_prof.ev[c][i], g_prof.ev[c][j]) != hipSuccess)
+                return GLMMOE_ERR_LAUNCH;
+            stage_ms[i] += ms;
+            n_calls[i] += 1;
+        }
+    }
+    g_prof.calls = 0;
+    return GLMMOE_OK;
+}
+
+}  // extern "C"

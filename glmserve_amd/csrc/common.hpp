@@ -1,0 +1,84 @@
+// Shared device helpers for the MI355X (gfx950) MoE-layer kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace glmmoe {
+
+constexpr int kWave = 64;
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// ---- bf16 -----------------------------------------------------------------
+__device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
+
+// Round-to-nearest-even f32 -> bf16 (NaN kept quiet), the same rule as the
+// reference's host conversion include/common.hpp:126-136.
+__device__ __forceinline__ uint32_t f32_to_bf16(float f) {
+    uint32_t b = __float_as_uint(f);
+    if ((b & 0x7f800000u) == 0x7f800000u && (b & 0x007fffffu)) return (b >> 16) | 0x40u;
+    b += 0x7fffu + ((b >> 16) & 1u);
+    return b >> 16;
+}
+
+// ---- exp / sigmoid ---------------------------------------------------------
+// One exp definition shared, operation for operation, with the CPU oracle:
+// Cody-Waite reduction x = n*ln2 + r with ln2 split hi/lo, degree-7 Taylor
+// polynomial of e^r in Horner form, scale by 2^n built from exponent bits.
+// The argument is clamped to [-80, 80] so 2^n is a normal float. Every step
+// is an IEEE-rounded mul/fma/rint, so sigmoid scores are bit-identical to the
+// oracle's and routing decisions match it exactly.
+__device__ __forceinline__ float exp_fixed(float x) {
+    if (x != x) return x;
+    x = x > 80.0f ? 80.0f : x;
+    x = x < -80.0f ? -80.0f : x;
+    const float n = __builtin_rintf(x * 1.44269504088896341f);
+    float r = __builtin_fmaf(-n, 0.693145751953125f, x);
+    r = __builtin_fmaf(-n, 1.42860682030941723e-06f, r);
+    float p = 1.0f / 5040.0f;
+    p = __builtin_fmaf(p, r, 1.0f / 720.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 120.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 24.0f);
+    p = __builtin_fmaf(p, r, 1.0f / 6.0f);
+    p = __builtin_fmaf(p, r, 0.5f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    p = __builtin_fmaf(p, r, 1.0f);
+    const float scale = __uint_as_float((uint32_t)((int)n + 127) << 23);
+    return p * scale;
+}
+
+// sigmoid = 1 / (1 + exp(-x)): src/model_glm52.cpp:96, cuda/common.cuh:54.
+__device__ __forceinline__ float sigmoid_fixed(float x) { return 1.0f / (1.0f + exp_fixed(-x)); }
+
+// SiLU for the expert activations (tolerance-checked, not bit-checked): the
+// hardware exp2 is accurate to ~1 ulp and much cheaper than exp_fixed.
+__device__ __forceinline__ float silu_fast(float x) {
+    return x / (1.0f + __builtin_amdgcn_exp2f(-x * 1.44269504088896341f));
+}
+
+// ---- int4 -> bf16 -----------------------------------------------------------
+// A packed dword holds 8 int4 codes c (the stored nibble, value c - 8) for 8
+// consecutive K positions e = 0..7: e = 2s in nibble s, e = 2s+1 in nibble
+// s+4. OR-ing 0x4300 into a 16-bit lane holding c gives the bf16 of 128 + c
+// exactly, so each pair costs one shift and one and-or. The -136 offset
+// (128 + 8) is removed after the MFMA with the activation group sum:
+//   sum_k (c_k - 8) x_k = sum_k (128 + c_k) x_k - 136 * sum_k x_k.
+__device__ __forceinline__ bf16x8 dq_w4(uint32_t w) {
+    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+    u32x4 v;
+    v.x = (w & 0x000F000Fu) | 0x43004300u;
+    v.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
+    v.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
+    v.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+    return __builtin_bit_cast(bf16x8, v);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+}  // namespace glmmoe

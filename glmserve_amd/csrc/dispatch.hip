@@ -1,0 +1,144 @@
+// Dispatch: expert histogram, prefix scan and a stable permute that groups
+// the (token, slot) rows by expert, plus the inverse map and the tile list
+// the grouped expert GEMMs walk.
+//
+// Reference: cuda/moe_dispatch.cu:16-45 (serial counting sort, stable in
+// token-then-slot order) and the atomic count/scan/scatter of
+// cuda/qgemm.cu:966-989 (whose order inside an expert is nondeterministic).
+// Here the order is the reference's stable one and the work is parallel:
+//   1. LDS histogram (atomics on counts only: order-free),
+//   2. block scan over experts,
+//   3. rows in chunks of 1024 in input order; inside a wave, equal expert ids
+//      are matched with one ballot per id bit (rank = lanes below with the
+//      same id); across the 16 waves of a chunk, per-wave counts in LDS give
+//      each row the number of equal ids in earlier waves. The result is a
+//      pure function of topk_ids.
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace glmmoe {
+
+constexpr int kDispThreads = 1024;
+constexpr int kDispWaves = kDispThreads / 64;
+constexpr int kDispMaxE = 512;
+
+// Inclusive block scan of one int per thread over kDispThreads threads.
+__device__ int block_scan_incl(int v, int* sh) {
+    const int tid = threadIdx.x;
+    sh[tid] = v;
+    __syncthreads();
+    for (int off = 1; off < kDispThreads; off <<= 1) {
+        const int add = tid >= off ? sh[tid - off] : 0;
+        __syncthreads();
+        sh[tid] += add;
+        __syncthreads();
+    }
+    const int r = sh[tid];
+    __syncthreads();
+    return r;
+}
+
+// mode bit 0: also emit inv[], shared rows and the tile list (layer path).
+__global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
+    const int* __restrict__ ids, int n, int topk, int E, int* __restrict__ offsets,
+    int* __restrict__ sorted_tok, int* __restrict__ sorted_slot, int* __restrict__ inv,
+    int4* __restrict__ tiles, int* __restrict__ ntiles, int tile_rows, int with_shared,
+    int mode) {
+    __shared__ int cnt[kDispMaxE + 1];
+    __shared__ int cursor[kDispMaxE + 1];
+    __shared__ int wc[kDispWaves][kDispMaxE];
+    __shared__ int scan[kDispThreads];
+    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
+    const int total = n * topk;
+    int nbits = 0;
+    while ((1 << nbits) < E) ++nbits;
+
+    for (int e = tid; e <= kDispMaxE; e += kDispThreads) cnt[e] = 0;
+    for (int i = tid; i < kDispWaves * kDispMaxE; i += kDispThreads) (&wc[0][0])[i] = 0;
+    __syncthreads();
+    for (int i = tid; i < total; i += kDispThreads) {
+        const int e = ids[i];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+
+    // Exclusive prefix over experts (E <= 512 < kDispThreads).
+    const int myc = tid < E ? cnt[tid] : 0;
+    const int incl = block_scan_incl(myc, scan);
+    if (tid < E) {
+        offsets[tid] = incl - myc;
+        cursor[tid] = incl - myc;
+    }
+    if (tid == E - 1) offsets[E] = incl;
+    if ((mode & 1) && tid == 0) offsets[E + 1] = total + (with_shared ? n : 0);
+    __syncthreads();
+
+    // Stable permute.
+    for (int base = 0; base < total; base += kDispThreads) {
+        const int i = base + tid;
+        const int e = i < total ? ids[i] : -1;
+        const bool valid = e >= 0 && e < E;
+        uint64_t m = __ballot(valid);
+        for (int b = 0; b < nbits; ++b) {
+            const bool bit = valid && ((e >> b) & 1);
+            const uint64_t bal = __ballot(bit);
+            m &= bit ? bal : ~bal;
+        }
+        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+        const int rank = __popcll(m & below);
+        const bool leader = valid && rank == 0;
+        if (leader) wc[wv][e] = __popcll(m);
+        __syncthreads();
+        if (valid) {
+            int pre = 0;
+            for (int w = 0; w < wv; ++w) pre += wc[w][e];
+            const int pos = cursor[e] + pre + rank;
+            sorted_tok[pos] = i / topk;
+            sorted_slot[pos] = i % topk;
+            if (mode & 1) inv[i] = pos;
+        }
+        __syncthreads();
+        if (leader) {
+            atomicAdd(&cursor[e], wc[wv][e]);
+            wc[wv][e] = 0;
+        }
+        __syncthreads();
+    }
+
+    if (!(mode & 1)) return;
+
+    // Shared-expert rows: one per token, after all routed rows.
+    if (with_shared)
+        for (int t = tid; t < n; t += kDispThreads) {
+            sorted_tok[total + t] = t;
+            sorted_slot[total + t] = -1;
+        }
+
+    // Tile list: expert e (e == E is the shared expert) contributes
+    // ceil(count / tile_rows) tiles of at most tile_rows consecutive rows.
+    const int nexp = E + (with_shared ? 1 : 0);
+    const int ce = tid < E ? cnt[tid] : (tid == E && with_shared ? n : 0);
+    const int nt = tid < nexp ? (ce + tile_rows - 1) / tile_rows : 0;
+    const int tincl = block_scan_incl(nt, scan);
+    if (tid < nexp) {
+        const int row0 = tid < E ? cursor[tid] - ce : total;  // cursor ended at offset+count
+        int tbase = tincl - nt;
+        for (int j = 0; j < nt; ++j) {
+            const int r0 = row0 + j * tile_rows;
+            tiles[tbase + j] = make_int4(tid, r0, min(tile_rows, ce - j * tile_rows), 0);
+        }
+    }
+    if (tid == kDispThreads - 1) *ntiles = tincl;
+}
+
+int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,
+                    int* sorted_slot, int* inv, int* tiles, int* ntiles, int tile_rows,
+                    int with_shared, int mode, hipStream_t s) {
+    if (E > kDispMaxE || E < 1) return -2;
+    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispThreads), 0, s, ids, n, topk, E,
+                       offsets, sorted_tok, sorted_slot, inv, reinterpret_cast<int4*>(tiles),
+                       ntiles, tile_rows, with_shared, mode);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+}  // namespace glmmoe

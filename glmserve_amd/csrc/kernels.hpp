@@ -1,0 +1,40 @@
+// Internal launchers shared by the kernel files and the C-ABI layer.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace glmmoe {
+
+// Grouped rows per tile of the expert GEMMs (four 16-token MFMA blocks).
+constexpr int kTileRows = 64;
+
+struct ExpertPtrs {
+    const uint8_t* gate_q; const uint16_t* gate_s;
+    const uint8_t* up_q; const uint16_t* up_s;
+    const uint8_t* down_q; const uint16_t* down_s;
+    const uint8_t* sh_gate_q; const uint16_t* sh_gate_s;
+    const uint8_t* sh_up_q; const uint16_t* sh_up_s;
+    const uint8_t* sh_down_q; const uint16_t* sh_down_s;
+};
+
+int launch_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
+                         float* logits, float* xsum, hipStream_t s);
+int launch_xsum(const uint16_t* x, int n, int H, float* xsum, hipStream_t s);
+int launch_router_topk(const float* logits, const float* e_bias, int n, int E, int topk,
+                       int norm_topk, float routed_scale, int* ids, float* w, hipStream_t s);
+int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,
+                    int* sorted_slot, int* inv, int* tiles, int* ntiles, int tile_rows,
+                    int with_shared, int mode, hipStream_t s);
+int launch_pack_w4(const uint8_t* q, const void* sc, int sc_bf16, int n_mats, int rows, int K,
+                   uint8_t* pq, uint16_t* ps, hipStream_t s);
+int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
+                   const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
+                   float* hsum, int H, int I, int E, hipStream_t s);
+int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
+                const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
+                hipStream_t s);
+int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
+                   int with_shared, float* out, hipStream_t s);
+
+}  // namespace glmmoe

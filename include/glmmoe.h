@@ -1,0 +1,176 @@
+/*
+ * glmmoe.h -- C-ABI of the MI355X (gfx950) MoE-layer hot path for glmserve.
+ *
+ * Every pointer argument is a DEVICE pointer owned by the caller unless noted;
+ * `stream` is a hipStream_t passed as void* (NULL = the null stream). No entry
+ * point allocates, frees or synchronizes; work is enqueued on `stream`.
+ * Return value: GLMMOE_OK (0) or a negative GLMMOE_ERR_* code; nothing throws
+ * across this boundary (the reference's wrappers return void and print launch
+ * errors, cuda/moe_expert.cu:126-129; callers here get a code instead).
+ *
+ * Data types: bf16 values travel as uint16_t bit patterns; fp32 as float.
+ *
+ * Citations are to the glmserve tree; each entry point names the
+ * cuda/kernels.cuh launcher it replaces. include/glmmoe/kernels.hpp re-exposes
+ * the reference-named subset as C++ inline functions.
+ */
+#ifndef GLMMOE_H
+#define GLMMOE_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GLMMOE_OK 0
+#define GLMMOE_ERR_ARG (-1)       /* NULL pointer or non-positive size */
+#define GLMMOE_ERR_SHAPE (-2)     /* shape outside what the kernels support */
+#define GLMMOE_ERR_WORKSPACE (-3) /* workspace smaller than required */
+#define GLMMOE_ERR_LAUNCH (-4)    /* the HIP runtime rejected a launch */
+
+/* Library version string (host memory, static). */
+const char* glmmoe_version(void);
+
+/* ---- Router ---------------------------------------------------------------
+ * Router-logit GEMM, logits[n,E] = x[n,H] . wr[E,H]^T, bf16 inputs, fp32 out.
+ * Replaces gemm_linear(s.normed, d.router, ...) (src/model_gpu.cpp:1448 ->
+ * gemm_fp32, cuda/kernels.cuh:37-38). Reduction order is fixed: K is cut into
+ * chunks of 128, each chunk summed from zero in ascending K, chunk sums added
+ * in ascending order -- restated by the CPU oracle, so logits are bit-exact.
+ * xsum (nullable) receives sum_{k in chunk} x[t,k] as [n, ceil(H/128)] fp32,
+ * the activation group sums the W4A16 expert kernels consume.
+ * Limits: H % 8 == 0, H <= 8192. */
+int glmmoe_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
+                         float* logits, float* xsum, void* stream);
+
+/* Sigmoid top-k routing with score-correction bias.
+ * Replaces moe_router (cuda/kernels.cuh:243-245, cuda/moe_router.cu:17-79):
+ * same arguments and meaning. e_bias is nullable. Ties choose the lower
+ * expert index; weights are the unbiased scores, normalized by their sum in
+ * selection order when norm_topk != 0, then scaled by routed_scale.
+ * Limits: 1 <= topk <= 8, topk <= E <= 512. */
+int glmmoe_moe_router(const float* logits, const float* e_bias, int n, int E, int topk,
+                      int norm_topk, float routed_scale, int* topk_ids, float* topk_weights,
+                      void* stream);
+
+/* Group the (token, slot) pairs by expert.
+ * Replaces moe_dispatch (cuda/kernels.cuh:249-250, cuda/moe_dispatch.cu:16-45):
+ * expert_offsets[E+1] (exclusive prefix), sorted_token_ids[n*topk],
+ * sorted_row[n*topk] (the slot). Order within an expert is (token asc, slot
+ * asc), deterministic, identical to the reference's serial counting sort.
+ * Limits: E <= 512, n*topk <= 2^24. Ids outside [0,E) give GLMMOE_ERR_ARG
+ * only if detected on the host side; on device they are skipped (counted in
+ * no expert) -- callers pass router output, which is always in range. */
+int glmmoe_moe_dispatch(const int* topk_ids, int n, int topk, int E, int* expert_offsets,
+                        int* sorted_token_ids, int* sorted_row, void* stream);
+
+/* ---- W4A16 weight format --------------------------------------------------
+ * Reference format (src/tensor.cpp:53-63, cuda/kernels.cuh:259-268): per
+ * matrix [rows, K] a packed u8 array [rows, K/2] (low nibble = even column,
+ * value = nibble - 8) and scales [rows, K/group].
+ * Native format ("packed"): 16-row x 128-K tiles of 1 KiB, tile (rb, kg) at
+ * ((rb * K/128) + kg) * 1024 bytes; inside a tile lane l = r + 16*q (r = row
+ * in block, q = 0..3) owns 16 bytes = K positions kg*128 + 32q + [0,32), one
+ * dword per 8 positions, position 2s in nibble s and 2s+1 in nibble s+4.
+ * Scales become bf16 [rows/16][K/128][16].
+ * glmmoe_pack_w4a16 converts n_mats stacked reference matrices (experts) to
+ * native. scales_dtype: 0 = fp32 (rounded to bf16, nearest-even), 1 = bf16.
+ * Limits: rows % 16 == 0, K % 128 == 0, group_size == 128. */
+size_t glmmoe_w4_packed_bytes(int rows, int K);       /* per matrix, weights */
+size_t glmmoe_w4_packed_scale_bytes(int rows, int K); /* per matrix, scales */
+int glmmoe_pack_w4a16(const uint8_t* qweight, const void* scales, int scales_dtype,
+                      int n_mats, int rows, int K, int group_size, uint8_t* packed_q,
+                      uint16_t* packed_scales, void* stream);
+
+/* ---- Whole layer ------------------------------------------------------------
+ * One GLM-5-class MoE layer: router GEMM -> routing -> dispatch -> grouped
+ * W4A16 gate/up/SiLU -> grouped down -> deterministic combine with the shared
+ * expert. Replaces the MoE branch of run_layer_step (src/model_gpu.cpp:
+ * 1446-1495: gemm_linear(router), moe_router, cudaMemset, moe_expert_ffn_w4a16,
+ * shared-expert gemm_w4a16 x3 + silu_mul + add_inplace). Output
+ *   out[t] = sum_{s<topk, in slot order} w[t,s] * y_{e(t,s)}(x_t) + y_shared(x_t)
+ * in fp32, the summation order of src/model_glm52.cpp:1133-1152.
+ * All expert weights are in the native packed format; routed experts are
+ * stacked (expert stride = packed bytes of one matrix). Shared expert
+ * pointers may be NULL (no shared expert); when present its intermediate
+ * size must equal moe_inter.
+ * Limits: hidden % 128 == 0, moe_inter % 128 == 0, hidden <= 8192,
+ * E <= 512, 1 <= topk <= 8. */
+typedef struct glmmoe_w4a16_layer {
+    int hidden;        /* H */
+    int moe_inter;     /* I (per expert, also the shared expert's) */
+    int n_experts;     /* E routed experts */
+    int topk;
+    int norm_topk;     /* norm_topk_prob */
+    float routed_scale;/* routed_scaling_factor */
+    const uint16_t* router_w;   /* [E, H] bf16 */
+    const float* e_bias;        /* [E] fp32 or NULL */
+    const uint8_t* gate_q;  const uint16_t* gate_s;  /* [E] x packed [I, H] */
+    const uint8_t* up_q;    const uint16_t* up_s;    /* [E] x packed [I, H] */
+    const uint8_t* down_q;  const uint16_t* down_s;  /* [E] x packed [H, I] */
+    const uint8_t* sh_gate_q; const uint16_t* sh_gate_s; /* packed [I, H] or NULL */
+    const uint8_t* sh_up_q;   const uint16_t* sh_up_s;
+    const uint8_t* sh_down_q; const uint16_t* sh_down_s; /* packed [H, I] */
+} glmmoe_w4a16_layer;
+
+/* Device workspace carved by the layer call; every field points inside the
+ * caller's workspace buffer. R = n*topk + n grouped rows (routed rows, then
+ * one shared-expert row per token). */
+typedef struct glmmoe_layer_ws {
+    float* logits;        /* [n, E] */
+    float* xsum;          /* [n, H/128] */
+    int* topk_ids;        /* [n, topk] */
+    float* topk_w;        /* [n, topk] */
+    int* expert_offsets;  /* [E + 2]: routed offsets, [E] = n*topk, [E+1] = R */
+    int* sorted_token_ids;/* [R] */
+    int* sorted_row;      /* [R] slot, -1 for shared rows */
+    int* inv;             /* [n*topk]: grouped row of (t, s) */
+    int* tiles;           /* [max_tiles * 4]: {expert, row0, nrows, 0} */
+    int* ntiles;          /* [1] */
+    uint16_t* h;          /* [R, I] bf16 SiLU(gate) * up */
+    float* hsum;          /* [R, I/16] partial sums of h */
+    float* dpart;         /* [R, H] fp32 per-row expert outputs (unweighted) */
+    size_t bytes;         /* total workspace bytes */
+} glmmoe_layer_ws;
+
+size_t glmmoe_layer_workspace_bytes(const glmmoe_w4a16_layer* L, int n);
+int glmmoe_layer_workspace_view(const glmmoe_w4a16_layer* L, int n, void* workspace,
+                                glmmoe_layer_ws* view);
+
+/* Runs the whole layer. x: [n, H] bf16; out: [n, H] fp32 (overwritten). */
+int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n,
+                           float* out, void* workspace, size_t workspace_bytes,
+                           void* stream);
+
+/* The routed + shared expert stage alone, for callers that route elsewhere.
+ * Replaces moe_expert_ffn_w4a16 (cuda/kernels.cuh:263-268) plus the shared
+ * expert and add_inplace of src/model_gpu.cpp:1486-1494. topk_ids/topk_w are
+ * [n, topk]; xsum may be NULL (then it is computed into the workspace). */
+int glmmoe_expert_ffn_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n,
+                            const int* topk_ids, const float* topk_w, float* out,
+                            void* workspace, size_t workspace_bytes, void* stream);
+
+/* ---- Stage timing (diagnostics; no reference counterpart) -----------------
+ * While enabled, every glmmoe_moe_layer_w4a16 / glmmoe_expert_ffn_w4a16 call
+ * records a HIP event on its stream before and after each stage, in a ring of
+ * GLMMOE_PROF_MAX_CALLS calls (events are created on the first enable; no
+ * device memory is allocated). glmmoe_profile_read waits for the recorded
+ * events and returns, per stage, the summed milliseconds and the number of
+ * calls summed, then clears the ring. Stages: */
+#define GLMMOE_STAGE_ROUTER_LOGITS 0
+#define GLMMOE_STAGE_ROUTER_TOPK 1
+#define GLMMOE_STAGE_DISPATCH 2
+#define GLMMOE_STAGE_GATE_UP 3
+#define GLMMOE_STAGE_DOWN 4
+#define GLMMOE_STAGE_COMBINE 5
+#define GLMMOE_N_STAGES 6
+#define GLMMOE_PROF_MAX_CALLS 512
+int glmmoe_profile_enable(int on);
+int glmmoe_profile_read(float* stage_ms, int* n_calls);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GLMMOE_H */

@@ -1,0 +1,404 @@
+/*
+ * moe_oracle.c -- CPU restatement of glmserve's MoE-layer hot path.
+ *
+ * TEST INFRASTRUCTURE ONLY: the checker for the HIP kernels, never part of
+ * the product path. Built with -ffp-contract=off so that every floating-point
+ * operation rounds exactly where it is written (fmaf() is called explicitly
+ * where a fused multiply-add is meant).
+ *
+ * Reference citations are paths in the glmserve tree.
+ */
+#include "moe_oracle.h"
+
+#include <math.h>
+#include <pthread.h>
+#include <stdlib.h>
+#include <string.h>
+
+/* ---------------------------------------------------------------------------
+ * exp / sigmoid / silu.
+ * The reference uses std::exp on the CPU (src/model_glm52.cpp:95-96) and the
+ * __expf intrinsic on the GPU (cuda/common.cuh:53-54); the two disagree in the
+ * last bits. This build defines ONE exp that the CPU oracle and the HIP
+ * kernels both evaluate operation-for-operation, so sigmoid scores (and thus
+ * routing) are bit-identical across the two:
+ *   Cody-Waite range reduction x = n*ln2 + r, |r| <= ln2/2, with ln2 split into
+ *   a 24-bit-exact high part and a low correction (Cody & Waite, "Software
+ *   Manual for the Elementary Functions", 1980), then the degree-7 Taylor
+ *   polynomial of e^r in Horner form (truncation error < 6e-9 relative on
+ *   |r| <= 0.347), then scaling by 2^n built from exponent bits.
+ * The argument is clamped to [-80, 80] so 2^n is always a normal float and no
+ * denormal handling differs between CPU and GPU. sigmoid(x) for |x| > 80 is
+ * therefore computed at +-80 (it differs from the true value only below
+ * 2e-35, or by less than 2^-24 from 1).
+ * ------------------------------------------------------------------------- */
+#define ORC_LOG2E 1.44269504088896341f
+#define ORC_LN2_HI 0.693145751953125f      /* 0x3f317200, exact in 16 bits */
+#define ORC_LN2_LO 1.42860682030941723e-06f /* ln2 - LN2_HI */
+
+float orc_expf(float x) {
+    if (x != x) return x;
+    if (x > 80.0f) x = 80.0f;
+    if (x < -80.0f) x = -80.0f;
+    float n = rintf(x * ORC_LOG2E);
+    float r = fmaf(-n, ORC_LN2_HI, x);
+    r = fmaf(-n, ORC_LN2_LO, r);
+    float p = 1.0f / 5040.0f;
+    p = fmaf(p, r, 1.0f / 720.0f);
+    p = fmaf(p, r, 1.0f / 120.0f);
+    p = fmaf(p, r, 1.0f / 24.0f);
+    p = fmaf(p, r, 1.0f / 6.0f);
+    p = fmaf(p, r, 0.5f);
+    p = fmaf(p, r, 1.0f);
+    p = fmaf(p, r, 1.0f);
+    int ni = (int)n;
+    uint32_t bits = (uint32_t)(ni + 127) << 23;
+    float scale;
+    memcpy(&scale, &bits, sizeof scale);
+    return p * scale;
+}
+
+/* sigmoidf: src/model_glm52.cpp:96 (1 / (1 + exp(-x))). */
+float orc_sigmoid(float x) { return 1.0f / (1.0f + orc_expf(-x)); }
+
+/* silu: src/model_glm52.cpp:95 (x / (1 + exp(-x))). */
+float orc_silu(float x) { return x / (1.0f + orc_expf(-x)); }
+
+/* bf16 <-> f32: include/common.hpp:121-136 (top 16 bits; RNE on the way down).
+ * NaN inputs are kept NaN (quiet bit forced), which the reference's add-bias
+ * trick does not guarantee; finite and infinite values match it exactly. */
+uint16_t orc_f32_to_bf16(float f) {
+    uint32_t bits;
+    memcpy(&bits, &f, sizeof bits);
+    if ((bits & 0x7f800000u) == 0x7f800000u && (bits & 0x007fffffu))
+        return (uint16_t)((bits >> 16) | 0x0040u);
+    uint32_t lsb = (bits >> 16) & 1u;
+    bits += 0x7fffu + lsb;
+    return (uint16_t)(bits >> 16);
+}
+
+float orc_bf16_to_f32(uint16_t h) {
+    uint32_t bits = (uint32_t)h << 16;
+    float f;
+    memcpy(&f, &bits, sizeof f);
+    return f;
+}
+
+void orc_f32_to_bf16_n(const float* src, uint16_t* dst, int64_t count) {
+    for (int64_t i = 0; i < count; ++i) dst[i] = orc_f32_to_bf16(src[i]);
+}
+
+void orc_bf16_to_f32_n(const uint16_t* src, float* dst, int64_t count) {
+    for (int64_t i = 0; i < count; ++i) dst[i] = orc_bf16_to_f32(src[i]);
+}
+
+/* FP8 e4m3 decode: include/common.hpp:182-200 (bias 7, no infinities; the
+ * reference decodes 0x7f/0xff as +-480 rather than NaN -- restated as is; the
+ * encoder below never produces those two codes). */
+float orc_e4m3_to_f32(uint8_t v) {
+    float sign = (v & 0x80u) ? -1.0f : 1.0f;
+    int e = (v >> 3) & 0xf;
+    int m = v & 0x7;
+    if (e == 0) return sign * ldexpf((float)m, -9);
+    return sign * ldexpf(1.0f + (float)m / 8.0f, e - 7);
+}
+
+/* FP8 e4m3 encode, round-to-nearest-even, saturating to +-448 (the largest
+ * OCP e4m3fn finite value), so the NaN codes never appear. No reference
+ * counterpart (the reference only decodes FP8, src/tensor.cpp:21-24). */
+uint8_t orc_f32_to_e4m3(float f) {
+    uint8_t s = signbit(f) ? 0x80u : 0u;
+    float a = fabsf(f);
+    if (a != a) return (uint8_t)(s | 0x7e);
+    if (a >= 448.0f) return (uint8_t)(s | 0x7e);
+    if (a < 0.015625f) { /* subnormal range, step 2^-9 */
+        int m = (int)rintf(a * 512.0f);
+        return (uint8_t)(s | m); /* m == 8 is exactly the min normal code 0x08 */
+    }
+    int ex;
+    float fr = frexpf(a, &ex); /* a = fr * 2^ex, fr in [0.5, 1) */
+    int e = ex - 1;
+    int m = (int)rintf((fr * 2.0f - 1.0f) * 8.0f);
+    if (m == 8) { m = 0; ++e; }
+    return (uint8_t)(s | ((e + 7) << 3) | m);
+}
+
+/* linear_forward: src/model_glm52.cpp:42-56. y[n,out] = x[n,in] . W[out,in]^T,
+ * one scalar fp32 accumulator per output, ascending i, acc += x*w with the
+ * product rounded before the add (the reference is built -std=c++17 -O2 for
+ * x86-64 without FMA, so no contraction). */
+void orc_linear_f32(const float* x, const float* w, int64_t n, int64_t in, int64_t out,
+                    float* y) {
+    for (int64_t t = 0; t < n; ++t) {
+        const float* xt = x + t * in;
+        for (int64_t o = 0; o < out; ++o) {
+            const float* wo = w + o * in;
+            float acc = 0.0f;
+            for (int64_t i = 0; i < in; ++i) {
+                float p = xt[i] * wo[i];
+                acc = acc + p;
+            }
+            y[t * out + o] = acc;
+        }
+    }
+}
+
+/* Router logits with bf16 inputs in this build's fixed reduction order (the
+ * reference's GPU path goes through cublasSgemm, cuda/gemm.cu:62-78, whose
+ * order is unspecified; its CPU path is linear_forward above):
+ *   K is cut into chunks of 128; each chunk is summed from zero in ascending
+ *   order, and the chunk sums are added to the total in ascending chunk order.
+ * bf16 x bf16 products are exact in fp32, so fmaf(x, w, s) == s + x*w and the
+ * per-chunk sum is exactly linear_forward's order restarted every 128 inputs.
+ * For H <= 128 this IS linear_forward. */
+#define ORC_ROUTER_KC 128
+void orc_router_logits_bf16(const uint16_t* x, const uint16_t* wr, int64_t n, int64_t H,
+                            int64_t E, float* logits) {
+    for (int64_t t = 0; t < n; ++t) {
+        const uint16_t* xt = x + t * H;
+        for (int64_t e = 0; e < E; ++e) {
+            const uint16_t* we = wr + e * H;
+            float total = 0.0f;
+            for (int64_t c = 0; c < H; c += ORC_ROUTER_KC) {
+                int64_t ce = c + ORC_ROUTER_KC < H ? c + ORC_ROUTER_KC : H;
+                float s = 0.0f;
+                for (int64_t i = c; i < ce; ++i)
+                    s = fmaf(orc_bf16_to_f32(xt[i]), orc_bf16_to_f32(we[i]), s);
+                total = total + s;
+            }
+            logits[t * E + e] = total;
+        }
+    }
+}
+
+/* Routing: the GPU kernel cuda/moe_router.cu:17-72 and the CPU loop
+ * src/model_glm52.cpp:1113-1129.
+ *   score = sigmoid(logit); choose = score + e_bias (e_bias may be NULL);
+ *   k rounds: pick the not-yet-taken expert with the largest choose, ties to
+ *   the lower expert index (moe_router.cu:48-53); NaN never wins;
+ *   weight = the UNBIASED score, wsum accumulated in selection order;
+ *   if norm_topk and wsum > 0: w /= wsum; then w *= routed_scale.
+ * Returns 0, or -1 on a bad shape (E < topk, topk < 1). */
+int orc_router_topk(const float* logits, const float* e_bias, int64_t n, int E, int topk,
+                    int norm_topk, float routed_scale, int* topk_ids, float* topk_w) {
+    if (topk < 1 || E < topk) return -1;
+    float* score = (float*)malloc(sizeof(float) * (size_t)E);
+    float* choose = (float*)malloc(sizeof(float) * (size_t)E);
+    unsigned char* taken = (unsigned char*)malloc((size_t)E);
+    for (int64_t t = 0; t < n; ++t) {
+        const float* lt = logits + t * E;
+        for (int e = 0; e < E; ++e) {
+            score[e] = orc_sigmoid(lt[e]);
+            choose[e] = score[e] + (e_bias ? e_bias[e] : 0.0f);
+            taken[e] = 0;
+        }
+        int* ids = topk_ids + t * topk;
+        float* w = topk_w + t * topk;
+        float wsum = 0.0f;
+        for (int k = 0; k < topk; ++k) {
+            int best = -1;
+            for (int e = 0; e < E; ++e) {
+                if (taken[e]) continue;
+                if (best < 0) { best = e; continue; }
+                float c = choose[e], b = choose[best];
+                if (b != b) { if (c == c) best = e; continue; }   /* NaN loses */
+                if (c > b) best = e;                               /* strict: ties keep lower */
+            }
+            taken[best] = 1;
+            ids[k] = best;
+            w[k] = score[best];
+            wsum = wsum + score[best];
+        }
+        for (int k = 0; k < topk; ++k) {
+            float v = w[k];
+            if (norm_topk && wsum > 0.0f) v = v / wsum;
+            w[k] = v * routed_scale;
+        }
+    }
+    free(score);
+    free(choose);
+    free(taken);
+    return 0;
+}
+
+/* Dispatch: cuda/moe_dispatch.cu:16-39 -- a counting sort over experts that
+ * is stable in (token ascending, slot ascending) order within each expert.
+ * expert_offsets[E+1] is the exclusive prefix of the per-expert counts;
+ * sorted_row holds the slot k of each grouped row. Returns -1 on an
+ * out-of-range id. */
+int orc_dispatch(const int* topk_ids, int64_t n, int topk, int E, int* expert_offsets,
+                 int* sorted_token_ids, int* sorted_row) {
+    int64_t total = n * topk;
+    for (int e = 0; e <= E; ++e) expert_offsets[e] = 0;
+    for (int64_t i = 0; i < total; ++i) {
+        int e = topk_ids[i];
+        if (e < 0 || e >= E) return -1;
+        expert_offsets[e + 1]++;
+    }
+    for (int e = 0; e < E; ++e) expert_offsets[e + 1] += expert_offsets[e];
+    int* cursor = (int*)malloc(sizeof(int) * (size_t)(E > 0 ? E : 1));
+    for (int e = 0; e < E; ++e) cursor[e] = expert_offsets[e];
+    for (int64_t t = 0; t < n; ++t)
+        for (int k = 0; k < topk; ++k) {
+            int e = topk_ids[t * topk + k];
+            int dst = cursor[e]++;
+            sorted_token_ids[dst] = (int)t;
+            sorted_row[dst] = k;
+        }
+    free(cursor);
+    return 0;
+}
+
+/* int4 dequant of a [rows, in] matrix stored as packed [rows, ceil(in/2)] plus
+ * scales [rows, ceil(in/g)]: src/tensor.cpp:53-63 per row (low nibble = even
+ * column, value = (nibble - 8) * scale), the row layout of
+ * cuda/moe_expert.cu:132-140. */
+void orc_dequant_int4_rows(const uint8_t* q, const float* scales, int64_t rows, int64_t in,
+                           int64_t group_size, float* out) {
+    int64_t packed_in = (in + 1) / 2, groups = (in + group_size - 1) / group_size;
+    for (int64_t r = 0; r < rows; ++r) {
+        const uint8_t* qr = q + r * packed_in;
+        const float* sr = scales + r * groups;
+        for (int64_t i = 0; i < in; ++i) {
+            uint8_t b = qr[i >> 1];
+            int v = (i & 1) ? (b >> 4) : (b & 0x0f);
+            out[r * in + i] = (float)(v - 8) * sr[i / group_size];
+        }
+    }
+}
+
+/* Symmetric int4 quantizer: tools/convert_hf_to_glmserve.py:216-252
+ * (scale = max|x_g| / 7, 1.0 when the group is all zero; q = clip(rint(x/s),
+ * -8, 7) + 8; low nibble = even column). */
+void orc_quantize_w4_rows(const float* w, int64_t rows, int64_t in, int64_t group_size,
+                          uint8_t* q, float* scales) {
+    int64_t packed_in = (in + 1) / 2, groups = (in + group_size - 1) / group_size;
+    memset(q, 0, (size_t)(rows * packed_in));
+    for (int64_t r = 0; r < rows; ++r) {
+        for (int64_t g = 0; g < groups; ++g) {
+            int64_t c0 = g * group_size, c1 = c0 + group_size < in ? c0 + group_size : in;
+            float amax = 0.0f;
+            for (int64_t i = c0; i < c1; ++i) {
+                float a = fabsf(w[r * in + i]);
+                if (a > amax) amax = a;
+            }
+            float s = amax / 7.0f;
+            if (!(s > 0.0f)) s = 1.0f;
+            scales[r * groups + g] = s;
+            for (int64_t i = c0; i < c1; ++i) {
+                float v = rintf(w[r * in + i] / s);
+                if (v < -8.0f) v = -8.0f;
+                if (v > 7.0f) v = 7.0f;
+                int qi = (int)v + 8;
+                q[r * packed_in + (i >> 1)] |= (uint8_t)((i & 1) ? (qi << 4) : qi);
+            }
+        }
+    }
+}
+
+/* ---------------------------------------------------------------------------
+ * Whole layer: GLM52Model::moe_mlp, src/model_glm52.cpp:1096-1154.
+ * Per token: route (above), then for each slot kk in selection order
+ *   g = gate.x, u = up.x (linear_forward), h = silu(g)*u, tmp = down.h,
+ *   out += w[kk]*tmp; then the shared expert adds with weight 1.
+ * out starts at zero (:1107).
+ * ------------------------------------------------------------------------- */
+typedef struct {
+    const float* x;
+    int64_t n, H, I, S;
+    int E, topk;
+    const float* logits;
+    const float* e_bias;
+    const float* const* gate;
+    const float* const* up;
+    const float* const* down;
+    const float *sh_gate, *sh_up, *sh_down;
+    int norm_topk;
+    float routed_scale;
+    float* out;
+    int* ids;
+    float* w;
+    int64_t t0, t1;
+    int status;
+} orc_job;
+
+static void orc_ffn(const float* xt, const float* g_w, const float* u_w, const float* d_w,
+                    int64_t H, int64_t I, float* g, float* u, float* tmp) {
+    orc_linear_f32(xt, g_w, 1, H, I, g);
+    orc_linear_f32(xt, u_w, 1, H, I, u);
+    for (int64_t i = 0; i < I; ++i) g[i] = orc_silu(g[i]) * u[i];
+    orc_linear_f32(g, d_w, 1, I, H, tmp);
+}
+
+static void* orc_moe_worker(void* arg) {
+    orc_job* j = (orc_job*)arg;
+    int64_t I = j->I > j->S ? j->I : j->S;
+    float* g = (float*)malloc(sizeof(float) * (size_t)I);
+    float* u = (float*)malloc(sizeof(float) * (size_t)I);
+    float* tmp = (float*)malloc(sizeof(float) * (size_t)j->H);
+    for (int64_t t = j->t0; t < j->t1; ++t) {
+        const float* xt = j->x + t * j->H;
+        int* ids = j->ids + t * j->topk;
+        float* w = j->w + t * j->topk;
+        orc_router_topk(j->logits + t * j->E, j->e_bias, 1, j->E, j->topk, j->norm_topk,
+                        j->routed_scale, ids, w);
+        float* ot = j->out + t * j->H;
+        for (int64_t i = 0; i < j->H; ++i) ot[i] = 0.0f;
+        for (int kk = 0; kk < j->topk; ++kk) {
+            int e = ids[kk];
+            if (!j->gate[e] || !j->up[e] || !j->down[e]) { j->status = -1; continue; }
+            orc_ffn(xt, j->gate[e], j->up[e], j->down[e], j->H, j->I, g, u, tmp);
+            for (int64_t i = 0; i < j->H; ++i) ot[i] = ot[i] + w[kk] * tmp[i];
+        }
+        if (j->sh_gate) {
+            orc_ffn(xt, j->sh_gate, j->sh_up, j->sh_down, j->H, j->S, g, u, tmp);
+            for (int64_t i = 0; i < j->H; ++i) ot[i] = ot[i] + tmp[i];
+        }
+    }
+    free(g);
+    free(u);
+    free(tmp);
+    return NULL;
+}
+
+int orc_moe_forward(const float* x, int64_t n, int64_t H, int E, int topk, int64_t I,
+                    int64_t S, const float* router_w, const float* logits_in,
+                    const float* e_bias, const float* const* gate, const float* const* up,
+                    const float* const* down, const float* sh_gate, const float* sh_up,
+                    const float* sh_down, int norm_topk, float routed_scale, int nthreads,
+                    float* out, int* ids_out, float* w_out) {
+    float* logits = NULL;
+    const float* lg = logits_in;
+    if (!lg) {
+        logits = (float*)malloc(sizeof(float) * (size_t)(n * E));
+        orc_linear_f32(x, router_w, n, H, E, logits);
+        lg = logits;
+    }
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > n) nthreads = (int)(n > 0 ? n : 1);
+    orc_job* jobs = (orc_job*)calloc((size_t)nthreads, sizeof(orc_job));
+    pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+    int64_t chunk = (n + nthreads - 1) / nthreads;
+    for (int i = 0; i < nthreads; ++i) {
+        orc_job* j = &jobs[i];
+        j->x = x; j->n = n; j->H = H; j->I = I; j->S = S; j->E = E; j->topk = topk;
+        j->logits = lg; j->e_bias = e_bias; j->gate = gate; j->up = up; j->down = down;
+        j->sh_gate = sh_gate; j->sh_up = sh_up; j->sh_down = sh_down;
+        j->norm_topk = norm_topk; j->routed_scale = routed_scale;
+        j->out = out; j->ids = ids_out; j->w = w_out;
+        j->t0 = i * chunk; j->t1 = (i + 1) * chunk < n ? (i + 1) * chunk : n;
+        if (j->t0 > j->t1) j->t0 = j->t1;
+    }
+    if (nthreads == 1) {
+        orc_moe_worker(&jobs[0]);
+    } else {
+        for (int i = 0; i < nthreads; ++i) pthread_create(&th[i], NULL, orc_moe_worker, &jobs[i]);
+        for (int i = 0; i < nthreads; ++i) pthread_join(th[i], NULL);
+    }
+    int status = 0;
+    for (int i = 0; i < nthreads; ++i) if (jobs[i].status) status = jobs[i].status;
+    free(jobs);
+    free(th);
+    free(logits);
+    return status;
+}

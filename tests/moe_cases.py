@@ -1,0 +1,114 @@
+"""Synthetic MoE layers of the benchmark shapes, shared by tests, smoke and bench.
+
+Layers are generated in the REFERENCE weight layout (cuda/kernels.cuh:259-268:
+packed int4 [rows, K/2], low nibble = even column, value = nibble - 8; scales
+[rows, K/128]) and packed to the native layout on the device by the library.
+Values follow the benchmark definition: int4 codes uniform over [-8, 7],
+scales |N(0, 0.01)| in bf16, router weights bf16 N(0, 0.02), correction bias
+U(-0.1, 0.1), activations bf16 N(0, 1).
+"""
+import numpy as np
+import torch
+
+
+def bf16_bits(a):
+    """fp32 numpy -> bf16 bit patterns (round to nearest even)."""
+    a = np.ascontiguousarray(a, np.float32)
+    b = a.view(np.uint32).astype(np.uint64)
+    b = (b + 0x7FFF + ((b >> 16) & 1)) >> 16
+    return b.astype(np.uint16)
+
+
+def bits_to_f32(u16):
+    return (np.ascontiguousarray(u16, np.uint16).astype(np.uint32) << 16).view(np.float32)
+
+
+def zipf_log_prior(E, s, gen):
+    """log-prior -s*ln(rank+1) over a seeded permutation of the experts."""
+    perm = torch.randperm(E, generator=gen, device="cpu")
+    rank = torch.empty(E, dtype=torch.float32)
+    rank[perm] = torch.arange(E, dtype=torch.float32)
+    return -s * torch.log(rank + 1.0)
+
+
+class SynthLayer:
+    """A W4A16 MoE layer generated on the GPU from a seed (reference layout kept
+    for the oracle), plus its packed device form."""
+
+    def __init__(self, H, E, k, I, seed=0, shared=True, zipf_s=None, device="cuda",
+                 norm_topk=True, routed_scale=2.5):
+        from glmserve_amd import W4A16MoELayer, pack_w4a16
+        self.H, self.E, self.k, self.I = H, E, k, I
+        self.norm_topk, self.routed_scale = norm_topk, routed_scale
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        gc = torch.Generator(device="cpu")
+        gc.manual_seed(seed + 7)
+        dev = device
+        self.router_w = (0.02 * torch.randn(E, H, generator=g, device=dev)).to(torch.bfloat16)
+        bias = (torch.rand(E, generator=gc) * 0.2 - 0.1)
+        if zipf_s is not None:
+            bias = bias + zipf_log_prior(E, zipf_s, gc)
+        self.e_bias = bias.to(torch.float32).to(dev)
+
+        def mat(n, rows, K):
+            q = torch.randint(0, 256, (n, rows, K // 2), generator=g, device=dev, dtype=torch.uint8)
+            s = (0.01 * torch.randn(n, rows, K // 128, generator=g, device=dev)).abs().to(torch.bfloat16)
+            return q, s
+
+        self.gate = mat(E, I, H)
+        self.up = mat(E, I, H)
+        self.down = mat(E, H, I)
+        self.shared = (mat(1, I, H), mat(1, I, H), mat(1, H, I)) if shared else None
+        pk = lambda m, rows, K: pack_w4a16(m[0], m[1], m[0].shape[0], rows, K)
+        sh_packed = None
+        if shared:
+            sh_packed = (pk(self.shared[0], I, H), pk(self.shared[1], I, H), pk(self.shared[2], H, I))
+        self.layer = W4A16MoELayer(H, I, E, k, self.router_w, self.e_bias, pk(self.gate, I, H),
+                                   pk(self.up, I, H), pk(self.down, H, I), sh_packed,
+                                   norm_topk=norm_topk, routed_scale=routed_scale)
+
+    def x(self, n, seed):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        return torch.randn(n, self.H, generator=g, device="cuda").to(torch.bfloat16)
+
+    # ---- oracle side (host) -------------------------------------------------
+    def dequant_expert(self, oracle, e):
+        """fp32 (gate, up, down) of routed expert e (or the shared one for e == E)."""
+        mats = self.shared if e == self.E else (self.gate, self.up, self.down)
+        idx = 0 if e == self.E else e
+        out = []
+        for (q, s), (rows, K) in zip(mats, [(self.I, self.H), (self.I, self.H), (self.H, self.I)]):
+            qn = q[idx].cpu().numpy()
+            sn = s[idx].float().cpu().numpy()
+            out.append(oracle.dequant_int4_rows(qn, sn, K, 128))
+        return out
+
+    def oracle_forward(self, oracle, x_bf16, tokens, logits, nthreads=8):
+        """Oracle layer output for the given token indices, with the given logits
+        (routing redone by the oracle from them). Materializes only the experts
+        those tokens select."""
+        xf = bits_to_f32(x_bf16[tokens].view(torch.int16).cpu().numpy().view(np.uint16))
+        lg = np.ascontiguousarray(logits[tokens], np.float32)
+        eb = self.e_bias.cpu().numpy()
+        ids, _ = oracle.router_topk(lg, eb, self.k, self.norm_topk, self.routed_scale)
+        need = sorted(set(ids.ravel().tolist()))
+        gate = [None] * self.E
+        up = [None] * self.E
+        down = [None] * self.E
+        for e in need:
+            gate[e], up[e], down[e] = self.dequant_expert(oracle, e)
+        sh = self.dequant_expert(oracle, self.E) if self.shared is not None else None
+        return oracle.moe_forward(xf, self.E, self.k, gate, up, down, sh, logits=lg, e_bias=eb,
+                                  norm_topk=self.norm_topk, routed_scale=self.routed_scale,
+                                  nthreads=nthreads)
+
+
+def rel_err(got, ref):
+    """max|got - ref| / max|ref|: the reference's tests/test_qgemm.cpp:17-26
+    check() without its max(1, .) floor, which would make small-magnitude
+    layers pass on absolute error alone."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    return float(np.max(np.abs(got - ref)) / max(1e-30, float(np.max(np.abs(ref)))))
