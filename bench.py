@@ -123,6 +123,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-tokens", type=int, default=16)
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--copy-calib", action="store_true",
+                    help="only run a 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -132,6 +134,14 @@ def main():
     import torch
     from moe_cases import SynthLayer
     assert torch.cuda.is_available(), "bench.py needs a GPU"
+    if args.copy_calib:
+        src = torch.ones(1 << 28, dtype=torch.float32, device="cuda")  # 1 GiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calib_bytes": src.numel() * 4, "reps": 3}))
+        return
     log("bench: building synthetic W4A16 layer H=6144 E=256 k=8 I=2048 (+shared)")
     L = SynthLayer(H, E, K, I, seed=1)
     torch.cuda.synchronize()
