@@ -111,11 +111,10 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     if (rc) return rc;
     const ExpertPtrs P = ptrs(L);
     mark(GLMMOE_STAGE_GATE_UP, s);
-    rc = launch_gate_up(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.hsum, H,
-                        I, E, s);
+    rc = launch_gate_up(P, x, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_DOWN, s);
-    rc = launch_down(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
+    rc = launch_down(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_COMBINE, s);
     rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s);

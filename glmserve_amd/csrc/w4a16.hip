@@ -70,199 +70,360 @@ int launch_pack_w4(const uint8_t* q, const void* sc, int sc_bf16, int n_mats, in
 }
 
 // ---------------------------------------------------------------------------
-// Grouped gate/up + SiLU.
+// Grouped expert products (decode / small-group regime).
+//
+// One kernel template serves both projections:
+//   NMAT = 2: gate and up of the same 16 features, SiLU(g) * u epilogue,
+//             B operand = activation rows gathered through rows_tok;
+//   NMAT = 1: down, B operand = the contiguous grouped h rows.
 // Lane l: r = l & 15 is both the weight row (A operand) and the token column
 // (B operand / output column); q = l >> 4 selects the 32-K quarter of each
 // 128-K tile. MFMA step d (0..3) covers K = 32q + 8d + [0,8) for this lane.
 // Output lane layout: rows 4q + j (j = 0..3), column r.
+//
+// Streaming. Everything a batch of PF 128-K groups needs -- each wave's
+// weight tiles and scales, and the tile's 16 activation rows (shared by the
+// workgroup's 4 waves, which always work on the same tile) -- is copied
+// global -> LDS by the LDS-DMA path (global_load_lds_dwordx4 / _dword), so
+// nothing in flight occupies registers. A ring of D batch slots keeps D-1
+// batches in flight per wave. Every wave issues the same number of DMA
+// instructions per batch (kDma), so "batch b has landed" is the immediate
+// s_waitcnt vmcnt(kDma * (D - 2)); one s_barrier per batch then publishes the
+// shared rows and frees the oldest slot. The pipeline runs across work items
+// (a wave's items are w0, w0 + nwaves, ...), so it never drains between
+// them. LDS reads are inline ds_read_b128 with their own lgkmcnt wait, which
+// keeps the compiler from inserting a vmcnt(0) for the pending DMA. Their
+// outputs are early-clobber: a read returns asynchronously, so no output may
+// share a register with an address still needed by a later read.
+//
+// The group sum X_j = sum_k x[k][j] that removes the +136 bias of the int4
+// decode comes from one more MFMA against an all-ones A operand.
 // ---------------------------------------------------------------------------
-struct GuArgs {
-    const uint4* gq; const uint4* uq; const uint16_t* gs; const uint16_t* us;
-    const uint4* sgq; const uint4* suq; const uint16_t* sgs; const uint16_t* sus;
-    const uint16_t* x; const float* xsum;
+struct ExpArgs {
+    const uint4* wq[2];      // routed experts, stacked native matrices
+    const uint16_t* ws[2];
+    const uint4* swq[2];     // shared expert
+    const uint16_t* sws[2];
+    const uint16_t* src;     // x [n, H] (NMAT = 2) or h [R, I] (NMAT = 1)
     const int4* tiles; const int* ntiles; const int* rows_tok;
-    uint16_t* h; float* hsum;
+    uint16_t* h; float* dpart;
     int H, I, E;
 };
 
-template <int NB>
-__global__ __launch_bounds__(256) void w4_gate_up_kernel(GuArgs a) {
-    const int lane = threadIdx.x & 63;
+typedef __attribute__((address_space(3))) char lds_char;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const lds_char*)p;
+}
+
+// 64 lanes x 16 B from per-lane global addresses to lds_base + 16 * lane.
+__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_char*)lds_base, 16, 0, 0);
+}
+// 64 lanes x 4 B to lds_base + 4 * lane.
+__device__ __forceinline__ void dma4(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_char*)lds_base, 4, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+constexpr int kTable = 32;     // item-table steps per refill
+constexpr int kTabInts = 20;   // ints per step
+
+template <int NMAT, int PF, int D>
+struct Ring {
+    static_assert(PF == 2 || PF == 4, "a batch row span is 512 or 1024 bytes");
+    static constexpr int kW = 1024;                           // one weight tile
+    static constexpr int kWBytes = 4 * NMAT * PF * kW;        // all waves' tiles
+    static constexpr int kSBytes = 4 * 256;                   // scale dwords per wave
+    static constexpr int kSpan = PF * 256;                    // bytes of one row per batch
+    static constexpr int kRPI = 1024 / kSpan;                 // rows per 1 KiB DMA
+    static constexpr int kPair = 1024 + 16;                   // padded stride of one DMA
+    static constexpr int kXBytes = (16 / kRPI) * kPair;
+    static constexpr int kSlot = kWBytes + kSBytes + kXBytes;
+    static constexpr int kBytes = D * kSlot;
+    static constexpr int kTotal = kBytes + kTable * kTabInts * 4;   // + the item table
+    static constexpr int kXDma = 4 / kRPI;                    // activation DMAs per wave
+    static constexpr int kDma = NMAT * PF + 1 + kXDma;        // DMA instructions per batch per wave
+    // Byte offset of activation row r inside the slot's activation area.
+    static __device__ __forceinline__ int row_off(int r) { return (r / kRPI) * kPair + (r % kRPI) * kSpan; }
+};
+
+// Work items of a workgroup come in steps k: the 4 waves take items
+// base + wave + k * nwaves, which share one tile. A chunk of up to kTable
+// steps is described in an LDS table read back with inline ds_read (no
+// vector-memory loads inside the pipeline, whose waits would drain the DMA
+// queue): per step {expert, row0, nrows, feature block of wave 0} and the 16
+// token ids of the tile rows (row 0's token past nrows).
+
+struct Item {
+    const uint4* wq[2];
+    const uint16_t* ws[2];
+    int r0, nr, fb;
+    int tok[4];   // tokens (NMAT = 2) or grouped rows (NMAT = 1) of this wave's 4 staged rows
+};
+
+__device__ __forceinline__ uint4 lds_bcast16(uint32_t addr) {
+    uint4 v;
+    asm volatile("ds_read_b128 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ int sgpr(uint32_t v) { return __builtin_amdgcn_readfirstlane((int)v); }
+
+template <int NMAT>
+__device__ __forceinline__ Item item_from_table(const ExpArgs& a, const int* table, int k,
+                                                int wave, int nfb, int KG) {
+    const uint32_t base = lds_addr(table + k * kTabInts);
+    const uint4 h = lds_bcast16(base);
+    const uint4 t = lds_bcast16(base + 16 + wave * 16);
+    Item it;
+    const int e = sgpr(h.x);
+    it.r0 = sgpr(h.y);
+    it.nr = sgpr(h.z);
+    it.fb = sgpr(h.w) + wave;
+    if (NMAT == 2) {
+        it.tok[0] = sgpr(t.x); it.tok[1] = sgpr(t.y); it.tok[2] = sgpr(t.z); it.tok[3] = sgpr(t.w);
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const int row = wave * 4 + j;
+            it.tok[j] = it.r0 + (row < it.nr ? row : 0);
+        }
+    }
+    const bool sh = e == a.E;
+    const size_t mstride_q = (size_t)nfb * KG * 64;   // uint4 per matrix
+    const size_t mstride_s = (size_t)nfb * KG * 16;   // u16 per matrix
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        const int mm = m < NMAT ? m : 0;
+        it.wq[m] = (sh ? a.swq[mm] : a.wq[mm] + (size_t)e * mstride_q) + (size_t)it.fb * KG * 64;
+        it.ws[m] = (sh ? a.sws[mm] : a.ws[mm] + (size_t)e * mstride_s) + (size_t)it.fb * KG * 16;
+    }
+    return it;
+}
+
+// Fills table steps [k0, k0 + cnt) (whole workgroup; ordinary loads; the
+// caller has drained all DMA and synchronizes afterwards).
+__device__ __forceinline__ void fill_table(const ExpArgs& a, int* table, long base, long nwaves,
+                                           int nfb, long k0, int cnt) {
+    for (int i = threadIdx.x; i < cnt * kTabInts; i += blockDim.x) {
+        const int k = i / kTabInts, f = i % kTabInts;
+        const long item = base + (k0 + k) * nwaves;
+        const int4 tile = a.tiles[item / nfb];
+        int v;
+        if (f == 0) v = tile.x;
+        else if (f == 1) v = tile.y;
+        else if (f == 2) v = tile.z;
+        else if (f == 3) v = (int)(item % nfb);
+        else {
+            const int row = f - 4;
+            v = a.rows_tok ? a.rows_tok[tile.y + (row < tile.z ? row : 0)] : 0;
+        }
+        table[i] = v;
+    }
+}
+
+// Issues batch bb of item `it` into ring slot `slot` (exactly kDma DMAs).
+template <int NMAT, int PF, int D>
+__device__ __forceinline__ void issue_batch(const ExpArgs& a, const Item& it, int bb, int K,
+                                            int KG, char* slot, int wave, int lane) {
+    using RG = Ring<NMAT, PF, D>;
+    const int kg0 = bb * PF;
+    // Weight tiles: [wave][m][i] 1 KiB each, lane-contiguous like the global tile.
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+        for (int i = 0; i < PF; ++i) {
+            const int kg = min(kg0 + i, KG - 1);
+            dma16(it.wq[m] + (size_t)kg * 64 + lane, slot + ((wave * NMAT + m) * PF + i) * RG::kW);
+        }
+    // Scales: lane l < NMAT*PF*8 fetches dword (l % 8) of group (l / 8) % PF of matrix
+    // l / (PF*8); the 16 bf16 scales of a (matrix, group) are 8 dwords.
+    {
+        const int m = min(lane / (PF * 8), NMAT - 1);
+        const int d = lane % (PF * 8);
+        const int kg = min(kg0 + d / 8, KG - 1);
+        dma4(it.ws[m] + (size_t)kg * 16 + (d % 8) * 2, slot + RG::kWBytes + wave * 256);
+    }
+    // Activation rows 4*wave .. 4*wave+3 of the tile, kRPI rows per DMA (row r0
+    // stands in past nr; those token columns are computed but never stored).
+#pragma unroll
+    for (int j = 0; j < RG::kXDma; ++j) {
+        const int sub = lane / (64 / RG::kRPI);          // row inside this DMA
+        const int li = lane % (64 / RG::kRPI);           // 16-byte chunk inside the row
+        const int jr = j * RG::kRPI + sub;               // 0..3: which of this wave's rows
+        size_t srow = (size_t)it.tok[0];
+#pragma unroll
+        for (int t = 1; t < 4; ++t) srow = jr == t ? (size_t)it.tok[t] : srow;
+        const int koff = min(kg0 * 128 + li * 8, K - 8);  // bf16 offset of this lane's 16 B
+        const int row0 = wave * 4 + j * RG::kRPI;         // first row of this DMA
+        dma16(a.src + srow * K + koff,
+              slot + RG::kWBytes + RG::kSBytes + (row0 / RG::kRPI) * RG::kPair);
+    }
+}
+
+template <int NMAT, int PF, int D>
+__device__ __forceinline__ void compute_batch(const char* slot, int bb, int KG, int wave,
+                                              int lane, f32x4 (&acc)[NMAT]) {
+    using RG = Ring<NMAT, PF, D>;
     const int r = lane & 15, q = lane >> 4;
-    const int KG = a.H / 128;
-    const int nfb = a.I / 16;
-    const long total = (long)(*a.ntiles) * nfb;
-    const long nwaves = (long)gridDim.x * 4;
-    for (long w = (long)blockIdx.x * 4 + (threadIdx.x >> 6); w < total; w += nwaves) {
-        const int4 tile = a.tiles[w / nfb];
-        const int fb = (int)(w % nfb);
-        const int e = tile.x, r0 = tile.y, nr = tile.z;
-        const bool sh = e == a.E;
-        const size_t mstride_q = (size_t)nfb * KG * 64;   // uint4 per matrix
-        const size_t mstride_s = (size_t)nfb * KG * 16;   // u16 per matrix
-        const uint4* gq = (sh ? a.sgq : a.gq + (size_t)e * mstride_q) + (size_t)fb * KG * 64;
-        const uint4* uq = (sh ? a.suq : a.uq + (size_t)e * mstride_q) + (size_t)fb * KG * 64;
-        const uint16_t* gs = (sh ? a.sgs : a.gs + (size_t)e * mstride_s) + (size_t)fb * KG * 16;
-        const uint16_t* us = (sh ? a.sus : a.us + (size_t)e * mstride_s) + (size_t)fb * KG * 16;
-        const int nb = (nr + 15) >> 4;
-
-        const uint16_t* xrow[NB];
-        const float* xsr[NB];
-        bool valid[NB];
+    const uint32_t wbase = lds_addr(slot) + (uint32_t)(wave * NMAT * PF * RG::kW + lane * 16);
+    const uint32_t sbase = lds_addr(slot + RG::kWBytes + wave * 256) + (uint32_t)(q * 8);
+    const uint32_t xbase = lds_addr(slot + RG::kWBytes + RG::kSBytes) + (uint32_t)(RG::row_off(r) + q * 64);
+    // bf16 1.0 in every element: the A operand of the group-sum MFMA.
+    const bf16x8 ones = __builtin_bit_cast(bf16x8, uint4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            valid[b] = b * 16 + r < nr;
-            const int tok = valid[b] ? a.rows_tok[r0 + b * 16 + r] : 0;
-            xrow[b] = a.x + (size_t)tok * a.H + 32 * q;
-            xsr[b] = a.xsum + (size_t)tok * KG;
+    for (int i = 0; i < PF; ++i) {
+        const bool live = bb * PF + i < KG;
+        uint4 x0, x1, x2, x3, w0, w1;
+        uint2 s0, s1;
+        const uint32_t xa = xbase + i * 256;
+        const uint32_t wa = wbase + i * RG::kW;
+        const uint32_t sa = sbase + i * 32;
+        if constexpr (NMAT == 2) {
+            asm volatile(
+                "ds_read_b128 %0, %8\n"
+                "ds_read_b128 %1, %8 offset:16\n"
+                "ds_read_b128 %2, %8 offset:32\n"
+                "ds_read_b128 %3, %8 offset:48\n"
+                "ds_read_b128 %4, %9\n"
+                "ds_read_b128 %5, %9 offset:%c11\n"
+                "ds_read_b64 %6, %10\n"
+                "ds_read_b64 %7, %10 offset:%c12\n"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(w0), "=&v"(w1), "=&v"(s0),
+                  "=&v"(s1)
+                : "v"(xa), "v"(wa), "v"(sa), "i"(PF * RG::kW), "i"(PF * 32));
+        } else {
+            asm volatile(
+                "ds_read_b128 %0, %6\n"
+                "ds_read_b128 %1, %6 offset:16\n"
+                "ds_read_b128 %2, %6 offset:32\n"
+                "ds_read_b128 %3, %6 offset:48\n"
+                "ds_read_b128 %4, %7\n"
+                "ds_read_b64 %5, %8\n"
+                "s_waitcnt lgkmcnt(0)"
+                : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(w0), "=&v"(s0)
+                : "v"(xa), "v"(wa), "v"(sa));
+            w1 = w0;
+            s1 = s0;
         }
-        f32x4 accg[NB], accu[NB];
+        f32x4 px = {0.f, 0.f, 0.f, 0.f};
+        px = mfma16x16x32(ones, as_bf16x8(x0), px);
+        px = mfma16x16x32(ones, as_bf16x8(x1), px);
+        px = mfma16x16x32(ones, as_bf16x8(x2), px);
+        px = mfma16x16x32(ones, as_bf16x8(x3), px);
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            accg[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-            accu[b] = f32x4{0.f, 0.f, 0.f, 0.f};
-        }
-
-        for (int kg = 0; kg < KG; ++kg) {
-            const uint4 wg = gq[(size_t)kg * 64 + lane];
-            const uint4 wu = uq[(size_t)kg * 64 + lane];
-            const uint2 sgv = *reinterpret_cast<const uint2*>(gs + (size_t)kg * 16 + 4 * q);
-            const uint2 suv = *reinterpret_cast<const uint2*>(us + (size_t)kg * 16 + 4 * q);
-            const float sg[4] = {bf16_to_f32(sgv.x & 0xffffu), bf16_to_f32(sgv.x >> 16),
-                                 bf16_to_f32(sgv.y & 0xffffu), bf16_to_f32(sgv.y >> 16)};
-            const float su[4] = {bf16_to_f32(suv.x & 0xffffu), bf16_to_f32(suv.x >> 16),
-                                 bf16_to_f32(suv.y & 0xffffu), bf16_to_f32(suv.y >> 16)};
-            const bf16x8 ag0 = dq_w4(wg.x), ag1 = dq_w4(wg.y), ag2 = dq_w4(wg.z), ag3 = dq_w4(wg.w);
-            const bf16x8 au0 = dq_w4(wu.x), au1 = dq_w4(wu.y), au2 = dq_w4(wu.z), au3 = dq_w4(wu.w);
+        for (int m = 0; m < NMAT; ++m) {
+            const uint4 wv = m == 0 ? w0 : w1;
+            const uint2 sv = m == 0 ? s0 : s1;
+            float sc[4];
+            sc[0] = bf16_to_f32(sv.x & 0xffffu); sc[1] = bf16_to_f32(sv.x >> 16);
+            sc[2] = bf16_to_f32(sv.y & 0xffffu); sc[3] = bf16_to_f32(sv.y >> 16);
+            f32x4 p = {0.f, 0.f, 0.f, 0.f};
+            p = mfma16x16x32(dq_w4(wv.x), as_bf16x8(x0), p);
+            p = mfma16x16x32(dq_w4(wv.y), as_bf16x8(x1), p);
+            p = mfma16x16x32(dq_w4(wv.z), as_bf16x8(x2), p);
+            p = mfma16x16x32(dq_w4(wv.w), as_bf16x8(x3), p);
 #pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                if (b >= nb) break;
-                uint4 x0 = {0, 0, 0, 0}, x1 = x0, x2 = x0, x3 = x0;
-                float X = 0.0f;
-                if (valid[b]) {
-                    const uint4* xp = reinterpret_cast<const uint4*>(xrow[b] + kg * 128);
-                    x0 = xp[0]; x1 = xp[1]; x2 = xp[2]; x3 = xp[3];
-                    X = xsr[b][kg];
-                }
-                f32x4 pg = {0.f, 0.f, 0.f, 0.f}, pu = pg;
-                pg = mfma16x16x32(ag0, as_bf16x8(x0), pg);
-                pu = mfma16x16x32(au0, as_bf16x8(x0), pu);
-                pg = mfma16x16x32(ag1, as_bf16x8(x1), pg);
-                pu = mfma16x16x32(au1, as_bf16x8(x1), pu);
-                pg = mfma16x16x32(ag2, as_bf16x8(x2), pg);
-                pu = mfma16x16x32(au2, as_bf16x8(x2), pu);
-                pg = mfma16x16x32(ag3, as_bf16x8(x3), pg);
-                pu = mfma16x16x32(au3, as_bf16x8(x3), pu);
-                const float off = -136.0f * X;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    accg[b][j] = __builtin_fmaf(sg[j], pg[j] + off, accg[b][j]);
-                    accu[b][j] = __builtin_fmaf(su[j], pu[j] + off, accu[b][j]);
-                }
-            }
-        }
-
-        // Epilogue: h = silu(g) * u as bf16; partial group sums of the
-        // rounded h over this block's 16 features.
-#pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            if (b >= nb) break;
-            uint32_t hb[4];
-            float part = 0.0f;
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                const float hv = silu_fast(accg[b][j]) * accu[b][j];
-                hb[j] = f32_to_bf16(hv);
-                part += bf16_to_f32(hb[j]);
-            }
-            part += __shfl_xor(part, 16);
-            part += __shfl_xor(part, 32);
-            if (valid[b]) {
-                const size_t row = (size_t)r0 + b * 16 + r;
-                uint2 st = {hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
-                *reinterpret_cast<uint2*>(a.h + row * a.I + fb * 16 + 4 * q) = st;
-                if (q == 0) a.hsum[row * nfb + fb] = part;
-            }
+            for (int j = 0; j < 4; ++j)
+                acc[m][j] = __builtin_fmaf(live ? sc[j] : 0.0f,
+                                           __builtin_fmaf(-136.0f, px[j], p[j]), acc[m][j]);
         }
     }
 }
 
-// ---------------------------------------------------------------------------
-// Grouped down projection: dpart[row, :] = down_e . h[row, :] (unweighted).
-// ---------------------------------------------------------------------------
-struct DownArgs {
-    const uint4* dq; const uint16_t* ds; const uint4* sdq; const uint16_t* sds;
-    const uint16_t* h; const float* hsum;
-    const int4* tiles; const int* ntiles;
-    float* dpart;
-    int H, I, E;
-};
-
-template <int NB>
-__global__ __launch_bounds__(256) void w4_down_kernel(DownArgs a) {
+template <int NMAT, int PF, int D>
+__global__ __launch_bounds__(256) void w4_expert_kernel(ExpArgs a) {
+    using RG = Ring<NMAT, PF, D>;
+    extern __shared__ __align__(16) char ring[];
     const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, q = lane >> 4;
-    const int KG = a.I / 128;
-    const int nfb = a.H / 16;
-    const int nhs = a.I / 16;   // h partial sums per row
+    const int K = NMAT == 2 ? a.H : a.I;
+    const int KG = K / 128;
+    const int nfb = (NMAT == 2 ? a.I : a.H) / 16;
+    const int nbatch = (KG + PF - 1) / PF;
     const long total = (long)(*a.ntiles) * nfb;
     const long nwaves = (long)gridDim.x * 4;
-    for (long w = (long)blockIdx.x * 4 + (threadIdx.x >> 6); w < total; w += nwaves) {
-        const int4 tile = a.tiles[w / nfb];
-        const int fb = (int)(w % nfb);
-        const int e = tile.x, r0 = tile.y, nr = tile.z;
-        const bool sh = e == a.E;
-        const size_t mstride_q = (size_t)nfb * KG * 64;
-        const size_t mstride_s = (size_t)nfb * KG * 16;
-        const uint4* dq = (sh ? a.sdq : a.dq + (size_t)e * mstride_q) + (size_t)fb * KG * 64;
-        const uint16_t* ds = (sh ? a.sds : a.ds + (size_t)e * mstride_s) + (size_t)fb * KG * 16;
-        const int nb = (nr + 15) >> 4;
-        bool valid[NB];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) valid[b] = b * 16 + r < nr;
-        f32x4 acc[NB];
-#pragma unroll
-        for (int b = 0; b < NB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const long base = (long)blockIdx.x * 4;
+    // Steps of this workgroup (equal for its 4 waves: total and nwaves are
+    // multiples of 4).
+    const long nitems = base < total ? (total - base + nwaves - 1) / nwaves : 0;
+    int* table = reinterpret_cast<int*>(ring + RG::kBytes);
 
-        for (int kg = 0; kg < KG; ++kg) {
-            const uint4 wd = dq[(size_t)kg * 64 + lane];
-            const uint2 sv = *reinterpret_cast<const uint2*>(ds + (size_t)kg * 16 + 4 * q);
-            const float sd[4] = {bf16_to_f32(sv.x & 0xffffu), bf16_to_f32(sv.x >> 16),
-                                 bf16_to_f32(sv.y & 0xffffu), bf16_to_f32(sv.y >> 16)};
-            const bf16x8 a0 = dq_w4(wd.x), a1 = dq_w4(wd.y), a2 = dq_w4(wd.z), a3 = dq_w4(wd.w);
-#pragma unroll
-            for (int b = 0; b < NB; ++b) {
-                if (b >= nb) break;
-                uint4 x0 = {0, 0, 0, 0}, x1 = x0, x2 = x0, x3 = x0;
-                float X = 0.0f;
-                if (valid[b]) {
-                    const size_t row = (size_t)r0 + b * 16 + r;
-                    const uint4* hp =
-                        reinterpret_cast<const uint4*>(a.h + row * a.I + kg * 128 + 32 * q);
-                    x0 = hp[0]; x1 = hp[1]; x2 = hp[2]; x3 = hp[3];
-                    const float4* hs = reinterpret_cast<const float4*>(a.hsum + row * nhs + kg * 8);
-                    const float4 s0 = hs[0], s1 = hs[1];
-                    X = ((s0.x + s0.y) + (s0.z + s0.w)) + ((s1.x + s1.y) + (s1.z + s1.w));
+    for (long k0 = 0; k0 < nitems; k0 += kTable) {
+        const int cnt = (int)min((long)kTable, nitems - k0);
+        fill_table(a, table, base, nwaves, nfb, k0, cnt);
+        __syncthreads();
+        const long nsteps = (long)cnt * nbatch;
+
+        // Prologue: batches 0 .. D-2 in flight.
+        int iss_k = 0, iss_b = 0;
+        Item iss = item_from_table<NMAT>(a, table, 0, wave, nfb, KG);
+        for (int j = 0; j < D - 1; ++j) {
+            if (j < nsteps) {
+                issue_batch<NMAT, PF, D>(a, iss, iss_b, K, KG, ring + (j % D) * RG::kSlot, wave,
+                                         lane);
+                if (++iss_b == nbatch) {
+                    iss_b = 0;
+                    if (++iss_k < cnt) iss = item_from_table<NMAT>(a, table, iss_k, wave, nfb, KG);
                 }
-                f32x4 p = {0.f, 0.f, 0.f, 0.f};
-                p = mfma16x16x32(a0, as_bf16x8(x0), p);
-                p = mfma16x16x32(a1, as_bf16x8(x1), p);
-                p = mfma16x16x32(a2, as_bf16x8(x2), p);
-                p = mfma16x16x32(a3, as_bf16x8(x3), p);
-                const float off = -136.0f * X;
-#pragma unroll
-                for (int j = 0; j < 4; ++j) acc[b][j] = __builtin_fmaf(sd[j], p[j] + off, acc[b][j]);
             }
         }
+
+        int cur_k = 0, cur_b = 0;
+        Item cur = item_from_table<NMAT>(a, table, 0, wave, nfb, KG);
+        f32x4 acc[NMAT];
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-            if (b >= nb) break;
-            if (valid[b]) {
-                const size_t row = (size_t)r0 + b * 16 + r;
-                *reinterpret_cast<float4*>(a.dpart + row * a.H + fb * 16 + 4 * q) =
-                    make_float4(acc[b][0], acc[b][1], acc[b][2], acc[b][3]);
+        for (int m = 0; m < NMAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        for (long step = 0; step < nsteps; ++step) {
+            // Batch `step` has landed once at most (D-2) newer batches are pending.
+            if (step + D - 2 < nsteps) wait_vmcnt<RG::kDma * (D - 2)>();
+            else wait_vmcnt<0>();
+            __builtin_amdgcn_s_barrier();
+            if (step + D - 1 < nsteps) {
+                issue_batch<NMAT, PF, D>(a, iss, iss_b, K, KG,
+                                         ring + ((step + D - 1) % D) * RG::kSlot, wave, lane);
+                if (++iss_b == nbatch) {
+                    iss_b = 0;
+                    if (++iss_k < cnt) iss = item_from_table<NMAT>(a, table, iss_k, wave, nfb, KG);
+                }
+            }
+            compute_batch<NMAT, PF, D>(ring + (step % D) * RG::kSlot, cur_b, KG, wave, lane, acc);
+
+            if (++cur_b == nbatch) {
+                const bool valid = r < cur.nr;
+                const size_t row = (size_t)cur.r0 + r;
+                if constexpr (NMAT == 2) {
+                    uint32_t hb[4];
+#pragma unroll
+                    for (int j = 0; j < 4; ++j)
+                        hb[j] = f32_to_bf16(silu_fast(acc[0][j]) * acc[1][j]);
+                    if (valid) {
+                        uint2 v = {hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
+                        *reinterpret_cast<uint2*>(a.h + row * a.I + cur.fb * 16 + 4 * q) = v;
+                    }
+                } else {
+                    if (valid)
+                        *reinterpret_cast<float4*>(a.dpart + row * a.H + cur.fb * 16 + 4 * q) =
+                            make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
+                }
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+                cur_b = 0;
+                if (++cur_k < cnt) cur = item_from_table<NMAT>(a, table, cur_k, wave, nfb, KG);
             }
         }
+        // All DMA has landed (the last step waited vmcnt(0)); every wave is
+        // done reading the ring and the table before the next chunk refills.
+        __syncthreads();
     }
 }
 
@@ -293,39 +454,59 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-static int grid_for(long max_work) {
+// Ring depth per projection; both fit the 160 KiB of LDS of one workgroup.
+// Batches of 2 groups keep two 4-wave workgroups resident per CU (8 waves).
+constexpr int kRingGU = 3;
+constexpr int kRingDown = 4;
+constexpr int kPFGU = 2;
+constexpr int kPFDown = 2;
+
+template <int NMAT, int PF, int D>
+static int launch_expert(const ExpArgs& a, long max_work, hipStream_t s) {
+    using RG = Ring<NMAT, PF, D>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4_expert_kernel<NMAT, PF, D>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, RG::kTotal) !=
+            hipSuccess)
+            return -4;
+        attr_set = true;
+    }
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    // As many workgroups as fit in LDS at once; persistent over items.
+    const int per_cu = (160 * 1024) / RG::kTotal;
     long blocks = (max_work + 3) / 4;
-    if (blocks > 4096) blocks = 4096;
+    if (blocks > (long)cus * per_cu) blocks = (long)cus * per_cu;
     if (blocks < 1) blocks = 1;
-    return (int)blocks;
-}
-
-int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
-                   const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
-                   float* hsum, int H, int I, int E, hipStream_t s) {
-    GuArgs a;
-    a.gq = reinterpret_cast<const uint4*>(P.gate_q); a.uq = reinterpret_cast<const uint4*>(P.up_q);
-    a.gs = P.gate_s; a.us = P.up_s;
-    a.sgq = reinterpret_cast<const uint4*>(P.sh_gate_q); a.suq = reinterpret_cast<const uint4*>(P.sh_up_q);
-    a.sgs = P.sh_gate_s; a.sus = P.sh_up_s;
-    a.x = x; a.xsum = xsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
-    a.rows_tok = rows_tok; a.h = h; a.hsum = hsum; a.H = H; a.I = I; a.E = E;
-    hipLaunchKernelGGL(w4_gate_up_kernel<kTileRows / 16>, dim3(grid_for((long)max_tiles * (I / 16))),
-                       dim3(256), 0, s, a);
+    hipLaunchKernelGGL((w4_expert_kernel<NMAT, PF, D>), dim3((unsigned)blocks), dim3(256),
+                       RG::kTotal, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
-                const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
-                hipStream_t s) {
-    DownArgs a;
-    a.dq = reinterpret_cast<const uint4*>(P.down_q); a.ds = P.down_s;
-    a.sdq = reinterpret_cast<const uint4*>(P.sh_down_q); a.sds = P.sh_down_s;
-    a.h = h; a.hsum = hsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
+int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const int* tiles, const int* ntiles,
+                   int max_tiles, const int* rows_tok, uint16_t* h, int H, int I, int E,
+                   hipStream_t s) {
+    ExpArgs a{};
+    a.wq[0] = reinterpret_cast<const uint4*>(P.gate_q); a.ws[0] = P.gate_s;
+    a.wq[1] = reinterpret_cast<const uint4*>(P.up_q); a.ws[1] = P.up_s;
+    a.swq[0] = reinterpret_cast<const uint4*>(P.sh_gate_q); a.sws[0] = P.sh_gate_s;
+    a.swq[1] = reinterpret_cast<const uint4*>(P.sh_up_q); a.sws[1] = P.sh_up_s;
+    a.src = x; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
+    a.rows_tok = rows_tok; a.h = h; a.H = H; a.I = I; a.E = E;
+    return launch_expert<2, kPFGU, kRingGU>(a, (long)max_tiles * (I / 16), s);
+}
+
+int launch_down(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
+                int max_tiles, float* dpart, int H, int I, int E, hipStream_t s) {
+    ExpArgs a{};
+    a.wq[0] = reinterpret_cast<const uint4*>(P.down_q); a.ws[0] = P.down_s;
+    a.swq[0] = reinterpret_cast<const uint4*>(P.sh_down_q); a.sws[0] = P.sh_down_s;
+    a.wq[1] = a.wq[0]; a.ws[1] = a.ws[0]; a.swq[1] = a.swq[0]; a.sws[1] = a.sws[0];
+    a.src = h; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.dpart = dpart; a.H = H; a.I = I; a.E = E;
-    hipLaunchKernelGGL(w4_down_kernel<kTileRows / 16>, dim3(grid_for((long)max_tiles * (H / 16))),
-                       dim3(256), 0, s, a);
-    return hipGetLastError() == hipSuccess ? 0 : -4;
+    return launch_expert<1, kPFDown, kRingDown>(a, (long)max_tiles * (H / 16), s);
 }
 
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,

@@ -55,7 +55,7 @@ def _check_routing(oracle, L, x, logits, ids, w, offs, st, sr):
     return ref_logits
 
 
-@pytest.mark.parametrize("n", [1, 7, 64])
+@pytest.mark.parametrize("n", [1, 7, 64, 300])
 def test_tiny_config(oracle, n):
     # configs[0] geometry: H 256, 16 experts, top-4, I = S = 128.
     L = SynthLayer(256, 16, 4, 128, seed=11)
@@ -65,7 +65,7 @@ def test_tiny_config(oracle, n):
     assert rel_err(out, ref) < TOL_W4A16
 
 
-@pytest.mark.parametrize("n", [1, 8])
+@pytest.mark.parametrize("n", [1, 8, 64])
 def test_decode_full_shape(oracle, n):
     # configs[1] geometry: H 6144, 256 experts, top-8, I = S = 2048.
     L = SynthLayer(6144, 256, 8, 2048, seed=1)

@@ -1,0 +1,107 @@
+"""GPU routing and dispatch through the reference-named entry points
+(moe_router / moe_dispatch, cuda/kernels.cuh:243-250), bit-exact vs the oracle."""
+import numpy as np
+import pytest
+import torch
+
+import glmserve_amd as G
+
+pytestmark = pytest.mark.gpu
+
+
+def _route(logits, bias, k, norm=True, scale=2.5):
+    n, E = logits.shape
+    lg = torch.from_numpy(logits).cuda()
+    b = None if bias is None else torch.from_numpy(bias).cuda()
+    ids = torch.empty(n, k, dtype=torch.int32, device="cuda")
+    w = torch.empty(n, k, dtype=torch.float32, device="cuda")
+    G.moe_router(lg, b, n, E, k, norm, scale, ids, w)
+    torch.cuda.synchronize()
+    return ids.cpu().numpy(), w.cpu().numpy()
+
+
+CASES = [
+    # (n, E, k, norm, scale, bias) -- the reference test's shape first
+    # (tests/test_moe_router.cpp:19-25: n=7, E=32, topk=4, norm, x2.5).
+    (7, 32, 4, True, 2.5, "normal"),
+    (64, 16, 4, True, 2.5, "uniform"),
+    (64, 256, 8, True, 2.5, "uniform"),
+    (33, 256, 8, False, 1.0, None),
+    (5, 100, 8, True, 2.5, "uniform"),    # E not a multiple of 64
+    (9, 512, 8, True, 2.5, "uniform"),    # largest supported E
+    (3, 8, 8, True, 2.5, "uniform"),      # topk == E
+    (1, 1, 1, True, 2.5, None),
+]
+
+
+@pytest.mark.parametrize("n,E,k,norm,scale,bias", CASES)
+def test_router_matches_oracle(oracle, n, E, k, norm, scale, bias):
+    rng = np.random.default_rng(n * 1000 + E)
+    logits = rng.standard_normal((n, E)).astype(np.float32)
+    b = None
+    if bias == "normal":
+        b = (0.05 * rng.standard_normal(E)).astype(np.float32)
+    elif bias == "uniform":
+        b = rng.uniform(-0.1, 0.1, E).astype(np.float32)
+    ids, w = _route(logits, b, k, norm, scale)
+    rid, rw = oracle.router_topk(logits, b, k, norm, scale)
+    assert np.array_equal(ids, rid)
+    assert np.array_equal(w.view(np.uint32), rw.view(np.uint32))
+
+
+def test_router_ties_and_specials(oracle):
+    n, E, k = 6, 64, 8
+    logits = np.zeros((n, E), np.float32)            # all scores equal -> lowest ids
+    logits[1, ::7] = 3.0                             # ties among the raised ones
+    logits[2] = -200.0                               # saturated scores, wsum tiny
+    logits[3, 5] = np.nan                            # NaN never beats a number
+    logits[4] = np.linspace(-1, 1, E, dtype=np.float32)[::-1]
+    logits[5] = 1e30                                 # saturated high
+    bias = np.zeros(E, np.float32)
+    bias[10] = 0.5                                   # bias flips selection but not weight
+    ids, w = _route(logits, bias, k)
+    rid, rw = oracle.router_topk(logits, bias, k)
+    assert np.array_equal(ids, rid)
+    assert np.array_equal(w.view(np.uint32), rw.view(np.uint32))
+    assert ids[0, 0] == 10 and list(ids[0, 1:]) == list(range(7))
+
+
+@pytest.mark.parametrize("n,k,E,mode", [(1, 8, 256, "rand"), (64, 8, 256, "rand"),
+                                        (4096, 8, 256, "rand"), (520, 8, 256, "skew"),
+                                        (100, 4, 16, "one"), (37, 3, 5, "rand"),
+                                        (8192, 8, 256, "rand")])
+def test_dispatch_matches_oracle(oracle, n, k, E, mode):
+    rng = np.random.default_rng(n + k + E)
+    if mode == "rand":
+        ids = np.stack([rng.permutation(E)[:k] for _ in range(n)]).astype(np.int32)
+    elif mode == "skew":
+        p = 1.0 / np.arange(1, E + 1) ** 1.1
+        p /= p.sum()
+        ids = np.stack([rng.choice(E, k, replace=False, p=p) for _ in range(n)]).astype(np.int32)
+    else:  # every token on the same experts
+        ids = np.tile(np.arange(k, dtype=np.int32), (n, 1))
+    d_ids = torch.from_numpy(ids).cuda()
+    off = torch.full((E + 1,), -7, dtype=torch.int32, device="cuda")
+    st = torch.full((n * k,), -7, dtype=torch.int32, device="cuda")
+    sr = torch.full((n * k,), -7, dtype=torch.int32, device="cuda")
+    G.moe_dispatch(d_ids, n, k, E, off, st, sr)
+    torch.cuda.synchronize()
+    roff, rst, rsr = oracle.dispatch(ids, E)
+    assert np.array_equal(off.cpu().numpy(), roff)
+    assert np.array_equal(st.cpu().numpy(), rst)
+    assert np.array_equal(sr.cpu().numpy(), rsr)
+
+
+def test_router_logits_bit_exact(oracle):
+    from moe_cases import bf16_bits
+    rng = np.random.default_rng(5)
+    for n, H, E in [(1, 6144, 256), (13, 6144, 256), (64, 256, 16), (3, 1000, 7)]:
+        x = bf16_bits(rng.standard_normal((n, H)))
+        w = bf16_bits(0.02 * rng.standard_normal((E, H)))
+        dx = torch.from_numpy(x.view(np.int16)).cuda().view(torch.bfloat16)
+        dw = torch.from_numpy(w.view(np.int16)).cuda().view(torch.bfloat16)
+        lg = torch.empty(n, E, dtype=torch.float32, device="cuda")
+        G.router_logits(dx, dw, lg)
+        torch.cuda.synchronize()
+        ref = oracle.router_logits_bf16(x, w)
+        assert np.array_equal(lg.cpu().numpy().view(np.uint32), ref.view(np.uint32)), (n, H, E)
