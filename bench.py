@@ -123,6 +123,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--cpu-tokens", type=int, default=16)
     ap.add_argument("--no-sweep", action="store_true")
+    ap.add_argument("--head-batch", type=int, default=64,
+                    help="batch of the headline line (64 = configs[1]'s largest); for profiling")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     args = ap.parse_args()
@@ -159,8 +161,8 @@ def main():
                 "stage_ms": st, "gate_up_bytes": gu_bytes,
                 "gate_up_GBps": gu_bytes / (gu_ms * 1e-3) / 1e9 if gu_ms else None}
 
-    log("bench: headline B=64")
-    head = measure(64, args.steps, args.warmup)
+    log(f"bench: headline B={args.head_batch}")
+    head = measure(args.head_batch, args.steps, args.warmup)
     sweep = {}
     if not args.no_sweep:
         for n in (1, 8, 32):
@@ -168,7 +170,7 @@ def main():
             sweep[f"decode_B{n}"] = measure(n, args.steps, args.warmup)
         log("bench: sweep prefill 4096")
         sweep["prefill_4096"] = measure(4096, max(3, args.steps // 10), 2)
-    sweep["decode_B64"] = head
+    sweep[f"decode_B{args.head_batch}"] = head
 
     gu_ms = head["stage_ms"]["gate_up"]
     roof = {"bound": "hbm", "kernel": "w4_gate_up_kernel (decode B=64)",

@@ -7,7 +7,7 @@
 // cuda/qgemm.cu:966-989 (whose order inside an expert is nondeterministic).
 // Here the order is the reference's stable one and the work is parallel:
 //   1. LDS histogram (atomics on counts only: order-free),
-//   2. block scan over experts,
+//   2. a one-wave prefix scan over experts,
 //   3. rows in chunks of 1024 in input order; inside a wave, equal expert ids
 //      are matched with one ballot per id bit (rank = lanes below with the
 //      same id); across the 16 waves of a chunk, per-wave counts in LDS give
@@ -22,20 +22,34 @@ constexpr int kDispThreads = 1024;
 constexpr int kDispWaves = kDispThreads / 64;
 constexpr int kDispMaxE = 512;
 
-// Inclusive block scan of one int per thread over kDispThreads threads.
-__device__ int block_scan_incl(int v, int* sh) {
-    const int tid = threadIdx.x;
-    sh[tid] = v;
-    __syncthreads();
-    for (int off = 1; off < kDispThreads; off <<= 1) {
-        const int add = tid >= off ? sh[tid - off] : 0;
-        __syncthreads();
-        sh[tid] += add;
-        __syncthreads();
+// Exclusive prefix of vals[0..count) (count <= 512) into pre[0..count], pre[count] =
+// total, by wave 0 alone: each lane sums 8 consecutive entries, then a wave
+// scan of the lane sums. Callers synchronize before and after.
+__device__ void wave0_exclusive_scan(const int* vals, int count, int* pre) {
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x >= 64) return;
+    int local[8];
+    int sum = 0;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int i = lane * 8 + j;
+        local[j] = i < count ? vals[i] : 0;
+        sum += local[j];
     }
-    const int r = sh[tid];
-    __syncthreads();
-    return r;
+    int incl = sum;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+        const int t = __shfl_up(incl, off);
+        if (lane >= off) incl += t;
+    }
+    int run = incl - sum;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+        const int i = lane * 8 + j;
+        if (i < count) pre[i] = run;
+        run += local[j];
+    }
+    if (lane == 63) pre[count] = incl;
 }
 
 // mode bit 0: also emit inv[], shared rows and the tile list (layer path).
@@ -47,7 +61,8 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
     __shared__ int cnt[kDispMaxE + 1];
     __shared__ int cursor[kDispMaxE + 1];
     __shared__ int wc[kDispWaves][kDispMaxE];
-    __shared__ int scan[kDispThreads];
+    __shared__ int pre[kDispMaxE + 2];
+    __shared__ int ntl[kDispMaxE + 1];
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int total = n * topk;
     int nbits = 0;
@@ -62,14 +77,13 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
     }
     __syncthreads();
 
-    // Exclusive prefix over experts (E <= 512 < kDispThreads).
-    const int myc = tid < E ? cnt[tid] : 0;
-    const int incl = block_scan_incl(myc, scan);
-    if (tid < E) {
-        offsets[tid] = incl - myc;
-        cursor[tid] = incl - myc;
+    // Exclusive prefix over experts.
+    wave0_exclusive_scan(cnt, E, pre);
+    __syncthreads();
+    for (int e = tid; e <= E; e += kDispThreads) {
+        offsets[e] = pre[e];
+        if (e < E) cursor[e] = pre[e];
     }
-    if (tid == E - 1) offsets[E] = incl;
     if ((mode & 1) && tid == 0) offsets[E + 1] = total + (with_shared ? n : 0);
     __syncthreads();
 
@@ -90,9 +104,9 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
         if (leader) wc[wv][e] = __popcll(m);
         __syncthreads();
         if (valid) {
-            int pre = 0;
-            for (int w = 0; w < wv; ++w) pre += wc[w][e];
-            const int pos = cursor[e] + pre + rank;
+            int earlier = 0;
+            for (int w = 0; w < wv; ++w) earlier += wc[w][e];
+            const int pos = cursor[e] + earlier + rank;
             sorted_tok[pos] = i / topk;
             sorted_slot[pos] = i % topk;
             if (mode & 1) inv[i] = pos;
@@ -117,18 +131,21 @@ __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
     // Tile list: expert e (e == E is the shared expert) contributes
     // ceil(count / tile_rows) tiles of at most tile_rows consecutive rows.
     const int nexp = E + (with_shared ? 1 : 0);
-    const int ce = tid < E ? cnt[tid] : (tid == E && with_shared ? n : 0);
-    const int nt = tid < nexp ? (ce + tile_rows - 1) / tile_rows : 0;
-    const int tincl = block_scan_incl(nt, scan);
-    if (tid < nexp) {
-        const int row0 = tid < E ? cursor[tid] - ce : total;  // cursor ended at offset+count
-        int tbase = tincl - nt;
-        for (int j = 0; j < nt; ++j) {
-            const int r0 = row0 + j * tile_rows;
-            tiles[tbase + j] = make_int4(tid, r0, min(tile_rows, ce - j * tile_rows), 0);
-        }
+    for (int e = tid; e < nexp; e += kDispThreads) {
+        const int ce = e < E ? cnt[e] : n;
+        ntl[e] = (ce + tile_rows - 1) / tile_rows;
     }
-    if (tid == kDispThreads - 1) *ntiles = tincl;
+    __syncthreads();
+    wave0_exclusive_scan(ntl, nexp, pre);
+    __syncthreads();
+    for (int e = tid; e < nexp; e += kDispThreads) {
+        const int ce = e < E ? cnt[e] : n;
+        const int row0 = e < E ? cursor[e] - ce : total;  // cursor ended at offset + count
+        const int tbase = pre[e];
+        for (int j = 0; j < ntl[e]; ++j)
+            tiles[tbase + j] = make_int4(e, row0 + j * tile_rows, min(tile_rows, ce - j * tile_rows), 0);
+    }
+    if (tid == 0) *ntiles = pre[nexp];
 }
 
 int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,

@@ -96,25 +96,35 @@ __global__ __launch_bounds__(256) void xsum_kernel(const uint16_t* __restrict__ 
 
 // ---------------------------------------------------------------------------
 // Top-k. One wave per token; lane l owns experts l, l+64, ... (E <= 512).
-// Candidate order: finite/inf choose values descending, ties to the lower
-// expert index (cuda/moe_router.cu:48-53), NaN after every number. Each of
-// the k rounds takes a lane-local best (ascending expert order, strict >),
-// then a butterfly arg-max across the wave; the total order makes every lane
-// agree on the winner.
+// Each candidate is one 64-bit key whose unsigned order is the selection
+// order of cuda/moe_router.cu:48-53: high word = choose mapped to a
+// monotone unsigned code (NaN just above "no candidate", below every number),
+// low word = ~expert, so equal choose values prefer the lower expert index.
+// Each of the k rounds: every lane offers its best untaken key; a max over
+// each 16-lane row with DPP row rotations (VALU latency, no LDS round trip),
+// then the 4 row maxima via readlane and a scalar max. The owner lane of
+// the winner retires it. Every lane sees the same winner (a uniform value).
 // ---------------------------------------------------------------------------
 constexpr int kMaxPerLane = 8;  // E <= 512
 
-struct Cand {
-    float c;   // choose
-    float s;   // unbiased score
-    int e;     // expert id, INT_MAX when none
-    int cls;   // 2 = number, 1 = NaN, 0 = none
-};
+__device__ __forceinline__ uint32_t order_code(float f) {
+    if (f != f) return 1u;
+    if (f == 0.0f) f = 0.0f;   // -0 == +0: equal values fall through to the index
+    const uint32_t u = __float_as_uint(f);
+    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
 
-__device__ __forceinline__ bool better(const Cand& a, const Cand& b) {
-    if (a.cls != b.cls) return a.cls > b.cls;
-    if (a.cls == 2 && a.c != b.c) return a.c > b.c;
-    return a.e < b.e;
+__device__ __forceinline__ void kmax(uint32_t& h, uint32_t& l, uint32_t oh, uint32_t ol) {
+    const bool take = oh > h || (oh == h && ol > l);
+    h = take ? oh : h;
+    l = take ? ol : l;
+}
+
+template <int CTRL>
+__device__ __forceinline__ void kmax_dpp(uint32_t& h, uint32_t& l) {
+    const uint32_t oh = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)h, CTRL, 0xf, 0xf, false);
+    const uint32_t ol = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)l, CTRL, 0xf, 0xf, false);
+    kmax(h, l, oh, ol);
 }
 
 __global__ __launch_bounds__(256) void router_topk_kernel(
@@ -122,51 +132,58 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     int norm_topk, float routed_scale, int* __restrict__ topk_ids, float* __restrict__ topk_w) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= n) return;
+    if (t >= n) return;   // whole wave
     const float* lt = logits + (size_t)t * E;
-    float score[kMaxPerLane], choose[kMaxPerLane];
-    int cnt = 0;
+    float score[kMaxPerLane];
+    uint32_t ch[kMaxPerLane];   // order codes, 0 = no candidate / taken
 #pragma unroll
     for (int j = 0; j < kMaxPerLane; ++j) {
         const int e = lane + 64 * j;
+        score[j] = 0.0f;
+        ch[j] = 0u;
         if (e < E) {
             const float sc = sigmoid_fixed(lt[e]);
             score[j] = sc;
-            choose[j] = sc + (e_bias ? e_bias[e] : 0.0f);
-            cnt = j + 1;
-        } else {
-            score[j] = 0.0f;
-            choose[j] = 0.0f;
+            ch[j] = order_code(sc + (e_bias ? e_bias[e] : 0.0f));
         }
     }
-    uint32_t taken = 0;
     float wsel[8];
     int idsel[8];
     float wsum = 0.0f;
 #pragma unroll
     for (int k = 0; k < 8; ++k) {
         if (k >= topk) break;
-        Cand best{0.0f, 0.0f, 0x7fffffff, 0};
+        // Lane-local best (ascending j == ascending expert; strict > keeps lower).
+        uint32_t h = 0u, l = 0u;
+#pragma unroll
+        for (int j = 0; j < kMaxPerLane; ++j)
+            kmax(h, l, ch[j], ch[j] ? ~(uint32_t)(lane + 64 * j) : 0u);
+        // Row max (row_ror:1,2,4,8 over 16 lanes), then across the 4 rows.
+        kmax_dpp<0x121>(h, l);
+        kmax_dpp<0x122>(h, l);
+        kmax_dpp<0x124>(h, l);
+        kmax_dpp<0x128>(h, l);
+        uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)h, 0);
+        uint32_t bl = (uint32_t)__builtin_amdgcn_readlane((int)l, 0);
+        kmax(bh, bl, (uint32_t)__builtin_amdgcn_readlane((int)h, 16),
+             (uint32_t)__builtin_amdgcn_readlane((int)l, 16));
+        kmax(bh, bl, (uint32_t)__builtin_amdgcn_readlane((int)h, 32),
+             (uint32_t)__builtin_amdgcn_readlane((int)l, 32));
+        kmax(bh, bl, (uint32_t)__builtin_amdgcn_readlane((int)h, 48),
+             (uint32_t)__builtin_amdgcn_readlane((int)l, 48));
+        const int e = (int)~bl;               // uniform winner
+        const int owner = e & 63, jw = e >> 6;
+        float sw = 0.0f;
 #pragma unroll
         for (int j = 0; j < kMaxPerLane; ++j) {
-            if (j < cnt && !((taken >> j) & 1u)) {
-                Cand c{choose[j], score[j], lane + 64 * j, (choose[j] != choose[j]) ? 1 : 2};
-                if (better(c, best)) best = c;
+            if (j == jw) {
+                sw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score[j]), owner));
+                if (lane == owner) ch[j] = 0u;
             }
         }
-#pragma unroll
-        for (int off = 32; off > 0; off >>= 1) {
-            Cand o;
-            o.c = __shfl_xor(best.c, off);
-            o.s = __shfl_xor(best.s, off);
-            o.e = __shfl_xor(best.e, off);
-            o.cls = __shfl_xor(best.cls, off);
-            if (better(o, best)) best = o;
-        }
-        if ((best.e & 63) == lane) taken |= 1u << (best.e >> 6);
-        idsel[k] = best.e;
-        wsel[k] = best.s;
-        wsum = wsum + best.s;
+        idsel[k] = e;
+        wsel[k] = sw;
+        wsum = wsum + sw;
     }
     if (lane == 0) {
 #pragma unroll
