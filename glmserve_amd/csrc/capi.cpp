@@ -13,16 +13,23 @@ inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+// Tile height of the expert GEMMs for a batch: 16-row tiles (decode kernels)
+// or 128-row tiles (large-group kernels).
+inline int tile_rows_for(int n, int topk, int with_shared) {
+    return (long)n * topk + (with_shared ? n : 0) >= kBigMinRows ? kBigRows : kTileRows;
+}
+
 int max_tiles_for(int n, int topk, int E, int with_shared) {
     // sum_e ceil(c_e / T) <= (n*topk)/T + E, plus ceil(n/T) shared tiles.
-    return (n * topk) / kTileRows + E + (with_shared ? (n + kTileRows - 1) / kTileRows : 0) + 1;
+    const int T = tile_rows_for(n, topk, with_shared);
+    return (n * topk) / T + E + (with_shared ? (n + T - 1) / T : 0) + 1;
 }
 
 int check_layer(const glmmoe_w4a16_layer* L, int n) {
     if (!L || n <= 0) return GLMMOE_ERR_ARG;
     if (L->hidden <= 0 || L->moe_inter <= 0 || L->n_experts <= 0 || L->topk <= 0)
         return GLMMOE_ERR_ARG;
-    if (L->hidden % 128 || L->moe_inter % 128 || L->hidden > 8192) return GLMMOE_ERR_SHAPE;
+    if (L->hidden % 256 || L->moe_inter % 128 || L->hidden > 8192) return GLMMOE_ERR_SHAPE;
     if (L->n_experts > 512 || L->topk > 8 || L->topk > L->n_experts) return GLMMOE_ERR_SHAPE;
     if (!L->gate_q || !L->gate_s || !L->up_q || !L->up_s || !L->down_q || !L->down_s)
         return GLMMOE_ERR_ARG;
@@ -105,16 +112,20 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
     const int sh = has_shared(L) ? 1 : 0;
     const int mt = max_tiles_for(n, k, E, sh);
+    const int T = tile_rows_for(n, k, sh);
+    const bool big = T == kBigRows;
     mark(GLMMOE_STAGE_DISPATCH, s);
     int rc = launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids, v.sorted_row,
-                             v.inv, v.tiles, v.ntiles, kTileRows, sh, 1, s);
+                             v.inv, v.tiles, v.ntiles, T, sh, 1, s);
     if (rc) return rc;
     const ExpertPtrs P = ptrs(L);
     mark(GLMMOE_STAGE_GATE_UP, s);
-    rc = launch_gate_up(P, x, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, H, I, E, s);
+    rc = big ? launch_gate_up_big(P, x, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, H, I, E, s)
+             : launch_gate_up(P, x, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_DOWN, s);
-    rc = launch_down(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
+    rc = big ? launch_down_big(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
+             : launch_down(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_COMBINE, s);
     rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s);

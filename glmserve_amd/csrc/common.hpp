@@ -81,4 +81,37 @@ __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
 }
 
+// ---- LDS-DMA streaming helpers --------------------------------------------
+typedef __attribute__((address_space(3))) char lds_char;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+    return (uint32_t)(uintptr_t)(const lds_char*)p;
+}
+
+// 64 lanes x 16 B from per-lane global addresses to lds_base + 16 * lane.
+__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_char*)lds_base, 16, 0, 0);
+}
+// 64 lanes x 4 B to lds_base + 4 * lane.
+__device__ __forceinline__ void dma4(const void* g, void* lds_base) {
+    __builtin_amdgcn_global_load_lds(g, (lds_char*)lds_base, 4, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained (gfx9 encoding).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt range");
+    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
+}
+
+constexpr int kTable = 32;     // item-table steps per refill
+constexpr int kTabInts = 20;   // ints per step
+
+__device__ __forceinline__ uint4 lds_bcast16(uint32_t addr) {
+    uint4 v;
+    asm volatile("ds_read_b128 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ int sgpr(uint32_t v) { return __builtin_amdgcn_readfirstlane((int)v); }
+
 }  // namespace glmmoe

@@ -8,6 +8,10 @@ namespace glmmoe {
 
 // Grouped rows per tile of the decode expert GEMMs (one 16-token MFMA block).
 constexpr int kTileRows = 16;
+// Grouped rows per tile of the large-group (prefill) expert GEMMs.
+constexpr int kBigRows = 128;
+// Grouped rows (n*topk + n) from which the layer uses the large-group kernels.
+constexpr int kBigMinRows = 1024;
 
 struct ExpertPtrs {
     const uint8_t* gate_q; const uint16_t* gate_s;
@@ -33,6 +37,11 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const int* tiles, con
                    hipStream_t s);
 int launch_down(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
                 int max_tiles, float* dpart, int H, int I, int E, hipStream_t s);
+int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, const int* tiles,
+                       const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h, int H,
+                       int I, int E, hipStream_t s);
+int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
+                    int max_tiles, float* dpart, int H, int I, int E, hipStream_t s);
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
                    int with_shared, float* out, hipStream_t s);
 

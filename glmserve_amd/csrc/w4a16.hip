@@ -110,31 +110,6 @@ struct ExpArgs {
     int H, I, E;
 };
 
-typedef __attribute__((address_space(3))) char lds_char;
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-    return (uint32_t)(uintptr_t)(const lds_char*)p;
-}
-
-// 64 lanes x 16 B from per-lane global addresses to lds_base + 16 * lane.
-__device__ __forceinline__ void dma16(const void* g, void* lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_char*)lds_base, 16, 0, 0);
-}
-// 64 lanes x 4 B to lds_base + 4 * lane.
-__device__ __forceinline__ void dma4(const void* g, void* lds_base) {
-    __builtin_amdgcn_global_load_lds(g, (lds_char*)lds_base, 4, 0, 0);
-}
-
-// s_waitcnt vmcnt(N) with expcnt / lgkmcnt left unconstrained (gfx9 encoding).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt range");
-    __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | (0x7 << 4) | (0xF << 8));
-}
-
-constexpr int kTable = 32;     // item-table steps per refill
-constexpr int kTabInts = 20;   // ints per step
-
 template <int NMAT, int PF, int D>
 struct Ring {
     static_assert(PF == 2 || PF == 4, "a batch row span is 512 or 1024 bytes");
@@ -167,13 +142,6 @@ struct Item {
     int r0, nr, fb;
     int tok[4];   // tokens (NMAT = 2) or grouped rows (NMAT = 1) of this wave's 4 staged rows
 };
-
-__device__ __forceinline__ uint4 lds_bcast16(uint32_t addr) {
-    uint4 v;
-    asm volatile("ds_read_b128 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
-    return v;
-}
-__device__ __forceinline__ int sgpr(uint32_t v) { return __builtin_amdgcn_readfirstlane((int)v); }
 
 template <int NMAT>
 __device__ __forceinline__ Item item_from_table(const ExpArgs& a, const int* table, int k,

@@ -74,3 +74,27 @@ def test_decode_full_shape(oracle, n):
     tok = np.arange(min(n, 4))
     ref, _, _ = L.oracle_forward(oracle, x, tok, ref_logits)
     assert rel_err(out[tok], ref) < TOL_W4A16
+
+
+def test_prefill_full_shape(oracle):
+    # 4096 tokens through the large-group kernels.
+    L = SynthLayer(6144, 256, 8, 2048, seed=1)
+    n = 4096
+    x, out, logits, ids, w, offs, st, sr = _run(L, n, seed=3)
+    ref_logits = _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
+    tok = np.array([0, 1, 2047, 4095])
+    ref, _, _ = L.oracle_forward(oracle, x, tok, ref_logits)
+    assert rel_err(out[tok], ref) < TOL_W4A16
+
+
+def test_spec_verify_zipf(oracle):
+    # 8 x 65 tokens, routing skewed by a Zipf(1.1) log-prior.
+    L = SynthLayer(6144, 256, 8, 2048, seed=4, zipf_s=1.1)
+    n = 520
+    x, out, logits, ids, w, offs, st, sr = _run(L, n, seed=6)
+    ref_logits = _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
+    counts = np.diff(offs)
+    assert counts.max() > 100   # the skew really produces large groups
+    tok = np.array([0, 64, 65, 519])
+    ref, _, _ = L.oracle_forward(oracle, x, tok, ref_logits)
+    assert rel_err(out[tok], ref) < TOL_W4A16
