@@ -6,6 +6,8 @@ import ctypes as C
 import os
 
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "libglmmoe.so")
+# Diagnostics only: load a differently built copy of the same library.
+LIB_PATH = os.environ.get("GLMMOE_LIB_PATH", LIB_PATH)
 
 # Every exported symbol of include/glmmoe.h, with its ctypes signature.
 _vp, _i, _f, _sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t

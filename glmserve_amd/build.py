@@ -21,16 +21,19 @@ HIP_FLAGS = [
 ]
 
 
-def build(verbose=False):
-    os.makedirs(OUT_DIR, exist_ok=True)
+def build(verbose=False, out_lib=None, defines=()):
+    """Compiles csrc/ into out_lib (default: the in-tree _lib/libglmmoe.so)."""
+    lib_path = out_lib or LIB
+    out_dir = os.path.dirname(lib_path)
+    os.makedirs(out_dir, exist_ok=True)
     srcs = sorted(glob.glob(os.path.join(CSRC, "*.hip"))) + sorted(
         glob.glob(os.path.join(CSRC, "*.cpp")))
     objs = []
     procs = []
     for src in srcs:
-        obj = os.path.join(OUT_DIR, os.path.basename(src) + ".o")
+        obj = os.path.join(out_dir, os.path.basename(src) + ".o")
         lang = ["-x", "hip"] if src.endswith(".cpp") else []
-        cmd = [HIPCC] + HIP_FLAGS + lang + ["-c", src, "-o", obj]
+        cmd = [HIPCC] + HIP_FLAGS + ["-D" + d for d in defines] + lang + ["-c", src, "-o", obj]
         procs.append((cmd, subprocess.Popen(cmd, stdout=subprocess.PIPE, stderr=subprocess.STDOUT)))
         objs.append(obj)
     failed = False
@@ -44,13 +47,13 @@ def build(verbose=False):
             sys.stderr.write(out + "\n")
     if failed:
         raise RuntimeError("hipcc failed")
-    tmp = LIB + ".tmp"
+    tmp = lib_path + ".tmp"
     subprocess.run([HIPCC, "--offload-arch=gfx950", "-shared", "-fPIC", "-o", tmp] + objs,
                    check=True)
-    os.replace(tmp, LIB)
+    os.replace(tmp, lib_path)
     for o in objs:
         os.remove(o)
-    return LIB
+    return lib_path
 
 
 if __name__ == "__main__":

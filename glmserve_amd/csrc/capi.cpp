@@ -72,7 +72,7 @@ size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v)
     w.tiles = reinterpret_cast<int*>(take(mt * 16));
     w.ntiles = reinterpret_cast<int*>(take(4));
     w.h = reinterpret_cast<uint16_t*>(take(R * I * 2));
-    w.hsum = reinterpret_cast<float*>(take(R * (I / 16) * 4));
+    w.hsum = reinterpret_cast<float*>(take(R * (I / 128) * 4));
     w.dpart = reinterpret_cast<float*>(take(R * H * 4));
     w.bytes = off;
     if (v) *v = w;
@@ -120,11 +120,12 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     if (rc) return rc;
     const ExpertPtrs P = ptrs(L);
     mark(GLMMOE_STAGE_GATE_UP, s);
-    rc = big ? launch_gate_up_big(P, x, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, H, I, E, s)
+    rc = big ? launch_gate_up_big(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h,
+                                  v.hsum, H, I, E, s)
              : launch_gate_up(P, x, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_DOWN, s);
-    rc = big ? launch_down_big(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
+    rc = big ? launch_down_big(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
              : launch_down(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_COMBINE, s);

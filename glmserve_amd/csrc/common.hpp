@@ -10,6 +10,9 @@ constexpr int kWave = 64;
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
+// Native vector types for inline-asm register operands ("+v" needs them).
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 // ---- bf16 -----------------------------------------------------------------
 __device__ __forceinline__ float bf16_to_f32(uint32_t h) { return __uint_as_float(h << 16); }
@@ -65,20 +68,41 @@ __device__ __forceinline__ float silu_fast(float x) {
 // exactly, so each pair costs one shift and one and-or. The -136 offset
 // (128 + 8) is removed after the MFMA with the activation group sum:
 //   sum_k (c_k - 8) x_k = sum_k (128 + c_k) x_k - 136 * sum_k x_k.
-__device__ __forceinline__ bf16x8 dq_w4(uint32_t w) {
-    typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+// The mask 0x000F000F and the bf16 exponent pattern 0x43004300 as opaque
+// registers: with literal constants the compiler emits a separate v_and and
+// v_or (a VOP3 v_and_or_b32 cannot take two literals); with register operands
+// it selects one v_and_or_b32 per pair. Call once at kernel entry, before any
+// MFMA: the moves are inline asm, which the hazard recognizer does not see.
+struct DqConst {
+    uint32_t mask, bias;
+};
+__device__ __forceinline__ DqConst dq_const() {
+    DqConst c;
+    asm volatile("v_mov_b32 %0, 0x000f000f\n v_mov_b32 %1, 0x43004300" : "=v"(c.mask), "=v"(c.bias));
+    return c;
+}
+
+__device__ __forceinline__ bf16x8 dq_w4(uint32_t w, const DqConst& c) {
     u32x4 v;
-    v.x = (w & 0x000F000Fu) | 0x43004300u;
-    v.y = ((w >> 4) & 0x000F000Fu) | 0x43004300u;
-    v.z = ((w >> 8) & 0x000F000Fu) | 0x43004300u;
-    v.w = ((w >> 12) & 0x000F000Fu) | 0x43004300u;
+    v.x = (w & c.mask) | c.bias;
+    v.y = ((w >> 4) & c.mask) | c.bias;
+    v.z = ((w >> 8) & c.mask) | c.bias;
+    v.w = ((w >> 12) & c.mask) | c.bias;
     return __builtin_bit_cast(bf16x8, v);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(uint4 v) { return __builtin_bit_cast(bf16x8, v); }
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 
 __device__ __forceinline__ f32x4 mfma16x16x32(bf16x8 a, bf16x8 b, f32x4 c) {
     return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+// 32x32x16 bf16: A lane l = row l % 32, K 8 (l / 32) + [0, 8); B lane l = column
+// l % 32, same K; D lane l = column l % 32, value i = row 8 (i / 4) + 4 (l / 32) + i % 4.
+__device__ __forceinline__ f32x16 mfma32x32x16(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
 // ---- LDS-DMA streaming helpers --------------------------------------------

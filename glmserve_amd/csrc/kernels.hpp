@@ -37,11 +37,12 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const int* tiles, con
                    hipStream_t s);
 int launch_down(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
                 int max_tiles, float* dpart, int H, int I, int E, hipStream_t s);
-int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, const int* tiles,
-                       const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h, int H,
-                       int I, int E, hipStream_t s);
-int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
-                    int max_tiles, float* dpart, int H, int I, int E, hipStream_t s);
+int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, const float* xsum,
+                       const int* tiles, const int* ntiles, int max_tiles, const int* rows_tok,
+                       uint16_t* h, float* hsum, int H, int I, int E, hipStream_t s);
+int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
+                    const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
+                    hipStream_t s);
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
                    int with_shared, float* out, hipStream_t s);
 

@@ -118,15 +118,20 @@ struct Ring {
     static constexpr int kSBytes = 4 * 256;                   // scale dwords per wave
     static constexpr int kSpan = PF * 256;                    // bytes of one row per batch
     static constexpr int kRPI = 1024 / kSpan;                 // rows per 1 KiB DMA
-    static constexpr int kPair = 1024 + 16;                   // padded stride of one DMA
+    static constexpr int kPair = 1024 + 16 * kRPI;            // padded stride of one DMA
     static constexpr int kXBytes = (16 / kRPI) * kPair;
     static constexpr int kSlot = kWBytes + kSBytes + kXBytes;
     static constexpr int kBytes = D * kSlot;
     static constexpr int kTotal = kBytes + kTable * kTabInts * 4;   // + the item table
+    static_assert(2 * kTotal <= 160 * 1024, "two workgroups per CU");
     static constexpr int kXDma = 4 / kRPI;                    // activation DMAs per wave
     static constexpr int kDma = NMAT * PF + 1 + kXDma;        // DMA instructions per batch per wave
-    // Byte offset of activation row r inside the slot's activation area.
-    static __device__ __forceinline__ int row_off(int r) { return (r / kRPI) * kPair + (r % kRPI) * kSpan; }
+    // Byte offset of chunk 0 of activation row r inside the slot's activation
+    // area. A DMA block holds kRPI rows interleaved at 16 B (chunk c of row r
+    // at block(r / kRPI) + 16 kRPI c + 16 (r % kRPI)); with the block stride
+    // kPair, the 16 rows an MFMA fragment reads fall on distinct banks.
+    static __device__ __forceinline__ int row_off(int r) { return (r / kRPI) * kPair + (r % kRPI) * 16; }
+    static constexpr int kChunk = 16 * kRPI;                  // stride between a row's chunks
 };
 
 // Work items of a workgroup come in steps k: the 4 waves take items
@@ -222,8 +227,8 @@ __device__ __forceinline__ void issue_batch(const ExpArgs& a, const Item& it, in
     // stands in past nr; those token columns are computed but never stored).
 #pragma unroll
     for (int j = 0; j < RG::kXDma; ++j) {
-        const int sub = lane / (64 / RG::kRPI);          // row inside this DMA
-        const int li = lane % (64 / RG::kRPI);           // 16-byte chunk inside the row
+        const int sub = lane % RG::kRPI;                 // row inside this DMA
+        const int li = lane / RG::kRPI;                  // 16-byte chunk inside the row
         const int jr = j * RG::kRPI + sub;               // 0..3: which of this wave's rows
         size_t srow = (size_t)it.tok[0];
 #pragma unroll
@@ -237,12 +242,13 @@ __device__ __forceinline__ void issue_batch(const ExpArgs& a, const Item& it, in
 
 template <int NMAT, int PF, int D>
 __device__ __forceinline__ void compute_batch(const char* slot, int bb, int KG, int wave,
-                                              int lane, f32x4 (&acc)[NMAT]) {
+                                              int lane, const DqConst& dqc, f32x4 (&acc)[NMAT]) {
     using RG = Ring<NMAT, PF, D>;
     const int r = lane & 15, q = lane >> 4;
     const uint32_t wbase = lds_addr(slot) + (uint32_t)(wave * NMAT * PF * RG::kW + lane * 16);
     const uint32_t sbase = lds_addr(slot + RG::kWBytes + wave * 256) + (uint32_t)(q * 8);
-    const uint32_t xbase = lds_addr(slot + RG::kWBytes + RG::kSBytes) + (uint32_t)(RG::row_off(r) + q * 64);
+    const uint32_t xbase =
+        lds_addr(slot + RG::kWBytes + RG::kSBytes) + (uint32_t)(RG::row_off(r) + 4 * q * RG::kChunk);
     // bf16 1.0 in every element: the A operand of the group-sum MFMA.
     const bf16x8 ones = __builtin_bit_cast(bf16x8, uint4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
 #pragma unroll
@@ -250,15 +256,15 @@ __device__ __forceinline__ void compute_batch(const char* slot, int bb, int KG, 
         const bool live = bb * PF + i < KG;
         uint4 x0, x1, x2, x3, w0, w1;
         uint2 s0, s1;
-        const uint32_t xa = xbase + i * 256;
+        const uint32_t xa = xbase + i * 16 * RG::kChunk;   // group i = chunks 16i ..
         const uint32_t wa = wbase + i * RG::kW;
         const uint32_t sa = sbase + i * 32;
         if constexpr (NMAT == 2) {
             asm volatile(
                 "ds_read_b128 %0, %8\n"
-                "ds_read_b128 %1, %8 offset:16\n"
-                "ds_read_b128 %2, %8 offset:32\n"
-                "ds_read_b128 %3, %8 offset:48\n"
+                "ds_read_b128 %1, %8 offset:%c13\n"
+                "ds_read_b128 %2, %8 offset:%c14\n"
+                "ds_read_b128 %3, %8 offset:%c15\n"
                 "ds_read_b128 %4, %9\n"
                 "ds_read_b128 %5, %9 offset:%c11\n"
                 "ds_read_b64 %6, %10\n"
@@ -266,18 +272,20 @@ __device__ __forceinline__ void compute_batch(const char* slot, int bb, int KG, 
                 "s_waitcnt lgkmcnt(0)"
                 : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(w0), "=&v"(w1), "=&v"(s0),
                   "=&v"(s1)
-                : "v"(xa), "v"(wa), "v"(sa), "i"(PF * RG::kW), "i"(PF * 32));
+                : "v"(xa), "v"(wa), "v"(sa), "i"(PF * RG::kW), "i"(PF * 32), "i"(RG::kChunk),
+                  "i"(2 * RG::kChunk), "i"(3 * RG::kChunk));
         } else {
             asm volatile(
                 "ds_read_b128 %0, %6\n"
-                "ds_read_b128 %1, %6 offset:16\n"
-                "ds_read_b128 %2, %6 offset:32\n"
-                "ds_read_b128 %3, %6 offset:48\n"
+                "ds_read_b128 %1, %6 offset:%c9\n"
+                "ds_read_b128 %2, %6 offset:%c10\n"
+                "ds_read_b128 %3, %6 offset:%c11\n"
                 "ds_read_b128 %4, %7\n"
                 "ds_read_b64 %5, %8\n"
                 "s_waitcnt lgkmcnt(0)"
                 : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(w0), "=&v"(s0)
-                : "v"(xa), "v"(wa), "v"(sa));
+                : "v"(xa), "v"(wa), "v"(sa), "i"(RG::kChunk), "i"(2 * RG::kChunk),
+                  "i"(3 * RG::kChunk));
             w1 = w0;
             s1 = s0;
         }
@@ -294,10 +302,10 @@ __device__ __forceinline__ void compute_batch(const char* slot, int bb, int KG, 
             sc[0] = bf16_to_f32(sv.x & 0xffffu); sc[1] = bf16_to_f32(sv.x >> 16);
             sc[2] = bf16_to_f32(sv.y & 0xffffu); sc[3] = bf16_to_f32(sv.y >> 16);
             f32x4 p = {0.f, 0.f, 0.f, 0.f};
-            p = mfma16x16x32(dq_w4(wv.x), as_bf16x8(x0), p);
-            p = mfma16x16x32(dq_w4(wv.y), as_bf16x8(x1), p);
-            p = mfma16x16x32(dq_w4(wv.z), as_bf16x8(x2), p);
-            p = mfma16x16x32(dq_w4(wv.w), as_bf16x8(x3), p);
+            p = mfma16x16x32(dq_w4(wv.x, dqc), as_bf16x8(x0), p);
+            p = mfma16x16x32(dq_w4(wv.y, dqc), as_bf16x8(x1), p);
+            p = mfma16x16x32(dq_w4(wv.z, dqc), as_bf16x8(x2), p);
+            p = mfma16x16x32(dq_w4(wv.w, dqc), as_bf16x8(x3), p);
 #pragma unroll
             for (int j = 0; j < 4; ++j)
                 acc[m][j] = __builtin_fmaf(live ? sc[j] : 0.0f,
@@ -310,6 +318,7 @@ template <int NMAT, int PF, int D>
 __global__ __launch_bounds__(256) void w4_expert_kernel(ExpArgs a) {
     using RG = Ring<NMAT, PF, D>;
     extern __shared__ __align__(16) char ring[];
+    const DqConst dqc = dq_const();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, q = lane >> 4;
@@ -364,7 +373,8 @@ __global__ __launch_bounds__(256) void w4_expert_kernel(ExpArgs a) {
                     if (++iss_k < cnt) iss = item_from_table<NMAT>(a, table, iss_k, wave, nfb, KG);
                 }
             }
-            compute_batch<NMAT, PF, D>(ring + (step % D) * RG::kSlot, cur_b, KG, wave, lane, acc);
+            compute_batch<NMAT, PF, D>(ring + (step % D) * RG::kSlot, cur_b, KG, wave, lane, dqc,
+                                       acc);
 
             if (++cur_b == nbatch) {
                 const bool valid = r < cur.nr;

@@ -96,7 +96,7 @@ int glmmoe_pack_w4a16(const uint8_t* qweight, const void* scales, int scales_dty
  * stacked (expert stride = packed bytes of one matrix). Shared expert
  * pointers may be NULL (no shared expert); when present its intermediate
  * size must equal moe_inter.
- * Limits: hidden % 128 == 0, moe_inter % 128 == 0, hidden <= 8192,
+ * Limits: hidden % 256 == 0, moe_inter % 128 == 0, hidden <= 8192,
  * E <= 512, 1 <= topk <= 8. */
 typedef struct glmmoe_w4a16_layer {
     int hidden;        /* H */
@@ -130,7 +130,7 @@ typedef struct glmmoe_layer_ws {
     int* tiles;           /* [max_tiles * 4]: {expert, row0, nrows, 0} */
     int* ntiles;          /* [1] */
     uint16_t* h;          /* [R, I] bf16 SiLU(gate) * up */
-    float* hsum;          /* [R, I/16] partial sums of h */
+    float* hsum;          /* [R, I/128] group sums of h (large-group path) */
     float* dpart;         /* [R, H] fp32 per-row expert outputs (unweighted) */
     size_t bytes;         /* total workspace bytes */
 } glmmoe_layer_ws;
