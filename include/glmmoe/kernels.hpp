@@ -1,0 +1,94 @@
+// glmmoe/kernels.hpp -- C++ face of the MI355X MoE-layer library with the
+// names and argument lists of glmserve's launch API (cuda/kernels.cuh:241-268)
+// for the MoE hot path.
+//
+// A caller written against kernels.cuh switches by including this header in
+// place of kernels.cuh for the MoE calls and passing hipStream_t streams
+// (any pointer converts to the void* stream parameter). Differences from the
+// reference, by design:
+//   * functions return the C-ABI status (int, 0 = ok) instead of void; a call
+//     site that ignores the result compiles unchanged;
+//   * the router logits come from glmmoe_router_logits (bf16 in, fixed
+//     reduction order) rather than gemm_fp32 on fp32 activations;
+//   * expert weights live in the native packed W4A16 layout produced once at
+//     load time by pack_w4a16 (from the reference's qweight/scales layout), and
+//     the routed + shared expert stage is one call (moe_expert_ffn_w4a16 with a
+//     glmmoe_w4a16_layer) instead of moe_expert_ffn_w4a16 + 3 gemm_w4a16 +
+//     silu_mul + add_inplace.
+// Define GLMMOE_GLMSERVE_NAMESPACE to also make these visible as
+// glmserve::cuda::* (only when kernels.cuh is not included in the same unit).
+#pragma once
+
+#include <cstddef>
+#include <cstdint>
+
+#include "../glmmoe.h"
+
+namespace glmmoe {
+namespace compat {
+
+// cuda/kernels.cuh:243-245
+inline int moe_router(const float* logits, const float* e_bias, int n, int E, int topk,
+                      bool norm_topk, float routed_scale, int* topk_ids, float* topk_weights,
+                      void* s = nullptr) {
+    return glmmoe_moe_router(logits, e_bias, n, E, topk, norm_topk ? 1 : 0, routed_scale,
+                             topk_ids, topk_weights, s);
+}
+
+// cuda/kernels.cuh:249-250
+inline int moe_dispatch(const int* topk_ids, int n, int topk, int E, int* expert_offsets,
+                        int* sorted_token_ids, int* sorted_row, void* s = nullptr) {
+    return glmmoe_moe_dispatch(topk_ids, n, topk, E, expert_offsets, sorted_token_ids,
+                               sorted_row, s);
+}
+
+// Router-logit GEMM (replaces gemm_linear(s.normed, d.router, ...) at
+// src/model_gpu.cpp:1448 for bf16 activations and router weights).
+inline int router_logits(const uint16_t* x_bf16, const uint16_t* wr_bf16, int n, int H, int E,
+                         float* logits, float* xsum = nullptr, void* s = nullptr) {
+    return glmmoe_router_logits(x_bf16, wr_bf16, n, H, E, logits, xsum, s);
+}
+
+// Load-time repack of reference-layout W4 experts (src/model_gpu.cpp:913-1010
+// uploads qweight [E, rows, K/2] and scales [E, rows, K/g]).
+inline int pack_w4a16(const uint8_t* qweight, const float* scales_f32, int n_mats, int rows,
+                      int K, int group_size, uint8_t* packed_q, uint16_t* packed_scales,
+                      void* s = nullptr) {
+    return glmmoe_pack_w4a16(qweight, scales_f32, 0, n_mats, rows, K, group_size, packed_q,
+                             packed_scales, s);
+}
+inline int pack_w4a16_bf16_scales(const uint8_t* qweight, const uint16_t* scales_bf16, int n_mats,
+                                  int rows, int K, int group_size, uint8_t* packed_q,
+                                  uint16_t* packed_scales, void* s = nullptr) {
+    return glmmoe_pack_w4a16(qweight, scales_bf16, 1, n_mats, rows, K, group_size, packed_q,
+                             packed_scales, s);
+}
+
+// Routed + shared experts with caller routing (cuda/kernels.cuh:263-268 plus
+// the shared-expert chain of src/model_gpu.cpp:1486-1494); out is overwritten.
+inline int moe_expert_ffn_w4a16(const glmmoe_w4a16_layer& layer, const uint16_t* x_bf16, int n,
+                                const int* topk_ids, const float* topk_weights, float* out,
+                                void* workspace, size_t workspace_bytes, void* s = nullptr) {
+    return glmmoe_expert_ffn_w4a16(&layer, x_bf16, n, topk_ids, topk_weights, out, workspace,
+                                   workspace_bytes, s);
+}
+
+// The whole MoE branch of run_layer_step (src/model_gpu.cpp:1446-1495).
+inline int moe_layer_w4a16(const glmmoe_w4a16_layer& layer, const uint16_t* x_bf16, int n,
+                           float* out, void* workspace, size_t workspace_bytes,
+                           void* s = nullptr) {
+    return glmmoe_moe_layer_w4a16(&layer, x_bf16, n, out, workspace, workspace_bytes, s);
+}
+
+inline size_t moe_layer_workspace_bytes(const glmmoe_w4a16_layer& layer, int n) {
+    return glmmoe_layer_workspace_bytes(&layer, n);
+}
+
+}  // namespace compat
+}  // namespace glmmoe
+
+#ifdef GLMMOE_GLMSERVE_NAMESPACE
+namespace glmserve {
+namespace cuda = ::glmmoe::compat;
+}
+#endif

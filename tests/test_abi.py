@@ -1,0 +1,111 @@
+"""The C-ABI library without a GPU: it loads, exports every function that
+include/glmmoe.h declares, validates arguments on the host (no HIP call is
+made before the checks), sizes workspaces, and the C++ header compiles
+against it."""
+import ctypes as C
+import os
+import re
+import subprocess
+
+import pytest
+
+from glmserve_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "glmmoe.h")
+
+
+def _declared():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(glmmoe_\w+)\s*\(", text)))
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    L = _lib.lib()
+    names = _declared()
+    assert len(names) >= 10
+    for name in names:
+        assert hasattr(L, name), name
+    # and the Python binding table covers the header exactly
+    assert set(names) == set(_lib.SIGNATURES), set(names) ^ set(_lib.SIGNATURES)
+    assert b"gfx950" in L.glmmoe_version()
+
+
+def test_host_argument_checks():
+    L = _lib.lib()
+    # NULL pointers / non-positive sizes -> GLMMOE_ERR_ARG before any HIP call.
+    assert L.glmmoe_moe_router(None, None, 4, 256, 8, 1, 2.5, None, None, None) == -1
+    assert L.glmmoe_moe_dispatch(None, 4, 8, 256, None, None, None, None) == -1
+    assert L.glmmoe_router_logits(None, None, 1, 6144, 256, None, None, None) == -1
+    dummy = C.c_void_p(16)   # never dereferenced: the shape checks reject first
+    # Shapes outside the kernels' range -> GLMMOE_ERR_SHAPE.
+    assert L.glmmoe_moe_router(dummy, None, 4, 256, 9, 1, 2.5, dummy, dummy, None) == -2
+    assert L.glmmoe_moe_router(dummy, None, 4, 600, 8, 1, 2.5, dummy, dummy, None) == -2
+    assert L.glmmoe_moe_router(dummy, None, 4, 4, 8, 1, 2.5, dummy, dummy, None) == -2
+    assert L.glmmoe_moe_dispatch(dummy, 4, 8, 513, dummy, dummy, dummy, None) == -2
+    assert L.glmmoe_router_logits(dummy, dummy, 1, 6145, 256, dummy, None, None) == -2
+    assert L.glmmoe_pack_w4a16(dummy, dummy, 0, 1, 15, 128, 128, dummy, dummy, None) == -2
+    assert L.glmmoe_pack_w4a16(dummy, dummy, 0, 1, 16, 100, 128, dummy, dummy, None) == -2
+    assert L.glmmoe_pack_w4a16(dummy, dummy, 0, 1, 16, 128, 64, dummy, dummy, None) == -2
+    assert L.glmmoe_pack_w4a16(dummy, dummy, 2, 1, 16, 128, 128, dummy, dummy, None) == -1
+
+
+def _layer(H=6144, I=2048, E=256, k=8, shared=True):
+    st = _lib.Layer()
+    st.hidden, st.moe_inter, st.n_experts, st.topk = H, I, E, k
+    st.norm_topk, st.routed_scale = 1, 2.5
+    p = 4096
+    for f in ("router_w", "gate_q", "gate_s", "up_q", "up_s", "down_q", "down_s"):
+        setattr(st, f, p)
+    if shared:
+        for f in ("sh_gate_q", "sh_gate_s", "sh_up_q", "sh_up_s", "sh_down_q", "sh_down_s"):
+            setattr(st, f, p)
+    return st
+
+
+def test_workspace_sizing_and_view():
+    L = _lib.lib()
+    st = _layer()
+    for n in (1, 64, 4096):
+        b = L.glmmoe_layer_workspace_bytes(C.byref(st), n)
+        assert b > 0
+        v = _lib.LayerWs()
+        base = 1 << 20
+        assert L.glmmoe_layer_workspace_view(C.byref(st), n, C.c_void_p(base), C.byref(v)) == 0
+        assert v.bytes == b
+        R = n * 8 + n
+        # regions are 256-byte aligned, ordered, inside [base, base + bytes)
+        regions = [v.logits, v.xsum, v.topk_ids, v.topk_w, v.expert_offsets, v.sorted_token_ids,
+                   v.sorted_row, v.inv, v.tiles, v.ntiles, v.h, v.hsum, v.dpart]
+        assert all(r % 256 == 0 for r in regions)
+        assert regions == sorted(regions) and regions[0] == base
+        assert v.dpart + R * 6144 * 4 <= base + b
+        assert v.h + R * 2048 * 2 <= v.hsum
+    # Unsupported layers size to 0 and are rejected.
+    assert L.glmmoe_layer_workspace_bytes(C.byref(_layer(H=6000)), 4) == 0
+    assert L.glmmoe_layer_workspace_bytes(C.byref(_layer(k=9)), 4) == 0
+    bad = _layer()
+    bad.sh_up_q = None          # a partial shared expert is an argument error
+    assert L.glmmoe_layer_workspace_bytes(C.byref(bad), 4) == 0
+    assert L.glmmoe_moe_layer_w4a16(C.byref(_layer()), C.c_void_p(16), 4, C.c_void_p(16),
+                                    C.c_void_p(16), 16, None) == -3
+
+
+def test_cpp_header_compiles_against_the_library(tmp_path):
+    src = tmp_path / "use.cpp"
+    src.write_text(
+        '#define GLMMOE_GLMSERVE_NAMESPACE\n'
+        '#include "glmmoe/kernels.hpp"\n'
+        'int main() {\n'
+        '  // reference call sites, unchanged apart from the include\n'
+        '  glmserve::cuda::moe_router(nullptr, nullptr, 1, 256, 8, true, 2.5f, nullptr, nullptr);\n'
+        '  glmserve::cuda::moe_dispatch(nullptr, 1, 8, 256, nullptr, nullptr, nullptr);\n'
+        '  glmmoe_w4a16_layer L{};\n'
+        '  return (int)glmserve::cuda::moe_layer_workspace_bytes(L, 1);\n'
+        '}\n')
+    exe = tmp_path / "use"
+    r = subprocess.run(["g++", "-std=c++17", "-I", os.path.join(ROOT, "include"), str(src), "-o",
+                        str(exe), _lib.LIB_PATH, "-Wl,-rpath," + os.path.dirname(_lib.LIB_PATH)],
+                       capture_output=True, text=True)
+    assert r.returncode == 0, r.stderr
