@@ -72,19 +72,21 @@ def stage_times(L, n, bufs, steps, torch):
     return {s: (ms[i] / cnt[i] if cnt[i] else None) for i, s in enumerate(STAGES)}
 
 
-def cpu_baseline(L, n_sample, torch):
+def cpu_baseline(L, n_sample, torch, seed):
     """The reference CPU MoE path (GLM52Model::moe_mlp compiled from the
     reference sources, oracle/_ref) -- or this build's C restatement when the
-    compiled reference is absent -- on a bounded sample of the B=64 batch:
-    one token per call with only that token's experts materialized in fp32
-    (dequantized, as the reference's CPU path holds them). Only the moe_mlp
-    calls are timed."""
+    compiled reference is absent -- on the headline batch itself (the same
+    seeded activations): one moe_mlp call per token with only that token's
+    experts materialized in fp32 (dequantized, as the reference's CPU path
+    holds them). The reference runs a batch below 256 tokens on one thread
+    (src/model_glm52.cpp:28-39), so per-token calls cost what one call would.
+    Only the moe_mlp calls are timed."""
     import numpy as np
     from moe_cases import bits_to_f32
     from oracle import load_oracle, load_ref
     oracle = load_oracle()
     ref = load_ref()
-    x = L.x(64, seed=123)
+    x = L.x(max(n_sample, 1), seed=seed)
     xb = x.view(torch.int16).cpu().numpy().view(np.uint16)
     xf = bits_to_f32(xb)
     wr = L.router_w.float().cpu().numpy()
@@ -109,10 +111,23 @@ def cpu_baseline(L, n_sample, torch):
     threads_used = 1  # the reference's parallel_for runs serially below 256 tokens
     return {"value": n_sample / total, "unit": "tokens/s", "cores": threads_used,
             "kind": "reference" if ref is not None else "port",
-            "sample": f"{n_sample} tokens of the B=64 decode batch, one moe_mlp call per token "
+            "sample": f"{n_sample} tokens of the headline decode batch, one moe_mlp call per token "
                       f"(n=1, serial as in the reference), fp32 dequantized weights; "
                       f"{total:.2f} s of timed CPU work; host hardware_concurrency="
                       f"{ref.hardware_concurrency() if ref is not None else os.cpu_count()}"}
+
+
+def profiled_traffic():
+    """HBM bytes per gate/up launch at B=64 from the committed rocprofv3 summary
+    (FETCH_SIZE / WRITE_SIZE passes scaled by a copy-kernel calibration)."""
+    path = os.path.join(ROOT, "profiles", "w4_expert_gate_up_decode_B64.md")
+    try:
+        for line in open(path):
+            if line.startswith("traffic_bytes_per_launch:"):
+                return float(line.split(":")[1])
+    except OSError:
+        pass
+    return None
 
 
 def main():
@@ -121,7 +136,8 @@ def main():
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=10)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
-    ap.add_argument("--cpu-tokens", type=int, default=16)
+    ap.add_argument("--cpu-tokens", type=int, default=64,
+                    help="tokens of the headline batch timed on the CPU (64 = all of B=64)")
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--head-batch", type=int, default=64,
                     help="batch of the headline line (64 = configs[1]'s largest); for profiling")
@@ -173,15 +189,17 @@ def main():
     sweep[f"decode_B{args.head_batch}"] = head
 
     gu_ms = head["stage_ms"]["gate_up"]
-    roof = {"bound": "hbm", "kernel": "w4_gate_up_kernel (decode B=64)",
+    roof = {"bound": "hbm", "kernel": f"w4_expert_kernel<2,2,3> grouped gate/up (decode B={args.head_batch})",
             "achieved": head["gate_up_GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
-            "frac": head["gate_up_GBps"] / (HBM_PEAK / 1e9), "traffic": None,
-            "avg_launch_ms": gu_ms, "alg_bytes_per_launch": head["gate_up_bytes"]}
+            "frac": head["gate_up_GBps"] / (HBM_PEAK / 1e9),
+            "traffic": profiled_traffic() if args.head_batch == 64 else None,
+            "avg_launch_ms": gu_ms, "alg_bytes_per_launch": head["gate_up_bytes"],
+            "alg_bytes_def": "(distinct routed experts + shared) x 2 x 6,488,064 B + batch x 12,288 B"}
 
     cpu = None
     if not args.no_cpu:
         log(f"bench: CPU baseline ({args.cpu_tokens} tokens)")
-        cpu = cpu_baseline(L, args.cpu_tokens, torch)
+        cpu = cpu_baseline(L, min(args.cpu_tokens, args.head_batch), torch, seed=100 + args.head_batch)
 
     res = {"metric": "MoE-layer tokens/s at B=1/64/4096; % HBM peak (decode), % MFMA peak (prefill)",
            "value": head["tokens_per_s"], "unit": "tokens/s", "n_gpus": 1,
