@@ -123,6 +123,37 @@ uint8_t orc_f32_to_e4m3(float f) {
     return (uint8_t)(s | ((e + 7) << 3) | m);
 }
 
+/* Per-token, per-128-channel FP8 quantization of activations (the FP8
+ * workload of this build's benchmark; the reference has no FP8 MoE, its FP8
+ * code only decodes weights, cuda/fp8_gemm.cu:14-35). For every row and every
+ * group of 128 columns: amax = max |x|, scale = amax / 448 (1 when amax is
+ * 0), q = e4m3(x / scale) with round-to-nearest-even and saturation. */
+void orc_quant_act_e4m3(const float* x, int64_t n, int64_t K, uint8_t* q, float* scale) {
+    int64_t G = K / 128;
+    for (int64_t t = 0; t < n; ++t)
+        for (int64_t g = 0; g < G; ++g) {
+            const float* xs = x + t * K + g * 128;
+            float amax = 0.0f;
+            for (int i = 0; i < 128; ++i) {
+                float a = fabsf(xs[i]);
+                if (a > amax) amax = a;
+            }
+            float s = amax > 0.0f ? amax / 448.0f : 1.0f;
+            scale[t * G + g] = s;
+            for (int i = 0; i < 128; ++i) q[t * K + g * 128 + i] = orc_f32_to_e4m3(xs[i] / s);
+        }
+}
+
+/* FP8 weight [rows, K] (row-major e4m3 bytes) with fp32 scales per 128 x 128
+ * block [rows/128, K/128] -> fp32 (w = e4m3(q) * block scale). */
+void orc_dequant_e4m3_blocks(const uint8_t* q, const float* scales, int64_t rows, int64_t K,
+                             float* out) {
+    int64_t KB = K / 128;
+    for (int64_t r = 0; r < rows; ++r)
+        for (int64_t k = 0; k < K; ++k)
+            out[r * K + k] = orc_e4m3_to_f32(q[r * K + k]) * scales[(r / 128) * KB + k / 128];
+}
+
 /* linear_forward: src/model_glm52.cpp:42-56. y[n,out] = x[n,in] . W[out,in]^T,
  * one scalar fp32 accumulator per output, ascending i, acc += x*w with the
  * product rounded before the add (the reference is built -std=c++17 -O2 for

@@ -29,8 +29,11 @@
  *                             (oracle/_ref) on the tiny config, and vs an fp64
  *                             brute force; special cases k=1/w=1 (plain SwiGLU),
  *                             zero up-projection gives zero routed output.
- *   orc_e4m3 conversions     : exhaustive 256-entry decode vs the OCP e4m3
- *                             definition; encode round-trip on all finite codes.
+ *   orc_e4m3 conversions     : exhaustive 256-entry decode and RNE encode vs
+ *                             torch float8_e4m3fn (tests/test_oracle.py).
+ *   orc_quant_act_e4m3       : vs torch's float8_e4m3fn conversion of x/scale,
+ *                             scale = amax/448 closed form, |x - deq| bound.
+ *   orc_dequant_e4m3_blocks  : closed form per element, block index mapping.
  */
 #ifndef GLMMOE_ORACLE_H
 #define GLMMOE_ORACLE_H
@@ -52,6 +55,9 @@ void orc_bf16_to_f32_n(const uint16_t* src, float* dst, int64_t count);
 
 float orc_e4m3_to_f32(uint8_t v);
 uint8_t orc_f32_to_e4m3(float f);
+void orc_quant_act_e4m3(const float* x, int64_t n, int64_t K, uint8_t* q, float* scale);
+void orc_dequant_e4m3_blocks(const uint8_t* q, const float* scales, int64_t rows, int64_t K,
+                             float* out);
 
 void orc_linear_f32(const float* x, const float* w, int64_t n, int64_t in, int64_t out,
                     float* y);

@@ -52,6 +52,8 @@ class Oracle:
         L.orc_e4m3_to_f32.argtypes = [C.c_uint8]
         L.orc_f32_to_e4m3.restype = C.c_uint8
         L.orc_f32_to_e4m3.argtypes = [C.c_float]
+        L.orc_quant_act_e4m3.argtypes = [_f32p, _i64, _i64, _u8p, _f32p]
+        L.orc_dequant_e4m3_blocks.argtypes = [_u8p, _f32p, _i64, _i64, _f32p]
         L.orc_linear_f32.argtypes = [_f32p, _f32p, _i64, _i64, _i64, _f32p]
         L.orc_router_logits_bf16.argtypes = [_u16p, _u16p, _i64, _i64, _i64, _f32p]
         L.orc_router_topk.argtypes = [_f32p, C.c_void_p, _i64, C.c_int, C.c_int, C.c_int,
@@ -91,6 +93,21 @@ class Oracle:
 
     def f32_to_e4m3(self, f):
         return self.L.orc_f32_to_e4m3(float(f))
+
+    def quant_act_e4m3(self, x):
+        x = np.ascontiguousarray(x, np.float32)
+        n, K = x.shape
+        q = np.empty((n, K), np.uint8)
+        s = np.empty((n, K // 128), np.float32)
+        self.L.orc_quant_act_e4m3(x, n, K, q, s)
+        return q, s
+
+    def dequant_e4m3_blocks(self, q, scales):
+        q = np.ascontiguousarray(q, np.uint8)
+        rows, K = q.shape
+        out = np.empty((rows, K), np.float32)
+        self.L.orc_dequant_e4m3_blocks(q, np.ascontiguousarray(scales, np.float32), rows, K, out)
+        return out
 
     def linear(self, x, w):
         x = np.ascontiguousarray(x, np.float32)

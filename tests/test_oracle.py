@@ -286,3 +286,36 @@ def test_moe_forward_special_cases(oracle):
     out_z, _, _ = oracle.moe_forward(x, 16, 4, L["g"], zu, L["d"], None, router_w=L["rw"],
                                      e_bias=L["bias"])
     assert np.all(out_z == 0.0)
+
+
+# ---- FP8 activation quantization / block dequant ------------------------------
+
+def test_quant_act_e4m3_vs_torch(oracle):
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(7)
+    x = rng.standard_normal((6, 512)).astype(np.float32)
+    x[2, 128:256] = 0.0                  # all-zero group -> scale 1, codes 0
+    x[3, :128] *= 1e-6                   # tiny group
+    q, s = oracle.quant_act_e4m3(x)
+    g = np.abs(x.reshape(6, 4, 128)).max(axis=2)
+    assert np.array_equal(s, np.where(g > 0, (g / np.float32(448.0)).astype(np.float32), 1.0))
+    scaled = (x.reshape(6, 4, 128) / s[:, :, None]).astype(np.float32).reshape(6, 512)
+    ref = torch.from_numpy(scaled).to(torch.float8_e4m3fn).view(torch.uint8).numpy()
+    assert np.array_equal(q, ref)
+    assert np.all(q[2, 128:256] == 0)
+    # each group's amax element maps to +-448 exactly
+    for t in range(6):
+        for gi in range(4):
+            if g[t, gi] > 0:
+                j = np.argmax(np.abs(x[t, gi * 128:(gi + 1) * 128]))
+                assert q[t, gi * 128 + j] & 0x7F == 0x7E
+
+
+def test_dequant_e4m3_blocks(oracle):
+    rng = np.random.default_rng(8)
+    q = rng.integers(0, 256, (256, 384), dtype=np.uint8)
+    q[(q & 0x7F) == 0x7F] = 0x7E         # the encoder never emits the NaN codes
+    s = rng.uniform(0.001, 0.01, (2, 3)).astype(np.float32)
+    out = oracle.dequant_e4m3_blocks(q, s)
+    for r, k in [(0, 0), (127, 127), (128, 0), (255, 383), (200, 130)]:
+        assert out[r, k] == np.float32(oracle.e4m3_to_f32(int(q[r, k]))) * s[r // 128, k // 128]
