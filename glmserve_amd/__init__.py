@@ -5,5 +5,5 @@ glmserve_amd/csrc/, C-ABI in include/glmmoe.h). This package is the host-side
 mirror of the reference's launch API (cuda/kernels.cuh) over torch tensors.
 """
 from ._lib import LIB_PATH, GlmMoeError, lib  # noqa: F401
-from .ops import (W4A16MoELayer, moe_dispatch, moe_router, pack_w4a16,  # noqa: F401
-                  router_logits)
+from .ops import (FP8MoELayer, W4A16MoELayer, moe_dispatch, moe_router,  # noqa: F401
+                  pack_fp8, pack_w4a16, quant_act_fp8, router_logits)

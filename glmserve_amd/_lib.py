@@ -23,6 +23,13 @@ SIGNATURES = {
     "glmmoe_layer_workspace_view": (_i, [_vp, _i, _vp, _vp]),
     "glmmoe_moe_layer_w4a16": (_i, [_vp, _vp, _i, _vp, _vp, _sz, _vp]),
     "glmmoe_expert_ffn_w4a16": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
+    "glmmoe_fp8_packed_bytes": (_sz, [_i, _i]),
+    "glmmoe_pack_fp8": (_i, [_vp, _i, _i, _i, _vp, _vp]),
+    "glmmoe_quant_act_fp8": (_i, [_vp, _i, _i, _vp, _vp, _vp]),
+    "glmmoe_fp8_layer_workspace_bytes": (_sz, [_vp, _i]),
+    "glmmoe_fp8_layer_workspace_view": (_i, [_vp, _i, _vp, _vp]),
+    "glmmoe_moe_layer_fp8": (_i, [_vp, _vp, _i, _vp, _vp, _sz, _vp]),
+    "glmmoe_expert_ffn_fp8": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "glmmoe_profile_enable": (_i, [_i]),
     "glmmoe_profile_read": (_i, [_vp, _vp]),
 }
@@ -46,12 +53,25 @@ class Layer(C.Structure):
                 ("sh_up_q", _vp), ("sh_up_s", _vp), ("sh_down_q", _vp), ("sh_down_s", _vp)]
 
 
+class Fp8Layer(Layer):
+    """glmmoe_fp8_layer (include/glmmoe.h): the same fields, fp32 block scales."""
+    _fields_ = []
+
+
 class LayerWs(C.Structure):
     """glmmoe_layer_ws (include/glmmoe.h)."""
     _fields_ = [("logits", _vp), ("xsum", _vp), ("topk_ids", _vp), ("topk_w", _vp),
                 ("expert_offsets", _vp), ("sorted_token_ids", _vp), ("sorted_row", _vp),
                 ("inv", _vp), ("tiles", _vp), ("ntiles", _vp), ("h", _vp), ("hsum", _vp),
                 ("dpart", _vp), ("bytes", _sz)]
+
+
+class Fp8Ws(C.Structure):
+    """glmmoe_fp8_ws (include/glmmoe.h)."""
+    _fields_ = [("logits", _vp), ("xq", _vp), ("xscale", _vp), ("topk_ids", _vp),
+                ("topk_w", _vp), ("expert_offsets", _vp), ("sorted_token_ids", _vp),
+                ("sorted_row", _vp), ("inv", _vp), ("tiles", _vp), ("ntiles", _vp),
+                ("hq", _vp), ("hscale", _vp), ("dpart", _vp), ("bytes", _sz)]
 
 
 _LIB = None

@@ -19,13 +19,18 @@ inline int tile_rows_for(int n, int topk, int with_shared) {
     return (long)n * topk + (with_shared ? n : 0) >= kBigMinRows ? kBigRows : kTileRows;
 }
 
-int max_tiles_for(int n, int topk, int E, int with_shared) {
+int max_tiles_for(int n, int topk, int E, int with_shared, int T) {
     // sum_e ceil(c_e / T) <= (n*topk)/T + E, plus ceil(n/T) shared tiles.
-    const int T = tile_rows_for(n, topk, with_shared);
     return (n * topk) / T + E + (with_shared ? (n + T - 1) / T : 0) + 1;
 }
 
-int check_layer(const glmmoe_w4a16_layer* L, int n) {
+int max_tiles_for(int n, int topk, int E, int with_shared) {
+    return max_tiles_for(n, topk, E, with_shared, tile_rows_for(n, topk, with_shared));
+}
+
+// Shape and pointer checks shared by the W4A16 and FP8 layer descriptors.
+template <class Layer>
+int check_layer(const Layer* L, int n) {
     if (!L || n <= 0) return GLMMOE_ERR_ARG;
     if (L->hidden <= 0 || L->moe_inter <= 0 || L->n_experts <= 0 || L->topk <= 0)
         return GLMMOE_ERR_ARG;
@@ -40,7 +45,8 @@ int check_layer(const glmmoe_w4a16_layer* L, int n) {
     return GLMMOE_OK;
 }
 
-inline bool has_shared(const glmmoe_w4a16_layer* L) { return L->sh_gate_q != nullptr; }
+template <class Layer>
+inline bool has_shared(const Layer* L) { return L->sh_gate_q != nullptr; }
 
 ExpertPtrs ptrs(const glmmoe_w4a16_layer* L) {
     return ExpertPtrs{L->gate_q, L->gate_s, L->up_q, L->up_s, L->down_q, L->down_s,
@@ -73,6 +79,43 @@ size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v)
     w.ntiles = reinterpret_cast<int*>(take(4));
     w.h = reinterpret_cast<uint16_t*>(take(R * I * 2));
     w.hsum = reinterpret_cast<float*>(take(R * (I / 128) * 4));
+    w.dpart = reinterpret_cast<float*>(take(R * H * 4));
+    w.bytes = off;
+    if (v) *v = w;
+    return off;
+}
+
+Fp8Ptrs ptrs8(const glmmoe_fp8_layer* L) {
+    return Fp8Ptrs{L->gate_q, L->gate_s, L->up_q, L->up_s, L->down_q, L->down_s,
+                   L->sh_gate_q, L->sh_gate_s, L->sh_up_q, L->sh_up_s, L->sh_down_q,
+                   L->sh_down_s};
+}
+
+size_t carve8(const glmmoe_fp8_layer* L, int n, char* base, glmmoe_fp8_ws* v) {
+    const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
+    const size_t nk = (size_t)n * k;
+    const size_t R = nk + (has_shared(L) ? (size_t)n : 0);
+    const size_t mt = (size_t)max_tiles_for(n, k, E, has_shared(L), kBigRows);
+    size_t off = 0;
+    auto take = [&](size_t bytes) -> char* {
+        char* p = base ? base + off : nullptr;
+        off += align256(bytes);
+        return p;
+    };
+    glmmoe_fp8_ws w{};
+    w.logits = reinterpret_cast<float*>(take((size_t)n * E * 4));
+    w.xq = reinterpret_cast<uint8_t*>(take((size_t)n * H));
+    w.xscale = reinterpret_cast<float*>(take((size_t)n * (H / 128) * 4));
+    w.topk_ids = reinterpret_cast<int*>(take(nk * 4));
+    w.topk_w = reinterpret_cast<float*>(take(nk * 4));
+    w.expert_offsets = reinterpret_cast<int*>(take((size_t)(E + 2) * 4));
+    w.sorted_token_ids = reinterpret_cast<int*>(take(R * 4));
+    w.sorted_row = reinterpret_cast<int*>(take(R * 4));
+    w.inv = reinterpret_cast<int*>(take(nk * 4));
+    w.tiles = reinterpret_cast<int*>(take(mt * 16));
+    w.ntiles = reinterpret_cast<int*>(take(4));
+    w.hq = reinterpret_cast<uint8_t*>(take(R * I));
+    w.hscale = reinterpret_cast<float*>(take(R * (I / 128) * 4));
     w.dpart = reinterpret_cast<float*>(take(R * H * 4));
     w.bytes = off;
     if (v) *v = w;
@@ -127,6 +170,34 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     mark(GLMMOE_STAGE_DOWN, s);
     rc = big ? launch_down_big(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
              : launch_down(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
+    if (rc) return rc;
+    mark(GLMMOE_STAGE_COMBINE, s);
+    rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s);
+    if (rc) return rc;
+    end_call(s);
+    return GLMMOE_OK;
+}
+
+// FP8: activation quantization, dispatch onto 128-row tiles, the two fp8
+// grouped GEMMs and the combine.
+int run_experts8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, const int* ids,
+                 const float* w, float* out, const glmmoe_fp8_ws& v, hipStream_t s) {
+    const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
+    const int sh = has_shared(L) ? 1 : 0;
+    const int mt = max_tiles_for(n, k, E, sh, kBigRows);
+    int rc = launch_quant_act_fp8(x, n, H, v.xq, v.xscale, s);
+    if (rc) return rc;
+    mark(GLMMOE_STAGE_DISPATCH, s);
+    rc = launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids, v.sorted_row, v.inv,
+                         v.tiles, v.ntiles, kBigRows, sh, 1, s);
+    if (rc) return rc;
+    const Fp8Ptrs P = ptrs8(L);
+    mark(GLMMOE_STAGE_GATE_UP, s);
+    rc = launch_gate_up_fp8(P, v.xq, v.xscale, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.hq,
+                            v.hscale, H, I, E, s);
+    if (rc) return rc;
+    mark(GLMMOE_STAGE_DOWN, s);
+    rc = launch_down_fp8(P, v.hq, v.hscale, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_COMBINE, s);
     rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s);
@@ -234,6 +305,71 @@ int glmmoe_expert_ffn_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int 
     rc = launch_xsum(x, n, L->hidden, v.xsum, s);
     if (rc) return rc;
     return run_experts(L, x, n, topk_ids, topk_w, v.xsum, out, v, s);
+}
+
+size_t glmmoe_fp8_packed_bytes(int rows, int K) { return (size_t)rows * K; }
+
+int glmmoe_pack_fp8(const uint8_t* w, int n_mats, int rows, int K, uint8_t* packed,
+                    void* stream) {
+    if (!w || !packed || n_mats <= 0 || rows <= 0 || K <= 0) return GLMMOE_ERR_ARG;
+    if (rows % 128 || K % 128) return GLMMOE_ERR_SHAPE;
+    return launch_pack_fp8(w, n_mats, rows, K, packed, S(stream));
+}
+
+int glmmoe_quant_act_fp8(const uint16_t* x, int n, int K, uint8_t* q, float* scale,
+                         void* stream) {
+    if (!x || !q || !scale || n <= 0 || K <= 0) return GLMMOE_ERR_ARG;
+    if (K % 128) return GLMMOE_ERR_SHAPE;
+    return launch_quant_act_fp8(x, n, K, q, scale, S(stream));
+}
+
+size_t glmmoe_fp8_layer_workspace_bytes(const glmmoe_fp8_layer* L, int n) {
+    if (check_layer(L, n)) return 0;
+    return carve8(L, n, nullptr, nullptr);
+}
+
+int glmmoe_fp8_layer_workspace_view(const glmmoe_fp8_layer* L, int n, void* workspace,
+                                    glmmoe_fp8_ws* view) {
+    const int rc = check_layer(L, n);
+    if (rc) return rc;
+    if (!workspace || !view) return GLMMOE_ERR_ARG;
+    carve8(L, n, static_cast<char*>(workspace), view);
+    return GLMMOE_OK;
+}
+
+int glmmoe_moe_layer_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, float* out,
+                         void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_layer(L, n);
+    if (rc) return rc;
+    if (!x || !out || !workspace || !L->router_w) return GLMMOE_ERR_ARG;
+    glmmoe_fp8_ws v;
+    if (carve8(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)
+        return GLMMOE_ERR_WORKSPACE;
+    hipStream_t s = S(stream);
+    const int H = L->hidden, E = L->n_experts, k = L->topk;
+    begin_call();
+    mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
+    rc = launch_router_logits(x, L->router_w, n, H, E, v.logits, nullptr, s);
+    if (rc) return rc;
+    mark(GLMMOE_STAGE_ROUTER_TOPK, s);
+    rc = launch_router_topk(v.logits, L->e_bias, n, E, k, L->norm_topk, L->routed_scale,
+                            v.topk_ids, v.topk_w, s);
+    if (rc) return rc;
+    return run_experts8(L, x, n, v.topk_ids, v.topk_w, out, v, s);
+}
+
+int glmmoe_expert_ffn_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n,
+                          const int* topk_ids, const float* topk_w, float* out,
+                          void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_layer(L, n);
+    if (rc) return rc;
+    if (!x || !out || !workspace || !topk_ids || !topk_w) return GLMMOE_ERR_ARG;
+    glmmoe_fp8_ws v;
+    if (carve8(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)
+        return GLMMOE_ERR_WORKSPACE;
+    begin_call();
+    mark(GLMMOE_STAGE_ROUTER_LOGITS, S(stream));   // the activation quantization
+    return run_experts8(L, x, n, topk_ids, topk_w, out, v, S(stream));
 }
 
 int glmmoe_profile_enable(int on) {

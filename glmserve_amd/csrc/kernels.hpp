@@ -22,6 +22,16 @@ struct ExpertPtrs {
     const uint8_t* sh_down_q; const uint16_t* sh_down_s;
 };
 
+// FP8 experts: packed e4m3 tiles and fp32 128 x 128 block scales per matrix.
+struct Fp8Ptrs {
+    const uint8_t* gate_q; const float* gate_s;
+    const uint8_t* up_q; const float* up_s;
+    const uint8_t* down_q; const float* down_s;
+    const uint8_t* sh_gate_q; const float* sh_gate_s;
+    const uint8_t* sh_up_q; const float* sh_up_s;
+    const uint8_t* sh_down_q; const float* sh_down_s;
+};
+
 int launch_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
                          float* logits, float* xsum, hipStream_t s);
 int launch_xsum(const uint16_t* x, int n, int H, float* xsum, hipStream_t s);
@@ -45,5 +55,16 @@ int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const float* hsum, c
                     hipStream_t s);
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
                    int with_shared, float* out, hipStream_t s);
+
+int launch_quant_act_fp8(const uint16_t* x, int n, int K, uint8_t* q, float* scale,
+                         hipStream_t s);
+int launch_pack_fp8(const uint8_t* w, int n_mats, int rows, int K, uint8_t* packed,
+                    hipStream_t s);
+int launch_gate_up_fp8(const Fp8Ptrs& P, const uint8_t* xq, const float* xscale,
+                       const int* tiles, const int* ntiles, int max_tiles, const int* rows_tok,
+                       uint8_t* hq, float* hscale, int H, int I, int E, hipStream_t s);
+int launch_down_fp8(const Fp8Ptrs& P, const uint8_t* hq, const float* hscale, const int* tiles,
+                    const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
+                    hipStream_t s);
 
 }  // namespace glmmoe

@@ -27,6 +27,7 @@
 // MFMA 32x32x16 is used because on gfx950 it sustains ~2.2 PFLOP/s of bf16
 // where 16x16x32 reaches ~1.2 (measured with back-to-back independent chains).
 #include "common.hpp"
+#include "bigtile.hpp"
 #include "kernels.hpp"
 
 namespace glmmoe {
@@ -43,10 +44,7 @@ struct BigArgs {
     int H, I, E;
 };
 
-constexpr int kBigWaves = 8;
 constexpr int kBigD = 3;
-constexpr int kBigTable = 3;              // items per table refill (LDS: ring + table <= 160 KiB)
-constexpr int kBigTabInts = 4 + kBigRows; // {expert, row0, nrows, feature group} + tokens
 
 struct BigRing {
     static constexpr int kWBytes = 16 * 1024;           // 16 weight tiles of 1 KiB
@@ -76,32 +74,6 @@ template <int NMAT>
 struct BigShape {
     static constexpr int kFeat = NMAT == 2 ? 128 : 256;   // features per item
 };
-
-struct BigItem {
-    int e, r0, nr, g;
-    uint32_t tab;              // LDS address of the item's table entry
-};
-
-__device__ __forceinline__ BigItem big_item(const char* lds, int k) {
-    const uint32_t base = lds_addr(lds + BigRing::kTab + k * kBigTabInts * 4);
-    const uint4 hd = lds_bcast16(base);
-    BigItem it;
-    it.e = sgpr(hd.x);
-    it.r0 = sgpr(hd.y);
-    it.nr = sgpr(hd.z);
-    it.g = sgpr(hd.w);
-    it.tab = base;
-    return it;
-}
-
-__device__ __forceinline__ uint32_t lds_read32(uint32_t addr) {
-    uint32_t v;
-    asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
-    return v;
-}
-__device__ __forceinline__ void lds_write32(uint32_t addr, float v) {
-    asm volatile("ds_write_b32 %0, %1\n s_waitcnt lgkmcnt(0)" : : "v"(addr), "v"(v) : "memory");
-}
 
 // Tile t (0..15) of an item: weight matrix and 16-row feature block. Tiles
 // 4 wn .. 4 wn + 3 belong to feature wave wn: for gate/up, 2 gate tiles then
@@ -278,38 +250,6 @@ __device__ __forceinline__ void big_compute(const char* slot, int wave, int lane
     }
 }
 
-// Item of workgroup b at round k. Workgroups are dispatched round-robin over
-// the 8 XCDs (b % 8), each with its own L2; the items of one round are laid
-// out so that each XCD takes a contiguous run of item ids -- the feature
-// groups of the same row tile -- and the tile's activation rows are fetched
-// into that XCD's L2 once instead of once per XCD.
-__device__ __forceinline__ long big_item_id(long k) {
-    const int nb = gridDim.x, b = blockIdx.x;
-    const int lane_in_round = (nb % 8 == 0) ? (b % 8) * (nb / 8) + b / 8 : b;
-    return k * nb + lane_in_round;
-}
-
-template <int NMAT>
-__device__ __forceinline__ void big_fill_table(const BigArgs& a, int* table, long k0, int cnt,
-                                               int nfg) {
-    for (int i = threadIdx.x; i < cnt * kBigTabInts; i += blockDim.x) {
-        const int k = i / kBigTabInts, f = i % kBigTabInts;
-        const long item = big_item_id(k0 + k);
-        const int4 tile = a.tiles[item / nfg];
-        int v;
-        if (f == 0) v = tile.x;
-        else if (f == 1) v = tile.y;
-        else if (f == 2) v = tile.z;
-        else if (f == 3) v = (int)(item % nfg);
-        else {
-            const int row = f - 4;
-            const int rr = row < tile.z ? row : 0;
-            v = NMAT == 2 ? a.rows_tok[tile.y + rr] : tile.y + rr;
-        }
-        table[i] = v;
-    }
-}
-
 template <int NMAT>
 __device__ __forceinline__ void big_epilogue(const BigArgs& a, const BigItem& cur, char* lds,
                                              int wave, int lane, f32x16 (&acc)[2][2]) {
@@ -392,33 +332,27 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
     const int KG = K / 128;
     const int nfg = (NMAT == 2 ? a.I : a.H) / BigShape<NMAT>::kFeat;
     const long total = (long)(*a.ntiles) * nfg;
-    // Rounds with at least one item for this workgroup (ids past total are skipped).
-    long nitems = 0;
-    {
-        const long rounds = (total + gridDim.x - 1) / gridDim.x;
-        nitems = rounds;
-        if (rounds > 0 && big_item_id(rounds - 1) >= total) nitems = rounds - 1;
-    }
+    const long nitems = big_rounds(total);
 
     for (long k0 = 0; k0 < nitems; k0 += kBigTable) {
         const int cnt = (int)min((long)kBigTable, nitems - k0);
-        big_fill_table<NMAT>(a, table, k0, cnt, nfg);
+        big_fill_table<NMAT == 2>(a.tiles, a.rows_tok, table, k0, cnt, nfg);
         __syncthreads();
         const long nsteps = (long)cnt * KG;
 
         int iss_k = 0, iss_g = 0;
-        BigItem iss = big_item(lds, 0);
+        BigItem iss = big_item(lds + RG::kTab, 0);
         for (int j = 0; j < kBigD - 1; ++j) {
             if (j < nsteps) {
                 big_issue<NMAT>(a, iss, iss_g, K, KG, lds + (j % kBigD) * RG::kSlot, wave, lane);
                 if (++iss_g == KG) {
                     iss_g = 0;
-                    if (++iss_k < cnt) iss = big_item(lds, iss_k);
+                    if (++iss_k < cnt) iss = big_item(lds + RG::kTab, iss_k);
                 }
             }
         }
         int cur_k = 0, cur_g = 0;
-        BigItem cur = big_item(lds, 0);
+        BigItem cur = big_item(lds + RG::kTab, 0);
         f32x16 acc[2][2];
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb)
@@ -434,7 +368,7 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
                                 wave, lane);
                 if (++iss_g == KG) {
                     iss_g = 0;
-                    if (++iss_k < cnt) iss = big_item(lds, iss_k);
+                    if (++iss_k < cnt) iss = big_item(lds + RG::kTab, iss_k);
                 }
             }
 #ifndef GLMMOE_BIG_NOCOMPUTE
@@ -448,7 +382,7 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
 #pragma unroll
                     for (int tb = 0; tb < 2; ++tb) acc[jb][tb] = f32x16{};
                 cur_g = 0;
-                if (++cur_k < cnt) cur = big_item(lds, cur_k);
+                if (++cur_k < cnt) cur = big_item(lds + RG::kTab, cur_k);
             }
         }
         __syncthreads();

@@ -6,7 +6,9 @@ Unlike the reference (void return, errors printed), failures raise GlmMoeError.
 """
 import torch
 
-from ._lib import GlmMoeError, Layer, LayerWs, check, lib
+import ctypes
+
+from ._lib import Fp8Layer, Fp8Ws, GlmMoeError, Layer, LayerWs, check, lib
 
 
 def _p(t):
@@ -78,20 +80,24 @@ def pack_w4a16(qweight, scales, n_mats, rows, K, group_size=128, stream=None):
     return pq, ps
 
 
-class W4A16MoELayer:
-    """One MoE layer's device-resident W4A16 weights in the native packed format.
+class _MoELayer:
+    """One MoE layer's device-resident expert weights in a native packed format.
 
-    The weight tensors are kept alive by this object; `struct` is the
-    glmmoe_w4a16_layer handed to the C-ABI.
+    The weight tensors are kept alive by this object; `struct` is the layer
+    descriptor handed to the C-ABI.
     """
+    _struct = Layer
+    _view = LayerWs
+    _fn = dict(ws_bytes="glmmoe_layer_workspace_bytes", ws_view="glmmoe_layer_workspace_view",
+               layer="glmmoe_moe_layer_w4a16", ffn="glmmoe_expert_ffn_w4a16")
 
     def __init__(self, hidden, moe_inter, n_experts, topk, router_w, e_bias, gate, up, down,
                  shared=None, norm_topk=True, routed_scale=2.5):
-        """gate/up/down: (packed_q, packed_scales) pairs of stacked experts; shared: a
+        """gate/up/down: (packed_q, scales) pairs of stacked experts; shared: a
         3-tuple of such pairs or None. router_w: [E, H] bf16; e_bias: [E] fp32 or None."""
         self.hidden, self.moe_inter, self.n_experts, self.topk = hidden, moe_inter, n_experts, topk
         self.keep = [router_w, e_bias, gate, up, down, shared]
-        st = Layer()
+        st = self._struct()
         st.hidden, st.moe_inter, st.n_experts, st.topk = hidden, moe_inter, n_experts, topk
         st.norm_topk, st.routed_scale = int(bool(norm_topk)), float(routed_scale)
         st.router_w, st.e_bias = _p(router_w), _p(e_bias)
@@ -105,24 +111,24 @@ class W4A16MoELayer:
             st.sh_down_q, st.sh_down_s = _p(sdq), _p(sds)
         self.struct = st
 
+    def _call(self, key, *args):
+        return getattr(lib(), self._fn[key])(*args)
+
+    def _ref(self):
+        return ctypes.byref(self.struct)
+
     def workspace_bytes(self, n):
-        b = lib().glmmoe_layer_workspace_bytes(self._ref(), n)
+        b = self._call("ws_bytes", self._ref(), n)
         if b == 0:
             raise GlmMoeError("layer shape not supported")
         return b
-
-    def _ref(self):
-        import ctypes
-        return ctypes.byref(self.struct)
 
     def alloc_workspace(self, n, device="cuda"):
         return torch.empty(self.workspace_bytes(n), dtype=torch.uint8, device=device)
 
     def workspace_view(self, n, ws):
-        import ctypes
-        v = LayerWs()
-        check(lib().glmmoe_layer_workspace_view(self._ref(), n, _p(ws), ctypes.byref(v)),
-              "layer_workspace_view")
+        v = self._view()
+        check(self._call("ws_view", self._ref(), n, _p(ws), ctypes.byref(v)), "workspace_view")
         return v
 
     def forward(self, x, out, ws, stream=None):
@@ -130,16 +136,52 @@ class W4A16MoELayer:
         n = x.shape[0]
         _need(x, torch.bfloat16, n * self.hidden, "x")
         _need(out, torch.float32, n * self.hidden, "out")
-        check(lib().glmmoe_moe_layer_w4a16(self._ref(), _p(x), n, _p(out), _p(ws), ws.numel(),
-                                           _s(stream)), "moe_layer_w4a16")
+        check(self._call("layer", self._ref(), _p(x), n, _p(out), _p(ws), ws.numel(),
+                         _s(stream)), self._fn["layer"])
 
     def expert_ffn(self, x, topk_ids, topk_w, out, ws, stream=None):
         n = x.shape[0]
+        _need(x, torch.bfloat16, n * self.hidden, "x")
+        _need(out, torch.float32, n * self.hidden, "out")
         _need(topk_ids, torch.int32, n * self.topk, "topk_ids")
         _need(topk_w, torch.float32, n * self.topk, "topk_w")
-        check(lib().glmmoe_expert_ffn_w4a16(self._ref(), _p(x), n, _p(topk_ids), _p(topk_w),
-                                            _p(out), _p(ws), ws.numel(), _s(stream)),
-              "expert_ffn_w4a16")
+        check(self._call("ffn", self._ref(), _p(x), n, _p(topk_ids), _p(topk_w), _p(out), _p(ws),
+                         ws.numel(), _s(stream)), self._fn["ffn"])
+
+
+class W4A16MoELayer(_MoELayer):
+    """W4A16 experts: (packed_q, packed bf16 scales) from pack_w4a16."""
+
+
+class FP8MoELayer(_MoELayer):
+    """FP8 experts: (packed e4m3 from pack_fp8, fp32 [.., rows/128, K/128] block scales)."""
+    _struct = Fp8Layer
+    _view = Fp8Ws
+    _fn = dict(ws_bytes="glmmoe_fp8_layer_workspace_bytes",
+               ws_view="glmmoe_fp8_layer_workspace_view", layer="glmmoe_moe_layer_fp8",
+               ffn="glmmoe_expert_ffn_fp8")
+
+
+def pack_fp8(w, n_mats, rows, K, out=None, stream=None):
+    """Row-major e4m3 [n_mats, rows, K] (uint8) -> the native tile layout (into
+    `out`, a uint8 tensor or view of n_mats * glmmoe_fp8_packed_bytes bytes)."""
+    _need(w, torch.uint8, n_mats * rows * K, "w")
+    nbytes = n_mats * lib().glmmoe_fp8_packed_bytes(rows, K)
+    if out is None:
+        out = torch.empty(nbytes, dtype=torch.uint8, device=w.device)
+    _need(out, torch.uint8, nbytes, "out")
+    check(lib().glmmoe_pack_fp8(_p(w), n_mats, rows, K, _p(out), _s(stream)), "pack_fp8")
+    return out
+
+
+def quant_act_fp8(x, stream=None):
+    """x [n, K] bf16 -> (q [n, K] uint8 e4m3, scale [n, K/128] fp32)."""
+    n, K = x.shape
+    _need(x, torch.bfloat16, n * K, "x")
+    q = torch.empty((n, K), dtype=torch.uint8, device=x.device)
+    s = torch.empty((n, K // 128), dtype=torch.float32, device=x.device)
+    check(lib().glmmoe_quant_act_fp8(_p(x), n, K, _p(q), _p(s), _s(stream)), "quant_act_fp8")
+    return q, s
 
 
 def ws_tensor(ws_base, view_ptr, ws, dtype, numel):

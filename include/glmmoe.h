@@ -152,8 +152,83 @@ int glmmoe_expert_ffn_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int 
                             const int* topk_ids, const float* topk_w, float* out,
                             void* workspace, size_t workspace_bytes, void* stream);
 
+/* ---- FP8 (e4m3) experts ----------------------------------------------------
+ * No counterpart in the reference's MoE (its FP8 code is the dense per-row-scale
+ * GEMV gemm_fp8, cuda/kernels.cuh 55-57, cuda/fp8_gemm.cu 14-35, never called
+ * by the forward; e4m3 decoding follows include/common.hpp 182-200). The same
+ * layer semantics as glmmoe_moe_layer_w4a16 (GLM52Model::moe_mlp,
+ * src/model_glm52.cpp 1096-1154) with:
+ *   weights     e4m3 (OCP fn) [rows, K] plus fp32 scales per 128 x 128 block
+ *               [rows/128, K/128]: w = e4m3(q) * scale. Codes 0x7f / 0xff are
+ *               NaN on the MFMA (the reference host decoder reads them as
+ *               +-480); quantizers must not emit them.
+ *   activations x (bf16) quantized per token and 128 channels:
+ *               scale = amax / 448 (1 for an all-zero group),
+ *               q = e4m3(x / scale) rounded to nearest even, saturating at 448.
+ *   h           SiLU(gate) * up quantized by the same rule before down.
+ * The router still reads the bf16 x (glmmoe_router_logits). All expert GEMMs
+ * run on 128-row tiles with fp8 MFMA. Shapes: H % 256 == 0, H <= 8192,
+ * I % 128 == 0, E <= 512, topk <= 8. */
+
+/* Bytes of one packed matrix [rows, K] (rows % 128 == 0, K % 128 == 0). */
+size_t glmmoe_fp8_packed_bytes(int rows, int K);
+
+/* Row-major e4m3 [n_mats, rows, K] -> the kernels' tile layout. Scales are
+ * used as given ([n_mats, rows/128, K/128] fp32), no packing. */
+int glmmoe_pack_fp8(const uint8_t* w, int n_mats, int rows, int K, uint8_t* packed,
+                    void* stream);
+
+/* x [n, K] bf16 -> q [n, K] e4m3 and scale [n, K/128] fp32 (K % 128 == 0), the
+ * activation rule above. */
+int glmmoe_quant_act_fp8(const uint16_t* x, int n, int K, uint8_t* q, float* scale,
+                         void* stream);
+
+typedef struct glmmoe_fp8_layer {
+    int hidden;
+    int moe_inter;
+    int n_experts;
+    int topk;
+    int norm_topk;
+    float routed_scale;
+    const uint16_t* router_w;   /* [E, H] bf16 */
+    const float* e_bias;        /* [E] fp32 or NULL */
+    const uint8_t* gate_q;  const float* gate_s;  /* [E] x packed [I, H]; scales [E, I/128, H/128] */
+    const uint8_t* up_q;    const float* up_s;    /* [E] x packed [I, H] */
+    const uint8_t* down_q;  const float* down_s;  /* [E] x packed [H, I]; scales [E, H/128, I/128] */
+    const uint8_t* sh_gate_q; const float* sh_gate_s; /* packed [I, H] or NULL */
+    const uint8_t* sh_up_q;   const float* sh_up_s;
+    const uint8_t* sh_down_q; const float* sh_down_s;
+} glmmoe_fp8_layer;
+
+typedef struct glmmoe_fp8_ws {
+    float* logits;        /* [n, E] */
+    uint8_t* xq;          /* [n, H] e4m3 */
+    float* xscale;        /* [n, H/128] */
+    int* topk_ids;        /* [n, topk] */
+    float* topk_w;        /* [n, topk] */
+    int* expert_offsets;  /* [E + 2] */
+    int* sorted_token_ids;/* [R] */
+    int* sorted_row;      /* [R] */
+    int* inv;             /* [n*topk] */
+    int* tiles;           /* [max_tiles * 4] */
+    int* ntiles;          /* [1] */
+    uint8_t* hq;          /* [R, I] e4m3 */
+    float* hscale;        /* [R, I/128] */
+    float* dpart;         /* [R, H] fp32 */
+    size_t bytes;
+} glmmoe_fp8_ws;
+
+size_t glmmoe_fp8_layer_workspace_bytes(const glmmoe_fp8_layer* L, int n);
+int glmmoe_fp8_layer_workspace_view(const glmmoe_fp8_layer* L, int n, void* workspace,
+                                    glmmoe_fp8_ws* view);
+int glmmoe_moe_layer_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, float* out,
+                         void* workspace, size_t workspace_bytes, void* stream);
+int glmmoe_expert_ffn_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n,
+                          const int* topk_ids, const float* topk_w, float* out,
+                          void* workspace, size_t workspace_bytes, void* stream);
+
 /* ---- Stage timing (diagnostics; no reference counterpart) -----------------
- * While enabled, every glmmoe_moe_layer_w4a16 / glmmoe_expert_ffn_w4a16 call
+ * While enabled, every layer / expert-FFN call (W4A16 and FP8)
  * records a HIP event on its stream before and after each stage, in a ring of
  * GLMMOE_PROF_MAX_CALLS calls (events are created on the first enable; no
  * device memory is allocated). glmmoe_profile_read waits for the recorded

@@ -350,14 +350,26 @@ typedef struct {
     int* ids;
     float* w;
     int64_t t0, t1;
+    int h_fp8;
     int status;
 } orc_job;
 
+/* h_fp8: the FP8 layer's intermediate, h quantized per 128 features with
+ * orc_quant_act_e4m3's rule and dequantized (e4m3(q) * scale) before the down
+ * projection. */
 static void orc_ffn(const float* xt, const float* g_w, const float* u_w, const float* d_w,
-                    int64_t H, int64_t I, float* g, float* u, float* tmp) {
+                    int64_t H, int64_t I, int h_fp8, float* g, float* u, float* tmp) {
     orc_linear_f32(xt, g_w, 1, H, I, g);
     orc_linear_f32(xt, u_w, 1, H, I, u);
     for (int64_t i = 0; i < I; ++i) g[i] = orc_silu(g[i]) * u[i];
+    if (h_fp8) {
+        for (int64_t g0 = 0; g0 < I; g0 += 128) {
+            uint8_t q[128];
+            float sc;
+            orc_quant_act_e4m3(g + g0, 1, 128, q, &sc);
+            for (int i = 0; i < 128; ++i) g[g0 + i] = orc_e4m3_to_f32(q[i]) * sc;
+        }
+    }
     orc_linear_f32(g, d_w, 1, I, H, tmp);
 }
 
@@ -378,11 +390,11 @@ static void* orc_moe_worker(void* arg) {
         for (int kk = 0; kk < j->topk; ++kk) {
             int e = ids[kk];
             if (!j->gate[e] || !j->up[e] || !j->down[e]) { j->status = -1; continue; }
-            orc_ffn(xt, j->gate[e], j->up[e], j->down[e], j->H, j->I, g, u, tmp);
+            orc_ffn(xt, j->gate[e], j->up[e], j->down[e], j->H, j->I, j->h_fp8, g, u, tmp);
             for (int64_t i = 0; i < j->H; ++i) ot[i] = ot[i] + w[kk] * tmp[i];
         }
         if (j->sh_gate) {
-            orc_ffn(xt, j->sh_gate, j->sh_up, j->sh_down, j->H, j->S, g, u, tmp);
+            orc_ffn(xt, j->sh_gate, j->sh_up, j->sh_down, j->H, j->S, j->h_fp8, g, u, tmp);
             for (int64_t i = 0; i < j->H; ++i) ot[i] = ot[i] + tmp[i];
         }
     }
@@ -398,6 +410,17 @@ int orc_moe_forward(const float* x, int64_t n, int64_t H, int E, int topk, int64
                     const float* const* down, const float* sh_gate, const float* sh_up,
                     const float* sh_down, int norm_topk, float routed_scale, int nthreads,
                     float* out, int* ids_out, float* w_out) {
+    return orc_moe_forward_ex(x, n, H, E, topk, I, S, router_w, logits_in, e_bias, gate, up,
+                              down, sh_gate, sh_up, sh_down, norm_topk, routed_scale, 0,
+                              nthreads, out, ids_out, w_out);
+}
+
+int orc_moe_forward_ex(const float* x, int64_t n, int64_t H, int E, int topk, int64_t I,
+                       int64_t S, const float* router_w, const float* logits_in,
+                       const float* e_bias, const float* const* gate, const float* const* up,
+                       const float* const* down, const float* sh_gate, const float* sh_up,
+                       const float* sh_down, int norm_topk, float routed_scale, int h_fp8,
+                       int nthreads, float* out, int* ids_out, float* w_out) {
     float* logits = NULL;
     const float* lg = logits_in;
     if (!lg) {
@@ -416,7 +439,7 @@ int orc_moe_forward(const float* x, int64_t n, int64_t H, int E, int topk, int64
         j->logits = lg; j->e_bias = e_bias; j->gate = gate; j->up = up; j->down = down;
         j->sh_gate = sh_gate; j->sh_up = sh_up; j->sh_down = sh_down;
         j->norm_topk = norm_topk; j->routed_scale = routed_scale;
-        j->out = out; j->ids = ids_out; j->w = w_out;
+        j->out = out; j->ids = ids_out; j->w = w_out; j->h_fp8 = h_fp8;
         j->t0 = i * chunk; j->t1 = (i + 1) * chunk < n ? (i + 1) * chunk : n;
         if (j->t0 > j->t1) j->t0 = j->t1;
     }

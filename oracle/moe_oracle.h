@@ -84,6 +84,16 @@ int orc_moe_forward(const float* x, int64_t n, int64_t H, int E, int topk, int64
                     const float* sh_down, int norm_topk, float routed_scale, int nthreads,
                     float* out, int* ids_out, float* w_out);
 
+/* Same, with h_fp8 != 0 quantizing the intermediate h per 128 features to
+ * e4m3 (orc_quant_act_e4m3's rule) and dequantizing it before the down
+ * projection, as the FP8 layer does. Pass x already quantized-dequantized. */
+int orc_moe_forward_ex(const float* x, int64_t n, int64_t H, int E, int topk, int64_t I,
+                       int64_t S, const float* router_w, const float* logits_in,
+                       const float* e_bias, const float* const* gate, const float* const* up,
+                       const float* const* down, const float* sh_gate, const float* sh_up,
+                       const float* sh_down, int norm_topk, float routed_scale, int h_fp8,
+                       int nthreads, float* out, int* ids_out, float* w_out);
+
 #ifdef __cplusplus
 }
 #endif

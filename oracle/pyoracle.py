@@ -65,6 +65,10 @@ class Oracle:
             _f32p, _i64, _i64, C.c_int, C.c_int, _i64, _i64, C.c_void_p, C.c_void_p,
             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
             C.c_void_p, C.c_int, C.c_float, C.c_int, _f32p, _i32p, _f32p]
+        L.orc_moe_forward_ex.argtypes = [
+            _f32p, _i64, _i64, C.c_int, C.c_int, _i64, _i64, C.c_void_p, C.c_void_p,
+            C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
+            C.c_void_p, C.c_int, C.c_float, C.c_int, C.c_int, _f32p, _i32p, _f32p]
 
     # scalar helpers
     def expf(self, x):
@@ -166,8 +170,9 @@ class Oracle:
         return q, s
 
     def moe_forward(self, x, E, topk, gate, up, down, sh=None, router_w=None, logits=None,
-                    e_bias=None, norm_topk=True, routed_scale=2.5, nthreads=1):
-        """gate/up/down: lists of E fp32 arrays (or None for an unmaterialized expert)."""
+                    e_bias=None, norm_topk=True, routed_scale=2.5, nthreads=1, h_fp8=False):
+        """gate/up/down: lists of E fp32 arrays (or None for an unmaterialized expert).
+        h_fp8: quantize the intermediate h per 128 features to e4m3 (FP8 layer)."""
         x = np.ascontiguousarray(x, np.float32)
         n, H = x.shape
         I = next(g for g in gate if g is not None).shape[0]
@@ -182,14 +187,14 @@ class Oracle:
         out = np.empty((n, H), np.float32)
         ids = np.empty((n, topk), np.int32)
         w = np.empty((n, topk), np.float32)
-        rc = self.L.orc_moe_forward(
+        rc = self.L.orc_moe_forward_ex(
             x, n, H, E, topk, I, S, None if rw is None else rw.ctypes.data,
             None if lg is None else lg.ctypes.data, None if eb is None else eb.ctypes.data,
             _ptr_array(g_), _ptr_array(u_), _ptr_array(d_),
             None if shk is None else shk[0].ctypes.data,
             None if shk is None else shk[1].ctypes.data,
             None if shk is None else shk[2].ctypes.data,
-            int(norm_topk), routed_scale, nthreads, out, ids, w)
+            int(norm_topk), routed_scale, int(h_fp8), nthreads, out, ids, w)
         if rc:
             raise ValueError("orc_moe_forward: routing selected an unmaterialized expert")
         return out, ids, w

@@ -112,3 +112,94 @@ def rel_err(got, ref):
     got = np.asarray(got, np.float64)
     ref = np.asarray(ref, np.float64)
     return float(np.max(np.abs(got - ref)) / max(1e-30, float(np.max(np.abs(ref)))))
+
+
+class SynthFp8Layer:
+    """An FP8 MoE layer (configs[4] format) generated on the GPU from a seed.
+
+    Each matrix is e4m3 codes [rows, K] with fp32 scales per 128 x 128 block:
+    codes are e4m3(clamp(N(0,1) * 96, +-448)) (round to nearest even by torch's
+    float8_e4m3fn conversion; never the NaN codes), block scales
+    0.02 / 96 * U(0.5, 1.5), so weights are ~N(0, 0.02) with per-block spread.
+    Every (matrix, expert) has its own seed, so the oracle side regenerates the
+    experts it needs instead of keeping a host copy of all of them."""
+
+    def __init__(self, H, E, k, I, seed=0, shared=True, zipf_s=None, device="cuda",
+                 norm_topk=True, routed_scale=2.5):
+        from glmserve_amd import FP8MoELayer, lib, pack_fp8
+        self.H, self.E, self.k, self.I, self.seed = H, E, k, I, seed
+        self.norm_topk, self.routed_scale = norm_topk, routed_scale
+        self.has_shared = shared
+        g = torch.Generator(device=device)
+        g.manual_seed(seed)
+        gc = torch.Generator(device="cpu")
+        gc.manual_seed(seed + 7)
+        self.router_w = (0.02 * torch.randn(E, H, generator=g, device=device)).to(torch.bfloat16)
+        bias = (torch.rand(E, generator=gc) * 0.2 - 0.1)
+        if zipf_s is not None:
+            bias = bias + zipf_log_prior(E, zipf_s, gc)
+        self.e_bias = bias.to(torch.float32).to(device)
+        shapes = [(I, H), (I, H), (H, I)]
+        self.packed, self.scales = [], []
+        for m, (rows, K) in enumerate(shapes):
+            nm = E + (1 if shared else 0)
+            pq = torch.empty(nm * lib().glmmoe_fp8_packed_bytes(rows, K), dtype=torch.uint8,
+                             device=device)
+            sc = torch.empty(nm, rows // 128, K // 128, dtype=torch.float32, device=device)
+            per = rows * K
+            for e in range(nm):
+                q, s = self.matrix(m, e)
+                pack_fp8(q, 1, rows, K, out=pq[e * per:(e + 1) * per])
+                sc[e] = s
+            self.packed.append(pq)
+            self.scales.append(sc)
+        torch.cuda.synchronize()
+        per = [r * K for r, K in shapes]
+        routed = [(self.packed[m][:E * per[m]], self.scales[m][:E]) for m in range(3)]
+        sh = None
+        if shared:
+            sh = tuple((self.packed[m][E * per[m]:], self.scales[m][E:]) for m in range(3))
+        self.layer = FP8MoELayer(H, I, E, k, self.router_w, self.e_bias, routed[0], routed[1],
+                                 routed[2], sh, norm_topk=norm_topk, routed_scale=routed_scale)
+
+    def matrix(self, m, e, device="cuda"):
+        """(codes uint8 [rows, K], scales fp32 [rows/128, K/128]) of matrix m
+        (0 gate, 1 up, 2 down) of expert e (e == E: the shared expert)."""
+        rows, K = [(self.I, self.H), (self.I, self.H), (self.H, self.I)][m]
+        g = torch.Generator(device=device)
+        g.manual_seed(self.seed * 1000003 + e * 3 + m + 1)
+        v = (torch.randn(rows, K, generator=g, device=device) * 96.0).clamp_(-448.0, 448.0)
+        q = v.to(torch.float8_e4m3fn).view(torch.uint8)
+        s = (0.02 / 96.0) * (0.5 + torch.rand(rows // 128, K // 128, generator=g, device=device))
+        return q, s.to(torch.float32)
+
+    def x(self, n, seed):
+        g = torch.Generator(device="cuda")
+        g.manual_seed(seed)
+        return torch.randn(n, self.H, generator=g, device="cuda").to(torch.bfloat16)
+
+    def dequant_expert(self, oracle, e):
+        out = []
+        for m in range(3):
+            q, s = self.matrix(m, e)
+            out.append(oracle.dequant_e4m3_blocks(q.cpu().numpy(), s.cpu().numpy()))
+        return out
+
+    def oracle_forward(self, oracle, x_bf16, tokens, logits, nthreads=8):
+        """Oracle output for the given tokens: x quantized per token and 128
+        channels (oracle rule) and dequantized, h quantized the same way."""
+        xf = bits_to_f32(x_bf16[tokens].view(torch.int16).cpu().numpy().view(np.uint16))
+        q, s = oracle.quant_act_e4m3(xf)
+        dec = np.array([oracle.e4m3_to_f32(c) for c in range(256)], np.float32)
+        xd = (dec[q].reshape(len(tokens), -1, 128) * s[:, :, None]).reshape(len(tokens), self.H)
+        lg = np.ascontiguousarray(logits[tokens], np.float32)
+        eb = self.e_bias.cpu().numpy()
+        ids, _ = oracle.router_topk(lg, eb, self.k, self.norm_topk, self.routed_scale)
+        need = sorted(set(ids.ravel().tolist()))
+        gate, up, down = [None] * self.E, [None] * self.E, [None] * self.E
+        for e in need:
+            gate[e], up[e], down[e] = self.dequant_expert(oracle, e)
+        sh = self.dequant_expert(oracle, self.E) if self.has_shared else None
+        return oracle.moe_forward(xd, self.E, self.k, gate, up, down, sh, logits=lg, e_bias=eb,
+                                  norm_topk=self.norm_topk, routed_scale=self.routed_scale,
+                                  nthreads=nthreads, h_fp8=True)

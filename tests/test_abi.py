@@ -109,3 +109,32 @@ def test_cpp_header_compiles_against_the_library(tmp_path):
                         str(exe), _lib.LIB_PATH, "-Wl,-rpath," + os.path.dirname(_lib.LIB_PATH)],
                        capture_output=True, text=True)
     assert r.returncode == 0, r.stderr
+
+
+def test_fp8_host_checks_and_workspace():
+    L = _lib.lib()
+    dummy = C.c_void_p(16)
+    assert L.glmmoe_fp8_packed_bytes(2048, 6144) == 2048 * 6144
+    assert L.glmmoe_pack_fp8(None, 1, 128, 128, dummy, None) == -1
+    assert L.glmmoe_pack_fp8(dummy, 1, 96, 128, dummy, None) == -2
+    assert L.glmmoe_pack_fp8(dummy, 1, 128, 200, dummy, None) == -2
+    assert L.glmmoe_quant_act_fp8(dummy, 4, 100, dummy, dummy, None) == -2
+    assert L.glmmoe_quant_act_fp8(None, 4, 128, dummy, dummy, None) == -1
+    st = _lib.Fp8Layer()
+    src = _layer()
+    for name, _ in _lib.Layer._fields_:
+        setattr(st, name, getattr(src, name))
+    for n in (1, 8192):
+        b = L.glmmoe_fp8_layer_workspace_bytes(C.byref(st), n)
+        v = _lib.Fp8Ws()
+        base = 1 << 20
+        assert L.glmmoe_fp8_layer_workspace_view(C.byref(st), n, C.c_void_p(base), C.byref(v)) == 0
+        assert v.bytes == b
+        R = n * 9
+        regions = [v.logits, v.xq, v.xscale, v.topk_ids, v.topk_w, v.expert_offsets,
+                   v.sorted_token_ids, v.sorted_row, v.inv, v.tiles, v.ntiles, v.hq, v.hscale,
+                   v.dpart]
+        assert all(r % 256 == 0 for r in regions) and regions == sorted(regions)
+        assert v.xscale - v.xq >= n * 6144 and v.hscale - v.hq >= R * 2048
+        assert v.dpart + R * 6144 * 4 <= base + b
+    assert L.glmmoe_moe_layer_fp8(C.byref(st), dummy, 4, dummy, dummy, 16, None) == -3

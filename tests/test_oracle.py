@@ -319,3 +319,27 @@ def test_dequant_e4m3_blocks(oracle):
     out = oracle.dequant_e4m3_blocks(q, s)
     for r, k in [(0, 0), (127, 127), (128, 0), (255, 383), (200, 130)]:
         assert out[r, k] == np.float32(oracle.e4m3_to_f32(int(q[r, k]))) * s[r // 128, k // 128]
+
+
+def test_moe_forward_h_fp8(oracle):
+    """FP8 layer intermediate: with k = 1, weight 1 and no shared expert the
+    output is down . dequant(e4m3(h / s)) * s, h quantized per 128 features
+    (the codes taken from torch's float8_e4m3fn conversion)."""
+    torch = pytest.importorskip("torch")
+    L, rng = _tiny_layer(3)
+    x = rng.standard_normal((4, 256)).astype(np.float32)
+    plain, ids, w = oracle.moe_forward(x, 16, 1, L["g"], L["u"], L["d"], None, router_w=L["rw"],
+                                       e_bias=L["bias"], routed_scale=1.0)
+    q8, _, _ = oracle.moe_forward(x, 16, 1, L["g"], L["u"], L["d"], None, router_w=L["rw"],
+                                  e_bias=L["bias"], routed_scale=1.0, h_fp8=True)
+    for t in range(4):
+        e = ids[t, 0]
+        h = np.array([oracle.silu(float(v)) for v in oracle.linear(x[t:t + 1], L["g"][e])[0]],
+                     np.float32) * oracle.linear(x[t:t + 1], L["u"][e])[0]
+        s = (np.abs(h).max() / np.float32(448.0)).astype(np.float32)   # I = 128: one group
+        codes = torch.from_numpy((h / s).astype(np.float32)).to(torch.float8_e4m3fn)
+        hd = (codes.to(torch.float32).numpy() * s).astype(np.float32)
+        ref = oracle.linear(hd[None], L["d"][e])[0]
+        assert np.array_equal(q8[t], ref)
+    # e4m3 keeps 3 mantissa bits: the layer moves by a few percent, not more.
+    assert np.max(np.abs(q8 - plain)) <= 0.08 * np.max(np.abs(plain))
