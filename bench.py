@@ -4,8 +4,9 @@ A step is one pass of the whole GLM-5-class W4A16 MoE layer (router GEMM ->
 routing -> dispatch -> grouped gate/up/SiLU -> grouped down -> combine with
 the shared expert) over one batch of synthetic bf16 activations, weights
 resident in HBM. The headline workload is configs[1] (decode) at its largest
-batch, B = 64; the same run also times B = 1, 8, 32 and the 4096-token
-prefill of configs[2] and reports them under "sweep".
+batch, B = 64; the same run also times B = 1, 8, 32, the 4096-token
+prefill of configs[2] and the 8192-token FP8 prefill of configs[4] and
+reports them under "sweep".
 
 Prints ONE JSON line (rank 0). Inputs are device-resident before timing.
 """
@@ -27,6 +28,9 @@ EXPERT_BYTES = 3 * W4_MAT                        # 19,464,192
 GATE_UP_BYTES = 2 * W4_MAT
 ROUTER_BYTES = E * H * 2 + E * 4
 FLOP_PER_TOKEN = 2 * H * E + (K + 1) * (2 * H * 2 * I + 2 * I * H)
+FP8_PEAK = 5.0e15          # flop/s, dense fp8 MFMA
+FP8_MAT = I * H + (I // 128) * (H // 128) * 4    # e4m3 bytes + fp32 128x128 block scales
+FP8_EXPERT_BYTES = 3 * FP8_MAT                   # 37,757,952
 
 
 def log(*a):
@@ -141,6 +145,9 @@ def main():
     ap.add_argument("--no-sweep", action="store_true")
     ap.add_argument("--head-batch", type=int, default=64,
                     help="batch of the headline line (64 = configs[1]'s largest); for profiling")
+    ap.add_argument("--no-fp8", action="store_true", help="skip the configs[4] FP8 sweep line")
+    ap.add_argument("--fp8-only", action="store_true",
+                    help="only time the FP8 8192-token prefill (for profiling)")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     args = ap.parse_args()
@@ -160,6 +167,31 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calib_bytes": src.numel() * 4, "reps": 3}))
         return
+    def measure_fp8(n, steps, warmup):
+        from moe_cases import SynthFp8Layer
+        log("bench: building synthetic FP8 layer (configs[4] format)")
+        L8 = SynthFp8Layer(H, E, K, I, seed=1)
+        ms, U, bufs = time_layer(L8, n, steps, warmup, seed=100 + n, torch=torch)
+        st = stage_times(L8, n, bufs, max(3, min(steps, 10)), torch)
+        bytes_alg = (U + 1) * FP8_EXPERT_BYTES + ROUTER_BYTES + n * H * 2 + n * H * 4
+        flops = n * FLOP_PER_TOKEN
+        roof_ms = max(bytes_alg / HBM_PEAK, flops / FP8_PEAK) * 1e3
+        gu_ms, dn_ms = st["gate_up"], st["down"]
+        rows = n * (K + 1)
+        del L8, bufs
+        torch.cuda.empty_cache()
+        return {"n": n, "ms": ms, "tokens_per_s": n / (ms * 1e-3), "distinct_experts": U,
+                "alg_bytes": bytes_alg, "hbm_frac_layer": bytes_alg / (ms * 1e-3) / HBM_PEAK,
+                "mfma_frac_layer": flops / (ms * 1e-3) / FP8_PEAK,
+                "roofline_ms": roof_ms, "roofline_frac": roof_ms / ms, "stage_ms": st,
+                "gate_up_fp8_TFLOPs": rows * 2 * H * 2 * I / (gu_ms * 1e-3) / 1e12 if gu_ms else None,
+                "down_fp8_TFLOPs": rows * 2 * I * H / (dn_ms * 1e-3) / 1e12 if dn_ms else None}
+
+    if args.fp8_only:
+        r = measure_fp8(8192, max(3, args.steps // 10), 2)
+        print(json.dumps({"fp8_prefill_8192": r}), flush=True)
+        return
+
     log("bench: building synthetic W4A16 layer H=6144 E=256 k=8 I=2048 (+shared)")
     L = SynthLayer(H, E, K, I, seed=1)
     torch.cuda.synchronize()
@@ -187,6 +219,9 @@ def main():
         log("bench: sweep prefill 4096")
         sweep["prefill_4096"] = measure(4096, max(3, args.steps // 10), 2)
     sweep[f"decode_B{args.head_batch}"] = head
+    if not args.no_sweep and not args.no_fp8:
+        log("bench: sweep FP8 prefill 8192")
+        sweep["fp8_prefill_8192"] = measure_fp8(8192, max(3, args.steps // 10), 2)
 
     gu_ms = head["stage_ms"]["gate_up"]
     roof = {"bound": "hbm", "kernel": f"w4_expert_kernel<2,2,3> grouped gate/up (decode B={args.head_batch})",

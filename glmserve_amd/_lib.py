@@ -13,7 +13,8 @@ LIB_PATH = os.environ.get("GLMMOE_LIB_PATH", LIB_PATH)
 _vp, _i, _f, _sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
 SIGNATURES = {
     "glmmoe_version": (C.c_char_p, []),
-    "glmmoe_router_logits": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp]),
+    "glmmoe_router_logits_workspace_bytes": (_sz, [_i, _i, _i]),
+    "glmmoe_router_logits": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
     "glmmoe_moe_router": (_i, [_vp, _vp, _i, _i, _i, _i, _f, _vp, _vp, _vp]),
     "glmmoe_moe_dispatch": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "glmmoe_w4_packed_bytes": (_sz, [_i, _i]),
@@ -60,7 +61,7 @@ class Fp8Layer(Layer):
 
 class LayerWs(C.Structure):
     """glmmoe_layer_ws (include/glmmoe.h)."""
-    _fields_ = [("logits", _vp), ("xsum", _vp), ("topk_ids", _vp), ("topk_w", _vp),
+    _fields_ = [("logits", _vp), ("rpart", _vp), ("xsum", _vp), ("topk_ids", _vp), ("topk_w", _vp),
                 ("expert_offsets", _vp), ("sorted_token_ids", _vp), ("sorted_row", _vp),
                 ("inv", _vp), ("tiles", _vp), ("ntiles", _vp), ("h", _vp), ("hsum", _vp),
                 ("dpart", _vp), ("bytes", _sz)]
@@ -68,7 +69,7 @@ class LayerWs(C.Structure):
 
 class Fp8Ws(C.Structure):
     """glmmoe_fp8_ws (include/glmmoe.h)."""
-    _fields_ = [("logits", _vp), ("xq", _vp), ("xscale", _vp), ("topk_ids", _vp),
+    _fields_ = [("logits", _vp), ("rpart", _vp), ("xq", _vp), ("xscale", _vp), ("topk_ids", _vp),
                 ("topk_w", _vp), ("expert_offsets", _vp), ("sorted_token_ids", _vp),
                 ("sorted_row", _vp), ("inv", _vp), ("tiles", _vp), ("ntiles", _vp),
                 ("hq", _vp), ("hscale", _vp), ("dpart", _vp), ("bytes", _sz)]

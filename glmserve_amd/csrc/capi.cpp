@@ -68,6 +68,7 @@ size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v)
     };
     glmmoe_layer_ws w{};
     w.logits = reinterpret_cast<float*>(take((size_t)n * E * 4));
+    w.rpart = reinterpret_cast<float*>(take(router_logits_scratch_bytes(n, H, E)));
     w.xsum = reinterpret_cast<float*>(take((size_t)n * (H / 128) * 4));
     w.topk_ids = reinterpret_cast<int*>(take(nk * 4));
     w.topk_w = reinterpret_cast<float*>(take(nk * 4));
@@ -104,6 +105,7 @@ size_t carve8(const glmmoe_fp8_layer* L, int n, char* base, glmmoe_fp8_ws* v) {
     };
     glmmoe_fp8_ws w{};
     w.logits = reinterpret_cast<float*>(take((size_t)n * E * 4));
+    w.rpart = reinterpret_cast<float*>(take(router_logits_scratch_bytes(n, H, E)));
     w.xq = reinterpret_cast<uint8_t*>(take((size_t)n * H));
     w.xscale = reinterpret_cast<float*>(take((size_t)n * (H / 128) * 4));
     w.topk_ids = reinterpret_cast<int*>(take(nk * 4));
@@ -212,12 +214,21 @@ extern "C" {
 
 const char* glmmoe_version(void) { return "glmmoe 0.1 (gfx950)"; }
 
+size_t glmmoe_router_logits_workspace_bytes(int n, int H, int E) {
+    if (n <= 0 || H <= 0 || E <= 0) return 0;
+    return router_logits_scratch_bytes(n, H, E);
+}
+
 int glmmoe_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
-                         float* logits, float* xsum, void* stream) {
+                         float* logits, float* xsum, void* workspace, size_t workspace_bytes,
+                         void* stream) {
     if (!x || !wr || !logits || n <= 0 || H <= 0 || E <= 0) return GLMMOE_ERR_ARG;
     if (H % 8 || H > 8192) return GLMMOE_ERR_SHAPE;
     if (xsum && H % 128) return GLMMOE_ERR_SHAPE;
-    return launch_router_logits(x, wr, n, H, E, logits, xsum, S(stream));
+    const size_t need = router_logits_scratch_bytes(n, H, E);
+    if (need && (!workspace || workspace_bytes < need)) return GLMMOE_ERR_WORKSPACE;
+    return launch_router_logits(x, wr, n, H, E, logits, xsum, static_cast<float*>(workspace),
+                                S(stream));
 }
 
 int glmmoe_moe_router(const float* logits, const float* e_bias, int n, int E, int topk,
@@ -281,7 +292,10 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     const int H = L->hidden, E = L->n_experts, k = L->topk;
     begin_call();
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
-    rc = launch_router_logits(x, L->router_w, n, H, E, v.logits, v.xsum, s);
+    // Activation group sums only feed the large-group kernels.
+    const bool big = tile_rows_for(n, k, has_shared(L) ? 1 : 0) == kBigRows;
+    rc = launch_router_logits(x, L->router_w, n, H, E, v.logits, big ? v.xsum : nullptr, v.rpart,
+                              s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_ROUTER_TOPK, s);
     rc = launch_router_topk(v.logits, L->e_bias, n, E, k, L->norm_topk, L->routed_scale,
@@ -302,8 +316,10 @@ int glmmoe_expert_ffn_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int 
     hipStream_t s = S(stream);
     begin_call();
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
-    rc = launch_xsum(x, n, L->hidden, v.xsum, s);
-    if (rc) return rc;
+    if (tile_rows_for(n, L->topk, has_shared(L) ? 1 : 0) == kBigRows) {
+        rc = launch_xsum(x, n, L->hidden, v.xsum, s);
+        if (rc) return rc;
+    }
     return run_experts(L, x, n, topk_ids, topk_w, v.xsum, out, v, s);
 }
 
@@ -349,7 +365,7 @@ int glmmoe_moe_layer_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, fl
     const int H = L->hidden, E = L->n_experts, k = L->topk;
     begin_call();
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
-    rc = launch_router_logits(x, L->router_w, n, H, E, v.logits, nullptr, s);
+    rc = launch_router_logits(x, L->router_w, n, H, E, v.logits, nullptr, v.rpart, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_ROUTER_TOPK, s);
     rc = launch_router_topk(v.logits, L->e_bias, n, E, k, L->norm_topk, L->routed_scale,

@@ -32,8 +32,10 @@ struct Fp8Ptrs {
     const uint8_t* sh_down_q; const float* sh_down_s;
 };
 
+// Scratch (bytes) the router-logit launch needs for n tokens; 0 for large n.
+size_t router_logits_scratch_bytes(int n, int H, int E);
 int launch_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
-                         float* logits, float* xsum, hipStream_t s);
+                         float* logits, float* xsum, float* scratch, hipStream_t s);
 int launch_xsum(const uint16_t* x, int n, int H, float* xsum, hipStream_t s);
 int launch_router_topk(const float* logits, const float* e_bias, int n, int E, int topk,
                        int norm_topk, float routed_scale, int* ids, float* w, hipStream_t s);

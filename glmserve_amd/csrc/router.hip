@@ -9,70 +9,222 @@
 namespace glmmoe {
 
 // ---------------------------------------------------------------------------
-// Router logits. One wave per (expert, group of 8 tokens). Lane c owns K
-// chunk c (128 consecutive inputs) and keeps 8 independent running sums, one
-// per token, each accumulated from zero in ascending K. The chunk sums of a
-// token are then added in ascending chunk order by one lane. That is exactly
-// the order the CPU oracle restates (chunked linear_forward), and since bf16
-// products are exact in fp32, fma(x, w, s) == s + x*w, so logits are
-// bit-identical to it.
+// Router logits in the fixed order the CPU oracle restates (chunked
+// linear_forward): K is cut into chunks of 128; each (token, expert, chunk)
+// partial is accumulated from zero in ascending K; a logit is the ascending
+// sum of its chunk partials. bf16 products are exact in fp32, so
+// fma(x, w, s) == s + x*w and both kernels below give logits bit-identical
+// to the oracle's.
 // ---------------------------------------------------------------------------
+// Small batches, two passes.
+// Pass 1: one single-wave workgroup per (64-expert block, 128-K chunk,
+// 8-token group); lane = expert, keeping one running sum per token. Decode
+// batches are latency-bound, so all loads are issued up front and coalesced:
+// the 64 x 256-byte weight chunk rows (4 rows per load instruction) and the
+// tokens' 8 x 256 activation bytes go through registers into LDS (weight rows
+// padded to 272 B so the per-lane row reads hit distinct banks); then each
+// weight value read feeds 8 FMAs, one per token, with the activations read
+// as wave-uniform LDS broadcasts. Partials go to part [n, nchunks, E].
+// Pass 2: one thread per (token, expert) loads its chunk partials (all in
+// flight together) and adds them in ascending chunk order.
 constexpr int kRouterTG = 8;    // tokens per wave
 constexpr int kRouterKC = 128;  // K chunk
 constexpr int kRouterMaxChunks = 64;
+constexpr int kRouterRow = kRouterKC / 2 + 4;   // LDS dwords per weight row (+16 B pad)
 
-__global__ __launch_bounds__(256) void router_logits_kernel(
+__global__ __launch_bounds__(64) void router_partials_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, int n, int H, int E,
-    float* __restrict__ logits, float* __restrict__ xsum) {
-    __shared__ float part[4][kRouterTG][kRouterMaxChunks + 1];
-    const int lane = threadIdx.x & 63;
-    const int wv = threadIdx.x >> 6;
-    const long wid = (long)blockIdx.x * 4 + wv;
-    const int ngroups = (n + kRouterTG - 1) / kRouterTG;
-    // Waves past the end stay resident until the barrier (no early return).
-    const bool active = wid < (long)E * ngroups;
-    const int e = active ? (int)(wid % E) : 0;
-    const int t0 = active ? (int)(wid / E) * kRouterTG : n;
+    float* __restrict__ part) {
+    __shared__ __align__(16) uint32_t wl[64 * kRouterRow];
+    __shared__ __align__(16) uint4 xs[kRouterTG][kRouterKC / 8];
     const int nchunks = (H + kRouterKC - 1) / kRouterKC;
+    const int eblocks = (E + 63) / 64;
+    const int lane = threadIdx.x;
+    long b = blockIdx.x;
+    const int c = (int)(b % nchunks); b /= nchunks;
+    const int eb = (int)(b % eblocks); b /= eblocks;
+    const int t0 = (int)b * kRouterTG;
+    const int nt = min(kRouterTG, n - t0);
+    const int k0 = c * kRouterKC;
+    const int klen = min(kRouterKC, H - k0);   // multiple of 8
+    const int oct = lane & 15;
+    // Branch-free loads: octets past the chunk end, experts past E and tokens
+    // past n re-read valid data that is never used.
+    const int octc = oct * 8 < klen ? oct : 0;
+    uint4 wv[16], xv[2];
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int row = j * 4 + (lane >> 4);
+        const int e = min(eb * 64 + row, E - 1);
+        wv[j] = reinterpret_cast<const uint4*>(wr + (size_t)e * H + k0)[octc];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int t = (lane >> 4) + 4 * j;
+        xv[j] = reinterpret_cast<const uint4*>(x + (size_t)(t0 + min(t, nt - 1)) * H + k0)[octc];
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+        const int row = j * 4 + (lane >> 4);
+        *reinterpret_cast<uint4*>(&wl[row * kRouterRow + oct * 4]) = wv[j];
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) xs[(lane >> 4) + 4 * j][oct] = xv[j];
+    __syncthreads();
 
-    if (active && lane < nchunks) {
-        const int k0 = lane * kRouterKC;
-        const int klen = min(kRouterKC, H - k0);  // multiple of 8
-        float s[kRouterTG];
-        float xs[kRouterTG];
+    float s[kRouterTG];
 #pragma unroll
-        for (int t = 0; t < kRouterTG; ++t) { s[t] = 0.0f; xs[t] = 0.0f; }
-        const uint4* wp = reinterpret_cast<const uint4*>(wr + (size_t)e * H + k0);
-        for (int i8 = 0; i8 < klen / 8; ++i8) {
-            const uint4 wv4 = wp[i8];
-            const uint32_t wd[4] = {wv4.x, wv4.y, wv4.z, wv4.w};
+    for (int t = 0; t < kRouterTG; ++t) s[t] = 0.0f;
+    for (int i8 = 0; i8 < klen / 8; ++i8) {
+        const uint4 w4 = *reinterpret_cast<const uint4*>(&wl[lane * kRouterRow + i8 * 4]);
+        const uint32_t wd[4] = {w4.x, w4.y, w4.z, w4.w};
+        float wf[8];
 #pragma unroll
-            for (int t = 0; t < kRouterTG; ++t) {
-                if (t0 + t >= n) break;
-                const uint4 xv4 =
-                    reinterpret_cast<const uint4*>(x + (size_t)(t0 + t) * H + k0)[i8];
-                const uint32_t xd[4] = {xv4.x, xv4.y, xv4.z, xv4.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float xl = bf16_to_f32(xd[j] & 0xffffu), xh = bf16_to_f32(xd[j] >> 16);
-                    const float wl = bf16_to_f32(wd[j] & 0xffffu), wh = bf16_to_f32(wd[j] >> 16);
-                    s[t] = __builtin_fmaf(xl, wl, s[t]);
-                    s[t] = __builtin_fmaf(xh, wh, s[t]);
-                    if (e == 0 && xsum) { xs[t] += xl; xs[t] += xh; }
-                }
-            }
+        for (int d = 0; d < 4; ++d) {
+            wf[2 * d] = bf16_to_f32(wd[d] & 0xffffu);
+            wf[2 * d + 1] = __uint_as_float(wd[d] & 0xffff0000u);
         }
 #pragma unroll
         for (int t = 0; t < kRouterTG; ++t) {
-            part[wv][t][lane] = s[t];
-            if (e == 0 && xsum && t0 + t < n) xsum[(size_t)(t0 + t) * nchunks + lane] = xs[t];
+            if (t < nt) {
+                const uint4 x4 = xs[t][i8];
+                const uint32_t xd[4] = {x4.x, x4.y, x4.z, x4.w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    s[t] = __builtin_fmaf(bf16_to_f32(xd[d] & 0xffffu), wf[2 * d], s[t]);
+                    s[t] = __builtin_fmaf(__uint_as_float(xd[d] & 0xffff0000u), wf[2 * d + 1], s[t]);
+                }
+            }
         }
     }
+    const int e = eb * 64 + lane;
+    if (e < E) {
+#pragma unroll
+        for (int t = 0; t < kRouterTG; ++t)
+            if (t < nt) part[((size_t)(t0 + t) * nchunks + c) * E + e] = s[t];
+    }
+}
+
+__global__ __launch_bounds__(256) void router_fold_kernel(const float* __restrict__ part, int n,
+                                                          int nchunks, int E,
+                                                          float* __restrict__ logits) {
+    const long i = (long)blockIdx.x * 256 + threadIdx.x;
+    if (i >= (long)n * E) return;
+    const long t = i / E;
+    const int e = (int)(i % E);
+    const float* p = part + (size_t)t * nchunks * E + e;
+    float v[kRouterMaxChunks];
+#pragma unroll
+    for (int c = 0; c < kRouterMaxChunks; ++c) v[c] = c < nchunks ? p[(size_t)c * E] : 0.0f;
+    float total = 0.0f;
+#pragma unroll
+    for (int c = 0; c < kRouterMaxChunks; ++c)
+        if (c < nchunks) total = total + v[c];
+    logits[i] = total;
+}
+
+// Large batches: a VALU GEMM tiled through LDS. Workgroup = 128 threads, tile
+// 32 tokens x 128 experts; thread (tt, ee) owns 8 tokens x 4 experts. K runs
+// in steps of 32: the step's x [32 x 32] and w [128 x 32] are unpacked to
+// fp32 once and stored k-major in LDS (double-buffered; the next step's
+// global loads are in flight during the current step's FMAs), so each k costs
+// a thread 3 LDS reads (x broadcast across the 32 threads of a token group)
+// for 32 FMAs. Every 4 steps (one 128-K chunk) the running chunk partials are
+// added into the totals in ascending chunk order and restarted from zero.
+constexpr int kTiledTok = 32;
+constexpr int kTiledExp = 128;
+constexpr int kTiledK = 32;
+constexpr int kTiledThreads = 128;
+constexpr int kTiledMinTokens = 256;   // below: the small-batch kernel
+
+__global__ __launch_bounds__(kTiledThreads) void router_logits_tiled_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, int n, int H, int E,
+    float* __restrict__ logits) {
+    __shared__ __align__(16) float xl[2][kTiledK][kTiledTok];   // [buffer][k][token]
+    __shared__ __align__(16) float wl[2][kTiledK][kTiledExp];
+    const int eblocks = (E + kTiledExp - 1) / kTiledExp;
+    const int eb = (int)(blockIdx.x % eblocks);
+    const int t0 = (int)(blockIdx.x / eblocks) * kTiledTok;
+    const int e0 = eb * kTiledExp;
+    const int tid = threadIdx.x;
+    const int tt = tid >> 5, ee = tid & 31;     // 4 token groups x 32 expert quads
+    // Staging roles: x -- token tid / 4, k-octet tid % 4; w -- expert tid, all 32 k.
+    const uint4* xsrc = reinterpret_cast<const uint4*>(x + (size_t)min(t0 + (tid >> 2), n - 1) * H) + (tid & 3);
+    const uint4* wsrc = reinterpret_cast<const uint4*>(wr + (size_t)min(e0 + tid, E - 1) * H);
+    const int nsteps = H / kTiledK;
+
+    uint4 xr, wrg[4];
+    auto load = [&](int st) {
+        xr = xsrc[st * 4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) wrg[j] = wsrc[st * 4 + j];
+    };
+    auto store = [&](int buf) {
+        const uint32_t xd[4] = {xr.x, xr.y, xr.z, xr.w};
+#pragma unroll
+        for (int d = 0; d < 4; ++d) {
+            const int k = (tid & 3) * 8 + 2 * d;
+            xl[buf][k][tid >> 2] = bf16_to_f32(xd[d] & 0xffffu);
+            xl[buf][k + 1][tid >> 2] = __uint_as_float(xd[d] & 0xffff0000u);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            const uint32_t wd[4] = {wrg[j].x, wrg[j].y, wrg[j].z, wrg[j].w};
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+                const int k = j * 8 + 2 * d;
+                wl[buf][k][tid] = bf16_to_f32(wd[d] & 0xffffu);
+                wl[buf][k + 1][tid] = __uint_as_float(wd[d] & 0xffff0000u);
+            }
+        }
+    };
+
+    float part[8][4], tot[8][4];
+#pragma unroll
+    for (int i = 0; i < 8; ++i)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) { part[i][j] = 0.0f; tot[i][j] = 0.0f; }
+
+    load(0);
+    store(0);
     __syncthreads();
-    if (active && lane < kRouterTG && t0 + lane < n) {
-        float total = 0.0f;
-        for (int c = 0; c < nchunks; ++c) total = total + part[wv][lane][c];
-        logits[(size_t)(t0 + lane) * E + e] = total;
+    for (int st = 0; st < nsteps; ++st) {
+        const int buf = st & 1;
+        if (st + 1 < nsteps) load(st + 1);
+#pragma unroll 8
+        for (int k = 0; k < kTiledK; ++k) {
+            const float4 xa = *reinterpret_cast<const float4*>(&xl[buf][k][tt * 8]);
+            const float4 xb = *reinterpret_cast<const float4*>(&xl[buf][k][tt * 8 + 4]);
+            const float4 wv = *reinterpret_cast<const float4*>(&wl[buf][k][ee * 4]);
+            const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+            const float wf[4] = {wv.x, wv.y, wv.z, wv.w};
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) part[i][j] = __builtin_fmaf(xv[i], wf[j], part[i][j]);
+        }
+        if ((st & 3) == 3 || st + 1 == nsteps) {   // end of a 128-K chunk
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) { tot[i][j] = tot[i][j] + part[i][j]; part[i][j] = 0.0f; }
+        }
+        if (st + 1 < nsteps) store(buf ^ 1);
+        __syncthreads();
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int t = t0 + tt * 8 + i;
+        if (t >= n) continue;
+        const int e = e0 + ee * 4;
+        if (e + 3 < E && (E & 3) == 0) {
+            *reinterpret_cast<float4*>(logits + (size_t)t * E + e) =
+                make_float4(tot[i][0], tot[i][1], tot[i][2], tot[i][3]);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                if (e + j < E) logits[(size_t)t * E + e + j] = tot[i][j];
+        }
     }
 }
 
@@ -197,13 +349,31 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     }
 }
 
+size_t router_logits_scratch_bytes(int n, int H, int E) {
+    if (n >= kTiledMinTokens && H % kRouterKC == 0) return 0;
+    return (size_t)n * ((H + kRouterKC - 1) / kRouterKC) * E * 4;
+}
+
 int launch_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
-                         float* logits, float* xsum, hipStream_t s) {
-    const long waves = (long)E * ((n + kRouterTG - 1) / kRouterTG);
-    const long blocks = (waves + 3) / 4;
-    hipLaunchKernelGGL(router_logits_kernel, dim3((unsigned)blocks), dim3(256), 0, s, x, wr, n,
-                       H, E, logits, xsum);
-    return hipGetLastError() == hipSuccess ? 0 : -4;
+                         float* logits, float* xsum, float* scratch, hipStream_t s) {
+    const int nchunks = (H + kRouterKC - 1) / kRouterKC;
+    if (nchunks > kRouterMaxChunks) return -2;
+    if (n >= kTiledMinTokens && H % kRouterKC == 0) {
+        const long blocks = (long)((E + kTiledExp - 1) / kTiledExp) * ((n + kTiledTok - 1) / kTiledTok);
+        hipLaunchKernelGGL(router_logits_tiled_kernel, dim3((unsigned)blocks), dim3(kTiledThreads),
+                           0, s, x, wr, n, H, E, logits);
+    } else {
+        if (!scratch) return -3;
+        const long blocks = (long)nchunks * ((E + 63) / 64) * ((n + kRouterTG - 1) / kRouterTG);
+        hipLaunchKernelGGL(router_partials_kernel, dim3((unsigned)blocks), dim3(64), 0, s, x, wr,
+                           n, H, E, scratch);
+        if (hipGetLastError() != hipSuccess) return -4;
+        const long outs = (long)n * E;
+        hipLaunchKernelGGL(router_fold_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0,
+                           s, scratch, n, nchunks, E, logits);
+    }
+    if (hipGetLastError() != hipSuccess) return -4;
+    return xsum ? launch_xsum(x, n, H, xsum, s) : 0;
 }
 
 int launch_xsum(const uint16_t* x, int n, int H, float* xsum, hipStream_t s) {

@@ -35,8 +35,10 @@ def router_logits(x, wr, logits, xsum=None, stream=None):
     _need(logits, torch.float32, n * E, "logits")
     if xsum is not None:
         _need(xsum, torch.float32, n * (H // 128), "xsum")
-    check(lib().glmmoe_router_logits(_p(x), _p(wr), n, H, E, _p(logits), _p(xsum), _s(stream)),
-          "router_logits")
+    nb = lib().glmmoe_router_logits_workspace_bytes(n, H, E)
+    ws = torch.empty(nb, dtype=torch.uint8, device=x.device) if nb else None
+    check(lib().glmmoe_router_logits(_p(x), _p(wr), n, H, E, _p(logits), _p(xsum), _p(ws), nb,
+                                     _s(stream)), "router_logits")
 
 
 def moe_router(logits, e_bias, n, E, topk, norm_topk, routed_scale, topk_ids, topk_weights,

@@ -39,11 +39,15 @@ const char* glmmoe_version(void);
  * gemm_fp32, cuda/kernels.cuh:37-38). Reduction order is fixed: K is cut into
  * chunks of 128, each chunk summed from zero in ascending K, chunk sums added
  * in ascending order -- restated by the CPU oracle, so logits are bit-exact.
- * xsum (nullable) receives sum_{k in chunk} x[t,k] as [n, ceil(H/128)] fp32,
- * the activation group sums the W4A16 expert kernels consume.
- * Limits: H % 8 == 0, H <= 8192. */
+ * xsum (nullable) receives sum_{k in chunk} x[t,k] as [n, H/128] fp32 (H %
+ * 128 == 0), the activation group sums the W4A16 expert kernels consume.
+ * workspace: device scratch of glmmoe_router_logits_workspace_bytes(n, H, E)
+ * bytes (chunk partials of small batches; 0 bytes, NULL allowed, from 256
+ * tokens with H % 128 == 0). Limits: H % 8 == 0, H <= 8192. */
+size_t glmmoe_router_logits_workspace_bytes(int n, int H, int E);
 int glmmoe_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
-                         float* logits, float* xsum, void* stream);
+                         float* logits, float* xsum, void* workspace, size_t workspace_bytes,
+                         void* stream);
 
 /* Sigmoid top-k routing with score-correction bias.
  * Replaces moe_router (cuda/kernels.cuh:243-245, cuda/moe_router.cu:17-79):
@@ -120,6 +124,7 @@ typedef struct glmmoe_w4a16_layer {
  * one shared-expert row per token). */
 typedef struct glmmoe_layer_ws {
     float* logits;        /* [n, E] */
+    float* rpart;         /* router chunk partials (glmmoe_router_logits workspace) */
     float* xsum;          /* [n, H/128] */
     int* topk_ids;        /* [n, topk] */
     float* topk_w;        /* [n, topk] */
@@ -202,6 +207,7 @@ typedef struct glmmoe_fp8_layer {
 
 typedef struct glmmoe_fp8_ws {
     float* logits;        /* [n, E] */
+    float* rpart;         /* router chunk partials */
     uint8_t* xq;          /* [n, H] e4m3 */
     float* xscale;        /* [n, H/128] */
     int* topk_ids;        /* [n, topk] */

@@ -45,8 +45,10 @@ inline int moe_dispatch(const int* topk_ids, int n, int topk, int E, int* expert
 // Router-logit GEMM (replaces gemm_linear(s.normed, d.router, ...) at
 // src/model_gpu.cpp:1448 for bf16 activations and router weights).
 inline int router_logits(const uint16_t* x_bf16, const uint16_t* wr_bf16, int n, int H, int E,
-                         float* logits, float* xsum = nullptr, void* s = nullptr) {
-    return glmmoe_router_logits(x_bf16, wr_bf16, n, H, E, logits, xsum, s);
+                         float* logits, float* xsum, void* workspace, size_t workspace_bytes,
+                         void* s = nullptr) {
+    return glmmoe_router_logits(x_bf16, wr_bf16, n, H, E, logits, xsum, workspace,
+                                workspace_bytes, s);
 }
 
 // Load-time repack of reference-layout W4 experts (src/model_gpu.cpp:913-1010

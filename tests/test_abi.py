@@ -37,14 +37,18 @@ def test_host_argument_checks():
     # NULL pointers / non-positive sizes -> GLMMOE_ERR_ARG before any HIP call.
     assert L.glmmoe_moe_router(None, None, 4, 256, 8, 1, 2.5, None, None, None) == -1
     assert L.glmmoe_moe_dispatch(None, 4, 8, 256, None, None, None, None) == -1
-    assert L.glmmoe_router_logits(None, None, 1, 6144, 256, None, None, None) == -1
+    assert L.glmmoe_router_logits(None, None, 1, 6144, 256, None, None, None, 0, None) == -1
     dummy = C.c_void_p(16)   # never dereferenced: the shape checks reject first
     # Shapes outside the kernels' range -> GLMMOE_ERR_SHAPE.
     assert L.glmmoe_moe_router(dummy, None, 4, 256, 9, 1, 2.5, dummy, dummy, None) == -2
     assert L.glmmoe_moe_router(dummy, None, 4, 600, 8, 1, 2.5, dummy, dummy, None) == -2
     assert L.glmmoe_moe_router(dummy, None, 4, 4, 8, 1, 2.5, dummy, dummy, None) == -2
     assert L.glmmoe_moe_dispatch(dummy, 4, 8, 513, dummy, dummy, dummy, None) == -2
-    assert L.glmmoe_router_logits(dummy, dummy, 1, 6145, 256, dummy, None, None) == -2
+    assert L.glmmoe_router_logits(dummy, dummy, 1, 6145, 256, dummy, None, None, 0, None) == -2
+    # small batches need the partials scratch; from 256 tokens none
+    assert L.glmmoe_router_logits_workspace_bytes(64, 6144, 256) == 64 * 48 * 256 * 4
+    assert L.glmmoe_router_logits_workspace_bytes(256, 6144, 256) == 0
+    assert L.glmmoe_router_logits(dummy, dummy, 64, 6144, 256, dummy, None, None, 0, None) == -3
     assert L.glmmoe_pack_w4a16(dummy, dummy, 0, 1, 15, 128, 128, dummy, dummy, None) == -2
     assert L.glmmoe_pack_w4a16(dummy, dummy, 0, 1, 16, 100, 128, dummy, dummy, None) == -2
     assert L.glmmoe_pack_w4a16(dummy, dummy, 0, 1, 16, 128, 64, dummy, dummy, None) == -2
@@ -76,7 +80,7 @@ def test_workspace_sizing_and_view():
         assert v.bytes == b
         R = n * 8 + n
         # regions are 256-byte aligned, ordered, inside [base, base + bytes)
-        regions = [v.logits, v.xsum, v.topk_ids, v.topk_w, v.expert_offsets, v.sorted_token_ids,
+        regions = [v.logits, v.rpart, v.xsum, v.topk_ids, v.topk_w, v.expert_offsets, v.sorted_token_ids,
                    v.sorted_row, v.inv, v.tiles, v.ntiles, v.h, v.hsum, v.dpart]
         assert all(r % 256 == 0 for r in regions)
         assert regions == sorted(regions) and regions[0] == base
@@ -131,7 +135,7 @@ def test_fp8_host_checks_and_workspace():
         assert L.glmmoe_fp8_layer_workspace_view(C.byref(st), n, C.c_void_p(base), C.byref(v)) == 0
         assert v.bytes == b
         R = n * 9
-        regions = [v.logits, v.xq, v.xscale, v.topk_ids, v.topk_w, v.expert_offsets,
+        regions = [v.logits, v.rpart, v.xq, v.xscale, v.topk_ids, v.topk_w, v.expert_offsets,
                    v.sorted_token_ids, v.sorted_row, v.inv, v.tiles, v.ntiles, v.hq, v.hscale,
                    v.dpart]
         assert all(r % 256 == 0 for r in regions) and regions == sorted(regions)

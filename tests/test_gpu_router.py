@@ -95,13 +95,22 @@ def test_dispatch_matches_oracle(oracle, n, k, E, mode):
 def test_router_logits_bit_exact(oracle):
     from moe_cases import bf16_bits
     rng = np.random.default_rng(5)
-    for n, H, E in [(1, 6144, 256), (13, 6144, 256), (64, 256, 16), (3, 1000, 7)]:
+    # (n >= 256 with H % 128 == 0 runs the LDS-tiled kernel; the rest the small-batch one)
+    for n, H, E in [(1, 6144, 256), (13, 6144, 256), (64, 256, 16), (3, 1000, 7), (37, 8192, 300),
+                    (9, 6144, 1), (300, 6144, 256), (260, 8192, 300), (512, 256, 16), (257, 1024, 5),
+                    (300, 1000, 7)]:
         x = bf16_bits(rng.standard_normal((n, H)))
         w = bf16_bits(0.02 * rng.standard_normal((E, H)))
         dx = torch.from_numpy(x.view(np.int16)).cuda().view(torch.bfloat16)
         dw = torch.from_numpy(w.view(np.int16)).cuda().view(torch.bfloat16)
         lg = torch.empty(n, E, dtype=torch.float32, device="cuda")
-        G.router_logits(dx, dw, lg)
+        xs = torch.empty(n, max(1, H // 128), dtype=torch.float32, device="cuda") if H % 128 == 0 else None
+        G.router_logits(dx, dw, lg, xs)
         torch.cuda.synchronize()
         ref = oracle.router_logits_bf16(x, w)
         assert np.array_equal(lg.cpu().numpy().view(np.uint32), ref.view(np.uint32)), (n, H, E)
+        if xs is not None:
+            # group sums: ascending sequential fp32 sum of each 128-channel group
+            xf = (x.astype(np.uint32) << 16).view(np.float32).reshape(n, H // 128, 128)
+            rx = np.cumsum(xf, axis=2, dtype=np.float32)[:, :, -1]
+            assert np.array_equal(xs.cpu().numpy().view(np.uint32), rx.view(np.uint32)), (n, H)
