@@ -26,6 +26,14 @@ __device__ __forceinline__ uint32_t f32_to_bf16(float f) {
     return b >> 16;
 }
 
+// Two f32 -> packed bf16 (a in the low half), round-to-nearest-even, one
+// v_cvt_pk_bf16_f32.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2){a, b}, bf16x2));
+}
+
 // ---- exp / sigmoid ---------------------------------------------------------
 // One exp definition shared, operation for operation, with the CPU oracle:
 // Cody-Waite reduction x = n*ln2 + r with ln2 split hi/lo, degree-7 Taylor
@@ -56,9 +64,10 @@ __device__ __forceinline__ float exp_fixed(float x) {
 __device__ __forceinline__ float sigmoid_fixed(float x) { return 1.0f / (1.0f + exp_fixed(-x)); }
 
 // SiLU for the expert activations (tolerance-checked, not bit-checked): the
-// hardware exp2 is accurate to ~1 ulp and much cheaper than exp_fixed.
+// hardware exp2 and reciprocal are accurate to ~1 ulp and much cheaper than
+// exp_fixed and an IEEE division.
 __device__ __forceinline__ float silu_fast(float x) {
-    return x / (1.0f + __builtin_amdgcn_exp2f(-x * 1.44269504088896341f));
+    return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-x * 1.44269504088896341f));
 }
 
 // ---- int4 -> bf16 -----------------------------------------------------------

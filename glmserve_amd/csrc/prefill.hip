@@ -7,22 +7,33 @@
 // GLMSERVE_MMA_MOE_MIN_TS) and its W4A16 expert FFN semantics
 // (cuda/moe_expert.cu:143-222).
 //
-// Workgroup = 8 waves as a 4 (features) x 2 (rows) grid; every wave owns 64
-// features x 64 rows = 2 x 2 MFMA blocks of 32 x 32. For gate/up a wave's two
-// feature blocks are 32 gate features and the same 32 up features, so
-// SiLU(g) * u is formed in registers. The K loop runs over 128-K groups (one
-// int4 scale group): per group, the workgroup's 16 weight tiles (16 KiB), their
-// scales, the group sums of the 128 rows and the 128 activation rows
-// (gathered by token id for gate/up) are streamed global -> LDS by LDS-DMA into
-// a 3-slot ring, as in the decode kernels: each wave issues the same kDma DMAs
-// per group, waits with an immediate vmcnt, and one s_barrier per group
-// publishes the slot.
+// Workgroup = 8 waves as a 4 (features) x 2 (rows) grid; every wave owns
+// 64 rows x 64 weight rows = 2 x 2 MFMA blocks of 32 x 32. The activations
+// are the MFMA A operand (rows = grouped token rows) and the int4 weights the
+// B operand (columns = output features), so each lane's output column is one
+// feature and needs one weight scale per 128-K group. For gate/up a wave's two
+// weight blocks are 32 gate features and the same 32 up features, so
+// SiLU(g) * u is formed in registers.
 //
-// Per group and 32 x 32 block: P = sum_k (128 + c) x over the group's 128 K
-// (8 MFMAs), then acc += scale_row * (P - 136 * X_col), where X_col is the
-// group sum of the column's activations: xsum from the router pass for gate/up,
-// and for down the hsum this kernel's gate/up epilogue writes (the 4 feature
-// waves of a workgroup cover exactly one 128-feature group of h).
+// Streaming. The K loop runs over 128-K groups (one int4 scale group): per
+// group, the workgroup's 16 weight tiles (16 KiB), their scales, the group
+// sums of the 128 rows and the 128 activation rows (gathered by token id for
+// gate/up) are copied global -> LDS by LDS-DMA into a 3-slot ring. Each wave
+// issues the same kDma DMAs per group from per-lane source pointers computed
+// once per work item, waits with an immediate vmcnt, and one s_barrier per
+// group publishes the slot.
+//
+// Arithmetic per group and 32 x 32 block. The int4 code c decodes exactly to
+// the bf16 of 128 + c (see dq_w4), so the MFMAs produce
+//   P = sum_k (128 + c) x = sum_k (c - 8) x + 136 X,   X = sum_k x (group sum).
+// The chain is seeded with -136 X from one extra MFMA whose A operand holds X
+// split into bf16 hi + lo parts (K slots 0 and 1; X - hi is exact in fp32 and
+// its bf16 rounding leaves a relative error below 2^-16 of X) against a
+// constant B of -136; the seed depends only on the rows, so both weight
+// blocks of a wave share it. Then acc += scale_col * P: one fma per
+// accumulator element per group. X is xsum from the router pass for gate/up
+// and, for down, the hsum this kernel's gate/up epilogue writes (the 4
+// feature waves of a workgroup cover exactly one 128-feature group of h).
 //
 // MFMA 32x32x16 is used because on gfx950 it sustains ~2.2 PFLOP/s of bf16
 // where 16x16x32 reaches ~1.2 (measured with back-to-back independent chains).
@@ -52,7 +63,7 @@ struct BigRing {
     static constexpr int kGOff = kSOff + 512;           // group sums: row r at 4 r (512 B)
     static constexpr int kJunk = kGOff + 512;           // target of the placeholder DMAs
     static constexpr int kXOff = kJunk + 256;
-    static constexpr int kQuad = 1024 + 64;             // one DMA = 4 rows x 256 B (+ pad)
+    static constexpr int kQuad = 1024;                  // one DMA = 4 rows x 256 B
     static constexpr int kSlot = kXOff + (kBigRows / 4) * kQuad;
     static constexpr int kBytes = kBigD * kSlot;
     static constexpr int kRed = kBytes;                 // [4][128] floats: h group-sum partials
@@ -61,13 +72,20 @@ struct BigRing {
     static_assert(kTotal <= 160 * 1024, "one workgroup's LDS");
 #ifdef GLMMOE_BIG_NODMA
     static constexpr int kDma = 0;   // diagnostics: compute on stale LDS, no streaming
+#elif defined(GLMMOE_BIG_NOXDMA)
+    static constexpr int kDma = 2 + 1 + 1;   // diagnostics: no activation streaming
+#elif defined(GLMMOE_BIG_NOWDMA)
+    static constexpr int kDma = 1 + 1 + 4;   // diagnostics: no weight-tile streaming
 #else
     static constexpr int kDma = 2 + 1 + 1 + 4;          // per wave per group
 #endif
-    // A DMA block holds 4 rows interleaved at 16 B: chunk c (8 bf16) of row r
-    // sits at block(r / 4) + 64 c + 16 (r % 4); with the 1088-byte block stride
-    // the 32 rows an MFMA fragment reads fall on distinct banks.
-    static __device__ __forceinline__ int row_off(int r) { return (r >> 2) * kQuad + (r & 3) * 16; }
+    // Activation rows are 256 B each, row r at 256 r, so one DMA of 64 lanes
+    // reads 4 whole rows, 16 consecutive lanes per row (lanes that share
+    // cache lines are adjacent, which the address coalescer needs for full
+    // L2 bandwidth). Inside a row, 16-byte chunk c sits at slot c ^ (r & 15):
+    // the 16 rows an MFMA fragment pass reads at one chunk land on 16
+    // distinct bank groups.
+    static __device__ __forceinline__ int row_off(int r) { return r * 256; }
 };
 
 template <int NMAT>
@@ -89,13 +107,20 @@ __device__ __forceinline__ void tile_of(int t, int g, int& m, int& fb) {
     }
 }
 
+// DMA sources of one item at K-group 0; group kg adds kg times the per-group
+// stride of each stream. The weight-tile bases are wave-uniform (SGPRs); the
+// per-lane parts are 32-bit element offsets to keep the loop's VGPRs low.
+struct IssuePtrs {
+    const uint4* w[2];       // this wave's weight tiles 2 wave, 2 wave + 1 (lane added at issue)
+    const uint16_t* s;       // scale dword of this lane (waves 0, 1)
+    uint32_t g;              // gsum offset of one row (waves 2, 3)
+    uint32_t x[4];           // src offset of 16 B of one activation row, per row DMA
+};
+
 template <int NMAT>
-__device__ __forceinline__ void big_issue(const BigArgs& a, const BigItem& it, int kg, int K,
-                                          int KG, char* slot, int wave, int lane) {
-    using RG = BigRing;
-#ifdef GLMMOE_BIG_NODMA
-    return;
-#endif
+__device__ __forceinline__ IssuePtrs issue_ptrs(const BigArgs& a, const BigItem& it, int K, int KG,
+                                                int wave, int lane) {
+    IssuePtrs p;
     const bool sh = it.e == a.E;
     const int frows = NMAT == 2 ? a.I : a.H;
     const size_t mstride_q = (size_t)(frows / 16) * KG * 64;
@@ -108,145 +133,149 @@ __device__ __forceinline__ void big_issue(const BigArgs& a, const BigItem& it, i
         wbase[m] = sh ? a.swq[mm] : a.wq[mm] + (size_t)it.e * mstride_q;
         sbase[m] = sh ? a.sws[mm] : a.ws[mm] + (size_t)it.e * mstride_s;
     }
-    // Weight tiles 2 wave, 2 wave + 1.
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int t = wave * 2 + j;
         int m, fb;
-        tile_of<NMAT>(t, it.g, m, fb);
-        dma16(wbase[m] + ((size_t)fb * KG + kg) * 64 + lane, slot + t * 1024);
+        tile_of<NMAT>(wave * 2 + j, it.g, m, fb);
+        p.w[j] = wbase[m] + (size_t)fb * KG * 64;
     }
-    // Scales: waves 0 / 1 fetch tiles 0-7 / 8-15 (lane -> tile lane / 8, dword
-    // lane % 8); the other waves issue a placeholder so every wave issues kDma.
     {
-        const int t = (wave & 1) * 8 + (lane >> 3);
         int m, fb;
-        tile_of<NMAT>(t, it.g, m, fb);
-        dma4(sbase[m] + ((size_t)fb * KG + kg) * 16 + (lane & 7) * 2,
-             slot + (wave < 2 ? RG::kSOff + (wave & 1) * 256 : RG::kJunk));
+        tile_of<NMAT>((wave & 1) * 8 + (lane >> 3), it.g, m, fb);
+        p.s = sbase[m] + (size_t)fb * KG * 16 + (lane & 7) * 2;
     }
-    // Group sums: waves 2 / 3 fetch rows 0-63 / 64-127 (lane = row).
-    {
-        const int row = (wave & 1) * 64 + lane;
-        const int rr = row < it.nr ? row : 0;
-        const float* gp;
-        if (NMAT == 2) {
-            const uint32_t tok = lds_read32(it.tab + 16 + rr * 4);
-            gp = a.gsum + (size_t)tok * KG + kg;
-        } else {
-            gp = a.gsum + (size_t)(it.r0 + rr) * KG + kg;
-        }
-        dma4(gp, slot + ((wave >> 1) == 1 ? RG::kGOff + (wave & 1) * 256 : RG::kJunk));
-    }
-    // Rows wave*16 .. wave*16+15: 4 DMAs of 4 rows x 256 B, rows interleaved
-    // at 16 B (lane -> row lane % 4, chunk lane / 4).
+    // The table's row map holds the token (gate/up) or the grouped row (down)
+    // of each tile row; rows past the tile's end repeat row 0.
+    p.g = lds_read32(it.tab + 16 + ((wave & 1) * 64 + lane) * 4) * (uint32_t)KG;
+    // DMA j of this wave fills rows 16 wave + 4 j + lane / 16; lane's LDS slot
+    // lane % 16 holds chunk (lane % 16) ^ (row & 15) of its row.
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int sub = lane & 3;
-        const int chunk = lane >> 2;
-        const uint4 t4 = lds_bcast16(it.tab + 16 + (wave * 16 + j * 4) * 4);
-        const uint32_t tk = sub == 0 ? t4.x : sub == 1 ? t4.y : sub == 2 ? t4.z : t4.w;
-        dma16(a.src + (size_t)tk * K + kg * 128 + chunk * 8,
-              slot + RG::kXOff + (wave * 4 + j) * RG::kQuad);
+        const int row = wave * 16 + j * 4 + (lane >> 4);
+        p.x[j] = lds_read32(it.tab + 16 + row * 4) * (uint32_t)K +
+                 (uint32_t)((lane & 15) ^ (row & 15)) * 8;
     }
+    return p;
 }
 
-// One 128-K group of the wave's 64 x 64 tile. Row blocks at or past nr
-// (padding of an expert's last tile) are skipped; nr is wave-uniform.
-__device__ __forceinline__ void big_compute(const char* slot, int wave, int lane, int nr,
+// Exactly kDma DMAs per wave: group kg of the item into `slot`.
+__device__ __forceinline__ void big_issue(const BigArgs& a, const IssuePtrs& p, int kg, char* slot,
+                                          int wave, int lane) {
+    using RG = BigRing;
+#ifdef GLMMOE_BIG_NODMA
+    return;
+#endif
+#ifndef GLMMOE_BIG_NOWDMA
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        dma16(p.w[j] + (size_t)kg * 64 + lane, slot + (wave * 2 + j) * 1024);
+#endif
+    dma4(p.s + (size_t)kg * 16, slot + (wave < 2 ? RG::kSOff + (wave & 1) * 256 : RG::kJunk));
+    dma4(a.gsum + (p.g + (uint32_t)kg), slot + ((wave >> 1) == 1 ? RG::kGOff + (wave & 1) * 256 : RG::kJunk));
+#ifndef GLMMOE_BIG_NOXDMA
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+        dma16(a.src + (p.x[j] + (uint32_t)kg * 128), slot + RG::kXOff + (wave * 4 + j) * RG::kQuad);
+#endif
+}
+
+// bf16 pair {hi(X), bf16(X - hi(X))} in the low dword of an MFMA A fragment
+// (K slots 0, 1) for lanes 0-31; zero for lanes 32-63 (K slots 8-15).
+__device__ __forceinline__ bf16x8 corr_a(float X, int h) {
+    const float hi = __uint_as_float(__float_as_uint(X) & 0xffff0000u);
+    const uint32_t v = pack_bf16x2(hi, X - hi);
+    return __builtin_bit_cast(bf16x8, u32x4{h ? 0u : v, 0u, 0u, 0u});
+}
+
+// One 128-K group of the wave's 64 x 64 tile.
+__device__ __forceinline__ void big_compute(const char* slot, int wave, int lane,
                                             const DqConst& dqc, f32x16 (&acc)[2][2]) {
     using RG = BigRing;
     const int wn = wave >> 1, wm = wave & 1;
     const int col = lane & 31, h = lane >> 5;
-    const int ntb = min(2, max(0, (nr - wm * 64 + 31) >> 5));   // live 32-row blocks
-    if (ntb == 0) return;
-    // A fragments: block jb = tiles 4 wn + 2 jb (+1 for rows 16-31); lane row
-    // col holds K chunks 8h .. 8h+7 = packed-tile lane slots q = 2h, 2h+1.
-    u32x4 aw[2][2];
+    // B (weights): block jb = tiles 4 wn + 2 jb (+1 for features 16-31); the
+    // lane's feature row col & 15 holds K chunks 8h .. 8h + 7 = packed-tile
+    // lane slots q = 2h, 2h + 1, i.e. dword s of the pair is MFMA step s.
+    u32x4 bw[2][2];
+    uint32_t sc[2];
+    float xs[2];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
         const int t = wn * 4 + jb * 2 + (col >> 4);
         const uint32_t wa = lds_addr(slot + t * 1024) + (uint32_t)(((col & 15) + 32 * h) * 16);
         asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:256"
-                     : "=&v"(aw[jb][0]), "=&v"(aw[jb][1]) : "v"(wa));
+                     : "=&v"(bw[jb][0]), "=&v"(bw[jb][1]) : "v"(wa));
+        const uint32_t sa = lds_addr(slot + RG::kSOff + t * 32) + (uint32_t)((col & 15) * 2);
+        asm volatile("ds_read_u16 %0, %1" : "=&v"(sc[jb]) : "v"(sa));
     }
-    // Scales of this lane's 16 output rows per block: rows 8j + 4h + [0, 4).
-    u32x2 sv[2][4];
-#pragma unroll
-    for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = 8 * j + 4 * h;
-            const int t = wn * 4 + jb * 2 + (row >> 4);
-            const uint32_t sa = lds_addr(slot + RG::kSOff + t * 32) + (uint32_t)((row & 15) * 2);
-            asm volatile("ds_read_b64 %0, %1" : "=&v"(sv[jb][j]) : "v"(sa));
-        }
-    // Group sums of this lane's two columns.
-    float xs[2];
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) {
         const uint32_t ga = lds_addr(slot + RG::kGOff) + (uint32_t)((wm * 64 + tb * 32 + col) * 4);
         asm volatile("ds_read_b32 %0, %1" : "=&v"(xs[tb]) : "v"(ga));
     }
+    // A (activations): row R = wm*64 + tb*32 + col, chunk 8h + s for step s,
+    // stored at slot (8h + s) ^ (R & 15) = (8h ^ (col & 15)) ^ s. Rows are
+    // 256 B and the area is 256-B aligned, so step s's address is step 0's
+    // with bits 4-6 flipped by s; token block 1 is 32 rows (8 KiB) further.
+    const uint32_t xa0 = lds_addr(slot + RG::kXOff) + (uint32_t)RG::row_off(wm * 64 + col) +
+                         ((uint32_t)((8 * h) ^ (col & 15)) << 4);
+    u32x4 av[2][2];
+    asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:8192"
+                 : "=&v"(av[0][0]), "=&v"(av[0][1]) : "v"(xa0));
     asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(aw[0][0]), "+v"(aw[0][1]), "+v"(aw[1][0]), "+v"(aw[1][1]),
-                   "+v"(sv[0][0]), "+v"(sv[0][1]), "+v"(sv[0][2]), "+v"(sv[0][3]),
-                   "+v"(sv[1][0]), "+v"(sv[1][1]), "+v"(sv[1][2]), "+v"(sv[1][3]),
-                   "+v"(xs[0]), "+v"(xs[1]));
-    const uint32_t xb = lds_addr(slot + RG::kXOff);
-    uint32_t xa[2];
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
-        xa[tb] = xb + (uint32_t)(RG::row_off(wm * 64 + tb * 32 + col) + 8 * h * 64);
+                 : "+v"(bw[0][0]), "+v"(bw[0][1]), "+v"(bw[1][0]), "+v"(bw[1][1]), "+v"(sc[0]),
+                   "+v"(sc[1]), "+v"(xs[0]), "+v"(xs[1]), "+v"(av[0][0]), "+v"(av[0][1]));
 
-    // Activation fragments double-buffered across the 8 K-steps: the reads of
-    // step s+1 are in flight during step s's MFMAs.
-    f32x16 p[2][2];
-    u32x4 xv[2][2];
+    // Seeds: -136 X per row, shared by both weight blocks.
+    const bf16x8 bneg = __builtin_bit_cast(bf16x8, u32x4{0xC308C308u, 0u, 0u, 0u});
+    f32x16 seed[2];
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb)
-        asm volatile("ds_read_b128 %0, %1" : "=&v"(xv[0][tb]) : "v"(xa[tb]));
+    for (int tb = 0; tb < 2; ++tb) seed[tb] = mfma32x32x16(corr_a(xs[tb], h), bneg, f32x16{});
+
+    f32x16 p[2][2];
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
         const int cb = s & 1, nb = cb ^ 1;
-        asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(xv[cb][0]), "+v"(xv[cb][1]));
+        if (s > 0) {
+            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(av[cb][0]), "+v"(av[cb][1]));
+        }
         if (s < 7) {
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-                asm volatile("ds_read_b128 %0, %1 offset:%c2"
-                             : "=&v"(xv[nb][tb]) : "v"(xa[tb]), "i"((s + 1) * 64));
+            const uint32_t xs_addr = xa0 ^ (uint32_t)((s + 1) << 4);
+            asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:8192"
+                         : "=&v"(av[nb][0]), "=&v"(av[nb][1]) : "v"(xs_addr));
         }
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb) {
-            const bf16x8 av = dq_w4(aw[jb][s >> 2][s & 3], dqc);
+            const bf16x8 bv = dq_w4(bw[jb][s >> 2][s & 3], dqc);
 #pragma unroll
-            for (int tb = 0; tb < 2; ++tb) {
-                if (tb < ntb) {
-                    if (s == 0) p[jb][tb] = mfma32x32x16(av, as_bf16x8(xv[cb][tb]), f32x16{});
-                    else p[jb][tb] = mfma32x32x16(av, as_bf16x8(xv[cb][tb]), p[jb][tb]);
-                }
-            }
+            for (int tb = 0; tb < 2; ++tb)
+                p[jb][tb] = mfma32x32x16(as_bf16x8(av[cb][tb]), bv, s == 0 ? seed[tb] : p[jb][tb]);
         }
     }
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
-        float sc[16];
+        const float scale = bf16_to_f32(sc[jb]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            sc[4 * j + 0] = bf16_to_f32(sv[jb][j].x & 0xffffu);
-            sc[4 * j + 1] = bf16_to_f32(sv[jb][j].x >> 16);
-            sc[4 * j + 2] = bf16_to_f32(sv[jb][j].y & 0xffffu);
-            sc[4 * j + 3] = bf16_to_f32(sv[jb][j].y >> 16);
-        }
+        for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            if (tb < ntb) {
-                const float off = -136.0f * xs[tb];
+            for (int i = 0; i < 16; ++i) acc[jb][tb][i] = __builtin_fmaf(scale, p[jb][tb][i], acc[jb][tb][i]);
+    }
+}
+
+// Row (0..127) of accumulator element i of token block tb for wave row half wm.
+__device__ __forceinline__ int acc_row(int wm, int tb, int i, int h) {
+    return wm * 64 + tb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+}
+
+// One step of the recursive-halving lane reduction over the first 2N values.
+template <int N>
+__device__ __forceinline__ void halve(float (&v)[32], int col) {
+    const bool upper = (col & N) != 0;
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    acc[jb][tb][i] = __builtin_fmaf(sc[i], p[jb][tb][i] + off, acc[jb][tb][i]);
-            }
-        }
+    for (int j = 0; j < N; ++j) {
+        const float send = upper ? v[j] : v[j + N];
+        const float keep = upper ? v[j + N] : v[j];
+        v[j] = keep + __shfl_xor(send, N);
     }
 }
 
@@ -254,68 +283,64 @@ template <int NMAT>
 __device__ __forceinline__ void big_epilogue(const BigArgs& a, const BigItem& cur, char* lds,
                                              int wave, int lane, f32x16 (&acc)[2][2]) {
     const int wn = wave >> 1, wm = wave & 1;
-    const int col = lane & 31, h = lane >> 5;
+    // Laundered lane index: keeps the compiler from hoisting the per-row
+    // addresses below out of the streaming loop (they would stay live across
+    // it and spill).
+    int ln = lane;
+    asm volatile("" : "+v"(ln));
+    const int col = ln & 31, h = ln >> 5;
     if constexpr (NMAT == 2) {
-        // h = silu(g) * u (bf16) for 32 features x this lane's 2 columns; and
-        // the sum of the rounded h over the workgroup's 128 features (one
-        // group of I), reduced across the 4 feature waves in fixed order.
-        float part[2];
+        // h = silu(g) * u (bf16) for this lane's feature and 32 rows; then the
+        // sum of the rounded h over the workgroup's 128 features (one group of
+        // I) per row: a fixed butterfly over the 32 lanes of the wave that
+        // share rows, then the 4 feature waves in order.
+        uint16_t* hbase = a.h + (size_t)cur.r0 * a.I + cur.g * 128 + wn * 32;
+        float v[32];
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            const int lr = wm * 64 + tb * 32 + col;
-            const bool valid = lr < cur.nr;
-            const size_t row = (size_t)cur.r0 + lr;
-            float ps = 0.0f;
+        for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                uint32_t hb[4];
+            for (int i = 0; i < 16; i += 2) {
+                const uint32_t hb = pack_bf16x2(silu_fast(acc[0][tb][i]) * acc[1][tb][i],
+                                                silu_fast(acc[0][tb][i + 1]) * acc[1][tb][i + 1]);
 #pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    hb[e] = f32_to_bf16(silu_fast(acc[0][tb][4 * j + e]) * acc[1][tb][4 * j + e]);
-                    ps += bf16_to_f32(hb[e]);
+                for (int e = 0; e < 2; ++e) {
+                    const int lr = acc_row(wm, tb, i + e, h);
+                    const uint32_t he = e ? hb >> 16 : hb & 0xffffu;
+                    if (lr < cur.nr) hbase[lr * a.I + col] = (uint16_t)he;
+                    v[tb * 16 + i + e] = bf16_to_f32(he);
                 }
-                const int f = cur.g * 128 + wn * 32 + 8 * j + 4 * h;
-                if (valid)
-                    *reinterpret_cast<uint2*>(a.h + row * a.I + f) =
-                        uint2{hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
             }
-            part[tb] = ps + __shfl_xor(ps, 32);   // both row halves of the 32 features
-        }
+        // Recursive halving: after the step with lane mask m the lane keeps the
+        // half of its values whose index bit matches (col & m); at the end lane
+        // col holds the 32-lane sum of value index col.
+        halve<16>(v, col);
+        halve<8>(v, col);
+        halve<4>(v, col);
+        halve<2>(v, col);
+        halve<1>(v, col);
         const uint32_t red = lds_addr(lds + BigRing::kRed);
-        if (h == 0) {
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-                lds_write32(red + (uint32_t)((wn * kBigRows + wm * 64 + tb * 32 + col) * 4), part[tb]);
-        }
+        const int myrow = acc_row(wm, col >> 4, col & 15, h);
+        lds_write32(red + (uint32_t)((wn * kBigRows + myrow) * 4), v[0]);
         __builtin_amdgcn_s_barrier();
-        if (wn == 0 && h == 0) {
+        if (wn == 0) {
+            float s = 0.0f;
 #pragma unroll
-            for (int tb = 0; tb < 2; ++tb) {
-                const int lr = wm * 64 + tb * 32 + col;
-                float s = 0.0f;
-#pragma unroll
-                for (int w = 0; w < 4; ++w)
-                    s += __uint_as_float(lds_read32(red + (uint32_t)((w * kBigRows + lr) * 4)));
-                if (lr < cur.nr) a.hsum[((size_t)cur.r0 + lr) * (a.I / 128) + cur.g] = s;
-            }
+            for (int w = 0; w < 4; ++w)
+                s += __uint_as_float(lds_read32(red + (uint32_t)((w * kBigRows + myrow) * 4)));
+            if (myrow < cur.nr) a.hsum[((size_t)cur.r0 + myrow) * (a.I / 128) + cur.g] = s;
         }
         __builtin_amdgcn_s_barrier();   // partials consumed before the next item reuses them
     } else {
 #pragma unroll
-        for (int tb = 0; tb < 2; ++tb) {
-            const int lr = wm * 64 + tb * 32 + col;
-            if (lr < cur.nr) {
-                const size_t row = (size_t)cur.r0 + lr;
+        for (int jb = 0; jb < 2; ++jb) {
+            float* dbase = a.dpart + (size_t)cur.r0 * a.H + cur.g * 256 + wn * 64 + jb * 32;
 #pragma unroll
-                for (int jb = 0; jb < 2; ++jb)
+            for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
-                    for (int j = 0; j < 4; ++j) {
-                        const int f = cur.g * 256 + wn * 64 + jb * 32 + 8 * j + 4 * h;
-                        *reinterpret_cast<float4*>(a.dpart + row * a.H + f) =
-                            make_float4(acc[jb][tb][4 * j], acc[jb][tb][4 * j + 1],
-                                        acc[jb][tb][4 * j + 2], acc[jb][tb][4 * j + 3]);
-                    }
-            }
+                for (int i = 0; i < 16; ++i) {
+                    const int lr = acc_row(wm, tb, i, h);
+                    if (lr < cur.nr) dbase[lr * a.H + col] = acc[jb][tb][i];
+                }
         }
     }
 }
@@ -328,6 +353,7 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
     int* table = reinterpret_cast<int*>(lds + RG::kTab);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave & 1;
     const int K = NMAT == 2 ? a.H : a.I;
     const int KG = K / 128;
     const int nfg = (NMAT == 2 ? a.I : a.H) / BigShape<NMAT>::kFeat;
@@ -341,18 +367,21 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
         const long nsteps = (long)cnt * KG;
 
         int iss_k = 0, iss_g = 0;
-        BigItem iss = big_item(lds + RG::kTab, 0);
+        IssuePtrs iss = issue_ptrs<NMAT>(a, big_item(lds + RG::kTab, 0), K, KG, wave, lane);
         for (int j = 0; j < kBigD - 1; ++j) {
             if (j < nsteps) {
-                big_issue<NMAT>(a, iss, iss_g, K, KG, lds + (j % kBigD) * RG::kSlot, wave, lane);
+                big_issue(a, iss, iss_g, lds + (j % kBigD) * RG::kSlot, wave, lane);
                 if (++iss_g == KG) {
                     iss_g = 0;
-                    if (++iss_k < cnt) iss = big_item(lds + RG::kTab, iss_k);
+                    if (++iss_k < cnt)
+                        iss = issue_ptrs<NMAT>(a, big_item(lds + RG::kTab, iss_k), K, KG, wave, lane);
                 }
             }
         }
         int cur_k = 0, cur_g = 0;
         BigItem cur = big_item(lds + RG::kTab, 0);
+        // Whether this wave's 64 rows hold any live row (wave-uniform per item).
+        bool live = cur.nr > wm * 64;
         f32x16 acc[2][2];
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb)
@@ -364,15 +393,19 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
             else wait_vmcnt<0>();
             __builtin_amdgcn_s_barrier();
             if (step + kBigD - 1 < nsteps) {
-                big_issue<NMAT>(a, iss, iss_g, K, KG, lds + ((step + kBigD - 1) % kBigD) * RG::kSlot,
-                                wave, lane);
+                big_issue(a, iss, iss_g, lds + ((step + kBigD - 1) % kBigD) * RG::kSlot, wave, lane);
                 if (++iss_g == KG) {
                     iss_g = 0;
-                    if (++iss_k < cnt) iss = big_item(lds + RG::kTab, iss_k);
+                    if (++iss_k < cnt)
+                        iss = issue_ptrs<NMAT>(a, big_item(lds + RG::kTab, iss_k), K, KG, wave, lane);
                 }
             }
+            char* slot = lds + (step % kBigD) * RG::kSlot;
 #ifndef GLMMOE_BIG_NOCOMPUTE
-            big_compute(lds + (step % kBigD) * RG::kSlot, wave, lane, cur.nr, dqc, acc);
+            // A wave whose 64 rows are all past the tile's end skips the group;
+            // a half-live wave computes both 32-row blocks (one branch-free body
+            // keeps the accumulators in fixed registers).
+            if (live) big_compute(slot, wave, lane, dqc, acc);
 #endif
 
             if (++cur_g == KG) {
@@ -382,7 +415,10 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
 #pragma unroll
                     for (int tb = 0; tb < 2; ++tb) acc[jb][tb] = f32x16{};
                 cur_g = 0;
-                if (++cur_k < cnt) cur = big_item(lds + RG::kTab, cur_k);
+                if (++cur_k < cnt) {
+                    cur = big_item(lds + RG::kTab, cur_k);
+                    live = cur.nr > wm * 64;
+                }
             }
         }
         __syncthreads();
