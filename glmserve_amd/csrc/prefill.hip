@@ -187,71 +187,106 @@ __device__ __forceinline__ bf16x8 corr_a(float X, int h) {
     return __builtin_bit_cast(bf16x8, u32x4{h ? 0u : v, 0u, 0u, 0u});
 }
 
-// One 128-K group of the wave's 64 x 64 tile.
-__device__ __forceinline__ void big_compute(const char* slot, int wave, int lane,
-                                            const DqConst& dqc, f32x16 (&acc)[2][2]) {
+// Operands a wave reads from one ring slot before its first MFMA: its weight
+// fragments, their scales, the group sums of its rows and step 0's
+// activation fragments. Issued one group ahead (see the main loop).
+struct BigOps {
+    u32x4 bw[2][2];
+    uint32_t sc[2];
+    float xs[2];
+    u32x4 av0[2];
+};
+
+// A (activations): row R = wm*64 + tb*32 + col, chunk 8h + s for step s,
+// stored at slot (8h + s) ^ (R & 15) = (8h ^ (col & 15)) ^ s. Rows are 256 B
+// and the area is 256-B aligned, so step s's address is step 0's with bits
+// 4-6 flipped by s; token block 1 is 32 rows (8 KiB) further.
+__device__ __forceinline__ uint32_t big_xa0(const char* slot, int wave, int lane) {
+    const int wm = wave & 1, col = lane & 31, h = lane >> 5;
+    return lds_addr(slot + BigRing::kXOff) + (uint32_t)BigRing::row_off(wm * 64 + col) +
+           ((uint32_t)((8 * h) ^ (col & 15)) << 4);
+}
+
+// Issues the reads of BigOps (no wait).
+__device__ __forceinline__ void big_load_ops(const char* slot, int wave, int lane, BigOps& o) {
     using RG = BigRing;
     const int wn = wave >> 1, wm = wave & 1;
     const int col = lane & 31, h = lane >> 5;
     // B (weights): block jb = tiles 4 wn + 2 jb (+1 for features 16-31); the
     // lane's feature row col & 15 holds K chunks 8h .. 8h + 7 = packed-tile
     // lane slots q = 2h, 2h + 1, i.e. dword s of the pair is MFMA step s.
-    u32x4 bw[2][2];
-    uint32_t sc[2];
-    float xs[2];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
         const int t = wn * 4 + jb * 2 + (col >> 4);
         const uint32_t wa = lds_addr(slot + t * 1024) + (uint32_t)(((col & 15) + 32 * h) * 16);
         asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:256"
-                     : "=&v"(bw[jb][0]), "=&v"(bw[jb][1]) : "v"(wa));
+                     : "=&v"(o.bw[jb][0]), "=&v"(o.bw[jb][1]) : "v"(wa));
         const uint32_t sa = lds_addr(slot + RG::kSOff + t * 32) + (uint32_t)((col & 15) * 2);
-        asm volatile("ds_read_u16 %0, %1" : "=&v"(sc[jb]) : "v"(sa));
+        asm volatile("ds_read_u16 %0, %1" : "=&v"(o.sc[jb]) : "v"(sa));
     }
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-        const uint32_t ga = lds_addr(slot + RG::kGOff) + (uint32_t)((wm * 64 + tb * 32 + col) * 4);
-        asm volatile("ds_read_b32 %0, %1" : "=&v"(xs[tb]) : "v"(ga));
-    }
-    // A (activations): row R = wm*64 + tb*32 + col, chunk 8h + s for step s,
-    // stored at slot (8h + s) ^ (R & 15) = (8h ^ (col & 15)) ^ s. Rows are
-    // 256 B and the area is 256-B aligned, so step s's address is step 0's
-    // with bits 4-6 flipped by s; token block 1 is 32 rows (8 KiB) further.
-    const uint32_t xa0 = lds_addr(slot + RG::kXOff) + (uint32_t)RG::row_off(wm * 64 + col) +
-                         ((uint32_t)((8 * h) ^ (col & 15)) << 4);
-    u32x4 av[2][2];
+    const uint32_t ga = lds_addr(slot + RG::kGOff) + (uint32_t)((wm * 64 + col) * 4);
+    asm volatile("ds_read_b32 %0, %2\n ds_read_b32 %1, %2 offset:128"
+                 : "=&v"(o.xs[0]), "=&v"(o.xs[1]) : "v"(ga));
     asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:8192"
-                 : "=&v"(av[0][0]), "=&v"(av[0][1]) : "v"(xa0));
-    asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(bw[0][0]), "+v"(bw[0][1]), "+v"(bw[1][0]), "+v"(bw[1][1]), "+v"(sc[0]),
-                   "+v"(sc[1]), "+v"(xs[0]), "+v"(xs[1]), "+v"(av[0][0]), "+v"(av[0][1]));
+                 : "=&v"(o.av0[0]), "=&v"(o.av0[1]) : "v"(big_xa0(slot, wave, lane)));
+}
 
+// One 128-K group of the wave's 64 x 64 tile: p = sum_k (128 + c) x - 136 X
+// per 32 x 32 block (the caller applies the group's scales).
+__device__ __forceinline__ void big_compute(const char* slot, int wave, int lane,
+                                            const DqConst& dqc, BigOps& o, f32x16 (&p)[2][2]) {
+    const int h = lane >> 5;
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(o.bw[0][0]), "+v"(o.bw[0][1]), "+v"(o.bw[1][0]), "+v"(o.bw[1][1]),
+                   "+v"(o.sc[0]), "+v"(o.sc[1]), "+v"(o.xs[0]), "+v"(o.xs[1]), "+v"(o.av0[0]),
+                   "+v"(o.av0[1]));
     // Seeds: -136 X per row, shared by both weight blocks.
     const bf16x8 bneg = __builtin_bit_cast(bf16x8, u32x4{0xC308C308u, 0u, 0u, 0u});
     f32x16 seed[2];
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) seed[tb] = mfma32x32x16(corr_a(xs[tb], h), bneg, f32x16{});
+    for (int tb = 0; tb < 2; ++tb) seed[tb] = mfma32x32x16(corr_a(o.xs[tb], h), bneg, f32x16{});
 
-    f32x16 p[2][2];
+    const uint32_t xa0 = big_xa0(slot, wave, lane);
+    u32x4 av[2][2];
+    av[0][0] = o.av0[0];
+    av[0][1] = o.av0[1];
+    // Software pipeline per K-step s: the activation reads of s + 1 and the
+    // int4 decode of s + 1 run under the MFMAs of s. sched_barrier keeps the
+    // compiler from sinking the reads next to their wait (which would expose
+    // the LDS latency every step).
+    bf16x8 bv[2][2];
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) bv[0][jb] = dq_w4(o.bw[jb][0][0], dqc);
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
         const int cb = s & 1, nb = cb ^ 1;
-        if (s > 0) {
-            asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(av[cb][0]), "+v"(av[cb][1]));
-        }
+        if (s > 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(av[cb][0]), "+v"(av[cb][1]));
+#ifdef GLMMOE_BIG_NOAREAD
+        if (false) {
+#else
         if (s < 7) {
+#endif
             const uint32_t xs_addr = xa0 ^ (uint32_t)((s + 1) << 4);
             asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:8192"
                          : "=&v"(av[nb][0]), "=&v"(av[nb][1]) : "v"(xs_addr));
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb) {
-            const bf16x8 bv = dq_w4(bw[jb][s >> 2][s & 3], dqc);
+        for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb)
-                p[jb][tb] = mfma32x32x16(as_bf16x8(av[cb][tb]), bv, s == 0 ? seed[tb] : p[jb][tb]);
+                p[jb][tb] = mfma32x32x16(as_bf16x8(av[cb][tb]), bv[cb][jb], s == 0 ? seed[tb] : p[jb][tb]);
+        if (s < 7) {
+#pragma unroll
+            for (int jb = 0; jb < 2; ++jb) bv[nb][jb] = dq_w4(o.bw[jb][(s + 1) >> 2][(s + 1) & 3], dqc);
         }
+        __builtin_amdgcn_sched_barrier(0);
     }
+}
+
+// acc += scale_col * p (one fma per element).
+__device__ __forceinline__ void big_rescale(const uint32_t (&sc)[2], const f32x16 (&p)[2][2],
+                                            f32x16 (&acc)[2][2]) {
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
         const float scale = bf16_to_f32(sc[jb]);
@@ -366,18 +401,30 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
         __syncthreads();
         const long nsteps = (long)cnt * KG;
 
+        // Ring of kBigD slots; group g lives in slot g % kBigD. Per group:
+        // compute g; wait for g + 1's DMA and barrier (every wave is then done
+        // with slot g, and g + 1 is visible); refill slot g with group
+        // g + kBigD; issue the reads of g + 1's operands; apply g's scales
+        // while those reads are in flight.
         int iss_k = 0, iss_g = 0;
         IssuePtrs iss = issue_ptrs<NMAT>(a, big_item(lds + RG::kTab, 0), K, KG, wave, lane);
-        for (int j = 0; j < kBigD - 1; ++j) {
-            if (j < nsteps) {
-                big_issue(a, iss, iss_g, lds + (j % kBigD) * RG::kSlot, wave, lane);
-                if (++iss_g == KG) {
-                    iss_g = 0;
-                    if (++iss_k < cnt)
-                        iss = issue_ptrs<NMAT>(a, big_item(lds + RG::kTab, iss_k), K, KG, wave, lane);
-                }
+        auto issue_next = [&](long g) {
+            big_issue(a, iss, iss_g, lds + (g % kBigD) * RG::kSlot, wave, lane);
+            if (++iss_g == KG) {
+                iss_g = 0;
+                if (++iss_k < cnt)
+                    iss = issue_ptrs<NMAT>(a, big_item(lds + RG::kTab, iss_k), K, KG, wave, lane);
             }
-        }
+        };
+        for (int j = 0; j < kBigD; ++j)
+            if (j < nsteps) issue_next(j);
+        if (nsteps >= 3) wait_vmcnt<RG::kDma * 2>();
+        else if (nsteps == 2) wait_vmcnt<RG::kDma>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        BigOps ops;
+        big_load_ops(lds, wave, lane, ops);
+
         int cur_k = 0, cur_g = 0;
         BigItem cur = big_item(lds + RG::kTab, 0);
         // Whether this wave's 64 rows hold any live row (wave-uniform per item).
@@ -389,25 +436,24 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
             for (int tb = 0; tb < 2; ++tb) acc[jb][tb] = f32x16{};
 
         for (long step = 0; step < nsteps; ++step) {
-            if (step + kBigD - 2 < nsteps) wait_vmcnt<RG::kDma * (kBigD - 2)>();
-            else wait_vmcnt<0>();
-            __builtin_amdgcn_s_barrier();
-            if (step + kBigD - 1 < nsteps) {
-                big_issue(a, iss, iss_g, lds + ((step + kBigD - 1) % kBigD) * RG::kSlot, wave, lane);
-                if (++iss_g == KG) {
-                    iss_g = 0;
-                    if (++iss_k < cnt)
-                        iss = issue_ptrs<NMAT>(a, big_item(lds + RG::kTab, iss_k), K, KG, wave, lane);
-                }
-            }
-            char* slot = lds + (step % kBigD) * RG::kSlot;
+            f32x16 p[2][2];
 #ifndef GLMMOE_BIG_NOCOMPUTE
             // A wave whose 64 rows are all past the tile's end skips the group;
             // a half-live wave computes both 32-row blocks (one branch-free body
             // keeps the accumulators in fixed registers).
-            if (live) big_compute(slot, wave, lane, dqc, acc);
+            if (live) big_compute(lds + (step % kBigD) * RG::kSlot, wave, lane, dqc, ops, p);
 #endif
-
+            if (step + 2 < nsteps) wait_vmcnt<RG::kDma>();
+            else wait_vmcnt<0>();
+#ifndef GLMMOE_BIG_NOBARRIER
+            __builtin_amdgcn_s_barrier();
+#endif
+            if (step + kBigD < nsteps) issue_next(step + kBigD);
+            const uint32_t sc[2] = {ops.sc[0], ops.sc[1]};
+            if (step + 1 < nsteps) big_load_ops(lds + ((step + 1) % kBigD) * RG::kSlot, wave, lane, ops);
+#ifndef GLMMOE_BIG_NOCOMPUTE
+            if (live) big_rescale(sc, p, acc);
+#endif
             if (++cur_g == KG) {
                 big_epilogue<NMAT>(a, cur, lds, wave, lane, acc);
 #pragma unroll
@@ -421,6 +467,7 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
                 }
             }
         }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
     }
 }
