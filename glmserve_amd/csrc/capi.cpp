@@ -167,11 +167,12 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     mark(GLMMOE_STAGE_GATE_UP, s);
     rc = big ? launch_gate_up_big(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h,
                                   v.hsum, H, I, E, s)
-             : launch_gate_up(P, x, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, H, I, E, s);
+             : launch_gate_up(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.hsum,
+                              H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_DOWN, s);
     rc = big ? launch_down_big(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
-             : launch_down(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
+             : launch_down(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_COMBINE, s);
     rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s);
@@ -292,10 +293,9 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     const int H = L->hidden, E = L->n_experts, k = L->topk;
     begin_call();
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
-    // Activation group sums only feed the large-group kernels.
-    const bool big = tile_rows_for(n, k, has_shared(L) ? 1 : 0) == kBigRows;
-    rc = launch_router_logits(x, L->router_w, n, H, E, v.logits, big ? v.xsum : nullptr, v.rpart,
-                              s);
+    // The router pass also writes the activation group sums the expert
+    // kernels use to remove the int4 decode offset.
+    rc = launch_router_logits(x, L->router_w, n, H, E, v.logits, v.xsum, v.rpart, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_ROUTER_TOPK, s);
     rc = launch_router_topk(v.logits, L->e_bias, n, E, k, L->norm_topk, L->routed_scale,
@@ -316,10 +316,8 @@ int glmmoe_expert_ffn_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int 
     hipStream_t s = S(stream);
     begin_call();
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
-    if (tile_rows_for(n, L->topk, has_shared(L) ? 1 : 0) == kBigRows) {
-        rc = launch_xsum(x, n, L->hidden, v.xsum, s);
-        if (rc) return rc;
-    }
+    rc = launch_xsum(x, n, L->hidden, v.xsum, s);
+    if (rc) return rc;
     return run_experts(L, x, n, topk_ids, topk_w, v.xsum, out, v, s);
 }
 

@@ -145,6 +145,14 @@ __device__ __forceinline__ uint4 lds_bcast16(uint32_t addr) {
     asm volatile("ds_read_b128 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
     return v;
 }
+__device__ __forceinline__ uint32_t lds_read_u32(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_b32 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
+    return v;
+}
+__device__ __forceinline__ void lds_write_f32(uint32_t addr, float v) {
+    asm volatile("ds_write_b32 %0, %1\n s_waitcnt lgkmcnt(0)" : : "v"(addr), "v"(v) : "memory");
+}
 __device__ __forceinline__ int sgpr(uint32_t v) { return __builtin_amdgcn_readfirstlane((int)v); }
 
 }  // namespace glmmoe

@@ -44,11 +44,12 @@ int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* s
                     int with_shared, int mode, hipStream_t s);
 int launch_pack_w4(const uint8_t* q, const void* sc, int sc_bf16, int n_mats, int rows, int K,
                    uint8_t* pq, uint16_t* ps, hipStream_t s);
-int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const int* tiles, const int* ntiles,
-                   int max_tiles, const int* rows_tok, uint16_t* h, int H, int I, int E,
-                   hipStream_t s);
-int launch_down(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
-                int max_tiles, float* dpart, int H, int I, int E, hipStream_t s);
+int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
+                   const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
+                   float* hsum, int H, int I, int E, hipStream_t s);
+int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
+                const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
+                hipStream_t s);
 int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, const float* xsum,
                        const int* tiles, const int* ntiles, int max_tiles, const int* rows_tok,
                        uint16_t* h, float* hsum, int H, int I, int E, hipStream_t s);

@@ -34,7 +34,7 @@ constexpr int kRouterRow = kRouterKC / 2 + 4;   // LDS dwords per weight row (+1
 
 __global__ __launch_bounds__(64) void router_partials_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, int n, int H, int E,
-    float* __restrict__ part) {
+    float* __restrict__ part, float* __restrict__ xsum) {
     __shared__ __align__(16) uint32_t wl[64 * kRouterRow];
     __shared__ __align__(16) uint4 xs[kRouterTG][kRouterKC / 8];
     const int nchunks = (H + kRouterKC - 1) / kRouterKC;
@@ -71,6 +71,20 @@ __global__ __launch_bounds__(64) void router_partials_kernel(
 #pragma unroll
     for (int j = 0; j < 2; ++j) xs[(lane >> 4) + 4 * j][oct] = xv[j];
     __syncthreads();
+
+    // Group sums of the staged activations (xsum [n, H/128]), written by the
+    // first expert block: ascending K, low half then high half of each dword
+    // (the order of xsum_kernel).
+    if (xsum && eb == 0 && lane < nt && klen == kRouterKC) {
+        float xsv = 0.0f;
+        for (int j = 0; j < kRouterKC / 8; ++j) {
+            const uint4 v = xs[lane][j];
+            const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) { xsv += bf16_to_f32(d[q] & 0xffffu); xsv += bf16_to_f32(d[q] >> 16); }
+        }
+        xsum[(size_t)(t0 + lane) * nchunks + c] = xsv;
+    }
 
     float s[kRouterTG];
 #pragma unroll
@@ -366,14 +380,15 @@ int launch_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, in
         if (!scratch) return -3;
         const long blocks = (long)nchunks * ((E + 63) / 64) * ((n + kRouterTG - 1) / kRouterTG);
         hipLaunchKernelGGL(router_partials_kernel, dim3((unsigned)blocks), dim3(64), 0, s, x, wr,
-                           n, H, E, scratch);
+                           n, H, E, scratch, H % kRouterKC == 0 ? xsum : nullptr);
         if (hipGetLastError() != hipSuccess) return -4;
         const long outs = (long)n * E;
         hipLaunchKernelGGL(router_fold_kernel, dim3((unsigned)((outs + 255) / 256)), dim3(256), 0,
                            s, scratch, n, nchunks, E, logits);
     }
     if (hipGetLastError() != hipSuccess) return -4;
-    return xsum ? launch_xsum(x, n, H, xsum, s) : 0;
+    const bool small = !(n >= kTiledMinTokens && H % kRouterKC == 0);
+    return xsum && !small ? launch_xsum(x, n, H, xsum, s) : 0;
 }
 
 int launch_xsum(const uint16_t* x, int n, int H, float* xsum, hipStream_t s) {

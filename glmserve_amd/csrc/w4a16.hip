@@ -81,20 +81,29 @@ int launch_pack_w4(const uint8_t* q, const void* sc, int sc_bf16, int n_mats, in
 // 128-K tile. MFMA step d (0..3) covers K = 32q + 8d + [0,8) for this lane.
 // Output lane layout: rows 4q + j (j = 0..3), column r.
 //
+// Work. A workgroup of 8 waves takes one tile (up to 16 grouped rows of one
+// expert) and 8 consecutive 16-row weight blocks of it, one per wave; the
+// activation rows the tile needs are streamed once for all 8 waves.
+//
 // Streaming. Everything a batch of PF 128-K groups needs -- each wave's
-// weight tiles and scales, and the tile's 16 activation rows (shared by the
-// workgroup's 4 waves, which always work on the same tile) -- is copied
+// weight tiles and scales, and the tile's 16 activation rows -- is copied
 // global -> LDS by the LDS-DMA path (global_load_lds_dwordx4 / _dword), so
 // nothing in flight occupies registers. A ring of D batch slots keeps D-1
-// batches in flight per wave. Every wave issues the same number of DMA
-// instructions per batch (kDma), so "batch b has landed" is the immediate
+// batches in flight. Every wave issues the same number of DMA instructions
+// per batch (kDma), so "batch b has landed" is the immediate
 // s_waitcnt vmcnt(kDma * (D - 2)); one s_barrier per batch then publishes the
-// shared rows and frees the oldest slot. The pipeline runs across work items
-// (a wave's items are w0, w0 + nwaves, ...), so it never drains between
-// them. LDS reads are inline ds_read_b128 with their own lgkmcnt wait, which
-// keeps the compiler from inserting a vmcnt(0) for the pending DMA. Their
-// outputs are early-clobber: a read returns asynchronously, so no output may
-// share a register with an address still needed by a later read.
+// shared rows and frees the oldest slot. The pipeline runs across work items,
+// so it never drains between them. LDS reads are inline ds_read_b128 with
+// their own lgkmcnt wait, which keeps the compiler from inserting a vmcnt(0)
+// for the pending DMA. Their outputs are early-clobber: a read returns
+// asynchronously, so no output may share a register with an address still
+// needed by a later read.
+//
+// Activation rows sit at a stride of PF * 256 B in a slot, so each DMA's 64
+// lanes read whole rows (consecutive lanes, consecutive 16 B: full-speed L2
+// coalescing). Inside a row, 16-byte chunk c is stored at slot c ^ (r & 15),
+// which puts the 16 rows an MFMA B fragment reads at one chunk on 16
+// distinct bank groups.
 //
 // The group sum X_j = sum_k x[k][j] that removes the +136 bias of the int4
 // decode comes from one more MFMA against an all-ones A operand.
@@ -105,68 +114,82 @@ struct ExpArgs {
     const uint4* swq[2];     // shared expert
     const uint16_t* sws[2];
     const uint16_t* src;     // x [n, H] (NMAT = 2) or h [R, I] (NMAT = 1)
+    const float* gsum;       // group sums of src rows: xsum [n, H/128] or hsum [R, I/128]
     const int4* tiles; const int* ntiles; const int* rows_tok;
-    uint16_t* h; float* dpart;
+    uint16_t* h; float* hsum; float* dpart;
     int H, I, E;
 };
 
-template <int NMAT, int PF, int D>
+
+template <int NMAT, int PF, int D, int NW>
 struct Ring {
-    static_assert(PF == 2 || PF == 4, "a batch row span is 512 or 1024 bytes");
-    static constexpr int kW = 1024;                           // one weight tile
-    static constexpr int kWBytes = 4 * NMAT * PF * kW;        // all waves' tiles
-    static constexpr int kSBytes = 4 * 256;                   // scale dwords per wave
-    static constexpr int kSpan = PF * 256;                    // bytes of one row per batch
-    static constexpr int kRPI = 1024 / kSpan;                 // rows per 1 KiB DMA
-    static constexpr int kPair = 1024 + 16 * kRPI;            // padded stride of one DMA
-    static constexpr int kXBytes = (16 / kRPI) * kPair;
-    static constexpr int kSlot = kWBytes + kSBytes + kXBytes;
+    static_assert(PF == 1 || PF == 2 || PF == 4, "a batch row span is 256, 512 or 1024 bytes");
+    static constexpr int kW = 1024;                               // one weight tile
+    static constexpr int kWBytes = NW * NMAT * PF * kW;    // all waves' tiles
+    static constexpr int kSBytes = NW * 256;               // scale dwords per wave
+    static constexpr int kRS = PF * 256;                          // activation row stride
+    static constexpr int kXBytes = kTileRows * kRS;
+    static constexpr int kCPR = 16 * PF;                          // 16-B chunks per row
+    static constexpr int kRPD = 64 / kCPR;                        // rows per activation DMA
+    static constexpr int kNX = kTileRows / kRPD;                  // activation DMAs per batch
+    // Activation DMAs per wave; with fewer DMAs than waves, the waves past
+    // them issue one placeholder DMA into kJunk so every wave issues kDma.
+    static constexpr int kXDma = kNX >= NW ? kNX / NW : 1;
+    static_assert(kNX < NW || kXDma * NW == kNX, "activation DMAs split evenly");
+    static constexpr int kJunkBytes = kNX < NW ? 1024 : 0;
+    // Group sums X[i][r] of the batch's PF groups and 16 rows (256 B), and
+    // the target of the other waves' placeholder group-sum DMA.
+    static constexpr int kGOff = kWBytes + kSBytes + kXBytes + kJunkBytes;
+    static constexpr int kSlot = kGOff + 512;
     static constexpr int kBytes = D * kSlot;
-    static constexpr int kTotal = kBytes + kTable * kTabInts * 4;   // + the item table
-    static_assert(2 * kTotal <= 160 * 1024, "two workgroups per CU");
-    static constexpr int kXDma = 4 / kRPI;                    // activation DMAs per wave
-    static constexpr int kDma = NMAT * PF + 1 + kXDma;        // DMA instructions per batch per wave
-    // Byte offset of chunk 0 of activation row r inside the slot's activation
-    // area. A DMA block holds kRPI rows interleaved at 16 B (chunk c of row r
-    // at block(r / kRPI) + 16 kRPI c + 16 (r % kRPI)); with the block stride
-    // kPair, the 16 rows an MFMA fragment reads fall on distinct banks.
-    static __device__ __forceinline__ int row_off(int r) { return (r / kRPI) * kPair + (r % kRPI) * 16; }
-    static constexpr int kChunk = 16 * kRPI;                  // stride between a row's chunks
+    static constexpr int kRed = kBytes;                               // [NW][16] h group-sum partials
+    static constexpr int kTotal = kRed + NW * 64 + kTable * kTabInts * 4;   // + the item table
+    static_assert(kTotal * (8 / NW) <= 160 * 1024, "8 / NW workgroups per CU");
+#ifdef GLMMOE_EXP_NODMA
+    static constexpr int kDma = 0;   // diagnostics: compute on stale LDS, no streaming
+#else
+    static constexpr int kDma = NMAT * PF + 2 + kXDma;            // DMA instructions per batch per wave
+#endif
 };
 
-// Work items of a workgroup come in steps k: the 4 waves take items
-// base + wave + k * nwaves, which share one tile. A chunk of up to kTable
-// steps is described in an LDS table read back with inline ds_read (no
-// vector-memory loads inside the pipeline, whose waits would drain the DMA
-// queue): per step {expert, row0, nrows, feature block of wave 0} and the 16
+// Work items of a workgroup come in steps k: WG-item base + k * nwg is
+// (tile, block group), and wave w takes weight block 8 * group + w. A chunk of
+// up to kTable steps is described in an LDS table read back with inline
+// ds_read (no vector-memory loads inside the pipeline, whose waits would
+// drain the DMA queue): per step {expert, row0, nrows, block group} and the 16
 // token ids of the tile rows (row 0's token past nrows).
 
 struct Item {
     const uint4* wq[2];
     const uint16_t* ws[2];
     int r0, nr, fb;
-    int tok[4];   // tokens (NMAT = 2) or grouped rows (NMAT = 1) of this wave's 4 staged rows
+    uint32_t tok[2];   // src row of this lane in each of this wave's activation DMAs
+    uint32_t gtok;     // gsum row of tile row lane % 16
 };
 
-template <int NMAT>
+template <int NMAT, int PF, int D, int NW>
 __device__ __forceinline__ Item item_from_table(const ExpArgs& a, const int* table, int k,
-                                                int wave, int nfb, int KG) {
+                                                int wave, int lane, int nfb, int KG) {
+    using RG = Ring<NMAT, PF, D, NW>;
     const uint32_t base = lds_addr(table + k * kTabInts);
     const uint4 h = lds_bcast16(base);
-    const uint4 t = lds_bcast16(base + 16 + wave * 16);
     Item it;
     const int e = sgpr(h.x);
     it.r0 = sgpr(h.y);
     it.nr = sgpr(h.z);
-    it.fb = sgpr(h.w) + wave;
-    if (NMAT == 2) {
-        it.tok[0] = sgpr(t.x); it.tok[1] = sgpr(t.y); it.tok[2] = sgpr(t.z); it.tok[3] = sgpr(t.w);
-    } else {
+    it.fb = sgpr(h.w) * NW + wave;
+    // Activation DMA j of this wave covers tile rows (wave * kXDma + j) * kRPD + [0, kRPD);
+    // this lane's row is the lane / kCPR-th of them.
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            const int row = wave * 4 + j;
-            it.tok[j] = it.r0 + (row < it.nr ? row : 0);
-        }
+    for (int j = 0; j < RG::kXDma; ++j) {
+        const int row = ((wave * RG::kXDma + j) * RG::kRPD + lane / RG::kCPR) % kTileRows;
+        if (NMAT == 2) it.tok[j] = lds_read_u32(base + 16 + row * 4);
+        else it.tok[j] = (uint32_t)(it.r0 + (row < it.nr ? row : 0));
+    }
+    {
+        const int row = lane & 15;
+        it.gtok = NMAT == 2 ? lds_read_u32(base + 16 + row * 4)
+                            : (uint32_t)(it.r0 + (row < it.nr ? row : 0));
     }
     const bool sh = e == a.E;
     const size_t mstride_q = (size_t)nfb * KG * 64;   // uint4 per matrix
@@ -182,17 +205,17 @@ __device__ __forceinline__ Item item_from_table(const ExpArgs& a, const int* tab
 
 // Fills table steps [k0, k0 + cnt) (whole workgroup; ordinary loads; the
 // caller has drained all DMA and synchronizes afterwards).
-__device__ __forceinline__ void fill_table(const ExpArgs& a, int* table, long base, long nwaves,
-                                           int nfb, long k0, int cnt) {
+__device__ __forceinline__ void fill_table(const ExpArgs& a, int* table, int base, int nwg,
+                                           int ngrp, int k0, int cnt) {
     for (int i = threadIdx.x; i < cnt * kTabInts; i += blockDim.x) {
         const int k = i / kTabInts, f = i % kTabInts;
-        const long item = base + (k0 + k) * nwaves;
-        const int4 tile = a.tiles[item / nfb];
+        const int item = base + (k0 + k) * nwg;
+        const int4 tile = a.tiles[item / ngrp];
         int v;
         if (f == 0) v = tile.x;
         else if (f == 1) v = tile.y;
         else if (f == 2) v = tile.z;
-        else if (f == 3) v = (int)(item % nfb);
+        else if (f == 3) v = (int)(item % ngrp);
         else {
             const int row = f - 4;
             v = a.rows_tok ? a.rows_tok[tile.y + (row < tile.z ? row : 0)] : 0;
@@ -202,10 +225,13 @@ __device__ __forceinline__ void fill_table(const ExpArgs& a, int* table, long ba
 }
 
 // Issues batch bb of item `it` into ring slot `slot` (exactly kDma DMAs).
-template <int NMAT, int PF, int D>
+template <int NMAT, int PF, int D, int NW>
 __device__ __forceinline__ void issue_batch(const ExpArgs& a, const Item& it, int bb, int K,
                                             int KG, char* slot, int wave, int lane) {
-    using RG = Ring<NMAT, PF, D>;
+    using RG = Ring<NMAT, PF, D, NW>;
+#ifdef GLMMOE_EXP_NODMA
+    return;
+#endif
     const int kg0 = bb * PF;
     // Weight tiles: [wave][m][i] 1 KiB each, lane-contiguous like the global tile.
 #pragma unroll
@@ -223,100 +249,94 @@ __device__ __forceinline__ void issue_batch(const ExpArgs& a, const Item& it, in
         const int kg = min(kg0 + d / 8, KG - 1);
         dma4(it.ws[m] + (size_t)kg * 16 + (d % 8) * 2, slot + RG::kWBytes + wave * 256);
     }
-    // Activation rows 4*wave .. 4*wave+3 of the tile, kRPI rows per DMA (row r0
-    // stands in past nr; those token columns are computed but never stored).
+    // Group sums: wave 0 lane l fetches X of tile row l % 16, group kg0 + l / 16.
+    {
+        const int kg = min(kg0 + (lane >> 4) % PF, KG - 1);
+        dma4(a.gsum + (size_t)it.gtok * KG + kg, slot + RG::kGOff + (wave == 0 ? 0 : 256));
+    }
+    // Activation rows: whole rows per DMA, chunk slot p of a row holds chunk
+    // p ^ (row & 15) of the batch's PF * 128 K (row r0 stands in past nr;
+    // those token columns are computed but never stored).
 #pragma unroll
     for (int j = 0; j < RG::kXDma; ++j) {
-        const int sub = lane % RG::kRPI;                 // row inside this DMA
-        const int li = lane / RG::kRPI;                  // 16-byte chunk inside the row
-        const int jr = j * RG::kRPI + sub;               // 0..3: which of this wave's rows
-        size_t srow = (size_t)it.tok[0];
-#pragma unroll
-        for (int t = 1; t < 4; ++t) srow = jr == t ? (size_t)it.tok[t] : srow;
-        const int koff = min(kg0 * 128 + li * 8, K - 8);  // bf16 offset of this lane's 16 B
-        const int row0 = wave * 4 + j * RG::kRPI;         // first row of this DMA
-        dma16(a.src + srow * K + koff,
-              slot + RG::kWBytes + RG::kSBytes + (row0 / RG::kRPI) * RG::kPair);
+        const int blk = wave * RG::kXDma + j;
+        const int row = (blk * RG::kRPD + lane / RG::kCPR) % kTileRows;
+        const int c = (lane % RG::kCPR) ^ (row & 15);
+        const int koff = min(kg0 * 128 + c * 8, K - 8);
+        char* dst = blk < RG::kNX ? slot + RG::kWBytes + RG::kSBytes + blk * 1024
+                                  : slot + RG::kWBytes + RG::kSBytes + RG::kXBytes;
+        dma16(a.src + (size_t)it.tok[j] * K + koff, dst);
     }
 }
 
-template <int NMAT, int PF, int D>
-__device__ __forceinline__ void compute_batch(const char* slot, int bb, int KG, int wave,
-                                              int lane, const DqConst& dqc, f32x4 (&acc)[NMAT]) {
-    using RG = Ring<NMAT, PF, D>;
+// One 128-K group's LDS operands of a wave: its 4 activation fragments
+// (the 16 token columns), its weight tile(s) and their 4 row scales.
+struct ExpOps {
+    u32x4 x[4], w[2];
+    u32x2 s[2];
+    float g;      // X of this lane's token column
+};
+
+// Issues the reads of group i of the batch in `slot` (no wait).
+template <int NMAT, int PF, int D, int NW>
+__device__ __forceinline__ void exp_load_ops(const char* slot, int i, int wave, int lane,
+                                             ExpOps& o) {
+    using RG = Ring<NMAT, PF, D, NW>;
     const int r = lane & 15, q = lane >> 4;
-    const uint32_t wbase = lds_addr(slot) + (uint32_t)(wave * NMAT * PF * RG::kW + lane * 16);
-    const uint32_t sbase = lds_addr(slot + RG::kWBytes + wave * 256) + (uint32_t)(q * 8);
-    const uint32_t xbase =
-        lds_addr(slot + RG::kWBytes + RG::kSBytes) + (uint32_t)(RG::row_off(r) + 4 * q * RG::kChunk);
-    // bf16 1.0 in every element: the A operand of the group-sum MFMA.
-    const bf16x8 ones = __builtin_bit_cast(bf16x8, uint4{0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u});
+    const uint32_t wa = lds_addr(slot) + (uint32_t)(wave * NMAT * PF * RG::kW + lane * 16) + i * RG::kW;
+    const uint32_t sa = lds_addr(slot + RG::kWBytes + wave * 256) + (uint32_t)(q * 8) + i * 32;
+    // Chunk 16 i + 4 q + d of row r is at r * kRS + 256 i + 16 ((4 q + d) ^ r).
+    const uint32_t xrow = lds_addr(slot + RG::kWBytes + RG::kSBytes) + (uint32_t)(r * RG::kRS + 256 * i);
 #pragma unroll
-    for (int i = 0; i < PF; ++i) {
-        const bool live = bb * PF + i < KG;
-        uint4 x0, x1, x2, x3, w0, w1;
-        uint2 s0, s1;
-        const uint32_t xa = xbase + i * 16 * RG::kChunk;   // group i = chunks 16i ..
-        const uint32_t wa = wbase + i * RG::kW;
-        const uint32_t sa = sbase + i * 32;
-        if constexpr (NMAT == 2) {
-            asm volatile(
-                "ds_read_b128 %0, %8\n"
-                "ds_read_b128 %1, %8 offset:%c13\n"
-                "ds_read_b128 %2, %8 offset:%c14\n"
-                "ds_read_b128 %3, %8 offset:%c15\n"
-                "ds_read_b128 %4, %9\n"
-                "ds_read_b128 %5, %9 offset:%c11\n"
-                "ds_read_b64 %6, %10\n"
-                "ds_read_b64 %7, %10 offset:%c12\n"
-                "s_waitcnt lgkmcnt(0)"
-                : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(w0), "=&v"(w1), "=&v"(s0),
-                  "=&v"(s1)
-                : "v"(xa), "v"(wa), "v"(sa), "i"(PF * RG::kW), "i"(PF * 32), "i"(RG::kChunk),
-                  "i"(2 * RG::kChunk), "i"(3 * RG::kChunk));
-        } else {
-            asm volatile(
-                "ds_read_b128 %0, %6\n"
-                "ds_read_b128 %1, %6 offset:%c9\n"
-                "ds_read_b128 %2, %6 offset:%c10\n"
-                "ds_read_b128 %3, %6 offset:%c11\n"
-                "ds_read_b128 %4, %7\n"
-                "ds_read_b64 %5, %8\n"
-                "s_waitcnt lgkmcnt(0)"
-                : "=&v"(x0), "=&v"(x1), "=&v"(x2), "=&v"(x3), "=&v"(w0), "=&v"(s0)
-                : "v"(xa), "v"(wa), "v"(sa), "i"(RG::kChunk), "i"(2 * RG::kChunk),
-                  "i"(3 * RG::kChunk));
-            w1 = w0;
-            s1 = s0;
-        }
-        f32x4 px = {0.f, 0.f, 0.f, 0.f};
-        px = mfma16x16x32(ones, as_bf16x8(x0), px);
-        px = mfma16x16x32(ones, as_bf16x8(x1), px);
-        px = mfma16x16x32(ones, as_bf16x8(x2), px);
-        px = mfma16x16x32(ones, as_bf16x8(x3), px);
-#pragma unroll
-        for (int m = 0; m < NMAT; ++m) {
-            const uint4 wv = m == 0 ? w0 : w1;
-            const uint2 sv = m == 0 ? s0 : s1;
-            float sc[4];
-            sc[0] = bf16_to_f32(sv.x & 0xffffu); sc[1] = bf16_to_f32(sv.x >> 16);
-            sc[2] = bf16_to_f32(sv.y & 0xffffu); sc[3] = bf16_to_f32(sv.y >> 16);
-            f32x4 p = {0.f, 0.f, 0.f, 0.f};
-            p = mfma16x16x32(dq_w4(wv.x, dqc), as_bf16x8(x0), p);
-            p = mfma16x16x32(dq_w4(wv.y, dqc), as_bf16x8(x1), p);
-            p = mfma16x16x32(dq_w4(wv.z, dqc), as_bf16x8(x2), p);
-            p = mfma16x16x32(dq_w4(wv.w, dqc), as_bf16x8(x3), p);
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                acc[m][j] = __builtin_fmaf(live ? sc[j] : 0.0f,
-                                           __builtin_fmaf(-136.0f, px[j], p[j]), acc[m][j]);
-        }
+    for (int d = 0; d < 4; ++d) {
+        const uint32_t xa = xrow + (uint32_t)(((4 * q + d) ^ r) * 16);
+        asm volatile("ds_read_b128 %0, %1" : "=&v"(o.x[d]) : "v"(xa));
+    }
+    const uint32_t ga = lds_addr(slot + RG::kGOff) + (uint32_t)((i * 16 + r) * 4);
+    asm volatile("ds_read_b32 %0, %1" : "=&v"(o.g) : "v"(ga));
+    if constexpr (NMAT == 2) {
+        asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:%c3"
+                     : "=&v"(o.w[0]), "=&v"(o.w[1]) : "v"(wa), "i"(PF * RG::kW));
+        asm volatile("ds_read_b64 %0, %2\n ds_read_b64 %1, %2 offset:%c3"
+                     : "=&v"(o.s[0]), "=&v"(o.s[1]) : "v"(sa), "i"(PF * 32));
+    } else {
+        asm volatile("ds_read_b128 %0, %1" : "=&v"(o.w[0]) : "v"(wa));
+        asm volatile("ds_read_b64 %0, %1" : "=&v"(o.s[0]) : "v"(sa));
     }
 }
 
-template <int NMAT, int PF, int D>
-__global__ __launch_bounds__(256) void w4_expert_kernel(ExpArgs a) {
-    using RG = Ring<NMAT, PF, D>;
+__device__ __forceinline__ void exp_wait_ops(ExpOps& o) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(o.x[0]), "+v"(o.x[1]), "+v"(o.x[2]), "+v"(o.x[3]), "+v"(o.w[0]),
+                   "+v"(o.w[1]), "+v"(o.s[0]), "+v"(o.s[1]), "+v"(o.g));
+}
+
+// One 128-K group: acc[m] += scale * (sum_k (128 + c) x - 136 X), X the
+// group sum of the token column. The matrices' MFMA chains are interleaved.
+template <int NMAT>
+__device__ __forceinline__ void exp_compute_group(const ExpOps& o, const DqConst& dqc,
+                                                  f32x4 (&acc)[NMAT]) {
+    const float off = -136.0f * o.g;
+    f32x4 p[NMAT];
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+            p[m] = mfma16x16x32(dq_w4(o.w[m][d], dqc), as_bf16x8(o.x[d]),
+                                d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : p[m]);
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+        const u32x2 sv = o.s[m];
+        const float sc[4] = {bf16_to_f32(sv.x & 0xffffu), __uint_as_float(sv.x & 0xffff0000u),
+                             bf16_to_f32(sv.y & 0xffffu), __uint_as_float(sv.y & 0xffff0000u)};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[m][j] = __builtin_fmaf(sc[j], p[m][j] + off, acc[m][j]);
+    }
+}
+
+template <int NMAT, int PF, int D, int NW>
+__global__ __launch_bounds__(NW * 64) void w4_expert_kernel(ExpArgs a) {
+    using RG = Ring<NMAT, PF, D, NW>;
     extern __shared__ __align__(16) char ring[];
     const DqConst dqc = dq_const();
     const int lane = threadIdx.x & 63;
@@ -325,69 +345,113 @@ __global__ __launch_bounds__(256) void w4_expert_kernel(ExpArgs a) {
     const int K = NMAT == 2 ? a.H : a.I;
     const int KG = K / 128;
     const int nfb = (NMAT == 2 ? a.I : a.H) / 16;
+    const int ngrp = nfb / NW;
     const int nbatch = (KG + PF - 1) / PF;
-    const long total = (long)(*a.ntiles) * nfb;
-    const long nwaves = (long)gridDim.x * 4;
-    const long base = (long)blockIdx.x * 4;
-    // Steps of this workgroup (equal for its 4 waves: total and nwaves are
-    // multiples of 4).
-    const long nitems = base < total ? (total - base + nwaves - 1) / nwaves : 0;
-    int* table = reinterpret_cast<int*>(ring + RG::kBytes);
+    const int total = *a.ntiles * ngrp;
+    const int nwg = (int)gridDim.x;
+    const int base = (int)blockIdx.x;
+    const int nitems = base < total ? (total - base + nwg - 1) / nwg : 0;
+    int* table = reinterpret_cast<int*>(ring + RG::kRed + NW * 64);
 
-    for (long k0 = 0; k0 < nitems; k0 += kTable) {
-        const int cnt = (int)min((long)kTable, nitems - k0);
-        fill_table(a, table, base, nwaves, nfb, k0, cnt);
+    for (int k0 = 0; k0 < nitems; k0 += kTable) {
+        const int cnt = min(kTable, nitems - k0);
+        fill_table(a, table, base, nwg, ngrp, k0, cnt);
         __syncthreads();
-        const long nsteps = (long)cnt * nbatch;
+        const int nsteps = cnt * nbatch;
 
-        // Prologue: batches 0 .. D-2 in flight.
+        // Ring of D batch slots; batch b lives in slot b % D (the step loop is
+        // unrolled D times so every slot address is a constant). The prologue
+        // fills every slot. Per batch: compute its groups, each one's LDS
+        // reads issued under the previous group's MFMAs; before the last
+        // group, wait for batch b + 1 and barrier (every wave is then done
+        // reading slot b, and b + 1 is visible), refill slot b with batch
+        // b + D and issue the reads of b + 1's first group.
         int iss_k = 0, iss_b = 0;
-        Item iss = item_from_table<NMAT>(a, table, 0, wave, nfb, KG);
-        for (int j = 0; j < D - 1; ++j) {
-            if (j < nsteps) {
-                issue_batch<NMAT, PF, D>(a, iss, iss_b, K, KG, ring + (j % D) * RG::kSlot, wave,
-                                         lane);
-                if (++iss_b == nbatch) {
-                    iss_b = 0;
-                    if (++iss_k < cnt) iss = item_from_table<NMAT>(a, table, iss_k, wave, nfb, KG);
-                }
+        Item iss = item_from_table<NMAT, PF, D, NW>(a, table, 0, wave, lane, nfb, KG);
+        auto issue_next = [&](char* slot) {
+            issue_batch<NMAT, PF, D, NW>(a, iss, iss_b, K, KG, slot, wave, lane);
+            if (++iss_b == nbatch) {
+                iss_b = 0;
+                if (++iss_k < cnt)
+                    iss = item_from_table<NMAT, PF, D, NW>(a, table, iss_k, wave, lane, nfb, KG);
             }
-        }
+        };
+#pragma unroll
+        for (int j = 0; j < D; ++j)
+            if (j < nsteps) issue_next(ring + j * RG::kSlot);
+        if (nsteps >= D) wait_vmcnt<RG::kDma * (D - 1)>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        ExpOps ops[2];
+        exp_load_ops<NMAT, PF, D, NW>(ring, 0, wave, lane, ops[0]);
 
         int cur_k = 0, cur_b = 0;
-        Item cur = item_from_table<NMAT>(a, table, 0, wave, nfb, KG);
+        Item cur = item_from_table<NMAT, PF, D, NW>(a, table, 0, wave, lane, nfb, KG);
         f32x4 acc[NMAT];
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-        for (long step = 0; step < nsteps; ++step) {
-            // Batch `step` has landed once at most (D-2) newer batches are pending.
-            if (step + D - 2 < nsteps) wait_vmcnt<RG::kDma * (D - 2)>();
-            else wait_vmcnt<0>();
-            __builtin_amdgcn_s_barrier();
-            if (step + D - 1 < nsteps) {
-                issue_batch<NMAT, PF, D>(a, iss, iss_b, K, KG,
-                                         ring + ((step + D - 1) % D) * RG::kSlot, wave, lane);
-                if (++iss_b == nbatch) {
-                    iss_b = 0;
-                    if (++iss_k < cnt) iss = item_from_table<NMAT>(a, table, iss_k, wave, nfb, KG);
+        for (int step0 = 0; step0 < nsteps; step0 += D) {
+#pragma unroll
+        for (int u = 0; u < D; ++u) {
+            const int step = step0 + u;
+            if (step >= nsteps) break;
+            char* slot = ring + u * RG::kSlot;
+#pragma unroll
+            for (int i = 0; i < PF; ++i) {
+                ExpOps& o = ops[i & 1];
+                exp_wait_ops(o);
+                if (i + 1 < PF) {
+                    exp_load_ops<NMAT, PF, D, NW>(slot, i + 1, wave, lane, ops[(i + 1) & 1]);
+                } else {
+                    // Batch step + 1 has landed once at most the batches issued
+                    // after it (up to step + D - 1) are pending.
+                    if (step + D - 1 < nsteps) wait_vmcnt<RG::kDma * (D - 2)>();
+                    else wait_vmcnt<0>();
+                    __builtin_amdgcn_s_barrier();
+                    if (step + D < nsteps) issue_next(slot);
+                    if (step + 1 < nsteps)
+                        exp_load_ops<NMAT, PF, D, NW>(ring + ((u + 1) % D) * RG::kSlot, 0, wave,
+                                                      lane, ops[(i + 1) & 1]);
                 }
+#ifndef GLMMOE_EXP_NOCOMPUTE
+                // The clamped group past an odd K-group count adds nothing.
+                if (PF == 1 || cur_b * PF + i < KG) exp_compute_group<NMAT>(o, dqc, acc);
+#endif
             }
-            compute_batch<NMAT, PF, D>(ring + (step % D) * RG::kSlot, cur_b, KG, wave, lane, dqc,
-                                       acc);
-
+            // With an odd batch size the next batch's first group was read
+            // into buffer 1; batches always start from buffer 0.
+            if (PF & 1) ops[0] = ops[1];
             if (++cur_b == nbatch) {
                 const bool valid = r < cur.nr;
                 const size_t row = (size_t)cur.r0 + r;
                 if constexpr (NMAT == 2) {
-                    uint32_t hb[4];
+                    static_assert(NMAT == 1 || NW == 8, "a workgroup step covers one 128-feature group");
+                    const uint32_t h01 = pack_bf16x2(silu_fast(acc[0][0]) * acc[1][0],
+                                                     silu_fast(acc[0][1]) * acc[1][1]);
+                    const uint32_t h23 = pack_bf16x2(silu_fast(acc[0][2]) * acc[1][2],
+                                                     silu_fast(acc[0][3]) * acc[1][3]);
+                    if (valid)
+                        *reinterpret_cast<uint2*>(a.h + row * a.I + cur.fb * 16 + 4 * q) =
+                            uint2{h01, h23};
+                    // hsum of the rounded h over the step's 128 features (one
+                    // group of I) per tile row: 4 features per lane, the 4 row
+                    // quarters, then the 8 waves in order.
+                    float ps = (bf16_to_f32(h01 & 0xffffu) + __uint_as_float(h01 & 0xffff0000u)) +
+                               (bf16_to_f32(h23 & 0xffffu) + __uint_as_float(h23 & 0xffff0000u));
+                    ps = ps + __shfl_xor(ps, 16);
+                    ps = ps + __shfl_xor(ps, 32);
+                    const uint32_t red = lds_addr(ring + RG::kRed);
+                    if (q == 0) lds_write_f32(red + (uint32_t)((wave * 16 + r) * 4), ps);
+                    __builtin_amdgcn_s_barrier();
+                    if (wave == 0 && q == 0) {
+                        float tot = 0.0f;
 #pragma unroll
-                    for (int j = 0; j < 4; ++j)
-                        hb[j] = f32_to_bf16(silu_fast(acc[0][j]) * acc[1][j]);
-                    if (valid) {
-                        uint2 v = {hb[0] | (hb[1] << 16), hb[2] | (hb[3] << 16)};
-                        *reinterpret_cast<uint2*>(a.h + row * a.I + cur.fb * 16 + 4 * q) = v;
+                        for (int w = 0; w < NW; ++w)
+                            tot += __uint_as_float(lds_read_u32(red + (uint32_t)((w * 16 + r) * 4)));
+                        if (valid) a.hsum[row * (a.I / 128) + cur.fb / NW] = tot;
                     }
+                    __builtin_amdgcn_s_barrier();   // partials consumed before reuse
                 } else {
                     if (valid)
                         *reinterpret_cast<float4*>(a.dpart + row * a.H + cur.fb * 16 + 4 * q) =
@@ -396,8 +460,10 @@ __global__ __launch_bounds__(256) void w4_expert_kernel(ExpArgs a) {
 #pragma unroll
                 for (int m = 0; m < NMAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
                 cur_b = 0;
-                if (++cur_k < cnt) cur = item_from_table<NMAT>(a, table, cur_k, wave, nfb, KG);
+                if (++cur_k < cnt)
+                    cur = item_from_table<NMAT, PF, D, NW>(a, table, cur_k, wave, lane, nfb, KG);
             }
+        }
         }
         // All DMA has landed (the last step waited vmcnt(0)); every wave is
         // done reading the ring and the table before the next chunk refills.
@@ -432,19 +498,30 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 }
 
 // ---------------------------------------------------------------------------
-// Ring depth per projection; both fit the 160 KiB of LDS of one workgroup.
-// Batches of 2 groups keep two 4-wave workgroups resident per CU (8 waves).
-constexpr int kRingGU = 3;
-constexpr int kRingDown = 4;
-constexpr int kPFGU = 2;
-constexpr int kPFDown = 2;
+// Ring depth and batch size per projection (one 8-wave workgroup per CU).
+#ifndef GLMMOE_RING_GU
+#define GLMMOE_RING_GU 3
+#define GLMMOE_PF_GU 2
+#define GLMMOE_NW_GU 8
+#endif
+#ifndef GLMMOE_RING_DOWN
+#define GLMMOE_RING_DOWN 4
+#define GLMMOE_PF_DOWN 2
+#define GLMMOE_NW_DOWN 8
+#endif
+constexpr int kRingGU = GLMMOE_RING_GU;
+constexpr int kRingDown = GLMMOE_RING_DOWN;
+constexpr int kPFGU = GLMMOE_PF_GU;
+constexpr int kPFDown = GLMMOE_PF_DOWN;
+constexpr int kNWGU = GLMMOE_NW_GU;
+constexpr int kNWDown = GLMMOE_NW_DOWN;
 
-template <int NMAT, int PF, int D>
+template <int NMAT, int PF, int D, int NW>
 static int launch_expert(const ExpArgs& a, long max_work, hipStream_t s) {
-    using RG = Ring<NMAT, PF, D>;
+    using RG = Ring<NMAT, PF, D, NW>;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4_expert_kernel<NMAT, PF, D>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4_expert_kernel<NMAT, PF, D, NW>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, RG::kTotal) !=
             hipSuccess)
             return -4;
@@ -453,38 +530,38 @@ static int launch_expert(const ExpArgs& a, long max_work, hipStream_t s) {
     int dev = 0, cus = 256;
     if (hipGetDevice(&dev) == hipSuccess)
         (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
-    // As many workgroups as fit in LDS at once; persistent over items.
-    const int per_cu = (160 * 1024) / RG::kTotal;
-    long blocks = (max_work + 3) / 4;
-    if (blocks > (long)cus * per_cu) blocks = (long)cus * per_cu;
+    // Persistent: 8 waves per CU, never more workgroups than items.
+    long blocks = max_work;
+    if (blocks > (long)cus * (8 / NW)) blocks = (long)cus * (8 / NW);
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL((w4_expert_kernel<NMAT, PF, D>), dim3((unsigned)blocks), dim3(256),
+    hipLaunchKernelGGL((w4_expert_kernel<NMAT, PF, D, NW>), dim3((unsigned)blocks), dim3(NW * 64),
                        RG::kTotal, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const int* tiles, const int* ntiles,
-                   int max_tiles, const int* rows_tok, uint16_t* h, int H, int I, int E,
-                   hipStream_t s) {
+int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
+                   const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
+                   float* hsum, int H, int I, int E, hipStream_t s) {
     ExpArgs a{};
     a.wq[0] = reinterpret_cast<const uint4*>(P.gate_q); a.ws[0] = P.gate_s;
     a.wq[1] = reinterpret_cast<const uint4*>(P.up_q); a.ws[1] = P.up_s;
     a.swq[0] = reinterpret_cast<const uint4*>(P.sh_gate_q); a.sws[0] = P.sh_gate_s;
     a.swq[1] = reinterpret_cast<const uint4*>(P.sh_up_q); a.sws[1] = P.sh_up_s;
-    a.src = x; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
-    a.rows_tok = rows_tok; a.h = h; a.H = H; a.I = I; a.E = E;
-    return launch_expert<2, kPFGU, kRingGU>(a, (long)max_tiles * (I / 16), s);
+    a.src = x; a.gsum = xsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
+    a.rows_tok = rows_tok; a.h = h; a.hsum = hsum; a.H = H; a.I = I; a.E = E;
+    return launch_expert<2, kPFGU, kRingGU, kNWGU>(a, (long)max_tiles * (I / 16 / kNWGU), s);
 }
 
-int launch_down(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
-                int max_tiles, float* dpart, int H, int I, int E, hipStream_t s) {
+int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
+                const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
+                hipStream_t s) {
     ExpArgs a{};
     a.wq[0] = reinterpret_cast<const uint4*>(P.down_q); a.ws[0] = P.down_s;
     a.swq[0] = reinterpret_cast<const uint4*>(P.sh_down_q); a.sws[0] = P.sh_down_s;
     a.wq[1] = a.wq[0]; a.ws[1] = a.ws[0]; a.swq[1] = a.swq[0]; a.sws[1] = a.sws[0];
-    a.src = h; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
+    a.src = h; a.gsum = hsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.dpart = dpart; a.H = H; a.I = I; a.E = E;
-    return launch_expert<1, kPFDown, kRingDown>(a, (long)max_tiles * (H / 16), s);
+    return launch_expert<1, kPFDown, kRingDown, kNWDown>(a, (long)max_tiles * (H / 16 / kNWDown), s);
 }
 
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
