@@ -165,11 +165,12 @@ constexpr int kF8D = 3;
 struct F8Ring {
     static constexpr int kWBytes = 8 * 4096;            // 8 weight tiles
     static constexpr int kXOff = kWBytes;
-    // One activation DMA = 8 rows x 128 B, chunk c of row r at 128 c + 16 (r % 8);
-    // the 1152-byte block stride puts rows 8..15 of a 16-lane read phase on
-    // the other half of the banks.
-    static constexpr int kOct = 1024 + 128;
-    static constexpr int kSOff = kXOff + (kBigRows / 8) * kOct;   // activation scales
+    // Activation rows are 128 B, row r at 128 r, so one DMA (64 lanes x 16 B)
+    // reads 8 whole rows with adjacent lanes on adjacent bytes (full-speed L2
+    // coalescing). Chunk c of row r sits at slot c ^ ((r >> 1) & 7): the 16
+    // rows an MFMA fragment pass reads at one chunk land on 16 distinct bank
+    // groups.
+    static constexpr int kSOff = kXOff + kBigRows * 128;          // activation scales
     static constexpr int kWSOff = kSOff + 4 * kBigRows;          // weight block scales
     static constexpr int kJunk = kWSOff + 256;                   // placeholder DMA target
     static constexpr int kSlot = kJunk + 256;
@@ -178,122 +179,167 @@ struct F8Ring {
     static constexpr int kTab = kRed + 4 * kBigRows * 4;
     static constexpr int kTotal = kTab + kBigTable * kBigTabInts * 4;
     static_assert(kTotal <= 160 * 1024, "one workgroup's LDS");
+#ifdef GLMMOE_F8_NODMA
+    static constexpr int kDma = 0;   // diagnostics: compute on stale LDS, no streaming
+#else
     static constexpr int kDma = 4 + 2 + 1;                       // per wave per group
-    static __device__ __forceinline__ int row_off(int r) { return (r >> 3) * kOct + (r & 7) * 16; }
+#endif
+    static __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
+};
+
+// DMA sources of one item at K-group 0 (group kg adds kg * 4 KiB to the weight
+// stream, kg * 128 B to the activation rows and kg to the scale streams).
+struct F8Issue {
+    const uint8_t* w;        // this wave's weight tile (lane offset included)
+    const float* sc;         // wave 0: weight block scale; waves 1, 2: activation scale
+    uint32_t x[2];           // src offsets of this lane's 16 B in the two activation DMAs
 };
 
 template <int NMAT>
-__device__ __forceinline__ void f8_issue(const F8Args& a, const BigItem& it, int kg, int K, int KG,
-                                         char* slot, int wave, int lane) {
-    using RG = F8Ring;
+__device__ __forceinline__ F8Issue f8_issue_ptrs(const F8Args& a, const BigItem& it, int K, int KG,
+                                                 int wave, int lane) {
+    F8Issue p;
     const bool sh = it.e == a.E;
     const int frows = NMAT == 2 ? a.I : a.H;
     const size_t mstride_q = (size_t)frows * K;
     const size_t mstride_s = (size_t)(frows / 128) * KG;
-    // Weight tile of this wave: (wn, jb) = (wave / 2, wave % 2).
     {
+        // Weight tile of this wave: (wn, jb) = (wave / 2, wave % 2).
         const int wn = wave >> 1, jb = wave & 1;
         const int m = NMAT == 2 ? jb : 0;
         const int fb = NMAT == 2 ? it.g * 4 + wn : it.g * 8 + wn * 2 + jb;
         const uint8_t* base = sh ? a.swq[m] : a.wq[m] + (size_t)it.e * mstride_q;
-        const uint8_t* src = base + ((size_t)fb * KG + kg) * 4096 + lane * 16;
-        char* dst = slot + wave * 4096;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) dma16(src + j * 1024, dst + j * 1024);
+        p.w = base + (size_t)fb * KG * 4096 + lane * 16;
     }
-    // Activation rows 16 wave .. 16 wave + 15: lane -> row lane % 8, chunk lane / 8.
+    // Activation DMA j of this wave fills rows 8 (2 wave + j) + lane / 8; the
+    // lane's LDS slot lane % 8 holds chunk (lane % 8) ^ swz(row).
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
-        const int blk = wave * 2 + j;
-        const int row = blk * 8 + (lane & 7);
+        const int row = (wave * 2 + j) * 8 + (lane >> 3);
         const uint32_t tk = lds_read32(it.tab + 16 + row * 4);
-        dma16(a.src + (size_t)tk * K + kg * 128 + (lane >> 3) * 16,
-              slot + RG::kXOff + blk * RG::kOct);
+        p.x[j] = tk * (uint32_t)K + (uint32_t)(((lane & 7) ^ F8Ring::swz(row)) * 16);
     }
     // Scales: wave 0 the weight block scales (lane & 1 -> gate / up, or the
     // down item's two 128-feature blocks); waves 1 / 2 the activation scales
     // of rows 0-63 / 64-127; other waves a placeholder.
     if (wave == 0) {
-        // Both candidate bases are wave-uniform; the per-lane choice is a
-        // select (indexing the argument array by lane would load it from memory).
         const float* sb0 = sh ? a.sws[0] : a.ws[0] + (size_t)it.e * mstride_s;
         const float* sb1 = sh ? a.sws[1] : a.ws[1] + (size_t)it.e * mstride_s;
         const bool odd = lane & 1;
         const float* sb = NMAT == 2 && odd ? sb1 : sb0;
         const int fblk = NMAT == 2 ? it.g : it.g * 2 + (odd ? 1 : 0);
-        dma4(sb + (size_t)fblk * KG + kg, slot + RG::kWSOff);
+        p.sc = sb + (size_t)fblk * KG;
     } else if (wave == 1 || wave == 2) {
         const int row = (wave - 1) * 64 + lane;
         const uint32_t tk = lds_read32(it.tab + 16 + row * 4);
-        dma4(a.sscale + (size_t)tk * KG + kg, slot + RG::kSOff + (wave - 1) * 256);
+        p.sc = a.sscale + (size_t)tk * KG;
     } else {
-        dma4(a.sscale, slot + RG::kJunk);
+        p.sc = a.sscale;
     }
+    return p;
 }
 
-template <int NMAT>
-__device__ __forceinline__ void f8_compute(const char* slot, int wave, int lane, int nr,
-                                           f32x16 (&acc)[2][2]) {
+// Exactly kDma DMAs per wave: group kg of the item into `slot`.
+__device__ __forceinline__ void f8_issue(const F8Args& a, const F8Issue& p, int kg, char* slot,
+                                         int wave) {
+    using RG = F8Ring;
+#ifdef GLMMOE_F8_NODMA
+    return;
+#endif
+    const uint8_t* src = p.w + (size_t)kg * 4096;
+    char* dst = slot + wave * 4096;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) dma16(src + j * 1024, dst + j * 1024);
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+        dma16(a.src + (p.x[j] + (uint32_t)kg * 128), slot + RG::kXOff + (wave * 2 + j) * 1024);
+    char* sdst = wave == 0 ? slot + RG::kWSOff
+               : (wave == 1 || wave == 2) ? slot + RG::kSOff + (wave - 1) * 256
+               : slot + RG::kJunk;
+    dma4(wave < 3 ? p.sc + kg : p.sc, sdst);
+}
+
+// Operands a wave reads from one ring slot: its two weight blocks (4 chunk
+// rows each), its two 32-row activation blocks (4 chunks each: K step s,
+// half h, 16-B piece q at chunk 4 s + 2 h + q), the activation scales of its
+// rows and the weight block scales.
+struct F8Ops {
+    u32x4 aw[2][4];
+    u32x4 bx[2][4];
+    float xs[2], ws[2];
+};
+
+__device__ __forceinline__ void f8_load_ops(const char* slot, int wave, int lane, int nmat,
+                                            F8Ops& o) {
     using RG = F8Ring;
     const int wn = wave >> 1, wm = wave & 1;
     const int col = lane & 31, h = lane >> 5;
-    const int ntb = min(2, max(0, (nr - wm * 64 + 31) >> 5));   // live 32-row blocks
-    if (ntb == 0) return;
-    u32x4 aw[2][4];
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
         const uint32_t wa = lds_addr(slot + (wn * 2 + jb) * 4096) + (uint32_t)(lane * 16);
         asm volatile(
             "ds_read_b128 %0, %4\n ds_read_b128 %1, %4 offset:1024\n"
             " ds_read_b128 %2, %4 offset:2048\n ds_read_b128 %3, %4 offset:3072"
-            : "=&v"(aw[jb][0]), "=&v"(aw[jb][1]), "=&v"(aw[jb][2]), "=&v"(aw[jb][3])
+            : "=&v"(o.aw[jb][0]), "=&v"(o.aw[jb][1]), "=&v"(o.aw[jb][2]), "=&v"(o.aw[jb][3])
             : "v"(wa));
     }
-    // B: row r's K chunk 4 s + 2 h + q, matching A's chunk (j = 2 s + q, half h).
-    u32x4 bx[2][4];
+    // Row R = wm*64 + tb*32 + col (tb = 1 is 32 rows = 4 KiB further, same
+    // swizzle); chunk c = 4 s + 2 h + q at slot c ^ swz(R).
+    const int R = wm * 64 + col;
+    const uint32_t xr = lds_addr(slot + RG::kXOff) + (uint32_t)(R * 128);
+    const int f = RG::swz(R);
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-        const int row = wm * 64 + tb * 32 + col;
-        const uint32_t xa =
-            lds_addr(slot + RG::kXOff) + (uint32_t)(RG::row_off(row) + 2 * h * 128);
-        asm volatile(
-            "ds_read_b128 %0, %4\n ds_read_b128 %1, %4 offset:128\n"
-            " ds_read_b128 %2, %4 offset:512\n ds_read_b128 %3, %4 offset:640"
-            : "=&v"(bx[tb][0]), "=&v"(bx[tb][1]), "=&v"(bx[tb][2]), "=&v"(bx[tb][3])
-            : "v"(xa));
-    }
-    float xs[2], ws[2];
+    for (int s = 0; s < 2; ++s)
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-        const uint32_t sa = lds_addr(slot + RG::kSOff) + (uint32_t)((wm * 64 + tb * 32 + col) * 4);
-        asm volatile("ds_read_b32 %0, %1" : "=&v"(xs[tb]) : "v"(sa));
-    }
+        for (int q = 0; q < 2; ++q) {
+            const uint32_t xa = xr + (uint32_t)((((4 * s + 2 * h + q) ^ f)) * 16);
+            asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:4096"
+                         : "=&v"(o.bx[0][2 * s + q]), "=&v"(o.bx[1][2 * s + q]) : "v"(xa));
+        }
+    const uint32_t sa = lds_addr(slot + RG::kSOff) + (uint32_t)(R * 4);
+    asm volatile("ds_read_b32 %0, %2\n ds_read_b32 %1, %2 offset:128"
+                 : "=&v"(o.xs[0]), "=&v"(o.xs[1]) : "v"(sa));
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
-        const int idx = NMAT == 2 ? jb : (wn >> 1);
+        const int idx = nmat == 2 ? jb : (wn >> 1);
         const uint32_t wa = lds_addr(slot + RG::kWSOff) + (uint32_t)(idx * 4);
-        asm volatile("ds_read_b32 %0, %1" : "=&v"(ws[jb]) : "v"(wa));
+        asm volatile("ds_read_b32 %0, %1" : "=&v"(o.ws[jb]) : "v"(wa));
     }
+}
+
+__device__ __forceinline__ void f8_wait_ops(F8Ops& o) {
     asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(aw[0][0]), "+v"(aw[0][1]), "+v"(aw[0][2]), "+v"(aw[0][3]),
-                   "+v"(aw[1][0]), "+v"(aw[1][1]), "+v"(aw[1][2]), "+v"(aw[1][3]),
-                   "+v"(bx[0][0]), "+v"(bx[0][1]), "+v"(bx[0][2]), "+v"(bx[0][3]),
-                   "+v"(bx[1][0]), "+v"(bx[1][1]), "+v"(bx[1][2]), "+v"(bx[1][3]),
-                   "+v"(xs[0]), "+v"(xs[1]), "+v"(ws[0]), "+v"(ws[1]));
+                 : "+v"(o.aw[0][0]), "+v"(o.aw[0][1]), "+v"(o.aw[0][2]), "+v"(o.aw[0][3]),
+                   "+v"(o.aw[1][0]), "+v"(o.aw[1][1]), "+v"(o.aw[1][2]), "+v"(o.aw[1][3]),
+                   "+v"(o.bx[0][0]), "+v"(o.bx[0][1]), "+v"(o.bx[0][2]), "+v"(o.bx[0][3]),
+                   "+v"(o.bx[1][0]), "+v"(o.bx[1][1]), "+v"(o.bx[1][2]), "+v"(o.bx[1][3]),
+                   "+v"(o.xs[0]), "+v"(o.xs[1]), "+v"(o.ws[0]), "+v"(o.ws[1]));
+}
+
+// One 128-K group: p = the two 64-K MFMA products per 32 x 32 block.
+__device__ __forceinline__ void f8_compute(const F8Ops& o, f32x16 (&p)[2][2]) {
 #pragma unroll
-    for (int jb = 0; jb < 2; ++jb) {
+    for (int s = 0; s < 2; ++s)
+#pragma unroll
+        for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+            for (int tb = 0; tb < 2; ++tb)
+                p[jb][tb] = mfma_f8_32x32x64(cat8(o.aw[jb][2 * s], o.aw[jb][2 * s + 1]),
+                                             cat8(o.bx[tb][2 * s], o.bx[tb][2 * s + 1]),
+                                             s == 0 ? f32x16{} : p[jb][tb]);
+}
+
+// acc += (w_scale * x_scale) * p.
+__device__ __forceinline__ void f8_rescale(const float (&xs)[2], const float (&ws)[2],
+                                           const f32x16 (&p)[2][2], f32x16 (&acc)[2][2]) {
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb) {
-            if (tb < ntb) {
-                f32x16 p = mfma_f8_32x32x64(cat8(aw[jb][0], aw[jb][1]),
-                                            cat8(bx[tb][0], bx[tb][1]), f32x16{});
-                p = mfma_f8_32x32x64(cat8(aw[jb][2], aw[jb][3]), cat8(bx[tb][2], bx[tb][3]), p);
-                const float sc = ws[jb] * xs[tb];
+            const float sc = ws[jb] * xs[tb];
 #pragma unroll
-                for (int i = 0; i < 16; ++i) acc[jb][tb][i] = __builtin_fmaf(sc, p[i], acc[jb][tb][i]);
-            }
+            for (int i = 0; i < 16; ++i) acc[jb][tb][i] = __builtin_fmaf(sc, p[jb][tb][i], acc[jb][tb][i]);
         }
-    }
 }
 
 template <int NMAT>
@@ -372,50 +418,67 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
     int* table = reinterpret_cast<int*>(lds + RG::kTab);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int wm = wave & 1;
     const int K = NMAT == 2 ? a.H : a.I;
     const int KG = K / 128;
     const int nfg = NMAT == 2 ? a.I / 128 : a.H / 256;
-    const long nitems = big_rounds((long)(*a.ntiles) * nfg);
+    const int nitems = (int)big_rounds((long)(*a.ntiles) * nfg);
 
-    for (long k0 = 0; k0 < nitems; k0 += kBigTable) {
-        const int cnt = (int)min((long)kBigTable, nitems - k0);
+    for (int k0 = 0; k0 < nitems; k0 += kBigTable) {
+        const int cnt = min(kBigTable, nitems - k0);
         big_fill_table<NMAT == 2>(a.tiles, a.rows_tok, table, k0, cnt, nfg);
         __syncthreads();
-        const long nsteps = (long)cnt * KG;
+        const int nsteps = cnt * KG;
 
+        // Ring of kF8D slots, group g in slot g % kF8D. Per group: compute g;
+        // wait for g + 1's DMA and barrier (every wave is then done with slot
+        // g, and g + 1 is visible); refill slot g with group g + kF8D; issue
+        // the reads of g + 1's operands; apply g's scales under those reads.
         int iss_k = 0, iss_g = 0;
-        BigItem iss = big_item(lds + RG::kTab, 0);
-        for (int j = 0; j < kF8D - 1; ++j) {
-            if (j < nsteps) {
-                f8_issue<NMAT>(a, iss, iss_g, K, KG, lds + (j % kF8D) * RG::kSlot, wave, lane);
-                if (++iss_g == KG) {
-                    iss_g = 0;
-                    if (++iss_k < cnt) iss = big_item(lds + RG::kTab, iss_k);
-                }
+        F8Issue iss = f8_issue_ptrs<NMAT>(a, big_item(lds + RG::kTab, 0), K, KG, wave, lane);
+        auto issue_next = [&](int g) {
+            f8_issue(a, iss, iss_g, lds + (g % kF8D) * RG::kSlot, wave);
+            if (++iss_g == KG) {
+                iss_g = 0;
+                if (++iss_k < cnt)
+                    iss = f8_issue_ptrs<NMAT>(a, big_item(lds + RG::kTab, iss_k), K, KG, wave, lane);
             }
-        }
+        };
+        for (int j = 0; j < kF8D; ++j)
+            if (j < nsteps) issue_next(j);
+        if (nsteps >= 3) wait_vmcnt<RG::kDma * 2>();
+        else if (nsteps == 2) wait_vmcnt<RG::kDma>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();
+        F8Ops ops;
+        f8_load_ops(lds, wave, lane, NMAT, ops);
+
         int cur_k = 0, cur_g = 0;
         BigItem cur = big_item(lds + RG::kTab, 0);
+        // Whether this wave's 64 rows hold any live row (wave-uniform per item).
+        bool live = cur.nr > wm * 64;
         f32x16 acc[2][2];
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb) acc[jb][tb] = f32x16{};
 
-        for (long step = 0; step < nsteps; ++step) {
-            if (step + kF8D - 2 < nsteps) wait_vmcnt<RG::kDma * (kF8D - 2)>();
+        for (int step = 0; step < nsteps; ++step) {
+            f8_wait_ops(ops);
+            f32x16 p[2][2];
+#ifndef GLMMOE_F8_NOCOMPUTE
+            if (live) f8_compute(ops, p);
+#endif
+            if (step + 2 < nsteps) wait_vmcnt<RG::kDma>();
             else wait_vmcnt<0>();
             __builtin_amdgcn_s_barrier();
-            if (step + kF8D - 1 < nsteps) {
-                f8_issue<NMAT>(a, iss, iss_g, K, KG, lds + ((step + kF8D - 1) % kF8D) * RG::kSlot,
-                               wave, lane);
-                if (++iss_g == KG) {
-                    iss_g = 0;
-                    if (++iss_k < cnt) iss = big_item(lds + RG::kTab, iss_k);
-                }
-            }
-            f8_compute<NMAT>(lds + (step % kF8D) * RG::kSlot, wave, lane, cur.nr, acc);
-
+            if (step + kF8D < nsteps) issue_next(step + kF8D);
+            const float xs[2] = {ops.xs[0], ops.xs[1]};
+            const float ws[2] = {ops.ws[0], ops.ws[1]};
+            if (step + 1 < nsteps) f8_load_ops(lds + ((step + 1) % kF8D) * RG::kSlot, wave, lane, NMAT, ops);
+#ifndef GLMMOE_F8_NOCOMPUTE
+            if (live) f8_rescale(xs, ws, p, acc);
+#endif
             if (++cur_g == KG) {
                 f8_epilogue<NMAT>(a, cur, lds, wave, lane, acc);
 #pragma unroll
@@ -423,9 +486,13 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
 #pragma unroll
                     for (int tb = 0; tb < 2; ++tb) acc[jb][tb] = f32x16{};
                 cur_g = 0;
-                if (++cur_k < cnt) cur = big_item(lds + RG::kTab, cur_k);
+                if (++cur_k < cnt) {
+                    cur = big_item(lds + RG::kTab, cur_k);
+                    live = cur.nr > wm * 64;
+                }
             }
         }
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
     }
 }

@@ -270,11 +270,12 @@ __device__ __forceinline__ void issue_batch(const ExpArgs& a, const Item& it, in
 }
 
 // One 128-K group's LDS operands of a wave: its 4 activation fragments
-// (the 16 token columns), its weight tile(s) and their 4 row scales.
+// (the 16 token columns), its weight tile(s), their 4 row scales and the
+// group sum of its token column.
 struct ExpOps {
     u32x4 x[4], w[2];
     u32x2 s[2];
-    float g;      // X of this lane's token column
+    float g;
 };
 
 // Issues the reads of group i of the batch in `slot` (no wait).
@@ -311,26 +312,55 @@ __device__ __forceinline__ void exp_wait_ops(ExpOps& o) {
                    "+v"(o.w[1]), "+v"(o.s[0]), "+v"(o.s[1]), "+v"(o.g));
 }
 
-// One 128-K group: acc[m] += scale * (sum_k (128 + c) x - 136 X), X the
-// group sum of the token column. The matrices' MFMA chains are interleaved.
-template <int NMAT>
-__device__ __forceinline__ void exp_compute_group(const ExpOps& o, const DqConst& dqc,
+// The PF groups of one batch.
+template <int PF>
+struct BatchOps {
+    ExpOps g[PF];
+};
+
+template <int NMAT, int PF, int D, int NW>
+__device__ __forceinline__ void exp_load_batch(const char* slot, int wave, int lane,
+                                               BatchOps<PF>& b) {
+#pragma unroll
+    for (int i = 0; i < PF; ++i) exp_load_ops<NMAT, PF, D, NW>(slot, i, wave, lane, b.g[i]);
+}
+
+template <int PF>
+__device__ __forceinline__ void exp_wait_batch(BatchOps<PF>& b) {
+    // One wait for all reads; the per-group asm statements only tie each
+    // group's registers to it.
+    asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+    for (int i = 0; i < PF; ++i) exp_wait_ops(b.g[i]);
+}
+
+// A batch's groups in one basic block, so the int4 decode of one group can be
+// scheduled under another group's MFMAs:
+// acc[m] += scale * (sum_k (128 + c) x - 136 X) per group, X the group sum of
+// the token column.
+template <int NMAT, int PF>
+__device__ __forceinline__ void exp_compute_batch(const BatchOps<PF>& b, const DqConst& dqc,
                                                   f32x4 (&acc)[NMAT]) {
-    const float off = -136.0f * o.g;
-    f32x4 p[NMAT];
+    f32x4 p[PF][NMAT];
 #pragma unroll
-    for (int d = 0; d < 4; ++d)
+    for (int i = 0; i < PF; ++i)
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m)
-            p[m] = mfma16x16x32(dq_w4(o.w[m][d], dqc), as_bf16x8(o.x[d]),
-                                d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : p[m]);
+        for (int d = 0; d < 4; ++d)
 #pragma unroll
-    for (int m = 0; m < NMAT; ++m) {
-        const u32x2 sv = o.s[m];
-        const float sc[4] = {bf16_to_f32(sv.x & 0xffffu), __uint_as_float(sv.x & 0xffff0000u),
-                             bf16_to_f32(sv.y & 0xffffu), __uint_as_float(sv.y & 0xffff0000u)};
+            for (int m = 0; m < NMAT; ++m)
+                p[i][m] = mfma16x16x32(dq_w4(b.g[i].w[m][d], dqc), as_bf16x8(b.g[i].x[d]),
+                                       d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : p[i][m]);
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[m][j] = __builtin_fmaf(sc[j], p[m][j] + off, acc[m][j]);
+    for (int i = 0; i < PF; ++i) {
+        const float off = -136.0f * b.g[i].g;
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) {
+            const u32x2 sv = b.g[i].s[m];
+            const float sc[4] = {bf16_to_f32(sv.x & 0xffffu), __uint_as_float(sv.x & 0xffff0000u),
+                                 bf16_to_f32(sv.y & 0xffffu), __uint_as_float(sv.y & 0xffff0000u)};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) acc[m][j] = __builtin_fmaf(sc[j], p[i][m][j] + off, acc[m][j]);
+        }
     }
 }
 
@@ -346,12 +376,15 @@ __global__ __launch_bounds__(NW * 64) void w4_expert_kernel(ExpArgs a) {
     const int KG = K / 128;
     const int nfb = (NMAT == 2 ? a.I : a.H) / 16;
     const int ngrp = nfb / NW;
-    const int nbatch = (KG + PF - 1) / PF;
+    const int nbatch = KG / PF;   // the launcher picks PF dividing KG
     const int total = *a.ntiles * ngrp;
     const int nwg = (int)gridDim.x;
     const int base = (int)blockIdx.x;
     const int nitems = base < total ? (total - base + nwg - 1) / nwg : 0;
     int* table = reinterpret_cast<int*>(ring + RG::kRed + NW * 64);
+    // Steps per unrolled block: a multiple of the ring depth (constant slot
+    // addresses) and of 2 (the two operand buffers alternate).
+    constexpr int kU = (D % 2 == 0) ? D : 2 * D;
 
     for (int k0 = 0; k0 < nitems; k0 += kTable) {
         const int cnt = min(kTable, nitems - k0);
@@ -359,13 +392,12 @@ __global__ __launch_bounds__(NW * 64) void w4_expert_kernel(ExpArgs a) {
         __syncthreads();
         const int nsteps = cnt * nbatch;
 
-        // Ring of D batch slots; batch b lives in slot b % D (the step loop is
-        // unrolled D times so every slot address is a constant). The prologue
-        // fills every slot. Per batch: compute its groups, each one's LDS
-        // reads issued under the previous group's MFMAs; before the last
-        // group, wait for batch b + 1 and barrier (every wave is then done
+        // Ring of D batch slots; batch b lives in slot b % D. The prologue
+        // fills every slot. Per batch b, with its operands already read into
+        // registers: wait for batch b + 1 and barrier (every wave is then done
         // reading slot b, and b + 1 is visible), refill slot b with batch
-        // b + D and issue the reads of b + 1's first group.
+        // b + D, issue the reads of b + 1's operands, then compute b under
+        // those reads.
         int iss_k = 0, iss_b = 0;
         Item iss = item_from_table<NMAT, PF, D, NW>(a, table, 0, wave, lane, nfb, KG);
         auto issue_next = [&](char* slot) {
@@ -382,8 +414,8 @@ __global__ __launch_bounds__(NW * 64) void w4_expert_kernel(ExpArgs a) {
         if (nsteps >= D) wait_vmcnt<RG::kDma * (D - 1)>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        ExpOps ops[2];
-        exp_load_ops<NMAT, PF, D, NW>(ring, 0, wave, lane, ops[0]);
+        BatchOps<PF> ops[2];
+        exp_load_batch<NMAT, PF, D, NW>(ring, wave, lane, ops[0]);
 
         int cur_k = 0, cur_b = 0;
         Item cur = item_from_table<NMAT, PF, D, NW>(a, table, 0, wave, lane, nfb, KG);
@@ -391,37 +423,25 @@ __global__ __launch_bounds__(NW * 64) void w4_expert_kernel(ExpArgs a) {
 #pragma unroll
         for (int m = 0; m < NMAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-        for (int step0 = 0; step0 < nsteps; step0 += D) {
+        for (int step0 = 0; step0 < nsteps; step0 += kU) {
 #pragma unroll
-        for (int u = 0; u < D; ++u) {
+        for (int u = 0; u < kU; ++u) {
             const int step = step0 + u;
             if (step >= nsteps) break;
-            char* slot = ring + u * RG::kSlot;
-#pragma unroll
-            for (int i = 0; i < PF; ++i) {
-                ExpOps& o = ops[i & 1];
-                exp_wait_ops(o);
-                if (i + 1 < PF) {
-                    exp_load_ops<NMAT, PF, D, NW>(slot, i + 1, wave, lane, ops[(i + 1) & 1]);
-                } else {
-                    // Batch step + 1 has landed once at most the batches issued
-                    // after it (up to step + D - 1) are pending.
-                    if (step + D - 1 < nsteps) wait_vmcnt<RG::kDma * (D - 2)>();
-                    else wait_vmcnt<0>();
-                    __builtin_amdgcn_s_barrier();
-                    if (step + D < nsteps) issue_next(slot);
-                    if (step + 1 < nsteps)
-                        exp_load_ops<NMAT, PF, D, NW>(ring + ((u + 1) % D) * RG::kSlot, 0, wave,
-                                                      lane, ops[(i + 1) & 1]);
-                }
+            BatchOps<PF>& now = ops[u & 1];
+            exp_wait_batch<PF>(now);
+            // Batch step + 1 has landed once at most the batches issued after
+            // it (up to step + D - 1) are pending.
+            if (step + D - 1 < nsteps) wait_vmcnt<RG::kDma * (D - 2)>();
+            else wait_vmcnt<0>();
+            __builtin_amdgcn_s_barrier();
+            if (step + D < nsteps) issue_next(ring + (u % D) * RG::kSlot);
+            if (step + 1 < nsteps)
+                exp_load_batch<NMAT, PF, D, NW>(ring + ((u + 1) % D) * RG::kSlot, wave, lane,
+                                                ops[(u + 1) & 1]);
 #ifndef GLMMOE_EXP_NOCOMPUTE
-                // The clamped group past an odd K-group count adds nothing.
-                if (PF == 1 || cur_b * PF + i < KG) exp_compute_group<NMAT>(o, dqc, acc);
+            exp_compute_batch<NMAT, PF>(now, dqc, acc);
 #endif
-            }
-            // With an odd batch size the next batch's first group was read
-            // into buffer 1; batches always start from buffer 0.
-            if (PF & 1) ops[0] = ops[1];
             if (++cur_b == nbatch) {
                 const bool valid = r < cur.nr;
                 const size_t row = (size_t)cur.r0 + r;
@@ -549,7 +569,9 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, co
     a.swq[1] = reinterpret_cast<const uint4*>(P.sh_up_q); a.sws[1] = P.sh_up_s;
     a.src = x; a.gsum = xsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.rows_tok = rows_tok; a.h = h; a.hsum = hsum; a.H = H; a.I = I; a.E = E;
-    return launch_expert<2, kPFGU, kRingGU, kNWGU>(a, (long)max_tiles * (I / 16 / kNWGU), s);
+    const long work = (long)max_tiles * (I / 16 / kNWGU);
+    if ((H / 128) % kPFGU == 0) return launch_expert<2, kPFGU, kRingGU, kNWGU>(a, work, s);
+    return launch_expert<2, 1, 6, kNWGU>(a, work, s);   // odd K-group count
 }
 
 int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
@@ -561,7 +583,9 @@ int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const
     a.wq[1] = a.wq[0]; a.ws[1] = a.ws[0]; a.swq[1] = a.swq[0]; a.sws[1] = a.sws[0];
     a.src = h; a.gsum = hsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.dpart = dpart; a.H = H; a.I = I; a.E = E;
-    return launch_expert<1, kPFDown, kRingDown, kNWDown>(a, (long)max_tiles * (H / 16 / kNWDown), s);
+    const long work = (long)max_tiles * (H / 16 / kNWDown);
+    if ((I / 128) % kPFDown == 0) return launch_expert<1, kPFDown, kRingDown, kNWDown>(a, work, s);
+    return launch_expert<1, 1, 6, kNWDown>(a, work, s);   // odd K-group count
 }
 
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
