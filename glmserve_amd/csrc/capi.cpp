@@ -68,7 +68,7 @@ size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v)
     };
     glmmoe_layer_ws w{};
     w.logits = reinterpret_cast<float*>(take((size_t)n * E * 4));
-    w.rpart = reinterpret_cast<float*>(take(router_logits_scratch_bytes(n, H, E)));
+    w.rpart = reinterpret_cast<float*>(take(router_select_scratch_bytes(n, H, E)));
     w.xsum = reinterpret_cast<float*>(take((size_t)n * (H / 128) * 4));
     w.topk_ids = reinterpret_cast<int*>(take(nk * 4));
     w.topk_w = reinterpret_cast<float*>(take(nk * 4));
@@ -105,7 +105,7 @@ size_t carve8(const glmmoe_fp8_layer* L, int n, char* base, glmmoe_fp8_ws* v) {
     };
     glmmoe_fp8_ws w{};
     w.logits = reinterpret_cast<float*>(take((size_t)n * E * 4));
-    w.rpart = reinterpret_cast<float*>(take(router_logits_scratch_bytes(n, H, E)));
+    w.rpart = reinterpret_cast<float*>(take(router_select_scratch_bytes(n, H, E)));
     w.xq = reinterpret_cast<uint8_t*>(take((size_t)n * H));
     w.xscale = reinterpret_cast<float*>(take((size_t)n * (H / 128) * 4));
     w.topk_ids = reinterpret_cast<int*>(take(nk * 4));
@@ -295,12 +295,10 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
     // The router pass also writes the activation group sums the expert
     // kernels use to remove the int4 decode offset.
-    rc = launch_router_logits(x, L->router_w, n, H, E, v.logits, v.xsum, v.rpart, s);
+    rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
+                              L->routed_scale, v.logits, v.xsum, v.rpart, v.topk_ids, v.topk_w, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_ROUTER_TOPK, s);
-    rc = launch_router_topk(v.logits, L->e_bias, n, E, k, L->norm_topk, L->routed_scale,
-                            v.topk_ids, v.topk_w, s);
-    if (rc) return rc;
     return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s);
 }
 
@@ -363,12 +361,10 @@ int glmmoe_moe_layer_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, fl
     const int H = L->hidden, E = L->n_experts, k = L->topk;
     begin_call();
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
-    rc = launch_router_logits(x, L->router_w, n, H, E, v.logits, nullptr, v.rpart, s);
+    rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
+                              L->routed_scale, v.logits, nullptr, v.rpart, v.topk_ids, v.topk_w, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_ROUTER_TOPK, s);
-    rc = launch_router_topk(v.logits, L->e_bias, n, E, k, L->norm_topk, L->routed_scale,
-                            v.topk_ids, v.topk_w, s);
-    if (rc) return rc;
     return run_experts8(L, x, n, v.topk_ids, v.topk_w, out, v, s);
 }
 

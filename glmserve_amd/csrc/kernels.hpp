@@ -37,6 +37,13 @@ size_t router_logits_scratch_bytes(int n, int H, int E);
 int launch_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
                          float* logits, float* xsum, float* scratch, hipStream_t s);
 int launch_xsum(const uint16_t* x, int n, int H, float* xsum, hipStream_t s);
+// Router logits + top-k for the layer (logits hold only what the selection
+// reads; ids and weights are those of the fixed-order logits). Scratch of
+// router_select_scratch_bytes.
+size_t router_select_scratch_bytes(int n, int H, int E);
+int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_bias, int n, int H,
+                         int E, int topk, int norm_topk, float routed_scale, float* logits,
+                         float* xsum, float* scratch, int* ids, float* w, hipStream_t s);
 int launch_router_topk(const float* logits, const float* e_bias, int n, int E, int topk,
                        int norm_topk, float routed_scale, int* ids, float* w, hipStream_t s);
 int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,

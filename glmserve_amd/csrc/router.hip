@@ -363,6 +363,276 @@ __global__ __launch_bounds__(256) void router_topk_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Large batches inside the layer: routing without the fixed-order GEMM over
+// every (token, expert) pair. The ids and weights are still exactly those of
+// the fixed-order logits:
+//   1. router_mfma_kernel: approximate logits L~ = x . w on bf16 MFMA, and
+//      S = |x| . |w| (the same MFMA on sign-cleared operands). bf16 products
+//      are exact in fp32, so both the fixed-order sum L and L~ are sums of the
+//      same exact terms and |L~ - L| is below a small multiple of u * K * S
+//      (u = 2^-24) for any fp32 summation order; eps = 2^-11 * S covers it
+//      with a wide margin (2^-11 / (2 * 2^-24 * 6144) = 0.67 x the worst case
+//      of two K-term sequential sums, and about 14 x the worst case of this
+//      build's orders).
+//   2. router_refine_kernel, one wave per token: lower/upper bounds of each
+//      expert's choose value from L~ -+ eps (choose = sigmoid(logit) + bias is
+//      monotone in the logit; 1e-6 absorbs sigmoid rounding); T = the k-th
+//      largest lower bound. An expert whose upper bound is below T is below
+//      at least k others for sure and cannot be selected. Every other expert
+//      (the candidates, k plus the near ties) gets its exact fixed-order
+//      logit; the rest get -inf (choose = bias < T). The wave also writes the
+//      activation group sums xsum.
+//   3. router_topk_kernel on those logits: the selection and weights only
+//      ever read candidates' logits, so they equal the oracle's bit for bit.
+// ---------------------------------------------------------------------------
+constexpr int kMfmaTok = 64;   // tokens per workgroup
+constexpr int kMfmaExp = 64;   // experts per workgroup
+constexpr int kMfmaK = 64;     // K per LDS stage
+constexpr int kMfmaD = 4;      // stages in flight + 1
+
+// Row r of a [64 x 64] bf16 stage tile: 128 B at 128 r; 16-byte chunk c at
+// slot c ^ ((r >> 1) & 7), so the 16 rows of an MFMA fragment pass read
+// distinct bank groups.
+__device__ __forceinline__ uint32_t mfma_tile_off(int r, int c) {
+    return (uint32_t)(r * 128 + ((c ^ ((r >> 1) & 7)) << 4));
+}
+
+// Stages (64 K of 64 token rows and 64 expert rows, 16 KiB) stream into a
+// kMfmaD-slot LDS ring by LDS-DMA: 4 DMAs per wave per stage, each 8 whole
+// 128-B rows (lane l: row l / 8, slot l % 8 holding chunk (l % 8) ^ swz(row)).
+__global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __restrict__ x,
+                                                          const uint16_t* __restrict__ wr, int n,
+                                                          int H, int E, float* __restrict__ lt,
+                                                          float* __restrict__ sb) {
+    extern __shared__ __align__(16) char tl[];   // [kMfmaD][x | w][64 rows x 128 B]
+    constexpr int kStage = 2 * kMfmaTok * 128;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int e0 = blockIdx.x * kMfmaExp, t0 = blockIdx.y * kMfmaTok;
+    const int tb = wave & 1, eb = wave >> 1;
+    // DMA j (0..3) of this wave: operand j / 2 (x, w), rows 8 (2 wave + j % 2) + lane / 8.
+    const uint16_t* src[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = 8 * (2 * wave + (j & 1)) + (lane >> 3);
+        const int c = (lane & 7) ^ ((row >> 1) & 7);
+        const uint16_t* rp = (j >> 1) == 0 ? x + (size_t)min(t0 + row, n - 1) * H
+                                           : wr + (size_t)min(e0 + row, E - 1) * H;
+        src[j] = rp + c * 8;
+    }
+    auto issue = [&](int ks) {
+        char* st = tl + (ks % kMfmaD) * kStage;
+#pragma unroll
+        for (int j = 0; j < 4; ++j)
+            dma16(src[j] + (size_t)ks * kMfmaK,
+                  st + (j >> 1) * (kMfmaTok * 128) + (2 * wave + (j & 1)) * 1024);
+    };
+    f32x16 accl = {}, accs = {};
+    const int ar = tb * 32 + (lane & 31), br = eb * 32 + (lane & 31), hh = lane >> 5;
+    const int nk = H / kMfmaK;
+    for (int j = 0; j < kMfmaD - 1; ++j)
+        if (j < nk) issue(j);
+    for (int ks = 0; ks < nk; ++ks) {
+        if (ks + kMfmaD - 2 < nk) wait_vmcnt<4 * (kMfmaD - 2)>();
+        else wait_vmcnt<0>();
+        __builtin_amdgcn_s_barrier();   // stage ks visible; stage ks - 1 free
+        if (ks + kMfmaD - 1 < nk) issue(ks + kMfmaD - 1);
+        const uint32_t xa = lds_addr(tl + (ks % kMfmaD) * kStage);
+        const uint32_t wa = xa + kMfmaTok * 128;
+        u32x4 av[4], bv[4];
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            const int c = 2 * s4 + hh;
+            asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %3"
+                         : "=&v"(av[s4]), "=&v"(bv[s4])
+                         : "v"(xa + mfma_tile_off(ar, c)), "v"(wa + mfma_tile_off(br, c)));
+        }
+        asm volatile("s_waitcnt lgkmcnt(0)"
+                     : "+v"(av[0]), "+v"(av[1]), "+v"(av[2]), "+v"(av[3]), "+v"(bv[0]),
+                       "+v"(bv[1]), "+v"(bv[2]), "+v"(bv[3]));
+        const u32x4 m = {0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu, 0x7fff7fffu};
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+            accl = mfma32x32x16(as_bf16x8(av[s4]), as_bf16x8(bv[s4]), accl);
+            accs = mfma32x32x16(as_bf16x8(av[s4] & m), as_bf16x8(bv[s4] & m), accs);
+        }
+    }
+    // D: lane -> expert column br, rows (tokens) 8 (i / 4) + 4 hh + i % 4 of the block.
+    const int e = e0 + br;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int t = t0 + tb * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
+        if (t < n && e < E) {
+            lt[(size_t)t * E + e] = accl[i];
+            sb[(size_t)t * E + e] = accs[i];
+        }
+    }
+}
+
+// Float -> 64-bit selection key helpers of the top-k kernel above.
+__device__ __forceinline__ void kmax_wave(uint32_t& h, uint32_t& l) {
+    kmax_dpp<0x121>(h, l);
+    kmax_dpp<0x122>(h, l);
+    kmax_dpp<0x124>(h, l);
+    kmax_dpp<0x128>(h, l);
+    uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)h, 0);
+    uint32_t bl = (uint32_t)__builtin_amdgcn_readlane((int)l, 0);
+#pragma unroll
+    for (int r = 1; r < 4; ++r)
+        kmax(bh, bl, (uint32_t)__builtin_amdgcn_readlane((int)h, 16 * r),
+             (uint32_t)__builtin_amdgcn_readlane((int)l, 16 * r));
+    h = bh;
+    l = bl;
+}
+
+__device__ __forceinline__ float code_to_float(uint32_t c) {
+    return __uint_as_float((c & 0x80000000u) ? (c & 0x7fffffffu) : ~c);
+}
+
+constexpr int kRefineWaves = 2;   // tokens (waves) per workgroup: small LDS, high occupancy
+
+__global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
+    const float* __restrict__ e_bias, const float* __restrict__ sb, int n, int H, int E, int topk,
+    float* __restrict__ logits, float* __restrict__ xsum) {
+    const int lane = threadIdx.x & 63;
+    const int t = blockIdx.x * kRefineWaves + (threadIdx.x >> 6);
+    if (t >= n) return;   // whole wave
+    const int nchunks = H / kRouterKC;
+    // This lane's 128-K chunk of x (lanes past the chunk count hold zeros),
+    // kept in LDS for the exact sums (registers go to the weight buffers).
+    __shared__ uint4 xl[kRefineWaves][kRouterKC / 8][64];
+    uint4 (*xw)[64] = xl[threadIdx.x >> 6];
+    {
+        const uint4* xp = reinterpret_cast<const uint4*>(x + (size_t)t * H + lane * kRouterKC);
+#pragma unroll
+        for (int j = 0; j < kRouterKC / 8; ++j) xw[j][lane] = lane < nchunks ? xp[j] : make_uint4(0, 0, 0, 0);
+    }
+    if (xsum && lane < nchunks) {
+        float s = 0.0f;
+#pragma unroll
+        for (int j = 0; j < kRouterKC / 8; ++j) {
+            const uint4 xv = xw[j][lane];
+            const uint32_t d[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+            for (int q = 0; q < 4; ++q) { s += bf16_to_f32(d[q] & 0xffffu); s += bf16_to_f32(d[q] >> 16); }
+        }
+        xsum[(size_t)t * nchunks + lane] = s;
+    }
+    float* lrow = logits + (size_t)t * E;
+    const float* srow = sb + (size_t)t * E;
+    uint32_t lo[kMaxPerLane];   // order codes of the lower bounds (0 = none / taken)
+    float up[kMaxPerLane];
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j) {
+        const int e = lane + 64 * j;
+        lo[j] = 0u;
+        up[j] = -INFINITY;
+        if (e < E) {
+            const float l = lrow[e];
+            const float eps = srow[e] * 0x1p-11f;
+            const float b = e_bias ? e_bias[e] : 0.0f;
+            if (l != l || eps != eps) {
+                up[j] = INFINITY;    // always a candidate; never sets the threshold
+                lo[j] = 1u;
+            } else {
+                lo[j] = order_code(sigmoid_fixed(l - eps) + b - 1e-6f);
+                up[j] = sigmoid_fixed(l + eps) + b + 1e-6f;
+            }
+        }
+    }
+    // T = k-th largest lower bound.
+    uint32_t tcode = 0u;
+    for (int k = 0; k < topk; ++k) {
+        uint32_t h = 0u, l = 0u;
+#pragma unroll
+        for (int j = 0; j < kMaxPerLane; ++j) kmax(h, l, lo[j], lo[j] ? ~(uint32_t)(lane + 64 * j) : 0u);
+        kmax_wave(h, l);
+        tcode = h;
+        const int e = (int)~l;
+#pragma unroll
+        for (int j = 0; j < kMaxPerLane; ++j)
+            if (lane + 64 * j == e) lo[j] = 0u;
+    }
+    const float T = tcode > 1u ? code_to_float(tcode) : -INFINITY;
+    // Candidates in ascending expert order into this wave's LDS list; the rest
+    // get -inf.
+    __shared__ int cl[kRefineWaves][64 * kMaxPerLane];
+    int* list = cl[threadIdx.x >> 6];
+    int ncand = 0;
+#pragma unroll
+    for (int j = 0; j < kMaxPerLane; ++j) {
+        const int e = lane + 64 * j;
+        const bool cand = e < E && up[j] >= T;
+        if (e < E && !cand) lrow[e] = -INFINITY;
+        const uint64_t mask = __ballot(cand);
+        const int before = __builtin_popcountll(mask & ((1ull << lane) - 1));
+        if (cand) list[ncand + before] = e;
+        ncand += __builtin_popcountll(mask);
+    }
+    __builtin_amdgcn_s_waitcnt(0xc07f);   // lgkmcnt(0): list writes done
+    __builtin_amdgcn_wave_barrier();
+    // Exact fixed-order logits of the candidates: lane c sums chunk c in
+    // ascending K, then the chunk sums are added in ascending c. Occupancy
+    // (few registers per wave) hides the weight loads.
+    for (int i = 0; i < ncand; ++i) {
+        const int ec = list[i];
+        const uint4* wp = reinterpret_cast<const uint4*>(wr + (size_t)ec * H + lane * kRouterKC);
+        float part = 0.0f;
+        if (lane < nchunks) {
+            uint4 wv[kRouterKC / 8];   // all loads in flight together
+#pragma unroll
+            for (int q = 0; q < kRouterKC / 8; ++q) wv[q] = wp[q];
+#pragma unroll
+            for (int q = 0; q < kRouterKC / 8; ++q) {
+                const uint4 w4 = wv[q];
+                const uint4 xv = xw[q][lane];
+                const uint32_t wd[4] = {w4.x, w4.y, w4.z, w4.w};
+                const uint32_t xd[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+                for (int d = 0; d < 4; ++d) {
+                    part = __builtin_fmaf(bf16_to_f32(xd[d] & 0xffffu), bf16_to_f32(wd[d] & 0xffffu), part);
+                    part = __builtin_fmaf(__uint_as_float(xd[d] & 0xffff0000u),
+                                          __uint_as_float(wd[d] & 0xffff0000u), part);
+                }
+            }
+        }
+        float total = 0.0f;
+        for (int c = 0; c < nchunks; ++c)
+            total = total + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), c));
+        if (lane == 0) lrow[ec] = total;
+    }
+}
+
+size_t router_select_scratch_bytes(int n, int H, int E) {
+    const size_t a = router_logits_scratch_bytes(n, H, E);
+    const size_t b = (size_t)n * E * 4;
+    return a > b ? a : b;
+}
+
+int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_bias, int n, int H,
+                         int E, int topk, int norm_topk, float routed_scale, float* logits,
+                         float* xsum, float* scratch, int* ids, float* w, hipStream_t s) {
+    const int nchunks = H / kRouterKC;
+    if (n >= kTiledMinTokens && H % kMfmaK == 0 && H % kRouterKC == 0 && nchunks <= 64 &&
+        E <= 64 * kMaxPerLane) {
+        if (!scratch) return -3;
+        dim3 grid((unsigned)((E + kMfmaExp - 1) / kMfmaExp), (unsigned)((n + kMfmaTok - 1) / kMfmaTok));
+        hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(256), kMfmaD * 2 * kMfmaTok * 128, s, x,
+                           wr, n, H, E, logits, scratch);
+        if (hipGetLastError() != hipSuccess) return -4;
+        hipLaunchKernelGGL(router_refine_kernel, dim3((unsigned)((n + kRefineWaves - 1) / kRefineWaves)),
+                           dim3(kRefineWaves * 64), 0, s, x,
+                           wr, e_bias, scratch, n, H, E, topk, logits, xsum);
+        if (hipGetLastError() != hipSuccess) return -4;
+    } else {
+        const int rc = launch_router_logits(x, wr, n, H, E, logits, xsum, scratch, s);
+        if (rc) return rc;
+    }
+    return launch_router_topk(logits, e_bias, n, E, topk, norm_topk, routed_scale, ids, w, s);
+}
+
 size_t router_logits_scratch_bytes(int n, int H, int E) {
     if (n >= kTiledMinTokens && H % kRouterKC == 0) return 0;
     return (size_t)n * ((H + kRouterKC - 1) / kRouterKC) * E * 4;

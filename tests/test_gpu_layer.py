@@ -44,9 +44,16 @@ def _check_routing(oracle, L, x, logits, ids, w, offs, st, sr):
     xb = x.view(torch.int16).cpu().numpy().view(np.uint16)
     wr = L.router_w.view(torch.int16).cpu().numpy().view(np.uint16)
     ref_logits = oracle.router_logits_bf16(xb, wr)
-    assert np.array_equal(logits.view(np.uint32), ref_logits.view(np.uint32)), "router logits"
+    # From 256 tokens the layer keeps exact logits only for the experts that
+    # can reach the top-k and -inf for the rest; below, every logit is exact.
+    live = np.isfinite(logits)
+    if logits.shape[0] < 256:
+        assert live.all(), "router logits"
+    assert np.array_equal(logits[live].view(np.uint32), ref_logits[live].view(np.uint32)), "router logits"
+    assert np.all(logits[~live] == -np.inf), "router logits"
     rid, rw = oracle.router_topk(ref_logits, L.e_bias.cpu().numpy(), L.k, L.norm_topk,
                                  L.routed_scale)
+    assert live[np.arange(len(rid))[:, None], rid].all(), "selected experts carry exact logits"
     assert np.array_equal(ids, rid), "topk ids"
     assert np.array_equal(w.view(np.uint32), rw.view(np.uint32)), "topk weights"
     roff, rst, rsr = oracle.dispatch(rid, L.E)

@@ -114,3 +114,36 @@ def test_router_logits_bit_exact(oracle):
             xf = (x.astype(np.uint32) << 16).view(np.float32).reshape(n, H // 128, 128)
             rx = np.cumsum(xf, axis=2, dtype=np.float32)[:, :, -1]
             assert np.array_equal(xs.cpu().numpy().view(np.uint32), rx.view(np.uint32)), (n, H)
+
+
+@pytest.mark.parametrize("n", [256, 1000, 4096])
+def test_layer_routing_bit_exact_large_batches(oracle, n):
+    """From 256 tokens the layer routes with MFMA logits plus an exact
+    fixed-order recompute of every expert that can reach the top-k; ids,
+    weights and the activation group sums must still equal the oracle's bit
+    for bit. Duplicate router rows force exact ties between experts."""
+    from moe_cases import SynthLayer
+    from glmserve_amd.ops import ws_tensor
+    H, E, k, I = 1024, 64, 8, 128
+    L = SynthLayer(H, E, k, I, seed=11)
+    L.router_w[5] = L.router_w[3]
+    L.router_w[40] = L.router_w[3]
+    L.router_w[63] = L.router_w[17]
+    x = L.x(n, seed=n)
+    ws = L.layer.alloc_workspace(n)
+    out = torch.empty(n, H, dtype=torch.float32, device="cuda")
+    L.layer.forward(x, out, ws)
+    torch.cuda.synchronize()
+    v = L.layer.workspace_view(n, ws)
+    ids = ws_tensor(None, v.topk_ids, ws, torch.int32, n * k).cpu().numpy().reshape(n, k)
+    w = ws_tensor(None, v.topk_w, ws, torch.float32, n * k).cpu().numpy().reshape(n, k)
+    xs = ws_tensor(None, v.xsum, ws, torch.float32, n * (H // 128)).cpu().numpy()
+    xb = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    wb = L.router_w.view(torch.int16).cpu().numpy().view(np.uint16)
+    logits = oracle.router_logits_bf16(xb, wb)
+    rid, rw = oracle.router_topk(logits, L.e_bias.cpu().numpy(), k, True, 2.5)
+    assert np.array_equal(ids, rid)
+    assert np.array_equal(w.view(np.uint32), rw.view(np.uint32))
+    xf = (xb.astype(np.uint32) << 16).view(np.float32).reshape(n, H // 128, 128)
+    rx = np.cumsum(xf, axis=2, dtype=np.float32)[:, :, -1].reshape(-1)
+    assert np.array_equal(xs.view(np.uint32), rx.view(np.uint32))
