@@ -196,18 +196,69 @@ def main():
     L = SynthLayer(H, E, K, I, seed=1)
     torch.cuda.synchronize()
 
-    def measure(n, steps, warmup):
-        ms, U, bufs = time_layer(L, n, steps, warmup, seed=100 + n, torch=torch)
-        st = stage_times(L, n, bufs, max(5, min(steps, 20)), torch)
+    def summarize(n, ms, U, st):
         bytes_alg = (U + 1) * EXPERT_BYTES + ROUTER_BYTES + n * H * 2 + n * H * 4
         flops = n * FLOP_PER_TOKEN
-        gu_ms = st["gate_up"]
+        gu_ms, dn_ms = st.get("gate_up"), st.get("down")
         gu_bytes = (U + 1) * GATE_UP_BYTES + n * H * 2
+        rows = n * (K + 1)
         return {"n": n, "ms": ms, "tokens_per_s": n / (ms * 1e-3), "distinct_experts": U,
                 "alg_bytes": bytes_alg, "hbm_frac_layer": bytes_alg / (ms * 1e-3) / HBM_PEAK,
                 "mfma_frac_layer": flops / (ms * 1e-3) / BF16_PEAK,
                 "stage_ms": st, "gate_up_bytes": gu_bytes,
-                "gate_up_GBps": gu_bytes / (gu_ms * 1e-3) / 1e9 if gu_ms else None}
+                "gate_up_GBps": gu_bytes / (gu_ms * 1e-3) / 1e9 if gu_ms else None,
+                "gate_up_TFLOPs": rows * 2 * H * 2 * I / (gu_ms * 1e-3) / 1e12 if gu_ms else None,
+                "down_TFLOPs": rows * 2 * I * H / (dn_ms * 1e-3) / 1e12 if dn_ms else None}
+
+    def measure(n, steps, warmup, layer=L):
+        ms, U, bufs = time_layer(layer, n, steps, warmup, seed=100 + n, torch=torch)
+        st = stage_times(layer, n, bufs, max(5, min(steps, 20)), torch)
+        return summarize(n, ms, U, st)
+
+    def measure_uniform(n, steps, warmup):
+        """the layer's routing runs on the real router logits (and
+        is timed), and the expert stage runs on uniform-random routing (k
+        distinct uniform experts per token), as the config specifies."""
+        x = L.x(n, seed=100 + n)
+        ws = L.layer.alloc_workspace(n)
+        out = torch.empty(n, H, dtype=torch.float32, device="cuda")
+        g = torch.Generator(device="cuda")
+        g.manual_seed(7 + n)
+        uid = torch.rand(n, E, generator=g, device="cuda").topk(K, dim=1).indices.to(torch.int32).contiguous()
+        uw = torch.full((n, K), 2.5 / K, dtype=torch.float32, device="cuda")
+        rid = torch.empty(n, K, dtype=torch.int32, device="cuda")
+        rw = torch.empty(n, K, dtype=torch.float32, device="cuda")
+
+        def step():
+            L.layer.route(x, rid, rw, ws)
+            L.layer.expert_ffn(x, uid, uw, out, ws)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize()
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            step()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        U = int(torch.unique(uid).numel())
+        import ctypes
+        from glmserve_amd import lib
+        from glmserve_amd._lib import STAGES
+        lib().glmmoe_profile_enable(1)
+        for _ in range(max(3, min(steps, 10))):
+            L.layer.expert_ffn(x, uid, uw, out, ws)
+        pm = (ctypes.c_float * 6)()
+        pc = (ctypes.c_int * 6)()
+        lib().glmmoe_profile_read(pm, pc)
+        lib().glmmoe_profile_enable(0)
+        st = {s: (pm[i] / pc[i] if pc[i] else None) for i, s in enumerate(STAGES)}
+        r = summarize(n, ms, U, st)
+        r["routing"] = "uniform-random expert ids (k distinct per token); router timed on the real logits"
+        return r
 
     log(f"bench: headline B={args.head_batch}")
     head = measure(args.head_batch, args.steps, args.warmup)
@@ -216,15 +267,23 @@ def main():
         for n in (1, 8, 32):
             log(f"bench: sweep B={n}")
             sweep[f"decode_B{n}"] = measure(n, args.steps, args.warmup)
-        log("bench: sweep prefill 4096")
-        sweep["prefill_4096"] = measure(4096, max(3, args.steps // 10), 2)
+        log("bench: sweep prefill 4096 (configs[2], uniform routing)")
+        sweep["prefill_4096"] = measure_uniform(4096, max(3, args.steps // 10), 2)
+        log("bench: sweep prefill 4096 (router-chosen routing)")
+        sweep["prefill_4096_router_routing"] = measure(4096, max(3, args.steps // 10), 2)
     sweep[f"decode_B{args.head_batch}"] = head
+    if not args.no_sweep:
+        log("bench: sweep spec-verify 520 (configs[3], Zipf s=1.1 skew)")
+        LZ = SynthLayer(H, E, K, I, seed=2, zipf_s=1.1)
+        sweep["verify_520_zipf"] = measure(520, max(5, args.steps // 5), 3, layer=LZ)
+        del LZ
+        torch.cuda.empty_cache()
     if not args.no_sweep and not args.no_fp8:
         log("bench: sweep FP8 prefill 8192")
         sweep["fp8_prefill_8192"] = measure_fp8(8192, max(3, args.steps // 10), 2)
 
     gu_ms = head["stage_ms"]["gate_up"]
-    roof = {"bound": "hbm", "kernel": f"w4_expert_kernel<2,2,3> grouped gate/up (decode B={args.head_batch})",
+    roof = {"bound": "hbm", "kernel": f"w4_expert_kernel<2,2,3,8> grouped gate/up (decode B={args.head_batch})",
             "achieved": head["gate_up_GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": head["gate_up_GBps"] / (HBM_PEAK / 1e9),
             "traffic": profiled_traffic() if args.head_batch == 64 else None,

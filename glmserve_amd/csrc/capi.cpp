@@ -302,6 +302,20 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s);
 }
 
+int glmmoe_moe_route_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n,
+                           int* topk_ids, float* topk_w, void* workspace,
+                           size_t workspace_bytes, void* stream) {
+    int rc = check_layer(L, n);
+    if (rc) return rc;
+    if (!x || !topk_ids || !topk_w || !workspace || !L->router_w) return GLMMOE_ERR_ARG;
+    glmmoe_layer_ws v;
+    if (carve(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)
+        return GLMMOE_ERR_WORKSPACE;
+    return launch_router_select(x, L->router_w, L->e_bias, n, L->hidden, L->n_experts, L->topk,
+                                L->norm_topk, L->routed_scale, v.logits, v.xsum, v.rpart,
+                                topk_ids, topk_w, S(stream));
+}
+
 int glmmoe_expert_ffn_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n,
                             const int* topk_ids, const float* topk_w, float* out,
                             void* workspace, size_t workspace_bytes, void* stream) {

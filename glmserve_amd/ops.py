@@ -141,6 +141,17 @@ class _MoELayer:
         check(self._call("layer", self._ref(), _p(x), n, _p(out), _p(ws), ws.numel(),
                          _s(stream)), self._fn["layer"])
 
+    def route(self, x, topk_ids, topk_w, ws, stream=None):
+        """The layer's routing alone (router logits + top-k) into topk_ids / topk_w."""
+        if self._fn["layer"] != "glmmoe_moe_layer_w4a16":
+            raise GlmMoeError("route: W4A16 layers only")
+        n = x.shape[0]
+        _need(x, torch.bfloat16, n * self.hidden, "x")
+        _need(topk_ids, torch.int32, n * self.topk, "topk_ids")
+        _need(topk_w, torch.float32, n * self.topk, "topk_w")
+        check(lib().glmmoe_moe_route_w4a16(self._ref(), _p(x), n, _p(topk_ids), _p(topk_w), _p(ws),
+                                           ws.numel(), _s(stream)), "glmmoe_moe_route_w4a16")
+
     def expert_ffn(self, x, topk_ids, topk_w, out, ws, stream=None):
         n = x.shape[0]
         _need(x, torch.bfloat16, n * self.hidden, "x")

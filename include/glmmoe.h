@@ -149,6 +149,15 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
                            float* out, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* The layer's routing alone: router logits and sigmoid top-k, as the layer
+ * runs them (replaces gemm_linear on the router and moe_router,
+ * src/model_gpu.cpp:1448-1450). topk_ids/topk_w: [n, topk], bit-identical to
+ * moe_router on the fixed-order logits of glmmoe_router_logits. The workspace
+ * is the layer's (its logits and xsum regions are written). */
+int glmmoe_moe_route_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n,
+                           int* topk_ids, float* topk_w, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
 /* The routed + shared expert stage alone, for callers that route elsewhere.
  * Replaces moe_expert_ffn_w4a16 (cuda/kernels.cuh:263-268) plus the shared
  * expert and add_inplace of src/model_gpu.cpp:1486-1494. topk_ids/topk_w are
