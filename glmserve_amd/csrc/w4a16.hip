@@ -14,6 +14,7 @@
 // once and applying each to every 16-token block of the tile, so each expert
 // weight byte is read from HBM once per tile. The MFMA sees weights as the A
 // operand (16 output features) and tokens as the B operand (16 tokens).
+#include <utility>
 #include "common.hpp"
 #include "kernels.hpp"
 
@@ -492,6 +493,389 @@ __global__ __launch_bounds__(NW * 64) void w4_expert_kernel(ExpArgs a) {
 }
 
 // ---------------------------------------------------------------------------
+// Streaming decode kernel (K-group count a multiple of 16): the same work
+// decomposition and arithmetic as w4_expert_kernel, with the two streams
+// decoupled.
+//   * Weights and scales are private to a wave: each wave loads its own
+//     tiles straight into registers (global_load_dwordx4 of the 1 KiB tile:
+//     lane l gets bytes 16 l .. 16 l + 15, exactly its MFMA A operand),
+//     SP groups ahead, with no LDS staging and no barrier.
+//   * The tile's activation rows and group sums, shared by the 8 waves, come
+//     through LDS in batches of 16 K-groups (64 KiB + 1 KiB) by LDS-DMA into
+//     two buffers; one barrier per batch. Batch b + 1 is issued half-way
+//     through batch b.
+// All loads complete in issue order, so every wait is an immediate vmcnt:
+// the number of loads issued after the one waited for (counted statically in
+// the 16-group unrolled batch body).
+// ---------------------------------------------------------------------------
+constexpr int kSGB = 16;
+
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+// f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order.
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}     // K-groups per activation batch
+constexpr int kSActDma = 9;  // activation + group-sum DMAs per wave per batch
+#ifndef GLMMOE_SP_GU
+#define GLMMOE_SP_GU 4
+#endif
+#ifndef GLMMOE_SP_DOWN
+#define GLMMOE_SP_DOWN 8
+#endif
+constexpr int kSPGU = GLMMOE_SP_GU;
+constexpr int kSPDown = GLMMOE_SP_DOWN;
+
+template <int NMAT>
+struct SLay {
+    static constexpr int kRowB = kSGB * 256;                 // one row's 16 groups
+    static constexpr int kXBytes = kTileRows * kRowB;        // 64 KiB
+    static constexpr int kGOff = kXBytes;                    // X [16 groups][16 rows] fp32
+    static constexpr int kBuf = kXBytes + kSGB * kTileRows * 4;
+    static constexpr int kJunk = 2 * kBuf;                   // placeholder DMA target
+    static constexpr int kRed = kJunk + 256;                 // [8][16] h group-sum partials
+    static constexpr int kTab = kRed + 8 * 16 * 4;
+    static constexpr int kTotal = kTab + kTable * kTabInts * 4;
+    static_assert(kTotal <= 160 * 1024, "one workgroup's LDS");
+    static constexpr int P = NMAT == 2 ? kSPGU : kSPDown;    // weight groups in flight per wave
+    static_assert(kSGB % P == 0, "ring slots stay static across batches");
+    static constexpr int kWL = 2 * NMAT;                     // loads per weight group
+};
+
+__device__ __forceinline__ void gload16(u32x4& d, const void* base, uint32_t voff) {
+    asm volatile("global_load_dwordx4 %0, %1, %2" : "=&v"(d) : "v"(voff), "s"(base));
+}
+__device__ __forceinline__ void gload8(u32x2& d, const void* base, uint32_t voff) {
+    asm volatile("global_load_dwordx2 %0, %1, %2" : "=&v"(d) : "v"(voff), "s"(base));
+}
+
+// Wave-uniform weight / scale bases of this wave's 16-row block in an item.
+struct SWItem {
+    const uint4* wq[2];
+    const uint16_t* ws[2];
+};
+
+template <int NMAT>
+__device__ __forceinline__ SWItem sw_item(const ExpArgs& a, const int* table, int k, int wave,
+                                          int nfb, int KG) {
+    const uint4 h = lds_bcast16(lds_addr(table + k * kTabInts));
+    const int e = sgpr(h.x);
+    const int fb = sgpr(h.w) * 8 + wave;
+    const bool sh = e == a.E;
+    const size_t mstride_q = (size_t)nfb * KG * 64;
+    const size_t mstride_s = (size_t)nfb * KG * 16;
+    SWItem it;
+#pragma unroll
+    for (int m = 0; m < 2; ++m) {
+        const int mm = m < NMAT ? m : 0;
+        it.wq[m] = (sh ? a.swq[mm] : a.wq[mm] + (size_t)e * mstride_q) + (size_t)fb * KG * 64;
+        it.ws[m] = (sh ? a.sws[mm] : a.ws[mm] + (size_t)e * mstride_s) + (size_t)fb * KG * 16;
+    }
+    return it;
+}
+
+// Activation-stream sources of one item: the src rows of this wave's two
+// staged rows (2 wave, 2 wave + 1) and of this lane's group-sum row.
+struct SAItem {
+    uint32_t tok[2];
+    uint32_t gtok;
+};
+
+template <int NMAT>
+__device__ __forceinline__ SAItem sa_item(const int* table, int k, int wave, int lane) {
+    const uint32_t base = lds_addr(table + k * kTabInts);
+    const uint4 h = lds_bcast16(base);
+    const int r0 = sgpr(h.y), nr = sgpr(h.z);
+    SAItem it;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+        const int row = 2 * wave + j;
+        it.tok[j] = NMAT == 2 ? (uint32_t)sgpr(lds_read_u32(base + 16 + row * 4))
+                              : (uint32_t)(r0 + (row < nr ? row : 0));
+    }
+    const int row = lane & 15;
+    it.gtok = NMAT == 2 ? lds_read_u32(base + 16 + row * 4) : (uint32_t)(r0 + (row < nr ? row : 0));
+    return it;
+}
+
+// Exactly kSActDma DMAs per wave: activation batch bi (K-groups 16 bi ..) of an
+// item into buffer `buf`. Row r of the batch sits at r * kRowB; chunk c of
+// group j at j * 256 + 16 (c ^ (r & 15)).
+template <int NMAT>
+__device__ __forceinline__ void s_issue_act(const ExpArgs& a, const SAItem& it, int bi, int K,
+                                            int KG, char* buf, char* junk, int wave, int lane) {
+    using LY = SLay<NMAT>;
+#pragma unroll
+    for (int m = 0; m < 8; ++m) {
+        const int j = m >> 2, quarter = m & 3;
+        const int row = 2 * wave + j;
+        const int grp = bi * kSGB + quarter * 4 + (lane >> 4);
+        const int c = (lane & 15) ^ (row & 15);
+        dma16(a.src + (size_t)it.tok[j] * K + grp * 128 + c * 8,
+              buf + row * LY::kRowB + quarter * 1024);
+    }
+    // Group sums: waves 0-3, lane l -> entry 64 wave + l = group 4 wave + l / 16, row l % 16.
+    const int grp = bi * kSGB + ((wave & 3) * 4 + (lane >> 4));
+    dma4(a.gsum + (size_t)it.gtok * KG + grp, wave < 4 ? buf + LY::kGOff + wave * 256 : junk);
+}
+
+template <int NMAT>
+__device__ __forceinline__ void s_issue_w(const SWItem& it, int kg, int lane, u32x4 (&w)[2],
+                                          u32x2 (&sc)[2]) {
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+        gload16(w[m], reinterpret_cast<const char*>(it.wq[m]) + kg * 1024, (uint32_t)(lane * 16));
+        gload8(sc[m], reinterpret_cast<const char*>(it.ws[m]) + kg * 32, (uint32_t)((lane >> 4) * 8));
+    }
+}
+
+template <int NMAT, int N>
+__device__ __forceinline__ void s_wait_w(u32x4 (&w)[2], u32x2 (&sc)[2]) {
+    if constexpr (NMAT == 2)
+        asm volatile("s_waitcnt vmcnt(%c4)" : "+v"(w[0]), "+v"(w[1]), "+v"(sc[0]), "+v"(sc[1]) : "i"(N));
+    else
+        asm volatile("s_waitcnt vmcnt(%c2)" : "+v"(w[0]), "+v"(sc[0]) : "i"(N));
+}
+
+// LDS operands of group j of a batch: the 4 activation fragments and X.
+struct SOps {
+    u32x4 x[4];
+    float g;
+};
+
+// Per-lane LDS read bases of one activation buffer: fragment d of group j is
+// at x[d] + 256 j, X of group j at g + 64 j (both immediate offsets).
+struct SBase {
+    uint32_t x[4];
+    uint32_t g;
+};
+
+template <int NMAT>
+__device__ __forceinline__ SBase s_base(const char* buf, int lane) {
+    using LY = SLay<NMAT>;
+    const int r = lane & 15, q = lane >> 4;
+    SBase b;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+        b.x[d] = lds_addr(buf) + (uint32_t)(r * LY::kRowB + (((4 * q + d) ^ r) * 16));
+    b.g = lds_addr(buf + LY::kGOff) + (uint32_t)(r * 4);
+    return b;
+}
+
+template <int J>
+__device__ __forceinline__ void s_load_ops(const SBase& b, SOps& o) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+        asm volatile("ds_read_b128 %0, %1 offset:%c2" : "=&v"(o.x[d]) : "v"(b.x[d]), "i"(J * 256));
+    asm volatile("ds_read_b32 %0, %1 offset:%c2" : "=&v"(o.g) : "v"(b.g), "i"(J * 64));
+}
+
+__device__ __forceinline__ void s_wait_ops(SOps& o) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(o.x[0]), "+v"(o.x[1]), "+v"(o.x[2]), "+v"(o.x[3]), "+v"(o.g));
+}
+
+template <int NMAT>
+__device__ __forceinline__ void s_compute(const SOps& o, const u32x4 (&w)[2], const u32x2 (&sc)[2],
+                                          const DqConst& dqc, f32x4 (&acc)[NMAT]) {
+    const float off = -136.0f * o.g;
+    f32x4 p[NMAT];
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m)
+            p[m] = mfma16x16x32(dq_w4(w[m][d], dqc), as_bf16x8(o.x[d]),
+                                d == 0 ? f32x4{0.f, 0.f, 0.f, 0.f} : p[m]);
+#pragma unroll
+    for (int m = 0; m < NMAT; ++m) {
+        const float s4[4] = {bf16_to_f32(sc[m].x & 0xffffu), __uint_as_float(sc[m].x & 0xffff0000u),
+                             bf16_to_f32(sc[m].y & 0xffffu), __uint_as_float(sc[m].y & 0xffff0000u)};
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) acc[m][jj] = __builtin_fmaf(s4[jj], p[m][jj] + off, acc[m][jj]);
+    }
+}
+
+template <int NMAT>
+__global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
+    using LY = SLay<NMAT>;
+    constexpr int P = LY::P;
+    extern __shared__ __align__(16) char lds[];
+    const DqConst dqc = dq_const();
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int r = lane & 15, q = lane >> 4;
+    const int K = NMAT == 2 ? a.H : a.I;
+    const int KG = K / 128;
+    const int BPI = KG / kSGB;                 // activation batches per item
+    const int nfb = (NMAT == 2 ? a.I : a.H) / 16;
+    const int ngrp = nfb / 8;
+    const int total = *a.ntiles * ngrp;
+    const int nwg = (int)gridDim.x;
+    const int base = (int)blockIdx.x;
+    const int nitems = base < total ? (total - base + nwg - 1) / nwg : 0;
+    int* table = reinterpret_cast<int*>(lds + LY::kTab);
+    char* junk = lds + LY::kJunk;
+
+    for (int k0 = 0; k0 < nitems; k0 += kTable) {
+        const int cnt = min(kTable, nitems - k0);
+        fill_table(a, table, base, nwg, ngrp, k0, cnt);
+        __syncthreads();
+        const int ngroups = cnt * KG;          // weight groups of the chunk
+        const int nbatch = cnt * BPI;          // activation batches of the chunk
+
+        // Weight stream, P groups ahead (crosses items).
+        int wk = 0, wkg = 0;
+        SWItem wit = sw_item<NMAT>(a, table, 0, wave, nfb, KG);
+        u32x4 W[P][2];
+        u32x2 Sc[P][2];
+        // Past the chunk's last group both streams re-issue their final
+        // loads, so every step issues the same loads and all waits stay
+        // static; the surplus data is never read.
+        auto issue_w = [&](u32x4 (&w)[2], u32x2 (&sc)[2]) {
+            s_issue_w<NMAT>(wit, wkg, lane, w, sc);
+            if (wkg + 1 < KG) {
+                ++wkg;
+            } else if (wk + 1 < cnt) {
+                ++wk;
+                wkg = 0;
+                wit = sw_item<NMAT>(a, table, wk, wave, nfb, KG);
+            }
+        };
+        // Activation stream, one batch ahead.
+        int ak = 0, abi = 0;
+        SAItem ait = sa_item<NMAT>(table, 0, wave, lane);
+        auto issue_act = [&](int b) {
+            s_issue_act<NMAT>(a, ait, abi, K, KG, lds + (b & 1) * LY::kBuf, junk, wave, lane);
+            if (abi + 1 < BPI) {
+                ++abi;
+            } else if (ak + 1 < cnt) {
+                ++ak;
+                abi = 0;
+                ait = sa_item<NMAT>(table, ak, wave, lane);
+            }
+        };
+
+        issue_act(0);
+#pragma unroll
+        for (int i = 0; i < P; ++i) issue_w(W[i], Sc[i]);
+        wait_vmcnt<P * LY::kWL>();
+        __builtin_amdgcn_s_barrier();
+        SOps ops[2];
+        s_load_ops<0>(s_base<NMAT>(lds, lane), ops[0]);
+
+        int cur_k = 0, cur_bi = 0;
+        int cr0 = 0, cnr = 0, cfb = 0;
+        {
+            const uint4 h = lds_bcast16(lds_addr(table));
+            cr0 = sgpr(h.y); cnr = sgpr(h.z); cfb = sgpr(h.w) * 8 + wave;
+        }
+        f32x4 acc[NMAT];
+#pragma unroll
+        for (int m = 0; m < NMAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+        for (int B = 0; B < nbatch; ++B) {
+            const bool next_act = B + 1 < nbatch;
+            const SBase cb = s_base<NMAT>(lds + (B & 1) * LY::kBuf, lane);
+            static_for<kSGB>([&](auto jc) {
+                constexpr int j = decltype(jc)::value;
+                if constexpr (j == 8) issue_act(B + 1);
+                // Weights of group j: loads issued after them are the groups
+                // j + 1 .. j + P - 1 and, for 8 <= j < 8 + P, batch B + 1.
+                if constexpr (j >= 8 && j < 8 + P)
+                    s_wait_w<NMAT, (P - 1) * LY::kWL + kSActDma>(W[j % P], Sc[j % P]);
+                else
+                    s_wait_w<NMAT, (P - 1) * LY::kWL>(W[j % P], Sc[j % P]);
+                SOps& o = ops[j & 1];
+                s_wait_ops(o);
+                if constexpr (j + 1 < kSGB) s_load_ops<j + 1>(cb, ops[(j + 1) & 1]);
+#ifndef GLMMOE_EXP_NOCOMPUTE
+                s_compute<NMAT>(o, W[j % P], Sc[j % P], dqc, acc);
+                // Pin the rescale to this step (otherwise it is deferred and
+                // every step's partial products and scales stay live).
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) asm volatile("" : "+v"(acc[m]));
+#endif
+                // The slot is free again: group j + P goes into it.
+                issue_w(W[j % P], Sc[j % P]);
+                __builtin_amdgcn_sched_barrier(0);
+            });
+            // Item done?
+            if (++cur_bi == BPI) {
+                const bool valid = r < cnr;
+                const size_t row = (size_t)cr0 + r;
+                if constexpr (NMAT == 2) {
+                    const uint32_t h01 = pack_bf16x2(silu_fast(acc[0][0]) * acc[1][0],
+                                                     silu_fast(acc[0][1]) * acc[1][1]);
+                    const uint32_t h23 = pack_bf16x2(silu_fast(acc[0][2]) * acc[1][2],
+                                                     silu_fast(acc[0][3]) * acc[1][3]);
+                    if (valid)
+                        *reinterpret_cast<uint2*>(a.h + row * a.I + cfb * 16 + 4 * q) = uint2{h01, h23};
+                    float ps = (bf16_to_f32(h01 & 0xffffu) + __uint_as_float(h01 & 0xffff0000u)) +
+                               (bf16_to_f32(h23 & 0xffffu) + __uint_as_float(h23 & 0xffff0000u));
+                    ps = ps + __shfl_xor(ps, 16);
+                    ps = ps + __shfl_xor(ps, 32);
+                    const uint32_t red = lds_addr(lds + LY::kRed);
+                    if (q == 0) lds_write_f32(red + (uint32_t)((wave * 16 + r) * 4), ps);
+                    __builtin_amdgcn_s_barrier();
+                    if (wave == 0 && q == 0) {
+                        float tot = 0.0f;
+#pragma unroll
+                        for (int w = 0; w < 8; ++w)
+                            tot += __uint_as_float(lds_read_u32(red + (uint32_t)((w * 16 + r) * 4)));
+                        if (valid) a.hsum[row * (a.I / 128) + cfb / 8] = tot;
+                    }
+                    __builtin_amdgcn_s_barrier();
+                } else {
+                    if (valid)
+                        *reinterpret_cast<float4*>(a.dpart + row * a.H + cfb * 16 + 4 * q) =
+                            make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
+                }
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+                cur_bi = 0;
+                if (++cur_k < cnt) {
+                    const uint4 h = lds_bcast16(lds_addr(table + cur_k * kTabInts));
+                    cr0 = sgpr(h.y); cnr = sgpr(h.z); cfb = sgpr(h.w) * 8 + wave;
+                }
+            }
+            if (next_act) {
+                // Batch B + 1 has landed once only the 8 weight groups issued
+                // after it (from j = 8 on) are pending.
+                wait_vmcnt<8 * LY::kWL>();
+                __builtin_amdgcn_s_barrier();
+                s_load_ops<0>(s_base<NMAT>(lds + ((B + 1) & 1) * LY::kBuf, lane), ops[0]);
+            }
+        }
+        wait_vmcnt<0>();
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __syncthreads();
+    }
+}
+
+template <int NMAT>
+static int launch_stream(const ExpArgs& a, long max_work, hipStream_t s) {
+    using LY = SLay<NMAT>;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4_stream_kernel<NMAT>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, LY::kTotal) != hipSuccess)
+            return -4;
+        attr_set = true;
+    }
+    int dev = 0, cus = 256;
+    if (hipGetDevice(&dev) == hipSuccess)
+        (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+    long blocks = max_work;
+    if (blocks > (long)cus) blocks = cus;
+    if (blocks < 1) blocks = 1;
+    hipLaunchKernelGGL((w4_stream_kernel<NMAT>), dim3((unsigned)blocks), dim3(512), LY::kTotal, s, a);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// ---------------------------------------------------------------------------
 // Combine: out[t] = (((0 + w0*y0) + w1*y1) + ...) + y_shared, slot order then
 // shared (src/model_glm52.cpp:1133-1152). Gather, no atomics: deterministic.
 // ---------------------------------------------------------------------------
@@ -570,6 +954,9 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, co
     a.src = x; a.gsum = xsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.rows_tok = rows_tok; a.h = h; a.hsum = hsum; a.H = H; a.I = I; a.E = E;
     const long work = (long)max_tiles * (I / 16 / kNWGU);
+#ifndef GLMMOE_NO_STREAM
+    if ((H / 128) % kSGB == 0) return launch_stream<2>(a, (long)max_tiles * (I / 128), s);
+#endif
     if ((H / 128) % kPFGU == 0) return launch_expert<2, kPFGU, kRingGU, kNWGU>(a, work, s);
     return launch_expert<2, 1, 6, kNWGU>(a, work, s);   // odd K-group count
 }
@@ -584,6 +971,9 @@ int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const
     a.src = h; a.gsum = hsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.dpart = dpart; a.H = H; a.I = I; a.E = E;
     const long work = (long)max_tiles * (H / 16 / kNWDown);
+#ifndef GLMMOE_NO_STREAM
+    if ((I / 128) % kSGB == 0) return launch_stream<1>(a, (long)max_tiles * (H / 128), s);
+#endif
     if ((I / 128) % kPFDown == 0) return launch_expert<1, kPFDown, kRingDown, kNWDown>(a, work, s);
     return launch_expert<1, 1, 6, kNWDown>(a, work, s);   // odd K-group count
 }
