@@ -153,15 +153,16 @@ inline void end_call(hipStream_t s) {
 // Dispatch onward, given ids/weights/xsum in the workspace view.
 int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int* ids,
                 const float* w, const float* xsum, float* out, const glmmoe_layer_ws& v,
-                hipStream_t s) {
+                hipStream_t s, bool dispatched = false) {
     const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
     const int sh = has_shared(L) ? 1 : 0;
     const int mt = max_tiles_for(n, k, E, sh);
     const int T = tile_rows_for(n, k, sh);
     const bool big = T == kBigRows;
     mark(GLMMOE_STAGE_DISPATCH, s);
-    int rc = launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids, v.sorted_row,
-                             v.inv, v.tiles, v.ntiles, T, sh, 1, s);
+    int rc = dispatched ? 0
+                        : launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids,
+                                          v.sorted_row, v.inv, v.tiles, v.ntiles, T, sh, 1, s);
     if (rc) return rc;
     const ExpertPtrs P = ptrs(L);
     mark(GLMMOE_STAGE_GATE_UP, s);
@@ -184,15 +185,17 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
 // FP8: activation quantization, dispatch onto 128-row tiles, the two fp8
 // grouped GEMMs and the combine.
 int run_experts8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, const int* ids,
-                 const float* w, float* out, const glmmoe_fp8_ws& v, hipStream_t s) {
+                 const float* w, float* out, const glmmoe_fp8_ws& v, hipStream_t s,
+                 bool dispatched = false) {
     const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
     const int sh = has_shared(L) ? 1 : 0;
     const int mt = max_tiles_for(n, k, E, sh, kBigRows);
     int rc = launch_quant_act_fp8(x, n, H, v.xq, v.xscale, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_DISPATCH, s);
-    rc = launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids, v.sorted_row, v.inv,
-                         v.tiles, v.ntiles, kBigRows, sh, 1, s);
+    rc = dispatched ? 0
+                    : launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids,
+                                      v.sorted_row, v.inv, v.tiles, v.ntiles, kBigRows, sh, 1, s);
     if (rc) return rc;
     const Fp8Ptrs P = ptrs8(L);
     mark(GLMMOE_STAGE_GATE_UP, s);
@@ -295,11 +298,16 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
     // The router pass also writes the activation group sums the expert
     // kernels use to remove the int4 decode offset.
+    const int sh = has_shared(L) ? 1 : 0;
+    const DispOut disp{v.expert_offsets, v.sorted_token_ids, v.sorted_row, v.inv,
+                       reinterpret_cast<int4*>(v.tiles), v.ntiles, tile_rows_for(n, k, sh), sh, 1};
+    bool dispatched = false;
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
-                              L->routed_scale, v.logits, v.xsum, v.rpart, v.topk_ids, v.topk_w, s);
+                              L->routed_scale, v.logits, v.xsum, v.rpart, v.topk_ids, v.topk_w, s,
+                              &disp, &dispatched);
     if (rc) return rc;
     mark(GLMMOE_STAGE_ROUTER_TOPK, s);
-    return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s);
+    return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s, dispatched);
 }
 
 int glmmoe_moe_route_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n,
@@ -375,11 +383,16 @@ int glmmoe_moe_layer_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, fl
     const int H = L->hidden, E = L->n_experts, k = L->topk;
     begin_call();
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
+    const int sh = has_shared(L) ? 1 : 0;
+    const DispOut disp{v.expert_offsets, v.sorted_token_ids, v.sorted_row, v.inv,
+                       reinterpret_cast<int4*>(v.tiles), v.ntiles, kBigRows, sh, 1};
+    bool dispatched = false;
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
-                              L->routed_scale, v.logits, nullptr, v.rpart, v.topk_ids, v.topk_w, s);
+                              L->routed_scale, v.logits, nullptr, v.rpart, v.topk_ids, v.topk_w, s,
+                              &disp, &dispatched);
     if (rc) return rc;
     mark(GLMMOE_STAGE_ROUTER_TOPK, s);
-    return run_experts8(L, x, n, v.topk_ids, v.topk_w, out, v, s);
+    return run_experts8(L, x, n, v.topk_ids, v.topk_w, out, v, s, dispatched);
 }
 
 int glmmoe_expert_ffn_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n,

@@ -155,4 +155,28 @@ __device__ __forceinline__ void lds_write_f32(uint32_t addr, float v) {
 }
 __device__ __forceinline__ int sgpr(uint32_t v) { return __builtin_amdgcn_readfirstlane((int)v); }
 
+
+// ---- device-coherent plain loads/stores --------------------------------------
+// Data handed between workgroups of one launch (a ticket decides who reads
+// it) goes through device-scope relaxed atomics: on gfx950 these are plain
+// loads/stores with device-scope cache bits, coherent across the XCDs' L2s
+// without the L2 write-back/invalidate a device-scope fence costs. A writer
+// waits for its stores to complete (vmcnt 0) before it takes its ticket.
+template <class T>
+__device__ __forceinline__ void st_dev(T* p, T v) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+template <class T>
+__device__ __forceinline__ T ld_dev(const T* p) {
+    return __hip_atomic_load(const_cast<T*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ unsigned int ticket_dev(unsigned int* p) {
+    return __hip_atomic_fetch_add(p, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void reset_dev(unsigned int* p) {
+    __hip_atomic_store(p, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+// Waits until every memory operation this wave issued has completed.
+__device__ __forceinline__ void drain_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 }  // namespace glmmoe

@@ -1,160 +1,26 @@
-// Dispatch: expert histogram, prefix scan and a stable permute that groups
-// the (token, slot) rows by expert, plus the inverse map and the tile list
-// the grouped expert GEMMs walk.
+// Stand-alone dispatch kernel (the body is in dispatch.hpp).
 //
-// Reference: cuda/moe_dispatch.cu:16-45 (serial counting sort, stable in
-// token-then-slot order) and the atomic count/scan/scatter of
-// cuda/qgemm.cu:966-989 (whose order inside an expert is nondeterministic).
-// Here the order is the reference's stable one and the work is parallel:
-//   1. LDS histogram (atomics on counts only: order-free),
-//   2. a one-wave prefix scan over experts,
-//   3. rows in chunks of 1024 in input order; inside a wave, equal expert ids
-//      are matched with one ballot per id bit (rank = lanes below with the
-//      same id); across the 16 waves of a chunk, per-wave counts in LDS give
-//      each row the number of equal ids in earlier waves. The result is a
-//      pure function of topk_ids.
-#include "common.hpp"
+// Reference: cuda/moe_dispatch.cu:16-45, cuda/qgemm.cu:966-989.
+#include "dispatch.hpp"
 #include "kernels.hpp"
 
 namespace glmmoe {
 
 constexpr int kDispThreads = 1024;
-constexpr int kDispWaves = kDispThreads / 64;
-constexpr int kDispMaxE = 512;
 
-// Exclusive prefix of vals[0..count) (count <= 512) into pre[0..count], pre[count] =
-// total, by wave 0 alone: each lane sums 8 consecutive entries, then a wave
-// scan of the lane sums. Callers synchronize before and after.
-__device__ void wave0_exclusive_scan(const int* vals, int count, int* pre) {
-    const int lane = threadIdx.x & 63;
-    if (threadIdx.x >= 64) return;
-    int local[8];
-    int sum = 0;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int i = lane * 8 + j;
-        local[j] = i < count ? vals[i] : 0;
-        sum += local[j];
-    }
-    int incl = sum;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-        const int t = __shfl_up(incl, off);
-        if (lane >= off) incl += t;
-    }
-    int run = incl - sum;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int i = lane * 8 + j;
-        if (i < count) pre[i] = run;
-        run += local[j];
-    }
-    if (lane == 63) pre[count] = incl;
-}
-
-// mode bit 0: also emit inv[], shared rows and the tile list (layer path).
-__global__ __launch_bounds__(kDispThreads) void dispatch_kernel(
-    const int* __restrict__ ids, int n, int topk, int E, int* __restrict__ offsets,
-    int* __restrict__ sorted_tok, int* __restrict__ sorted_slot, int* __restrict__ inv,
-    int4* __restrict__ tiles, int* __restrict__ ntiles, int tile_rows, int with_shared,
-    int mode) {
-    __shared__ int cnt[kDispMaxE + 1];
-    __shared__ int cursor[kDispMaxE + 1];
-    __shared__ int wc[kDispWaves][kDispMaxE];
-    __shared__ int pre[kDispMaxE + 2];
-    __shared__ int ntl[kDispMaxE + 1];
-    const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
-    const int total = n * topk;
-    int nbits = 0;
-    while ((1 << nbits) < E) ++nbits;
-
-    for (int e = tid; e <= kDispMaxE; e += kDispThreads) cnt[e] = 0;
-    for (int i = tid; i < kDispWaves * kDispMaxE; i += kDispThreads) (&wc[0][0])[i] = 0;
-    __syncthreads();
-    for (int i = tid; i < total; i += kDispThreads) {
-        const int e = ids[i];
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
-    }
-    __syncthreads();
-
-    // Exclusive prefix over experts.
-    wave0_exclusive_scan(cnt, E, pre);
-    __syncthreads();
-    for (int e = tid; e <= E; e += kDispThreads) {
-        offsets[e] = pre[e];
-        if (e < E) cursor[e] = pre[e];
-    }
-    if ((mode & 1) && tid == 0) offsets[E + 1] = total + (with_shared ? n : 0);
-    __syncthreads();
-
-    // Stable permute.
-    for (int base = 0; base < total; base += kDispThreads) {
-        const int i = base + tid;
-        const int e = i < total ? ids[i] : -1;
-        const bool valid = e >= 0 && e < E;
-        uint64_t m = __ballot(valid);
-        for (int b = 0; b < nbits; ++b) {
-            const bool bit = valid && ((e >> b) & 1);
-            const uint64_t bal = __ballot(bit);
-            m &= bit ? bal : ~bal;
-        }
-        const uint64_t below = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-        const int rank = __popcll(m & below);
-        const bool leader = valid && rank == 0;
-        if (leader) wc[wv][e] = __popcll(m);
-        __syncthreads();
-        if (valid) {
-            int earlier = 0;
-            for (int w = 0; w < wv; ++w) earlier += wc[w][e];
-            const int pos = cursor[e] + earlier + rank;
-            sorted_tok[pos] = i / topk;
-            sorted_slot[pos] = i % topk;
-            if (mode & 1) inv[i] = pos;
-        }
-        __syncthreads();
-        if (leader) {
-            atomicAdd(&cursor[e], wc[wv][e]);
-            wc[wv][e] = 0;
-        }
-        __syncthreads();
-    }
-
-    if (!(mode & 1)) return;
-
-    // Shared-expert rows: one per token, after all routed rows.
-    if (with_shared)
-        for (int t = tid; t < n; t += kDispThreads) {
-            sorted_tok[total + t] = t;
-            sorted_slot[total + t] = -1;
-        }
-
-    // Tile list: expert e (e == E is the shared expert) contributes
-    // ceil(count / tile_rows) tiles of at most tile_rows consecutive rows.
-    const int nexp = E + (with_shared ? 1 : 0);
-    for (int e = tid; e < nexp; e += kDispThreads) {
-        const int ce = e < E ? cnt[e] : n;
-        ntl[e] = (ce + tile_rows - 1) / tile_rows;
-    }
-    __syncthreads();
-    wave0_exclusive_scan(ntl, nexp, pre);
-    __syncthreads();
-    for (int e = tid; e < nexp; e += kDispThreads) {
-        const int ce = e < E ? cnt[e] : n;
-        const int row0 = e < E ? cursor[e] - ce : total;  // cursor ended at offset + count
-        const int tbase = pre[e];
-        for (int j = 0; j < ntl[e]; ++j)
-            tiles[tbase + j] = make_int4(e, row0 + j * tile_rows, min(tile_rows, ce - j * tile_rows), 0);
-    }
-    if (tid == 0) *ntiles = pre[nexp];
+__global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int* __restrict__ ids,
+                                                                int n, int topk, int E,
+                                                                DispOut d) {
+    dispatch_block<kDispThreads>(ids, n, topk, E, d);
 }
 
 int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,
                     int* sorted_slot, int* inv, int* tiles, int* ntiles, int tile_rows,
                     int with_shared, int mode, hipStream_t s) {
     if (E > kDispMaxE || E < 1) return -2;
-    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispThreads), 0, s, ids, n, topk, E,
-                       offsets, sorted_tok, sorted_slot, inv, reinterpret_cast<int4*>(tiles),
-                       ntiles, tile_rows, with_shared, mode);
+    const DispOut d{offsets, sorted_tok, sorted_slot, inv, reinterpret_cast<int4*>(tiles),
+                    ntiles, tile_rows, with_shared, mode};
+    hipLaunchKernelGGL(dispatch_kernel, dim3(1), dim3(kDispThreads), 0, s, ids, n, topk, E, d);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

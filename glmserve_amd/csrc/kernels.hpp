@@ -32,6 +32,20 @@ struct Fp8Ptrs {
     const uint8_t* sh_down_q; const float* sh_down_s;
 };
 
+// Outputs of a dispatch. mode bit 0: also emit inv[], the shared-expert rows
+// and the tile list (layer path).
+struct DispOut {
+    int* offsets;
+    int* sorted_tok;
+    int* sorted_slot;
+    int* inv;
+    int4* tiles;
+    int* ntiles;
+    int tile_rows;
+    int with_shared;
+    int mode;
+};
+
 // Scratch (bytes) the router-logit launch needs for n tokens; 0 for large n.
 size_t router_logits_scratch_bytes(int n, int H, int E);
 int launch_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
@@ -43,7 +57,8 @@ int launch_xsum(const uint16_t* x, int n, int H, float* xsum, hipStream_t s);
 size_t router_select_scratch_bytes(int n, int H, int E);
 int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_bias, int n, int H,
                          int E, int topk, int norm_topk, float routed_scale, float* logits,
-                         float* xsum, float* scratch, int* ids, float* w, hipStream_t s);
+                         float* xsum, float* scratch, int* ids, float* w, hipStream_t s,
+                         const DispOut* disp = nullptr, bool* dispatched = nullptr);
 int launch_router_topk(const float* logits, const float* e_bias, int n, int E, int topk,
                        int norm_topk, float routed_scale, int* ids, float* w, hipStream_t s);
 int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,

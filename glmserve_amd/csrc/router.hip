@@ -4,6 +4,7 @@
 // Reference: src/model_gpu.cpp:1448-1450 (gemm_linear on the router, then
 // moe_router), cuda/moe_router.cu:17-79, src/model_glm52.cpp:1105-1129.
 #include "common.hpp"
+#include "dispatch.hpp"
 #include "kernels.hpp"
 
 namespace glmmoe {
@@ -266,10 +267,8 @@ __global__ __launch_bounds__(256) void xsum_kernel(const uint16_t* __restrict__ 
 // order of cuda/moe_router.cu:48-53: high word = choose mapped to a
 // monotone unsigned code (NaN just above "no candidate", below every number),
 // low word = ~expert, so equal choose values prefer the lower expert index.
-// Each of the k rounds: every lane offers its best untaken key; a max over
-// each 16-lane row with DPP row rotations (VALU latency, no LDS round trip),
-// then the 4 row maxima via readlane and a scalar max. The owner lane of
-// the winner retires it. Every lane sees the same winner (a uniform value).
+// kmax / kmax_dpp: a max over keys (each 16-lane row with DPP row rotations,
+// then the 4 row maxima via readlane), used where one key per wave is wanted.
 // ---------------------------------------------------------------------------
 constexpr int kMaxPerLane = 8;  // E <= 512
 
@@ -293,74 +292,137 @@ __device__ __forceinline__ void kmax_dpp(uint32_t& h, uint32_t& l) {
     kmax(h, l, oh, ol);
 }
 
-__global__ __launch_bounds__(256) void router_topk_kernel(
-    const float* __restrict__ logits, const float* __restrict__ e_bias, int n, int E, int topk,
-    int norm_topk, float routed_scale, int* __restrict__ topk_ids, float* __restrict__ topk_w) {
+constexpr int kTopkScratch = 40;   // LDS words per wave for topk_wave
+
+// Selection for token row lt (one wave; every lane calls it). The k winners
+// of the k rounds of cuda/moe_router.cu:48-53 are exactly the k largest keys
+// (order code of choose, ~expert), in descending key order, so:
+//   1. the k-th largest order code T by a most-significant-bit-first search
+//      (one ballot count per bit),
+//   2. the winners: codes above T, plus the lowest-index experts among
+//      those equal to T (the key's tie order),
+//   3. their descending order by ranking the k winners against each other,
+//   4. the weight sum in that order (the reference's summation order) and
+//      the normalized weights.
+// scratch: kTopkScratch LDS words private to the wave. COH: read the logits
+// with device-coherent loads and store ids/weights with device-coherent
+// stores.
+template <bool COH, int NJ>
+__device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
+                                          const float* __restrict__ e_bias, int E, int topk,
+                                          int norm_topk, float routed_scale,
+                                          int* __restrict__ ids_out, float* __restrict__ w_out,
+                                          uint32_t* scratch) {
     const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
-    if (t >= n) return;   // whole wave
-    const float* lt = logits + (size_t)t * E;
-    float score[kMaxPerLane];
-    uint32_t ch[kMaxPerLane];   // order codes, 0 = no candidate / taken
+    float score[NJ];
+    uint32_t ch[NJ];   // order codes, 0 = no candidate
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         const int e = lane + 64 * j;
         score[j] = 0.0f;
         ch[j] = 0u;
         if (e < E) {
-            const float sc = sigmoid_fixed(lt[e]);
+            const float sc = sigmoid_fixed(COH ? ld_dev(lt + e) : lt[e]);
             score[j] = sc;
             ch[j] = order_code(sc + (e_bias ? e_bias[e] : 0.0f));
         }
     }
-    float wsel[8];
-    int idsel[8];
+    auto count_ge = [&](uint32_t v) {
+        int cnt = 0;
+#pragma unroll
+        for (int j = 0; j < NJ; ++j)
+            cnt += __popcll(__ballot(ch[j] >= v));
+        return cnt;
+    };
+    // 1. T = the largest code with at least k codes >= T.
+    uint32_t T = 0u;
+    for (int b = 31; b >= 0; --b) {
+        const uint32_t cand = T | (1u << b);
+        if (count_ge(cand) >= topk) T = cand;
+    }
+    // 2. Winners; ties at T go to the lowest expert indices.
+    int above = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j)
+        above += __popcll(__ballot(ch[j] > T));
+    const int need = topk - above;
+    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+    uint32_t* s_hi = scratch;
+    uint32_t* s_lo = scratch + 8;
+    uint32_t* s_sc = scratch + 16;
+    int* s_id = reinterpret_cast<int*>(scratch + 24);
+    float* s_w = reinterpret_cast<float*>(scratch + 32);
+    int ties = 0, slot = 0;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) {
+        {
+            const uint64_t tm = __ballot(ch[j] == T);
+            const bool sel = ch[j] > T || (ch[j] == T && ties + __popcll(tm & below) < need);
+            ties += __popcll(tm);
+            const uint64_t sm = __ballot(sel);
+            if (sel) {
+                const int p = slot + __popcll(sm & below);
+                s_hi[p] = ch[j];
+                s_lo[p] = ~(uint32_t)(lane + 64 * j);
+                s_sc[p] = __float_as_uint(score[j]);
+            }
+            slot += __popcll(sm);
+        }
+    }
+    __builtin_amdgcn_wave_barrier();
+    // 3. Rank of winner i = number of winners with a larger key.
+    if (lane < topk) {
+        const uint32_t h = s_hi[lane], l = s_lo[lane];
+        int rank = 0;
+#pragma unroll
+        for (int q = 0; q < 8; ++q)
+            if (q < topk) {
+                const uint32_t hq = s_hi[q], lq = s_lo[q];
+                rank += (hq > h || (hq == h && lq > l)) ? 1 : 0;
+            }
+        s_id[rank] = (int)~l;
+        s_w[rank] = __uint_as_float(s_sc[lane]);
+    }
+    __builtin_amdgcn_wave_barrier();
+    // 4. Weight sum in selection order, then the normalized weights.
     float wsum = 0.0f;
 #pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        if (k >= topk) break;
-        // Lane-local best (ascending j == ascending expert; strict > keeps lower).
-        uint32_t h = 0u, l = 0u;
-#pragma unroll
-        for (int j = 0; j < kMaxPerLane; ++j)
-            kmax(h, l, ch[j], ch[j] ? ~(uint32_t)(lane + 64 * j) : 0u);
-        // Row max (row_ror:1,2,4,8 over 16 lanes), then across the 4 rows.
-        kmax_dpp<0x121>(h, l);
-        kmax_dpp<0x122>(h, l);
-        kmax_dpp<0x124>(h, l);
-        kmax_dpp<0x128>(h, l);
-        uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)h, 0);
-        uint32_t bl = (uint32_t)__builtin_amdgcn_readlane((int)l, 0);
-        kmax(bh, bl, (uint32_t)__builtin_amdgcn_readlane((int)h, 16),
-             (uint32_t)__builtin_amdgcn_readlane((int)l, 16));
-        kmax(bh, bl, (uint32_t)__builtin_amdgcn_readlane((int)h, 32),
-             (uint32_t)__builtin_amdgcn_readlane((int)l, 32));
-        kmax(bh, bl, (uint32_t)__builtin_amdgcn_readlane((int)h, 48),
-             (uint32_t)__builtin_amdgcn_readlane((int)l, 48));
-        const int e = (int)~bl;               // uniform winner
-        const int owner = e & 63, jw = e >> 6;
-        float sw = 0.0f;
-#pragma unroll
-        for (int j = 0; j < kMaxPerLane; ++j) {
-            if (j == jw) {
-                sw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score[j]), owner));
-                if (lane == owner) ch[j] = 0u;
-            }
-        }
-        idsel[k] = e;
-        wsel[k] = sw;
-        wsum = wsum + sw;
-    }
-    if (lane == 0) {
-#pragma unroll
-        for (int k = 0; k < 8; ++k) {
-            if (k >= topk) break;
-            float v = wsel[k];
-            if (norm_topk && wsum > 0.0f) v = v / wsum;
-            topk_ids[(size_t)t * topk + k] = idsel[k];
-            topk_w[(size_t)t * topk + k] = v * routed_scale;
+    for (int q = 0; q < 8; ++q)
+        if (q < topk) wsum = wsum + s_w[q];
+    if (lane < topk) {
+        float v = s_w[lane];
+        if (norm_topk && wsum > 0.0f) v = v / wsum;
+        if (COH) {
+            st_dev(ids_out + lane, s_id[lane]);
+            st_dev(w_out + lane, v * routed_scale);
+        } else {
+            ids_out[lane] = s_id[lane];
+            w_out[lane] = v * routed_scale;
         }
     }
+}
+
+// Dispatch on the experts per lane (E <= 64 * NJ).
+template <bool COH = false>
+__device__ __forceinline__ void topk_wave(const float* __restrict__ lt,
+                                          const float* __restrict__ e_bias, int E, int topk,
+                                          int norm_topk, float routed_scale,
+                                          int* __restrict__ ids_out, float* __restrict__ w_out,
+                                          uint32_t* scratch) {
+    if (E <= 64) topk_wave_nj<COH, 1>(lt, e_bias, E, topk, norm_topk, routed_scale, ids_out, w_out, scratch);
+    else if (E <= 128) topk_wave_nj<COH, 2>(lt, e_bias, E, topk, norm_topk, routed_scale, ids_out, w_out, scratch);
+    else if (E <= 256) topk_wave_nj<COH, 4>(lt, e_bias, E, topk, norm_topk, routed_scale, ids_out, w_out, scratch);
+    else topk_wave_nj<COH, 8>(lt, e_bias, E, topk, norm_topk, routed_scale, ids_out, w_out, scratch);
+}
+
+__global__ __launch_bounds__(256) void router_topk_kernel(
+    const float* __restrict__ logits, const float* __restrict__ e_bias, int n, int E, int topk,
+    int norm_topk, float routed_scale, int* __restrict__ topk_ids, float* __restrict__ topk_w) {
+    __shared__ uint32_t scratch[4][kTopkScratch];
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (t >= n) return;   // whole wave
+    topk_wave(logits + (size_t)t * E, e_bias, E, topk, norm_topk, routed_scale,
+              topk_ids + (size_t)t * topk, topk_w + (size_t)t * topk, scratch[threadIdx.x >> 6]);
 }
 
 // ---------------------------------------------------------------------------
@@ -605,6 +667,194 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
     }
 }
 
+// ---------------------------------------------------------------------------
+// Small batches inside the layer (n < kTiledMinTokens): logits, selection and
+// (optionally) the dispatch in one launch.
+// Grid (ceil(E / epw), ceil(n / 8)) of 256 threads. Thread i < epw * nchunks
+// owns (expert eb * epw + i / nchunks, chunk i % nchunks): it keeps the
+// chunk's 128 router weights in registers and, per token of its group,
+// accumulates the chunk partial from zero in ascending K into LDS (the fixed
+// order of router_partials_kernel). Threads (expert, token) then add the
+// chunk partials in ascending chunk order: the logit, bit-identical to the
+// two-pass path.
+// Tickets: after its logits are stored, each workgroup takes a ticket of its
+// token group; the one that takes the last ticket (all the group's logits
+// are then stored) runs the top-k of the group's tokens, one wave per token.
+// With a dispatch, those selecting workgroups then take a ticket of the
+// launch, and the last one runs the whole dispatch. A ticket counter is reset
+// by the workgroup that took its last ticket, so every launch starts from
+// zero; launches that overlap in time on one GPU (different streams) must not
+// use this path together.
+// ---------------------------------------------------------------------------
+constexpr int kSmallThreads = 256;
+constexpr int kSmallMaxChunks = 64;
+// Staged activation bytes: 8 tokens x nchunks rows of 256 B, whole 1 KiB DMAs.
+__host__ __device__ constexpr int small_x_bytes(int nchunks) {
+    return (kRouterTG * nchunks * 256 + 1023) / 1024 * 1024;
+}
+constexpr int kSmallMaxTG = (kTiledMinTokens + kRouterTG - 1) / kRouterTG;
+static __device__ unsigned int g_small_tick[kSmallMaxTG + 1];
+
+// NT independent token chains over one 128-K chunk c: the ascending-K sum
+// from zero of x[t] * w, for tokens t < nt (rows past nt repeat row nt - 1
+// and are not stored). The NT activation pieces of step j + 1 are read from
+// LDS while step j is computed.
+template <int NT>
+__device__ __forceinline__ void small_chunk_dots(const char* xl, const uint4 (&wv)[kRouterKC / 8],
+                                                 int c, int nchunks, int nt, float* out) {
+    uint32_t base[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) {
+        const int R = (t < nt ? t : nt - 1) * nchunks + c;
+        base[t] = (uint32_t)(R * 256);
+    }
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    auto rd = [&](int j, uint4 (&xv)[NT]) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            const uint32_t R15 = (base[t] >> 8) & 15;
+            xv[t] = *reinterpret_cast<const uint4*>(xl + base[t] + (((uint32_t)j ^ R15) << 4));
+        }
+    };
+    uint4 xa[NT], xb[NT];
+    rd(0, xa);
+#pragma unroll
+    for (int j = 0; j < kRouterKC / 8; ++j) {
+        uint4 (&cur)[NT] = (j & 1) ? xb : xa;
+        uint4 (&nxt)[NT] = (j & 1) ? xa : xb;
+        if (j + 1 < kRouterKC / 8) rd(j + 1, nxt);
+        const uint32_t wd[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+        float wf[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            wf[2 * q] = bf16_to_f32(wd[q] & 0xffffu);
+            wf[2 * q + 1] = __uint_as_float(wd[q] & 0xffff0000u);
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q)
+#pragma unroll
+            for (int t = 0; t < NT; ++t) {
+                const uint32_t xd[4] = {cur[t].x, cur[t].y, cur[t].z, cur[t].w};
+                acc[t] = __builtin_fmaf(bf16_to_f32(xd[q] & 0xffffu), wf[2 * q], acc[t]);
+                acc[t] = __builtin_fmaf(__uint_as_float(xd[q] & 0xffff0000u), wf[2 * q + 1], acc[t]);
+            }
+        // Pin each step's chains here (otherwise the reads of every step are
+        // hoisted and the arithmetic sunk, holding 16 * NT pieces live).
+#pragma unroll
+        for (int t = 0; t < NT; ++t) asm volatile("" : "+v"(acc[t]));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int t = 0; t < NT; ++t)
+        if (t < nt) out[t] = acc[t];
+}
+
+__global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
+    const float* __restrict__ e_bias, int n, int H, int E, int epw, int topk, int norm_topk,
+    float routed_scale, float* __restrict__ logits, float* __restrict__ xsum,
+    int* __restrict__ ids, float* __restrict__ w, DispOut d, int do_disp) {
+    extern __shared__ __align__(16) char small_lds[];
+    __shared__ int last;
+    const int nchunks = H / kRouterKC;
+    const int tid = threadIdx.x;
+    const int eb = blockIdx.x, tg = blockIdx.y;
+    const int t0 = tg * kRouterTG, nt = min(kRouterTG, n - t0);
+    // LDS: the group's activations as 256-byte rows R = t * nchunks + c
+    // (token t, chunk c), 16-byte piece o of row R at slot o ^ (R & 15) (the
+    // threads of consecutive chunks reading the same piece hit distinct
+    // banks), staged by LDS-DMA, 1 KiB (4 rows) per wave instruction; then
+    // the chunk partials part[thread][token].
+    char* xl = small_lds;
+    const int xrows = nt * nchunks;
+    const int xdma = (xrows + 3) / 4;
+    float* part = reinterpret_cast<float*>(small_lds + small_x_bytes(nchunks));
+    {
+        const int wave = tid >> 6, lane = tid & 63;
+        for (int b = wave; b < xdma; b += kSmallThreads / 64) {
+            int R = 4 * b + (lane >> 4);
+            if (R >= xrows) R = 0;
+            const int t = R / nchunks, cc = R - t * nchunks;
+            const int o = (lane & 15) ^ (R & 15);
+            dma16(x + (size_t)(t0 + t) * H + cc * kRouterKC + o * 8, xl + b * 1024);
+        }
+    }
+    const int el = tid / nchunks, c = tid - el * nchunks;
+    const int e = eb * epw + el;
+    const bool active = el < epw && e < E;
+    uint4 wv[kRouterKC / 8];
+    if (active) {
+        const uint4* wp = reinterpret_cast<const uint4*>(wr + (size_t)e * H + c * kRouterKC);
+#pragma unroll
+        for (int j = 0; j < kRouterKC / 8; ++j) wv[j] = wp[j];
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (active) {
+        if (nt == 1) small_chunk_dots<1>(xl, wv, c, nchunks, nt, part + tid * kRouterTG);
+        else if (nt == 2) small_chunk_dots<2>(xl, wv, c, nchunks, nt, part + tid * kRouterTG);
+        else if (nt <= 4) small_chunk_dots<4>(xl, wv, c, nchunks, nt, part + tid * kRouterTG);
+        else small_chunk_dots<8>(xl, wv, c, nchunks, nt, part + tid * kRouterTG);
+    }
+    // Activation group sums (xsum [n, H/128]) from the staged rows, by the
+    // first expert block: ascending K, low half then high half of each dword.
+    if (xsum && eb == 0) {
+        for (int i = tid; i < nt * nchunks; i += kSmallThreads) {
+            const int t = i / nchunks, cc = i - t * nchunks;
+            const int R = t * nchunks + cc;
+            const char* row = xl + R * 256;
+            float xs = 0.0f;
+            for (int j = 0; j < kRouterKC / 8; ++j) {
+                const uint4 v = *reinterpret_cast<const uint4*>(row + ((j ^ (R & 15)) << 4));
+                const uint32_t xd[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    xs += bf16_to_f32(xd[q] & 0xffffu);
+                    xs += bf16_to_f32(xd[q] >> 16);
+                }
+            }
+            xsum[(size_t)(t0 + t) * nchunks + cc] = xs;
+        }
+    }
+    __syncthreads();
+    if (tid < epw * kRouterTG) {
+        const int el2 = tid / kRouterTG, t = tid % kRouterTG;
+        const int e2 = eb * epw + el2;
+        if (e2 < E && t < nt) {
+            float total = 0.0f;
+            for (int cc = 0; cc < nchunks; ++cc)
+                total = total + part[(el2 * nchunks + cc) * kRouterTG + t];
+            st_dev(logits + (size_t)(t0 + t) * E + e2, total);
+        }
+    }
+    // This workgroup's logits are complete in memory; take the group ticket.
+    drain_vm();
+    __syncthreads();
+    if (tid == 0) {
+        last = ticket_dev(&g_small_tick[tg]) == gridDim.x - 1;
+        if (last) reset_dev(&g_small_tick[tg]);
+    }
+    __syncthreads();
+    if (!last || do_disp < 0) return;
+    __shared__ uint32_t tscratch[kSmallThreads / 64][kTopkScratch];
+    for (int t = tid >> 6; t < nt; t += kSmallThreads / 64)
+        topk_wave<true>(logits + (size_t)(t0 + t) * E, e_bias, E, topk, norm_topk, routed_scale,
+                        ids + (size_t)(t0 + t) * topk, w + (size_t)(t0 + t) * topk,
+                        tscratch[tid >> 6]);
+    if (do_disp <= 0) return;
+    drain_vm();
+    __syncthreads();
+    if (tid == 0) {
+        last = ticket_dev(&g_small_tick[kSmallMaxTG]) == gridDim.y - 1;
+        if (last) reset_dev(&g_small_tick[kSmallMaxTG]);
+    }
+    __syncthreads();
+    if (!last) return;
+    dispatch_block<kSmallThreads, true>(ids, n, topk, E, d);
+}
+
 size_t router_select_scratch_bytes(int n, int H, int E) {
     const size_t a = router_logits_scratch_bytes(n, H, E);
     const size_t b = (size_t)n * E * 4;
@@ -613,8 +863,44 @@ size_t router_select_scratch_bytes(int n, int H, int E) {
 
 int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_bias, int n, int H,
                          int E, int topk, int norm_topk, float routed_scale, float* logits,
-                         float* xsum, float* scratch, int* ids, float* w, hipStream_t s) {
+                         float* xsum, float* scratch, int* ids, float* w, hipStream_t s,
+                         const DispOut* disp, bool* dispatched) {
     const int nchunks = H / kRouterKC;
+    if (dispatched) *dispatched = false;
+#ifndef GLMMOE_NO_SMALL_ROUTER
+    if (n < kTiledMinTokens && H % kRouterKC == 0 && nchunks <= kSmallMaxChunks &&
+        E <= 64 * kMaxPerLane && topk <= 8) {
+        // Few tokens: spread the router weights over many workgroups; more
+        // tokens: more experts per workgroup share the staged activations.
+        int epw = n <= kRouterTG ? E / 128 : kSmallThreads / nchunks;
+        if (epw > kSmallThreads / nchunks) epw = kSmallThreads / nchunks;
+        if (epw < 1) epw = 1;
+        const bool dd = disp && E <= kDispMaxE;
+        dim3 grid((unsigned)((E + epw - 1) / epw), (unsigned)((n + kRouterTG - 1) / kRouterTG));
+#ifndef GLMMOE_SMALL_MODE
+#define GLMMOE_SMALL_MODE 2
+#endif
+        // mode: -1 logits only, 0 + top-k, 1 + top-k and dispatch.
+        const int mode = GLMMOE_SMALL_MODE == 0 ? -1 : GLMMOE_SMALL_MODE == 1 ? 0 : (dd ? 1 : 0);
+        const size_t lds = (size_t)small_x_bytes(nchunks) + kSmallThreads * kRouterTG * 4;
+        static bool attr_set = false;
+        if (!attr_set) {
+            if (hipFuncSetAttribute(reinterpret_cast<const void*>(&router_small_kernel),
+                                    hipFuncAttributeMaxDynamicSharedMemorySize,
+                                    small_x_bytes(kSmallMaxChunks) +
+                                        kSmallThreads * kRouterTG * 4) != hipSuccess)
+                return -4;
+            attr_set = true;
+        }
+        hipLaunchKernelGGL(router_small_kernel, grid, dim3(kSmallThreads), lds, s, x, wr, e_bias, n,
+                           H, E, epw, topk, norm_topk, routed_scale, logits, xsum, ids, w,
+                           dd ? *disp : DispOut{}, mode);
+        if (hipGetLastError() != hipSuccess) return -4;
+        if (mode < 0) return launch_router_topk(logits, e_bias, n, E, topk, norm_topk, routed_scale, ids, w, s);
+        if (dispatched) *dispatched = mode == 1;
+        return 0;
+    }
+#endif
     if (n >= kTiledMinTokens && H % kMfmaK == 0 && H % kRouterKC == 0 && nchunks <= 64 &&
         E <= 64 * kMaxPerLane) {
         if (!scratch) return -3;
