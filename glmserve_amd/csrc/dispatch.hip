@@ -11,7 +11,8 @@ constexpr int kDispThreads = 1024;
 __global__ __launch_bounds__(kDispThreads) void dispatch_kernel(const int* __restrict__ ids,
                                                                 int n, int topk, int E,
                                                                 DispOut d) {
-    dispatch_block<kDispThreads>(ids, n, topk, E, d);
+    __shared__ int lds[dispatch_lds_ints<kDispThreads>()];
+    dispatch_block<kDispThreads>(ids, n, topk, E, d, lds);
 }
 
 int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,

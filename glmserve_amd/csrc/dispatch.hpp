@@ -54,17 +54,23 @@ __device__ inline void wave0_exclusive_scan(const int* vals, int count, int* pre
 }
 
 // The whole dispatch, by one workgroup of NT threads (all of them call it).
+// LDS ints dispatch_block<NT> uses.
+template <int NT>
+__host__ __device__ constexpr int dispatch_lds_ints() {
+    return 4 * (kDispMaxE + 2) + (NT / 64) * kDispMaxE;
+}
+
 // COH: read ids with device-coherent loads (ids written by other workgroups
-// of the same launch).
+// of the same launch). lds: dispatch_lds_ints<NT>() ints of LDS.
 template <int NT, bool COH = false>
 __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int E,
-                               const DispOut& d) {
+                               const DispOut& d, int* lds) {
     auto id_at = [&](int i) { return COH ? ld_dev(ids + i) : ids[i]; };
-    static __shared__ int cnt[kDispMaxE + 1];
-    static __shared__ int cursor[kDispMaxE + 1];
-    static __shared__ int wc[(NT / 64)][kDispMaxE];
-    static __shared__ int pre[kDispMaxE + 2];
-    static __shared__ int ntl[kDispMaxE + 1];
+    int* cnt = lds;
+    int* cursor = cnt + (kDispMaxE + 2);
+    int* pre = cursor + (kDispMaxE + 2);
+    int* ntl = pre + (kDispMaxE + 2);
+    int (*wc)[kDispMaxE] = reinterpret_cast<int (*)[kDispMaxE]>(ntl + (kDispMaxE + 2));
     const int tid = threadIdx.x, lane = tid & 63, wv = tid >> 6;
     const int total = n * topk;
     int nbits = 0;

@@ -670,13 +670,13 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
 // ---------------------------------------------------------------------------
 // Small batches inside the layer (n < kTiledMinTokens): logits, selection and
 // (optionally) the dispatch in one launch.
-// Grid (ceil(E / epw), ceil(n / 8)) of 256 threads. Thread i < epw * nchunks
-// owns (expert eb * epw + i / nchunks, chunk i % nchunks): it keeps the
-// chunk's 128 router weights in registers and, per token of its group,
-// accumulates the chunk partial from zero in ascending K into LDS (the fixed
-// order of router_partials_kernel). Threads (expert, token) then add the
-// chunk partials in ascending chunk order: the logit, bit-identical to the
-// two-pass path.
+// Grid (ceil(E / epw), ceil(n / 8)) of 512 threads. The group's activations
+// are staged in LDS; thread (expert eb * epw + el, chunk c, token slice ts)
+// keeps the chunk's 128 router weights in registers and, for each token of
+// its slice, accumulates the chunk partial from zero in ascending K (the
+// fixed order of router_partials_kernel). Threads (expert, token) then add
+// the chunk partials in ascending chunk order: the logit, bit-identical to
+// the two-pass path.
 // Tickets: after its logits are stored, each workgroup takes a ticket of its
 // token group; the one that takes the last ticket (all the group's logits
 // are then stored) runs the top-k of the group's tokens, one wave per token.
@@ -686,7 +686,22 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
 // zero; launches that overlap in time on one GPU (different streams) must not
 // use this path together.
 // ---------------------------------------------------------------------------
-constexpr int kSmallThreads = 256;
+constexpr int kSmallThreads = 512;
+#ifdef GLMMOE_SMALL_TRACE
+// Diagnostics: shader-clock stamps of the phases of the workgroup that runs
+// the dispatch (slot 8 + i: of workgroup 0).
+__device__ unsigned long long g_small_trace[16];
+#define SMALL_STAMP(i)                                                               \
+    do {                                                                             \
+        const unsigned long long ts_ = __builtin_amdgcn_s_memtime();                 \
+        if (threadIdx.x == 0) {                                                      \
+            if (blockIdx.x == 0 && blockIdx.y == 0) g_small_trace[8 + (i)] = ts_;    \
+            g_small_trace[(i)] = ts_;                                                \
+        }                                                                            \
+    } while (0)
+#else
+#define SMALL_STAMP(i) do {} while (0)
+#endif
 constexpr int kSmallMaxChunks = 64;
 // Staged activation bytes: 8 tokens x nchunks rows of 256 B, whole 1 KiB DMAs.
 __host__ __device__ constexpr int small_x_bytes(int nchunks) {
@@ -696,16 +711,16 @@ constexpr int kSmallMaxTG = (kTiledMinTokens + kRouterTG - 1) / kRouterTG;
 static __device__ unsigned int g_small_tick[kSmallMaxTG + 1];
 
 // NT independent token chains over one 128-K chunk c: the ascending-K sum
-// from zero of x[t] * w, for tokens t < nt (rows past nt repeat row nt - 1
-// and are not stored). The NT activation pieces of step j + 1 are read from
+// from zero of x[t] * w, for tokens tb + t, t < nt (rows past nt repeat the
+// last one and are not stored). The NT activation pieces of step j + 1 are read from
 // LDS while step j is computed.
 template <int NT>
 __device__ __forceinline__ void small_chunk_dots(const char* xl, const uint4 (&wv)[kRouterKC / 8],
-                                                 int c, int nchunks, int nt, float* out) {
+                                                 int c, int nchunks, int tb, int nt, float* out) {
     uint32_t base[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) {
-        const int R = (t < nt ? t : nt - 1) * nchunks + c;
+        const int R = (tb + (t < nt ? t : nt - 1)) * nchunks + c;
         base[t] = (uint32_t)(R * 256);
     }
     float acc[NT];
@@ -748,16 +763,17 @@ __device__ __forceinline__ void small_chunk_dots(const char* xl, const uint4 (&w
     }
 #pragma unroll
     for (int t = 0; t < NT; ++t)
-        if (t < nt) out[t] = acc[t];
+        if (t < nt) out[tb + t] = acc[t];
 }
 
 __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const float* __restrict__ e_bias, int n, int H, int E, int epw, int topk, int norm_topk,
     float routed_scale, float* __restrict__ logits, float* __restrict__ xsum,
-    int* __restrict__ ids, float* __restrict__ w, DispOut d, int do_disp) {
+    int* __restrict__ ids, float* __restrict__ w, DispOut d, int do_disp, int slices) {
     extern __shared__ __align__(16) char small_lds[];
     __shared__ int last;
+    SMALL_STAMP(0);
     const int nchunks = H / kRouterKC;
     const int tid = threadIdx.x;
     const int eb = blockIdx.x, tg = blockIdx.y;
@@ -781,9 +797,15 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
             dma16(x + (size_t)(t0 + t) * H + cc * kRouterKC + o * 8, xl + b * 1024);
         }
     }
-    const int el = tid / nchunks, c = tid - el * nchunks;
+    // Thread -> (expert el, chunk c, token slice ts): slice ts holds tokens
+    // [ts * tps, ts * tps + tps) of the group.
+    const int ec = epw * nchunks;
+    const int pair = tid % ec, ts = tid / ec;
+    const int el = pair / nchunks, c = pair - el * nchunks;
     const int e = eb * epw + el;
-    const bool active = el < epw && e < E;
+    const int tps = kRouterTG / slices;
+    const int tb = ts * tps, tcnt = min(tps, nt - tb);
+    const bool active = ts < slices && e < E && tcnt > 0;
     uint4 wv[kRouterKC / 8];
     if (active) {
         const uint4* wp = reinterpret_cast<const uint4*>(wr + (size_t)e * H + c * kRouterKC);
@@ -792,11 +814,13 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     }
     wait_vmcnt<0>();
     __syncthreads();
+    SMALL_STAMP(1);
     if (active) {
-        if (nt == 1) small_chunk_dots<1>(xl, wv, c, nchunks, nt, part + tid * kRouterTG);
-        else if (nt == 2) small_chunk_dots<2>(xl, wv, c, nchunks, nt, part + tid * kRouterTG);
-        else if (nt <= 4) small_chunk_dots<4>(xl, wv, c, nchunks, nt, part + tid * kRouterTG);
-        else small_chunk_dots<8>(xl, wv, c, nchunks, nt, part + tid * kRouterTG);
+        float* out = part + pair * kRouterTG;
+        if (tcnt == 1) small_chunk_dots<1>(xl, wv, c, nchunks, tb, tcnt, out);
+        else if (tcnt == 2) small_chunk_dots<2>(xl, wv, c, nchunks, tb, tcnt, out);
+        else if (tcnt <= 4) small_chunk_dots<4>(xl, wv, c, nchunks, tb, tcnt, out);
+        else small_chunk_dots<8>(xl, wv, c, nchunks, tb, tcnt, out);
     }
     // Activation group sums (xsum [n, H/128]) from the staged rows, by the
     // first expert block: ascending K, low half then high half of each dword.
@@ -829,6 +853,7 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
             st_dev(logits + (size_t)(t0 + t) * E + e2, total);
         }
     }
+    SMALL_STAMP(2);
     // This workgroup's logits are complete in memory; take the group ticket.
     drain_vm();
     __syncthreads();
@@ -838,11 +863,13 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     }
     __syncthreads();
     if (!last || do_disp < 0) return;
+    SMALL_STAMP(3);
     __shared__ uint32_t tscratch[kSmallThreads / 64][kTopkScratch];
     for (int t = tid >> 6; t < nt; t += kSmallThreads / 64)
         topk_wave<true>(logits + (size_t)(t0 + t) * E, e_bias, E, topk, norm_topk, routed_scale,
                         ids + (size_t)(t0 + t) * topk, w + (size_t)(t0 + t) * topk,
                         tscratch[tid >> 6]);
+    SMALL_STAMP(4);
     if (do_disp <= 0) return;
     drain_vm();
     __syncthreads();
@@ -852,7 +879,7 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     }
     __syncthreads();
     if (!last) return;
-    dispatch_block<kSmallThreads, true>(ids, n, topk, E, d);
+    dispatch_block<kSmallThreads, true>(ids, n, topk, E, d, reinterpret_cast<int*>(small_lds));
 }
 
 size_t router_select_scratch_bytes(int n, int H, int E) {
@@ -872,9 +899,11 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         E <= 64 * kMaxPerLane && topk <= 8) {
         // Few tokens: spread the router weights over many workgroups; more
         // tokens: more experts per workgroup share the staged activations.
-        int epw = n <= kRouterTG ? E / 128 : kSmallThreads / nchunks;
+        int epw = n <= kRouterTG ? E / 128 : 240 / nchunks;
         if (epw > kSmallThreads / nchunks) epw = kSmallThreads / nchunks;
         if (epw < 1) epw = 1;
+        int slices = 1;
+        while (slices < kRouterTG && 2 * slices * epw * nchunks <= kSmallThreads) slices *= 2;
         const bool dd = disp && E <= kDispMaxE;
         dim3 grid((unsigned)((E + epw - 1) / epw), (unsigned)((n + kRouterTG - 1) / kRouterTG));
 #ifndef GLMMOE_SMALL_MODE
@@ -882,7 +911,9 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
 #endif
         // mode: -1 logits only, 0 + top-k, 1 + top-k and dispatch.
         const int mode = GLMMOE_SMALL_MODE == 0 ? -1 : GLMMOE_SMALL_MODE == 1 ? 0 : (dd ? 1 : 0);
-        const size_t lds = (size_t)small_x_bytes(nchunks) + kSmallThreads * kRouterTG * 4;
+        // The dispatch reuses the staging area.
+        size_t lds = (size_t)small_x_bytes(nchunks) + (size_t)epw * nchunks * kRouterTG * 4;
+        if (lds < (size_t)dispatch_lds_ints<kSmallThreads>() * 4) lds = dispatch_lds_ints<kSmallThreads>() * 4;
         static bool attr_set = false;
         if (!attr_set) {
             if (hipFuncSetAttribute(reinterpret_cast<const void*>(&router_small_kernel),
@@ -894,7 +925,7 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         }
         hipLaunchKernelGGL(router_small_kernel, grid, dim3(kSmallThreads), lds, s, x, wr, e_bias, n,
                            H, E, epw, topk, norm_topk, routed_scale, logits, xsum, ids, w,
-                           dd ? *disp : DispOut{}, mode);
+                           dd ? *disp : DispOut{}, mode, slices);
         if (hipGetLastError() != hipSuccess) return -4;
         if (mode < 0) return launch_router_topk(logits, e_bias, n, E, topk, norm_topk, routed_scale, ids, w, s);
         if (dispatched) *dispatched = mode == 1;

@@ -105,3 +105,24 @@ def test_spec_verify_zipf(oracle):
     tok = np.array([0, 64, 65, 519])
     ref, _, _ = L.oracle_forward(oracle, x, tok, ref_logits)
     assert rel_err(out[tok], ref) < TOL_W4A16
+
+
+def test_decode_poisoned_workspace_deterministic():
+    # Decode batches whose expert work splits items across workgroups (the
+    # last round of a launch) and whose routing runs the fused small-batch
+    # kernel: with every workspace byte 0xFF (NaN patterns) beforehand and
+    # batch sizes alternating, the output is finite and bit-identical to a
+    # run on a zeroed workspace -- no state leaks between launches.
+    L = SynthLayer(6144, 256, 8, 2048, seed=1)
+    for n in (8, 1, 33, 8, 64, 1):
+        x = L.x(n, 10 + n)
+        outs = []
+        for fill in (0xFF, 0x00):
+            ws = L.layer.alloc_workspace(n)
+            ws.fill_(fill)
+            out = torch.empty(n, L.H, dtype=torch.float32, device="cuda")
+            L.layer.forward(x, out, ws)
+            torch.cuda.synchronize()
+            outs.append(out.cpu())
+        assert torch.isfinite(outs[0]).all(), n
+        assert torch.equal(outs[0], outs[1]), n
