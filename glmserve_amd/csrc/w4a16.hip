@@ -581,6 +581,7 @@ __device__ __forceinline__ SWItem sw_item(const ExpArgs& a, const int* table, in
 // staged rows (2 wave, 2 wave + 1) and of this lane's group-sum row.
 struct SAItem {
     uint32_t tok[2];
+    uint32_t live[2];   // this wave's staged rows lie inside the tile (row < nrows)
     uint32_t gtok;
 };
 
@@ -595,6 +596,7 @@ __device__ __forceinline__ SAItem sa_item(const int* table, int k, int wave, int
         const int row = 2 * wave + j;
         it.tok[j] = NMAT == 2 ? (uint32_t)sgpr(lds_read_u32(base + 16 + row * 4))
                               : (uint32_t)(r0 + (row < nr ? row : 0));
+        it.live[j] = row < nr ? 1u : 0u;
     }
     const int row = lane & 15;
     it.gtok = NMAT == 2 ? lds_read_u32(base + 16 + row * 4) : (uint32_t)(r0 + (row < nr ? row : 0));
@@ -614,8 +616,11 @@ __device__ __forceinline__ void s_issue_act(const ExpArgs& a, const SAItem& it, 
         const int row = 2 * wave + j;
         const int grp = bi * kSGB + quarter * 4 + (lane >> 4);
         const int c = (lane & 15) ^ (row & 15);
-        dma16(a.src + (size_t)it.tok[j] * K + grp * 128 + c * 8,
-              buf + row * LY::kRowB + quarter * 1024);
+        // Rows past the tile's end feed MFMA columns that are never stored:
+        // every lane then fetches the same 16 bytes (one cache line per
+        // instruction) instead of a duplicate row.
+        const int off = it.live[j] ? grp * 128 + c * 8 : 0;
+        dma16(a.src + (size_t)it.tok[j] * K + off, buf + row * LY::kRowB + quarter * 1024);
     }
     // Group sums: waves 0-3, lane l -> entry 64 wave + l = group 4 wave + l / 16, row l % 16.
     const int grp = bi * kSGB + ((wave & 3) * 4 + (lane >> 4));
