@@ -124,7 +124,7 @@ def cpu_baseline(L, n_sample, torch, seed):
 def profiled_traffic():
     """HBM bytes per gate/up launch at B=64 from the committed rocprofv3 summary
     (FETCH_SIZE / WRITE_SIZE passes scaled by a copy-kernel calibration)."""
-    path = os.path.join(ROOT, "profiles", "w4_expert_gate_up_decode_B64.md")
+    path = os.path.join(ROOT, "profiles", "w4_stream_gate_up_decode_B64.md")
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):
@@ -283,7 +283,7 @@ def main():
         sweep["fp8_prefill_8192"] = measure_fp8(8192, max(3, args.steps // 10), 2)
 
     gu_ms = head["stage_ms"]["gate_up"]
-    roof = {"bound": "hbm", "kernel": f"w4_expert_kernel<2,2,3,8> grouped gate/up (decode B={args.head_batch})",
+    roof = {"bound": "hbm", "kernel": f"w4_stream_kernel<2> grouped gate/up + SiLU (decode B={args.head_batch})",
             "achieved": head["gate_up_GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": head["gate_up_GBps"] / (HBM_PEAK / 1e9),
             "traffic": profiled_traffic() if args.head_batch == 64 else None,
