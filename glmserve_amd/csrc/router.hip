@@ -312,7 +312,8 @@ __device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
                                           const float* __restrict__ e_bias, int E, int topk,
                                           int norm_topk, float routed_scale,
                                           int* __restrict__ ids_out, float* __restrict__ w_out,
-                                          uint32_t* scratch) {
+                                          uint32_t* scratch, const uint32_t* pcode,
+                                          const float* pscore) {
     const int lane = threadIdx.x & 63;
     float score[NJ];
     uint32_t ch[NJ];   // order codes, 0 = no candidate
@@ -322,9 +323,14 @@ __device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
         score[j] = 0.0f;
         ch[j] = 0u;
         if (e < E) {
-            const float sc = sigmoid_fixed(COH ? ld_dev(lt + e) : lt[e]);
-            score[j] = sc;
-            ch[j] = order_code(sc + (e_bias ? e_bias[e] : 0.0f));
+            if (pcode) {   // codes and scores already computed by the caller
+                ch[j] = COH ? ld_dev(pcode + e) : pcode[e];
+                score[j] = COH ? ld_dev(pscore + e) : pscore[e];
+            } else {
+                const float sc = sigmoid_fixed(COH ? ld_dev(lt + e) : lt[e]);
+                score[j] = sc;
+                ch[j] = order_code(sc + (e_bias ? e_bias[e] : 0.0f));
+            }
         }
     }
     auto count_ge = [&](uint32_t v) {
@@ -334,11 +340,13 @@ __device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
             cnt += __popcll(__ballot(ch[j] >= v));
         return cnt;
     };
-    // 1. T = the largest code with at least k codes >= T.
+    // 1. T = the largest code with at least k codes >= T, two bits per step
+    //    (the three candidate counts of a step are independent).
     uint32_t T = 0u;
-    for (int b = 31; b >= 0; --b) {
-        const uint32_t cand = T | (1u << b);
-        if (count_ge(cand) >= topk) T = cand;
+    for (int b = 30; b >= 0; b -= 2) {
+        const uint32_t c1 = T | (1u << b), c2 = T | (2u << b), c3 = T | (3u << b);
+        const int n1 = count_ge(c1), n2 = count_ge(c2), n3 = count_ge(c3);
+        T = n3 >= topk ? c3 : n2 >= topk ? c2 : n1 >= topk ? c1 : T;
     }
     // 2. Winners; ties at T go to the lowest expert indices.
     int above = 0;
@@ -402,17 +410,21 @@ __device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
     }
 }
 
-// Dispatch on the experts per lane (E <= 64 * NJ).
+// Dispatch on the experts per lane (E <= 64 * NJ). pcode / pscore: the
+// token's order codes and scores when the caller computed them (else null).
 template <bool COH = false>
 __device__ __forceinline__ void topk_wave(const float* __restrict__ lt,
                                           const float* __restrict__ e_bias, int E, int topk,
                                           int norm_topk, float routed_scale,
                                           int* __restrict__ ids_out, float* __restrict__ w_out,
-                                          uint32_t* scratch) {
-    if (E <= 64) topk_wave_nj<COH, 1>(lt, e_bias, E, topk, norm_topk, routed_scale, ids_out, w_out, scratch);
-    else if (E <= 128) topk_wave_nj<COH, 2>(lt, e_bias, E, topk, norm_topk, routed_scale, ids_out, w_out, scratch);
-    else if (E <= 256) topk_wave_nj<COH, 4>(lt, e_bias, E, topk, norm_topk, routed_scale, ids_out, w_out, scratch);
-    else topk_wave_nj<COH, 8>(lt, e_bias, E, topk, norm_topk, routed_scale, ids_out, w_out, scratch);
+                                          uint32_t* scratch, const uint32_t* pcode = nullptr,
+                                          const float* pscore = nullptr) {
+#define GLMMOE_TOPK_ARGS lt, e_bias, E, topk, norm_topk, routed_scale, ids_out, w_out, scratch, pcode, pscore
+    if (E <= 64) topk_wave_nj<COH, 1>(GLMMOE_TOPK_ARGS);
+    else if (E <= 128) topk_wave_nj<COH, 2>(GLMMOE_TOPK_ARGS);
+    else if (E <= 256) topk_wave_nj<COH, 4>(GLMMOE_TOPK_ARGS);
+    else topk_wave_nj<COH, 8>(GLMMOE_TOPK_ARGS);
+#undef GLMMOE_TOPK_ARGS
 }
 
 __global__ __launch_bounds__(256) void router_topk_kernel(
@@ -770,7 +782,8 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const float* __restrict__ e_bias, int n, int H, int E, int epw, int topk, int norm_topk,
     float routed_scale, float* __restrict__ logits, float* __restrict__ xsum,
-    int* __restrict__ ids, float* __restrict__ w, DispOut d, int do_disp, int slices) {
+    int* __restrict__ ids, float* __restrict__ w, DispOut d, int do_disp, int slices,
+    uint32_t* __restrict__ cs) {
     extern __shared__ __align__(16) char small_lds[];
     __shared__ int last;
     SMALL_STAMP(0);
@@ -851,6 +864,12 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
             for (int cc = 0; cc < nchunks; ++cc)
                 total = total + part[(el2 * nchunks + cc) * kRouterTG + t];
             st_dev(logits + (size_t)(t0 + t) * E + e2, total);
+            // The selection's inputs, computed here in parallel: the score
+            // and the order code of choose = score + bias.
+            const float sc = sigmoid_fixed(total);
+            const size_t o = (size_t)(t0 + t) * E + e2;
+            st_dev(cs + o, order_code(sc + (e_bias ? e_bias[e2] : 0.0f)));
+            st_dev(reinterpret_cast<float*>(cs) + (size_t)n * E + o, sc);
         }
     }
     SMALL_STAMP(2);
@@ -868,7 +887,8 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     for (int t = tid >> 6; t < nt; t += kSmallThreads / 64)
         topk_wave<true>(logits + (size_t)(t0 + t) * E, e_bias, E, topk, norm_topk, routed_scale,
                         ids + (size_t)(t0 + t) * topk, w + (size_t)(t0 + t) * topk,
-                        tscratch[tid >> 6]);
+                        tscratch[tid >> 6], cs + (size_t)(t0 + t) * E,
+                        reinterpret_cast<const float*>(cs) + (size_t)n * E + (size_t)(t0 + t) * E);
     SMALL_STAMP(4);
     if (do_disp <= 0) return;
     drain_vm();
@@ -897,6 +917,8 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
 #ifndef GLMMOE_NO_SMALL_ROUTER
     if (n < kTiledMinTokens && H % kRouterKC == 0 && nchunks <= kSmallMaxChunks &&
         E <= 64 * kMaxPerLane && topk <= 8) {
+        // scratch: the order codes and scores [2][n][E] handed to the top-k.
+        if (!scratch || router_select_scratch_bytes(n, H, E) < (size_t)2 * n * E * 4) return -3;
         // Few tokens: spread the router weights over many workgroups; more
         // tokens: more experts per workgroup share the staged activations.
         int epw = n <= kRouterTG ? E / 128 : 240 / nchunks;
@@ -925,7 +947,7 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         }
         hipLaunchKernelGGL(router_small_kernel, grid, dim3(kSmallThreads), lds, s, x, wr, e_bias, n,
                            H, E, epw, topk, norm_topk, routed_scale, logits, xsum, ids, w,
-                           dd ? *disp : DispOut{}, mode, slices);
+                           dd ? *disp : DispOut{}, mode, slices, reinterpret_cast<uint32_t*>(scratch));
         if (hipGetLastError() != hipSuccess) return -4;
         if (mode < 0) return launch_router_topk(logits, e_bias, n, E, topk, norm_topk, routed_scale, ids, w, s);
         if (dispatched) *dispatched = mode == 1;
