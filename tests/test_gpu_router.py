@@ -147,3 +147,45 @@ def test_layer_routing_bit_exact_large_batches(oracle, n):
     xf = (xb.astype(np.uint32) << 16).view(np.float32).reshape(n, H // 128, 128)
     rx = np.cumsum(xf, axis=2, dtype=np.float32)[:, :, -1].reshape(-1)
     assert np.array_equal(xs.view(np.uint32), rx.view(np.uint32))
+
+
+@pytest.mark.parametrize("H,E,k,n", [(1024, 64, 8, 1), (2048, 100, 6, 37), (8192, 512, 8, 9),
+                                     (6144, 256, 8, 255), (256, 16, 4, 8)])
+def test_layer_routing_bit_exact_small_batches(oracle, H, E, k, n):
+    """Below 256 tokens the layer computes logits, top-k and dispatch in one
+    launch (workgroups hand over through tickets). ids, weights, the
+    activation group sums and the dispatch must equal the oracle's bit for
+    bit, with duplicated router rows forcing exact ties, E not a multiple of
+    64, E = 512 and the largest hidden size."""
+    from moe_cases import SynthLayer
+    from glmserve_amd.ops import ws_tensor
+    L = SynthLayer(H, E, k, 128, seed=12)
+    L.router_w[5] = L.router_w[3]
+    L.router_w[E - 1] = L.router_w[3]
+    x = L.x(n, seed=n + 3)
+    ws = L.layer.alloc_workspace(n)
+    ws.fill_(0xFF)
+    out = torch.empty(n, H, dtype=torch.float32, device="cuda")
+    L.layer.forward(x, out, ws)
+    torch.cuda.synchronize()
+    v = L.layer.workspace_view(n, ws)
+    ids = ws_tensor(None, v.topk_ids, ws, torch.int32, n * k).cpu().numpy().reshape(n, k)
+    w = ws_tensor(None, v.topk_w, ws, torch.float32, n * k).cpu().numpy().reshape(n, k)
+    xs = ws_tensor(None, v.xsum, ws, torch.float32, n * (H // 128)).cpu().numpy()
+    offs = ws_tensor(None, v.expert_offsets, ws, torch.int32, E + 1).cpu().numpy()
+    st = ws_tensor(None, v.sorted_token_ids, ws, torch.int32, n * k).cpu().numpy()
+    xb = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    wb = L.router_w.view(torch.int16).cpu().numpy().view(np.uint16)
+    logits = oracle.router_logits_bf16(xb, wb)
+    rid, rw = oracle.router_topk(logits, L.e_bias.cpu().numpy(), k, True, 2.5)
+    assert np.array_equal(ids, rid)
+    assert np.array_equal(w.view(np.uint32), rw.view(np.uint32))
+    xf = (xb.astype(np.uint32) << 16).view(np.float32).reshape(n, H // 128, 128)
+    rx = np.cumsum(xf, axis=2, dtype=np.float32)[:, :, -1].reshape(-1)
+    assert np.array_equal(xs.view(np.uint32), rx.view(np.uint32))
+    # Stable counting sort of the (token, slot) rows by expert.
+    flat = rid.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    assert np.array_equal(st, (order // k).astype(np.int32))
+    ref_offs = np.concatenate([[0], np.cumsum(np.bincount(flat, minlength=E))]).astype(np.int32)
+    assert np.array_equal(offs, ref_offs)
