@@ -60,6 +60,29 @@ def time_layer(L, n, steps, warmup, seed, torch):
     return ms, U, (x, ws, out)
 
 
+def time_layer_cold(L, n, reps, seed, torch):
+    """Per-call time with the caches cold: before each timed call a 512 MiB
+    scrub buffer is rewritten (more than the 256 MiB of L2 + Infinity Cache),
+    so the weights come from HBM. Only the layer call is inside the events."""
+    x = L.x(n, seed)
+    ws = L.layer.alloc_workspace(n)
+    out = torch.empty(n, H, dtype=torch.float32, device="cuda")
+    scrub = torch.empty(512 << 20, dtype=torch.uint8, device="cuda")
+    L.layer.forward(x, out, ws)
+    total = 0.0
+    for i in range(reps):
+        scrub.fill_(i & 0xFF)
+        t0 = torch.cuda.Event(enable_timing=True)
+        t1 = torch.cuda.Event(enable_timing=True)
+        t0.record()
+        L.layer.forward(x, out, ws)
+        t1.record()
+        torch.cuda.synchronize()
+        total += t0.elapsed_time(t1)
+    del scrub
+    return total / reps
+
+
 def stage_times(L, n, bufs, steps, torch):
     """Per-stage average ms from the library's event ring (same stream)."""
     import ctypes
@@ -272,6 +295,15 @@ def main():
         log("bench: sweep prefill 4096 (router-chosen routing)")
         sweep["prefill_4096_router_routing"] = measure(4096, max(3, args.steps // 10), 2)
     sweep[f"decode_B{args.head_batch}"] = head
+    if not args.no_sweep:
+        for n in (1, 64):
+            log(f"bench: sweep cold-cache B={n}")
+            ms = time_layer_cold(L, n, 10, 100 + n, torch)
+            hot = sweep[f"decode_B{n}"]
+            sweep[f"decode_B{n}_cold"] = {
+                "n": n, "ms": ms, "tokens_per_s": n / (ms * 1e-3),
+                "hbm_frac_layer": hot["alg_bytes"] / (ms * 1e-3) / HBM_PEAK,
+                "note": "512 MiB scrub rewritten before each timed call (L2 and Infinity Cache cold)"}
     if not args.no_sweep:
         log("bench: sweep spec-verify 520 (configs[3], Zipf s=1.1 skew)")
         LZ = SynthLayer(H, E, K, I, seed=2, zipf_s=1.1)

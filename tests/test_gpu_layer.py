@@ -126,3 +126,23 @@ def test_decode_poisoned_workspace_deterministic():
             outs.append(out.cpu())
         assert torch.isfinite(outs[0]).all(), n
         assert torch.equal(outs[0], outs[1]), n
+
+
+def test_batch_composition_bit_identical():
+    # A token's routing, expert outputs and combine do not depend on the other
+    # tokens of the batch (MFMA columns are independent, the combine adds in
+    # slot order then the shared expert), so the same tokens give
+    # bit-identical outputs at batch 1, 16 and 17 -- across different tile
+    # layouts, workgroup assignments and ticket groupings.
+    L = SynthLayer(6144, 256, 8, 2048, seed=1)
+    x = L.x(17, 21)
+    outs = {}
+    for n in (17, 16, 1):
+        ws = L.layer.alloc_workspace(n)
+        out = torch.empty(n, L.H, dtype=torch.float32, device="cuda")
+        L.layer.forward(x[:n].contiguous(), out, ws)
+        torch.cuda.synchronize()
+        outs[n] = out.cpu()
+    assert torch.isfinite(outs[17]).all()
+    assert torch.equal(outs[16], outs[17][:16])
+    assert torch.equal(outs[1], outs[17][:1])
