@@ -54,6 +54,15 @@ ExpertPtrs ptrs(const glmmoe_w4a16_layer* L) {
                       L->sh_down_s};
 }
 
+// The router scratch is free once routing is done; a large batch's dispatch
+// uses it for its chunk histograms (when it is large enough).
+template <class Layer>
+int* dispatch_scratch(float* rpart, const Layer* L, int n) {
+    const size_t need = dispatch_scratch_bytes(n, L->topk, L->n_experts);
+    if (!need || router_select_scratch_bytes(n, L->hidden, L->n_experts) < need) return nullptr;
+    return reinterpret_cast<int*>(rpart);
+}
+
 // Carves the workspace; with base == nullptr only computes the size.
 size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v) {
     const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
@@ -162,7 +171,8 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     mark(GLMMOE_STAGE_DISPATCH, s);
     int rc = dispatched ? 0
                         : launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids,
-                                          v.sorted_row, v.inv, v.tiles, v.ntiles, T, sh, 1, s);
+                                          v.sorted_row, v.inv, v.tiles, v.ntiles, T, sh, 1, s,
+                                          dispatch_scratch(v.rpart, L, n));
     if (rc) return rc;
     const ExpertPtrs P = ptrs(L);
     mark(GLMMOE_STAGE_GATE_UP, s);
@@ -195,7 +205,8 @@ int run_experts8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, const int*
     mark(GLMMOE_STAGE_DISPATCH, s);
     rc = dispatched ? 0
                     : launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids,
-                                      v.sorted_row, v.inv, v.tiles, v.ntiles, kBigRows, sh, 1, s);
+                                      v.sorted_row, v.inv, v.tiles, v.ntiles, kBigRows, sh, 1, s,
+                                      dispatch_scratch(v.rpart, L, n));
     if (rc) return rc;
     const Fp8Ptrs P = ptrs8(L);
     mark(GLMMOE_STAGE_GATE_UP, s);

@@ -62,9 +62,16 @@ __host__ __device__ constexpr int dispatch_lds_ints() {
 
 // COH: read ids with device-coherent loads (ids written by other workgroups
 // of the same launch). lds: dispatch_lds_ints<NT>() ints of LDS.
+// Multi-workgroup form: this workgroup permutes ids [i0, i1) (chunk blk of
+// nblk); bcounts [nblk][E] holds every chunk's expert histogram, from which
+// the expert bases and this chunk's start inside each expert follow; chunk 0
+// also writes the offsets, the shared rows and the tile list. With
+// bcounts == nullptr the workgroup does the whole dispatch alone.
 template <int NT, bool COH = false>
 __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int E,
-                               const DispOut& d, int* lds) {
+                               const DispOut& d, int* lds, int i0 = 0, int i1 = -1,
+                               const int* __restrict__ bcounts = nullptr, int nblk = 1,
+                               int blk = 0) {
     auto id_at = [&](int i) { return COH ? ld_dev(ids + i) : ids[i]; };
     int* cnt = lds;
     int* cursor = cnt + (kDispMaxE + 2);
@@ -76,29 +83,46 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
     int nbits = 0;
     while ((1 << nbits) < E) ++nbits;
 
+    if (i1 < 0) i1 = total;
     for (int e = tid; e <= kDispMaxE; e += NT) cnt[e] = 0;
     for (int i = tid; i < (NT / 64) * kDispMaxE; i += NT) (&wc[0][0])[i] = 0;
     __syncthreads();
-    for (int i = tid; i < total; i += NT) {
-        const int e = id_at(i);
-        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    if (bcounts) {
+        // cnt = the experts' totals; ntl (scratch here) = ids of expert e in
+        // the chunks before this one.
+        for (int e = tid; e < E; e += NT) {
+            int before = 0, all = 0;
+            for (int b = 0; b < nblk; ++b) {
+                const int c = bcounts[(size_t)b * E + e];
+                before += b < blk ? c : 0;
+                all += c;
+            }
+            cnt[e] = all;
+            ntl[e] = before;
+        }
+    } else {
+        for (int i = tid; i < total; i += NT) {
+            const int e = id_at(i);
+            if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+        }
     }
     __syncthreads();
 
     // Exclusive prefix over experts.
     wave0_exclusive_scan(cnt, E, pre);
     __syncthreads();
+    const bool lead = blk == 0;
     for (int e = tid; e <= E; e += NT) {
-        d.offsets[e] = pre[e];
-        if (e < E) cursor[e] = pre[e];
+        if (lead) d.offsets[e] = pre[e];
+        if (e < E) cursor[e] = pre[e] + (bcounts ? ntl[e] : 0);
     }
-    if ((d.mode & 1) && tid == 0) d.offsets[E + 1] = total + (d.with_shared ? n : 0);
+    if (lead && (d.mode & 1) && tid == 0) d.offsets[E + 1] = total + (d.with_shared ? n : 0);
     __syncthreads();
 
     // Stable permute.
-    for (int base = 0; base < total; base += NT) {
+    for (int base = i0; base < i1; base += NT) {
         const int i = base + tid;
-        const int e = i < total ? id_at(i) : -1;
+        const int e = i < i1 ? id_at(i) : -1;
         const bool valid = e >= 0 && e < E;
         uint64_t m = __ballot(valid);
         for (int b = 0; b < nbits; ++b) {
@@ -127,7 +151,14 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
         __syncthreads();
     }
 
-    if (!(d.mode & 1)) return;
+    if (!(d.mode & 1) || !lead) return;
+    // The tile list below takes each expert's first row as cursor - count,
+    // i.e. it needs the cursors at the experts' ends. One workgroup doing the
+    // whole dispatch leaves them there; a chunk's cursors stop at its own ids.
+    if (bcounts) {
+        for (int e = tid; e < E; e += NT) cursor[e] = pre[e] + cnt[e];
+        __syncthreads();
+    }
 
     // Shared-expert rows: one per token, after all routed rows.
     if (d.with_shared)

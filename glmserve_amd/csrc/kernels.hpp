@@ -61,9 +61,11 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
                          const DispOut* disp = nullptr, bool* dispatched = nullptr);
 int launch_router_topk(const float* logits, const float* e_bias, int n, int E, int topk,
                        int norm_topk, float routed_scale, int* ids, float* w, hipStream_t s);
+// Scratch (bytes) the multi-workgroup dispatch of a large batch uses (0 below it).
+size_t dispatch_scratch_bytes(int n, int topk, int E);
 int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,
                     int* sorted_slot, int* inv, int* tiles, int* ntiles, int tile_rows,
-                    int with_shared, int mode, hipStream_t s);
+                    int with_shared, int mode, hipStream_t s, int* scratch = nullptr);
 int launch_pack_w4(const uint8_t* q, const void* sc, int sc_bf16, int n_mats, int rows, int K,
                    uint8_t* pq, uint16_t* ps, hipStream_t s);
 int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
