@@ -186,7 +186,7 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
              : launch_down(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_COMBINE, s);
-    rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s);
+    rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s, big);
     if (rc) return rc;
     end_call(s);
     return GLMMOE_OK;
@@ -217,7 +217,7 @@ int run_experts8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, const int*
     rc = launch_down_fp8(P, v.hq, v.hscale, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_COMBINE, s);
-    rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s);
+    rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s, true);
     if (rc) return rc;
     end_call(s);
     return GLMMOE_OK;

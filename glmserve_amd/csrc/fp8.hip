@@ -402,9 +402,10 @@ __device__ __forceinline__ void f8_epilogue(const F8Args& a, const BigItem& cur,
 #pragma unroll
                     for (int j = 0; j < 4; ++j) {
                         const int f = cur.g * 256 + wn * 64 + jb * 32 + 8 * j + 4 * h;
-                        *reinterpret_cast<float4*>(a.dpart + row * a.H + f) =
-                            make_float4(acc[jb][tb][4 * j], acc[jb][tb][4 * j + 1],
-                                        acc[jb][tb][4 * j + 2], acc[jb][tb][4 * j + 3]);
+                        // bf16 partial rows (the combine adds them in fp32).
+                        *reinterpret_cast<uint2*>(reinterpret_cast<uint16_t*>(a.dpart) + row * a.H + f) =
+                            uint2{pack_bf16x2(acc[jb][tb][4 * j], acc[jb][tb][4 * j + 1]),
+                                  pack_bf16x2(acc[jb][tb][4 * j + 2], acc[jb][tb][4 * j + 3])};
                     }
             }
         }

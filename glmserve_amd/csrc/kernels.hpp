@@ -80,8 +80,9 @@ int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, const float* xsum
 int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
                     const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
                     hipStream_t s);
+// bf16: the partial rows are bf16 (written by the large-group kernels).
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
-                   int with_shared, float* out, hipStream_t s);
+                   int with_shared, float* out, hipStream_t s, bool bf16 = false);
 
 int launch_quant_act_fp8(const uint16_t* x, int n, int K, uint8_t* q, float* scale,
                          hipStream_t s);

@@ -51,7 +51,8 @@ struct BigArgs {
     const uint16_t* src;     // x [n, H] (NMAT = 2, rows gathered) or h [R, I] (NMAT = 1)
     const float* gsum;       // xsum [n, H/128] (NMAT = 2) or hsum [R, I/128] (NMAT = 1)
     const int4* tiles; const int* ntiles; const int* rows_tok;
-    uint16_t* h; float* hsum; float* dpart;
+    uint16_t* h; float* hsum;
+    float* dpart;            // NMAT = 1: bf16 [R, H] partial rows (in the fp32-sized region)
     int H, I, E;
 };
 
@@ -366,15 +367,18 @@ __device__ __forceinline__ void big_epilogue(const BigArgs& a, const BigItem& cu
         }
         __builtin_amdgcn_s_barrier();   // partials consumed before the next item reuses them
     } else {
+        // Per-row expert outputs as bf16 (the combine adds them in fp32):
+        // half the bytes of the largest write and read of a prefill layer.
+        uint16_t* d16 = reinterpret_cast<uint16_t*>(a.dpart);
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb) {
-            float* dbase = a.dpart + (size_t)cur.r0 * a.H + cur.g * 256 + wn * 64 + jb * 32;
+            uint16_t* dbase = d16 + (size_t)cur.r0 * a.H + cur.g * 256 + wn * 64 + jb * 32;
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
                 for (int i = 0; i < 16; ++i) {
                     const int lr = acc_row(wm, tb, i, h);
-                    if (lr < cur.nr) dbase[lr * a.H + col] = acc[jb][tb][i];
+                    if (lr < cur.nr) dbase[lr * a.H + col] = (uint16_t)(pack_bf16x2(acc[jb][tb][i], 0.0f) & 0xffffu);
                 }
         }
     }

@@ -884,6 +884,19 @@ static int launch_stream(const ExpArgs& a, long max_work, hipStream_t s) {
 // Combine: out[t] = (((0 + w0*y0) + w1*y1) + ...) + y_shared, slot order then
 // shared (src/model_glm52.cpp:1133-1152). Gather, no atomics: deterministic.
 // ---------------------------------------------------------------------------
+template <bool BF16>
+__device__ __forceinline__ float4 combine_row(const float* dpart, size_t row, int H, int f4) {
+    if constexpr (BF16) {
+        const uint2 v = reinterpret_cast<const uint2*>(reinterpret_cast<const uint16_t*>(dpart) + row * H)[f4];
+        return make_float4(bf16_to_f32(v.x & 0xffffu), __uint_as_float(v.x & 0xffff0000u),
+                           bf16_to_f32(v.y & 0xffffu), __uint_as_float(v.y & 0xffff0000u));
+    } else {
+        return reinterpret_cast<const float4*>(dpart + row * H)[f4];
+    }
+}
+
+// BF16: the partial rows are bf16 (large-group kernels), else fp32.
+template <bool BF16>
 __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ dpart,
                                                       const int* __restrict__ inv,
                                                       const float* __restrict__ w, int n,
@@ -895,12 +908,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
     for (int s = 0; s < topk; ++s) {
         const float ws = w[(size_t)t * topk + s];
-        const float4 y = reinterpret_cast<const float4*>(dpart + (size_t)inv[(size_t)t * topk + s] * H)[f4];
+        const float4 y = combine_row<BF16>(dpart, (size_t)inv[(size_t)t * topk + s], H, f4);
         acc.x = acc.x + ws * y.x; acc.y = acc.y + ws * y.y;
         acc.z = acc.z + ws * y.z; acc.w = acc.w + ws * y.w;
     }
     if (with_shared) {
-        const float4 y = reinterpret_cast<const float4*>(dpart + ((size_t)n * topk + t) * H)[f4];
+        const float4 y = combine_row<BF16>(dpart, (size_t)n * topk + t, H, f4);
         acc.x = acc.x + y.x; acc.y = acc.y + y.y; acc.z = acc.z + y.z; acc.w = acc.w + y.w;
     }
     reinterpret_cast<float4*>(out + (size_t)t * H)[f4] = acc;
@@ -984,10 +997,14 @@ int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const
 }
 
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
-                   int with_shared, float* out, hipStream_t s) {
+                   int with_shared, float* out, hipStream_t s, bool bf16) {
     dim3 grid((unsigned)((H / 4 + 255) / 256), (unsigned)n);
-    hipLaunchKernelGGL(combine_kernel, grid, dim3(256), 0, s, dpart, inv, w, n, topk, H,
-                       with_shared, out);
+    if (bf16)
+        hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, s, dpart, inv, w, n, topk, H,
+                           with_shared, out);
+    else
+        hipLaunchKernelGGL(combine_kernel<false>, grid, dim3(256), 0, s, dpart, inv, w, n, topk,
+                           H, with_shared, out);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

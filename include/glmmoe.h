@@ -136,7 +136,8 @@ typedef struct glmmoe_layer_ws {
     int* ntiles;          /* [1] */
     uint16_t* h;          /* [R, I] bf16 SiLU(gate) * up */
     float* hsum;          /* [R, I/128] group sums of h (large-group path) */
-    float* dpart;         /* [R, H] fp32 per-row expert outputs (unweighted) */
+    float* dpart;         /* [R, H] per-row expert outputs (unweighted): fp32 below 1024 grouped
+                             rows (n*topk + n), bf16 (first half of the region) from there */
     size_t bytes;         /* total workspace bytes */
 } glmmoe_layer_ws;
 
@@ -229,7 +230,7 @@ typedef struct glmmoe_fp8_ws {
     int* ntiles;          /* [1] */
     uint8_t* hq;          /* [R, I] e4m3 */
     float* hscale;        /* [R, I/128] */
-    float* dpart;         /* [R, H] fp32 */
+    float* dpart;         /* [R, H] bf16 per-row expert outputs (fp32-sized region) */
     size_t bytes;
 } glmmoe_fp8_ws;
 
