@@ -700,16 +700,15 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kSmallThreads = 512;
 #ifdef GLMMOE_SMALL_TRACE
-// Diagnostics: shader-clock stamps of the phases of the workgroup that runs
-// the dispatch (slot 8 + i: of workgroup 0).
-__device__ unsigned long long g_small_trace[16];
+// Diagnostics: shader-clock stamps of each workgroup's phases (one row per
+// workgroup: start, staged, logits stored, top-k start/end, dispatch
+// start/end).
+__device__ unsigned long long g_small_trace[8192][8];
 #define SMALL_STAMP(i)                                                               \
     do {                                                                             \
         const unsigned long long ts_ = __builtin_amdgcn_s_memtime();                 \
-        if (threadIdx.x == 0) {                                                      \
-            if (blockIdx.x == 0 && blockIdx.y == 0) g_small_trace[8 + (i)] = ts_;    \
-            g_small_trace[(i)] = ts_;                                                \
-        }                                                                            \
+        if (threadIdx.x == 0)                                                        \
+            g_small_trace[blockIdx.y * gridDim.x + blockIdx.x][(i)] = ts_;           \
     } while (0)
 #else
 #define SMALL_STAMP(i) do {} while (0)
@@ -899,7 +898,9 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     }
     __syncthreads();
     if (!last) return;
+    SMALL_STAMP(5);
     dispatch_block<kSmallThreads, true>(ids, n, topk, E, d, reinterpret_cast<int*>(small_lds));
+    SMALL_STAMP(6);
 }
 
 size_t router_select_scratch_bytes(int n, int H, int E) {
@@ -919,9 +920,20 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         E <= 64 * kMaxPerLane && topk <= 8) {
         // scratch: the order codes and scores [2][n][E] handed to the top-k.
         if (!scratch || router_select_scratch_bytes(n, H, E) < (size_t)2 * n * E * 4) return -3;
-        // Few tokens: spread the router weights over many workgroups; more
-        // tokens: more experts per workgroup share the staged activations.
-        int epw = n <= kRouterTG ? E / 128 : 240 / nchunks;
+        // Experts per workgroup: as few as fill every CU once (one round of
+        // workgroups; with fewer experts per workgroup each thread runs
+        // fewer tokens), as many as keep a second round away.
+        static int cus = 0;
+        if (!cus) {
+            int dev = 0;
+            cus = 256;
+            if (hipGetDevice(&dev) == hipSuccess)
+                (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
+        }
+        const int ntg = (n + kRouterTG - 1) / kRouterTG;
+        // (One token group: two experts per workgroup, half as many copies
+        // of the staged activations as one would take.)
+        int epw = ntg == 1 ? E / 128 : (E * ntg + cus - 1) / cus;
         if (epw > kSmallThreads / nchunks) epw = kSmallThreads / nchunks;
         if (epw < 1) epw = 1;
         int slices = 1;
