@@ -294,19 +294,12 @@ __device__ __forceinline__ void kmax_dpp(uint32_t& h, uint32_t& l) {
 
 constexpr int kTopkScratch = 40;   // LDS words per wave for topk_wave
 
-// Selection for token row lt (one wave; every lane calls it). The k winners
-// of the k rounds of cuda/moe_router.cu:48-53 are exactly the k largest keys
-// (order code of choose, ~expert), in descending key order, so:
-//   1. the k-th largest order code T by a most-significant-bit-first search
-//      (one ballot count per bit),
-//   2. the winners: codes above T, plus the lowest-index experts among
-//      those equal to T (the key's tie order),
-//   3. their descending order by ranking the k winners against each other,
-//   4. the weight sum in that order (the reference's summation order) and
-//      the normalized weights.
-// scratch: kTopkScratch LDS words private to the wave. COH: read the logits
-// with device-coherent loads and store ids/weights with device-coherent
-// stores.
+// Selection for token row lt (one wave; every lane calls it): the k rounds of
+// cuda/moe_router.cu:48-53 over keys (order code of choose, ~expert), each
+// lane's keys pre-sorted so a round looks at one head per lane. scratch is
+// unused (kept for the callers' LDS layout). COH: read the logits (or codes
+// and scores) with device-coherent loads and store ids/weights with
+// device-coherent stores.
 template <bool COH, int NJ>
 __device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
                                           const float* __restrict__ e_bias, int E, int topk,
@@ -333,79 +326,78 @@ __device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
             }
         }
     }
-    auto count_ge = [&](uint32_t v) {
-        int cnt = 0;
+    // 1. Keys (order code, ~expert): a larger key is chosen first; equal
+    //    codes prefer the lower expert. Each lane sorts its NJ keys, largest
+    //    first, scores alongside (a fixed compare-exchange network).
+    uint32_t kl[NJ];
 #pragma unroll
-        for (int j = 0; j < NJ; ++j)
-            cnt += __popcll(__ballot(ch[j] >= v));
-        return cnt;
-    };
-    // 1. T = the largest code with at least k codes >= T, two bits per step
-    //    (the three candidate counts of a step are independent).
-    uint32_t T = 0u;
-    for (int b = 30; b >= 0; b -= 2) {
-        const uint32_t c1 = T | (1u << b), c2 = T | (2u << b), c3 = T | (3u << b);
-        const int n1 = count_ge(c1), n2 = count_ge(c2), n3 = count_ge(c3);
-        T = n3 >= topk ? c3 : n2 >= topk ? c2 : n1 >= topk ? c1 : T;
-    }
-    // 2. Winners; ties at T go to the lowest expert indices.
-    int above = 0;
+    for (int j = 0; j < NJ; ++j) kl[j] = ch[j] ? ~(uint32_t)(lane + 64 * j) : 0u;
 #pragma unroll
-    for (int j = 0; j < NJ; ++j)
-        above += __popcll(__ballot(ch[j] > T));
-    const int need = topk - above;
-    const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
-    uint32_t* s_hi = scratch;
-    uint32_t* s_lo = scratch + 8;
-    uint32_t* s_sc = scratch + 16;
-    int* s_id = reinterpret_cast<int*>(scratch + 24);
-    float* s_w = reinterpret_cast<float*>(scratch + 32);
-    int ties = 0, slot = 0;
+    for (int i = 0; i < NJ; ++i)
 #pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        {
-            const uint64_t tm = __ballot(ch[j] == T);
-            const bool sel = ch[j] > T || (ch[j] == T && ties + __popcll(tm & below) < need);
-            ties += __popcll(tm);
-            const uint64_t sm = __ballot(sel);
-            if (sel) {
-                const int p = slot + __popcll(sm & below);
-                s_hi[p] = ch[j];
-                s_lo[p] = ~(uint32_t)(lane + 64 * j);
-                s_sc[p] = __float_as_uint(score[j]);
-            }
-            slot += __popcll(sm);
+        for (int j = 0; j + 1 < NJ - i; ++j) {
+            const bool up = ch[j + 1] > ch[j] || (ch[j + 1] == ch[j] && kl[j + 1] > kl[j]);
+            const uint32_t h0 = ch[j], l0 = kl[j];
+            const float s0 = score[j];
+            ch[j] = up ? ch[j + 1] : ch[j];
+            kl[j] = up ? kl[j + 1] : kl[j];
+            score[j] = up ? score[j + 1] : score[j];
+            ch[j + 1] = up ? h0 : ch[j + 1];
+            kl[j + 1] = up ? l0 : kl[j + 1];
+            score[j + 1] = up ? s0 : score[j + 1];
         }
-    }
-    __builtin_amdgcn_wave_barrier();
-    // 3. Rank of winner i = number of winners with a larger key.
-    if (lane < topk) {
-        const uint32_t h = s_hi[lane], l = s_lo[lane];
-        int rank = 0;
-#pragma unroll
-        for (int q = 0; q < 8; ++q)
-            if (q < topk) {
-                const uint32_t hq = s_hi[q], lq = s_lo[q];
-                rank += (hq > h || (hq == h && lq > l)) ? 1 : 0;
-            }
-        s_id[rank] = (int)~l;
-        s_w[rank] = __uint_as_float(s_sc[lane]);
-    }
-    __builtin_amdgcn_wave_barrier();
-    // 4. Weight sum in selection order, then the normalized weights.
+    // 2. k rounds, as cuda/moe_router.cu:48-53 does them: the largest lane
+    //    head over the wave (a max over each 16-lane row with DPP row
+    //    rotations, then the 4 row maxima); the owner lane drops its head.
+    float wsel[8];
+    int idsel[8];
     float wsum = 0.0f;
 #pragma unroll
-    for (int q = 0; q < 8; ++q)
-        if (q < topk) wsum = wsum + s_w[q];
-    if (lane < topk) {
-        float v = s_w[lane];
-        if (norm_topk && wsum > 0.0f) v = v / wsum;
-        if (COH) {
-            st_dev(ids_out + lane, s_id[lane]);
-            st_dev(w_out + lane, v * routed_scale);
-        } else {
-            ids_out[lane] = s_id[lane];
-            w_out[lane] = v * routed_scale;
+    for (int k = 0; k < 8; ++k) {
+        if (k >= topk) break;
+        uint32_t h = ch[0], l = kl[0];
+        kmax_dpp<0x121>(h, l);
+        kmax_dpp<0x122>(h, l);
+        kmax_dpp<0x124>(h, l);
+        kmax_dpp<0x128>(h, l);
+        uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)h, 0);
+        uint32_t bl = (uint32_t)__builtin_amdgcn_readlane((int)l, 0);
+#pragma unroll
+        for (int r = 1; r < 4; ++r)
+            kmax(bh, bl, (uint32_t)__builtin_amdgcn_readlane((int)h, 16 * r),
+                 (uint32_t)__builtin_amdgcn_readlane((int)l, 16 * r));
+        const int e = (int)~bl;               // uniform winner
+        const int owner = e & 63;
+        const float sw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score[0]), owner));
+        if (lane == owner) {
+#pragma unroll
+            for (int j = 0; j + 1 < NJ; ++j) {
+                ch[j] = ch[j + 1];
+                kl[j] = kl[j + 1];
+                score[j] = score[j + 1];
+            }
+            ch[NJ - 1] = 0u;
+            kl[NJ - 1] = 0u;
+        }
+        idsel[k] = e;
+        wsel[k] = sw;
+        wsum = wsum + sw;
+    }
+    // 3. Weights in selection order, normalized by their sum in that order.
+    (void)scratch;
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+        if (k >= topk) break;
+        if (lane == k) {
+            float v = wsel[k];
+            if (norm_topk && wsum > 0.0f) v = v / wsum;
+            if (COH) {
+                st_dev(ids_out + k, idsel[k]);
+                st_dev(w_out + k, v * routed_scale);
+            } else {
+                ids_out[k] = idsel[k];
+                w_out[k] = v * routed_scale;
+            }
         }
     }
 }
