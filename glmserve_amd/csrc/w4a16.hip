@@ -529,6 +529,82 @@ constexpr int kSActDma = 9;  // activation + group-sum DMAs per wave per batch
 constexpr int kSPGU = GLMMOE_SP_GU;
 constexpr int kSPDown = GLMMOE_SP_DOWN;
 
+// Stream table step: {expert, row0, nrows, block group}, the 16 token ids,
+// then {first batch, batches, tail item or -1, 0}.
+constexpr int kSTabInts = 24;
+
+// Work schedule. An item (tile, block group) covers all K in BPI batches of
+// 16 groups; its result is the batch totals added in batch order,
+// T = ((t_0 + t_1) + t_2) ..., each t_b accumulated from zero. After R full
+// rounds of items over the workgroups, the rem items left over would keep rem
+// workgroups busy for a whole item while the rest idle; when splitting them
+// by batch shortens that last round, each of their batches is a unit of its
+// own (a "part"). A part stores t_b; at the end of the kernel the workgroup
+// that holds an item's last part (by ticket) adds the stored t_b in batch
+// order and finishes the item. Whole or split, an item's arithmetic is the
+// same, so results do not depend on how a batch's work was spread.
+constexpr int kMaxTail = 256;          // split items per launch
+constexpr int kMaxTailParts = 1024;    // their parts
+static __device__ unsigned int g_tail_tick[kMaxTail];
+static __device__ float g_tail_part[kMaxTailParts * 8 * 512];   // [part][value][thread] t_b
+
+struct SSched {
+    int R, rem, split, nunits;
+};
+
+__device__ __forceinline__ SSched s_sched(int total, int nwg, int base, int BPI) {
+    SSched sc;
+    sc.R = total / nwg;
+    sc.rem = total - sc.R * nwg;
+    const int parts = sc.rem * BPI;
+    // With no full round (a handful of items) the split's ticket and
+    // finishing cost more than the shorter round saves.
+    sc.split = BPI > 1 && sc.R > 0 && sc.rem > 0 && sc.rem <= kMaxTail && parts <= kMaxTailParts &&
+               (parts + nwg - 1) / nwg < BPI;
+#ifdef GLMMOE_NO_TAIL_SPLIT
+    sc.split = 0;
+#endif
+    if (sc.split)
+        sc.nunits = sc.R + (base < parts ? (parts - base + nwg - 1) / nwg : 0);
+    else
+        sc.nunits = base < total ? (total - base + nwg - 1) / nwg : 0;
+    return sc;
+}
+
+// Unit u of workgroup `base`: item, first batch, batches, tail item (-1: whole).
+__device__ __forceinline__ int4 s_unit(const SSched& sc, int base, int nwg, int BPI, int u) {
+    if (sc.split && u >= sc.R) {
+        const int t = base + (u - sc.R) * nwg;
+        return int4{sc.R * nwg + t / BPI, t % BPI, 1, t / BPI};
+    }
+    return int4{base + u * nwg, 0, BPI, -1};
+}
+
+// Fills stream-table steps [k0, k0 + cnt) (whole workgroup; the caller
+// synchronizes afterwards).
+__device__ __forceinline__ void fill_stream_table(const ExpArgs& a, int* table, const SSched& sc,
+                                                  int base, int nwg, int ngrp, int BPI, int k0,
+                                                  int cnt) {
+    for (int i = threadIdx.x; i < cnt * kSTabInts; i += blockDim.x) {
+        const int k = i / kSTabInts, f = i % kSTabInts;
+        const int4 un = s_unit(sc, base, nwg, BPI, k0 + k);
+        const int4 tile = a.tiles[un.x / ngrp];
+        int v;
+        if (f == 0) v = tile.x;
+        else if (f == 1) v = tile.y;
+        else if (f == 2) v = tile.z;
+        else if (f == 3) v = un.x % ngrp;
+        else if (f < 20) {
+            const int row = f - 4;
+            v = a.rows_tok ? a.rows_tok[tile.y + (row < tile.z ? row : 0)] : 0;
+        } else if (f == 20) v = un.y;
+        else if (f == 21) v = un.z;
+        else if (f == 22) v = un.w;
+        else v = 0;
+        table[i] = v;
+    }
+}
+
 template <int NMAT>
 struct SLay {
     static constexpr int kRowB = kSGB * 256;                 // one row's 16 groups
@@ -538,7 +614,7 @@ struct SLay {
     static constexpr int kJunk = 2 * kBuf;                   // placeholder DMA target
     static constexpr int kRed = kJunk + 256;                 // [8][16] h group-sum partials
     static constexpr int kTab = kRed + 8 * 16 * 4;
-    static constexpr int kTotal = kTab + kTable * kTabInts * 4;
+    static constexpr int kTotal = kTab + kTable * kSTabInts * 4;
     static_assert(kTotal <= 160 * 1024, "one workgroup's LDS");
     static constexpr int P = NMAT == 2 ? kSPGU : kSPDown;    // weight groups in flight per wave
     static_assert(kSGB % P == 0, "ring slots stay static across batches");
@@ -556,14 +632,17 @@ __device__ __forceinline__ void gload8(u32x2& d, const void* base, uint32_t voff
 struct SWItem {
     const uint4* wq[2];
     const uint16_t* ws[2];
+    int ng;   // weight groups of the unit
 };
 
 template <int NMAT>
 __device__ __forceinline__ SWItem sw_item(const ExpArgs& a, const int* table, int k, int wave,
                                           int nfb, int KG) {
-    const uint4 h = lds_bcast16(lds_addr(table + k * kTabInts));
+    const uint4 h = lds_bcast16(lds_addr(table + k * kSTabInts));
+    const uint4 u = lds_bcast16(lds_addr(table + k * kSTabInts + 20));
     const int e = sgpr(h.x);
     const int fb = sgpr(h.w) * 8 + wave;
+    const int g0 = sgpr(u.x) * kSGB;
     const bool sh = e == a.E;
     const size_t mstride_q = (size_t)nfb * KG * 64;
     const size_t mstride_s = (size_t)nfb * KG * 16;
@@ -571,9 +650,10 @@ __device__ __forceinline__ SWItem sw_item(const ExpArgs& a, const int* table, in
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
         const int mm = m < NMAT ? m : 0;
-        it.wq[m] = (sh ? a.swq[mm] : a.wq[mm] + (size_t)e * mstride_q) + (size_t)fb * KG * 64;
-        it.ws[m] = (sh ? a.sws[mm] : a.ws[mm] + (size_t)e * mstride_s) + (size_t)fb * KG * 16;
+        it.wq[m] = (sh ? a.swq[mm] : a.wq[mm] + (size_t)e * mstride_q) + ((size_t)fb * KG + g0) * 64;
+        it.ws[m] = (sh ? a.sws[mm] : a.ws[mm] + (size_t)e * mstride_s) + ((size_t)fb * KG + g0) * 16;
     }
+    it.ng = sgpr(u.y) * kSGB;
     return it;
 }
 
@@ -583,14 +663,18 @@ struct SAItem {
     uint32_t tok[2];
     uint32_t live[2];   // this wave's staged rows lie inside the tile (row < nrows)
     uint32_t gtok;
+    int kb0, nb;        // the unit's batches
 };
 
 template <int NMAT>
 __device__ __forceinline__ SAItem sa_item(const int* table, int k, int wave, int lane) {
-    const uint32_t base = lds_addr(table + k * kTabInts);
+    const uint32_t base = lds_addr(table + k * kSTabInts);
     const uint4 h = lds_bcast16(base);
+    const uint4 u = lds_bcast16(base + 80);
     const int r0 = sgpr(h.y), nr = sgpr(h.z);
     SAItem it;
+    it.kb0 = sgpr(u.x);
+    it.nb = sgpr(u.y);
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int row = 2 * wave + j;
@@ -720,16 +804,53 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
     const int total = *a.ntiles * ngrp;
     const int nwg = (int)gridDim.x;
     const int base = (int)blockIdx.x;
-    const int nitems = base < total ? (total - base + nwg - 1) / nwg : 0;
+    const SSched sch = s_sched(total, nwg, base, NMAT == 2 ? BPI : 1);
+    const int nitems = sch.nunits;
     int* table = reinterpret_cast<int*>(lds + LY::kTab);
     char* junk = lds + LY::kJunk;
 
+    // Finishes an item from its total T: h = silu(gate) * up as bf16 and the
+    // group sum of the rounded h per tile row (gate/up), or the fp32 partial
+    // row (down).
+    auto finish = [&](const f32x4 (&T)[NMAT], int r0, int nr, int fb) {
+        const bool valid = r < nr;
+        const size_t row = (size_t)r0 + r;
+        if constexpr (NMAT == 2) {
+            const uint32_t h01 = pack_bf16x2(silu_fast(T[0][0]) * T[1][0],
+                                             silu_fast(T[0][1]) * T[1][1]);
+            const uint32_t h23 = pack_bf16x2(silu_fast(T[0][2]) * T[1][2],
+                                             silu_fast(T[0][3]) * T[1][3]);
+            if (valid)
+                *reinterpret_cast<uint2*>(a.h + row * a.I + fb * 16 + 4 * q) = uint2{h01, h23};
+            float ps = (bf16_to_f32(h01 & 0xffffu) + __uint_as_float(h01 & 0xffff0000u)) +
+                       (bf16_to_f32(h23 & 0xffffu) + __uint_as_float(h23 & 0xffff0000u));
+            ps = ps + __shfl_xor(ps, 16);
+            ps = ps + __shfl_xor(ps, 32);
+            const uint32_t red = lds_addr(lds + LY::kRed);
+            if (q == 0) lds_write_f32(red + (uint32_t)((wave * 16 + r) * 4), ps);
+            __builtin_amdgcn_s_barrier();
+            if (wave == 0 && q == 0) {
+                float tot = 0.0f;
+#pragma unroll
+                for (int w = 0; w < 8; ++w)
+                    tot += __uint_as_float(lds_read_u32(red + (uint32_t)((w * 16 + r) * 4)));
+                if (valid) a.hsum[row * (a.I / 128) + fb / 8] = tot;
+            }
+            __builtin_amdgcn_s_barrier();
+        } else {
+            if (valid)
+                *reinterpret_cast<float4*>(a.dpart + row * a.H + fb * 16 + 4 * q) =
+                    make_float4(T[0][0], T[0][1], T[0][2], T[0][3]);
+        }
+    };
+
     for (int k0 = 0; k0 < nitems; k0 += kTable) {
         const int cnt = min(kTable, nitems - k0);
-        fill_table(a, table, base, nwg, ngrp, k0, cnt);
+        fill_stream_table(a, table, sch, base, nwg, ngrp, NMAT == 2 ? BPI : 1, k0, cnt);
         __syncthreads();
-        const int ngroups = cnt * KG;          // weight groups of the chunk
-        const int nbatch = cnt * BPI;          // activation batches of the chunk
+        // Activation batches of the chunk: whole items BPI each, parts 1.
+        const int nwhole = sch.split ? max(0, min(cnt, sch.R - k0)) : cnt;
+        const int nbatch = nwhole * BPI + (cnt - nwhole);
 
         // Weight stream, P groups ahead (crosses items).
         int wk = 0, wkg = 0;
@@ -741,7 +862,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
         // static; the surplus data is never read.
         auto issue_w = [&](u32x4 (&w)[2], u32x2 (&sc)[2]) {
             s_issue_w<NMAT>(wit, wkg, lane, w, sc);
-            if (wkg + 1 < KG) {
+            if (wkg + 1 < wit.ng) {
                 ++wkg;
             } else if (wk + 1 < cnt) {
                 ++wk;
@@ -753,8 +874,9 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
         int ak = 0, abi = 0;
         SAItem ait = sa_item<NMAT>(table, 0, wave, lane);
         auto issue_act = [&](int b) {
-            s_issue_act<NMAT>(a, ait, abi, K, KG, lds + (b & 1) * LY::kBuf, junk, wave, lane);
-            if (abi + 1 < BPI) {
+            s_issue_act<NMAT>(a, ait, ait.kb0 + abi, K, KG, lds + (b & 1) * LY::kBuf, junk, wave,
+                              lane);
+            if (abi + 1 < ait.nb) {
                 ++abi;
             } else if (ak + 1 < cnt) {
                 ++ak;
@@ -772,14 +894,17 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
         s_load_ops<0>(s_base<NMAT>(lds, lane), ops[0]);
 
         int cur_k = 0, cur_bi = 0;
-        int cr0 = 0, cnr = 0, cfb = 0;
-        {
-            const uint4 h = lds_bcast16(lds_addr(table));
+        int cr0 = 0, cnr = 0, cfb = 0, ckb = 0, cnb = 0, ctail = -1;
+        auto load_cur = [&]() {
+            const uint4 h = lds_bcast16(lds_addr(table + cur_k * kSTabInts));
+            const uint4 u = lds_bcast16(lds_addr(table + cur_k * kSTabInts + 20));
             cr0 = sgpr(h.y); cnr = sgpr(h.z); cfb = sgpr(h.w) * 8 + wave;
-        }
-        f32x4 acc[NMAT];
+            ckb = sgpr(u.x); cnb = sgpr(u.y); ctail = sgpr(u.z);
+        };
+        load_cur();
+        f32x4 acc[NMAT], T[NMAT];
 #pragma unroll
-        for (int m = 0; m < NMAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int m = 0; m < NMAT; ++m) acc[m] = T[m] = f32x4{0.f, 0.f, 0.f, 0.f};
 
         for (int B = 0; B < nbatch; ++B) {
             const bool next_act = B + 1 < nbatch;
@@ -807,44 +932,27 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
                 issue_w(W[j % P], Sc[j % P]);
                 __builtin_amdgcn_sched_barrier(0);
             });
-            // Item done?
-            if (++cur_bi == BPI) {
-                const bool valid = r < cnr;
-                const size_t row = (size_t)cr0 + r;
-                if constexpr (NMAT == 2) {
-                    const uint32_t h01 = pack_bf16x2(silu_fast(acc[0][0]) * acc[1][0],
-                                                     silu_fast(acc[0][1]) * acc[1][1]);
-                    const uint32_t h23 = pack_bf16x2(silu_fast(acc[0][2]) * acc[1][2],
-                                                     silu_fast(acc[0][3]) * acc[1][3]);
-                    if (valid)
-                        *reinterpret_cast<uint2*>(a.h + row * a.I + cfb * 16 + 4 * q) = uint2{h01, h23};
-                    float ps = (bf16_to_f32(h01 & 0xffffu) + __uint_as_float(h01 & 0xffff0000u)) +
-                               (bf16_to_f32(h23 & 0xffffu) + __uint_as_float(h23 & 0xffff0000u));
-                    ps = ps + __shfl_xor(ps, 16);
-                    ps = ps + __shfl_xor(ps, 32);
-                    const uint32_t red = lds_addr(lds + LY::kRed);
-                    if (q == 0) lds_write_f32(red + (uint32_t)((wave * 16 + r) * 4), ps);
-                    __builtin_amdgcn_s_barrier();
-                    if (wave == 0 && q == 0) {
-                        float tot = 0.0f;
+            // Batch total into the unit's running total, batch order.
 #pragma unroll
-                        for (int w = 0; w < 8; ++w)
-                            tot += __uint_as_float(lds_read_u32(red + (uint32_t)((w * 16 + r) * 4)));
-                        if (valid) a.hsum[row * (a.I / 128) + cfb / 8] = tot;
-                    }
-                    __builtin_amdgcn_s_barrier();
+            for (int m = 0; m < NMAT; ++m) {
+                T[m] = cur_bi == 0 ? acc[m] : T[m] + acc[m];
+                acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
+            }
+            if (++cur_bi == cnb) {
+                if (ctail < 0) {
+                    finish(T, cr0, cnr, cfb);
                 } else {
-                    if (valid)
-                        *reinterpret_cast<float4*>(a.dpart + row * a.H + cfb * 16 + 4 * q) =
-                            make_float4(acc[0][0], acc[0][1], acc[0][2], acc[0][3]);
-                }
+                    // A part: store t_b; the item is finished after the ticket.
+                    // [value][thread]: each store instruction covers 256
+                    // contiguous bytes (whole lines).
+                    float* dst = g_tail_part + (size_t)(ctail * BPI + ckb) * 4096 + threadIdx.x;
 #pragma unroll
-                for (int m = 0; m < NMAT; ++m) acc[m] = f32x4{0.f, 0.f, 0.f, 0.f};
-                cur_bi = 0;
-                if (++cur_k < cnt) {
-                    const uint4 h = lds_bcast16(lds_addr(table + cur_k * kTabInts));
-                    cr0 = sgpr(h.y); cnr = sgpr(h.z); cfb = sgpr(h.w) * 8 + wave;
+                    for (int m = 0; m < NMAT; ++m)
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) st_dev(dst + (m * 4 + i) * 512, T[m][i]);
                 }
+                cur_bi = 0;
+                if (++cur_k < cnt) load_cur();
             }
             if (next_act) {
                 // Batch B + 1 has landed once only the 8 weight groups issued
@@ -857,6 +965,35 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
         wait_vmcnt<0>();
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
+    }
+    if constexpr (NMAT == 2) {
+        // Parts: every wave's stores have completed (vmcnt(0) above); the
+        // workgroup with an item's last ticket finishes it.
+        int* flag = reinterpret_cast<int*>(junk);
+        for (int u = sch.split ? sch.R : nitems; u < nitems; ++u) {
+            const int4 un = s_unit(sch, base, nwg, BPI, u);
+            if (threadIdx.x == 0) {
+                const bool last = ticket_dev(&g_tail_tick[un.w]) == (unsigned)(BPI - 1);
+                if (last) reset_dev(&g_tail_tick[un.w]);
+                *flag = last ? 1 : 0;
+            }
+            __syncthreads();
+            const bool last = *flag != 0;
+            __syncthreads();
+            if (!last) continue;
+            f32x4 T[NMAT];
+            for (int b = 0; b < BPI; ++b) {
+                const float* src = g_tail_part + (size_t)(un.w * BPI + b) * 4096 + threadIdx.x;
+#pragma unroll
+                for (int m = 0; m < NMAT; ++m) {
+                    const f32x4 t{ld_dev(src + (m * 4) * 512), ld_dev(src + (m * 4 + 1) * 512),
+                                  ld_dev(src + (m * 4 + 2) * 512), ld_dev(src + (m * 4 + 3) * 512)};
+                    T[m] = b == 0 ? t : T[m] + t;
+                }
+            }
+            const int4 tile = a.tiles[un.x / ngrp];
+            finish(T, tile.y, tile.z, (un.x % ngrp) * 8 + wave);
+        }
     }
 }
 
@@ -973,7 +1110,8 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, co
     a.rows_tok = rows_tok; a.h = h; a.hsum = hsum; a.H = H; a.I = I; a.E = E;
     const long work = (long)max_tiles * (I / 16 / kNWGU);
 #ifndef GLMMOE_NO_STREAM
-    if ((H / 128) % kSGB == 0) return launch_stream<2>(a, (long)max_tiles * (I / 128), s);
+    if ((H / 128) % kSGB == 0)
+        return launch_stream<2>(a, (long)max_tiles * (I / 128) * (H / 128 / kSGB), s);
 #endif
     if ((H / 128) % kPFGU == 0) return launch_expert<2, kPFGU, kRingGU, kNWGU>(a, work, s);
     return launch_expert<2, 1, 6, kNWGU>(a, work, s);   // odd K-group count
