@@ -315,7 +315,7 @@ def main():
         sweep["fp8_prefill_8192"] = measure_fp8(8192, max(3, args.steps // 10), 2)
 
     gu_ms = head["stage_ms"]["gate_up"]
-    roof = {"bound": "hbm", "kernel": f"w4_stream_kernel<2> grouped gate/up + SiLU (decode B={args.head_batch})",
+    roof = {"bound": "hbm", "kernel": f"w4_stream_kernel<0> grouped gate/up + SiLU (decode B={args.head_batch})",
             "achieved": head["gate_up_GBps"], "peak": HBM_PEAK / 1e9, "unit": "GB/s",
             "frac": head["gate_up_GBps"] / (HBM_PEAK / 1e9),
             "traffic": profiled_traffic() if args.head_batch == 64 else None,

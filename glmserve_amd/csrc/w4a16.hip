@@ -635,13 +635,15 @@ struct SWItem {
     int ng;   // weight groups of the unit
 };
 
-template <int NMAT>
+// PAIR (second projection): stream m is row block 16 g + 8 m + wave of the one
+// matrix instead of block 8 g + wave of matrix m.
+template <int NMAT, bool PAIR>
 __device__ __forceinline__ SWItem sw_item(const ExpArgs& a, const int* table, int k, int wave,
                                           int nfb, int KG) {
     const uint4 h = lds_bcast16(lds_addr(table + k * kSTabInts));
     const uint4 u = lds_bcast16(lds_addr(table + k * kSTabInts + 20));
     const int e = sgpr(h.x);
-    const int fb = sgpr(h.w) * 8 + wave;
+    const int fb0 = sgpr(h.w) * (PAIR ? 16 : 8) + wave;
     const int g0 = sgpr(u.x) * kSGB;
     const bool sh = e == a.E;
     const size_t mstride_q = (size_t)nfb * KG * 64;
@@ -649,7 +651,8 @@ __device__ __forceinline__ SWItem sw_item(const ExpArgs& a, const int* table, in
     SWItem it;
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
-        const int mm = m < NMAT ? m : 0;
+        const int mm = PAIR ? 0 : (m < NMAT ? m : 0);
+        const int fb = PAIR ? fb0 + 8 * m : fb0;
         it.wq[m] = (sh ? a.swq[mm] : a.wq[mm] + (size_t)e * mstride_q) + ((size_t)fb * KG + g0) * 64;
         it.ws[m] = (sh ? a.sws[mm] : a.ws[mm] + (size_t)e * mstride_s) + ((size_t)fb * KG + g0) * 16;
     }
@@ -666,7 +669,9 @@ struct SAItem {
     int kb0, nb;        // the unit's batches
 };
 
-template <int NMAT>
+// GATHER (first projection): src rows are the tile's token ids; else the
+// tile's own rows r0 + row.
+template <bool GATHER>
 __device__ __forceinline__ SAItem sa_item(const int* table, int k, int wave, int lane) {
     const uint32_t base = lds_addr(table + k * kSTabInts);
     const uint4 h = lds_bcast16(base);
@@ -678,12 +683,12 @@ __device__ __forceinline__ SAItem sa_item(const int* table, int k, int wave, int
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
         const int row = 2 * wave + j;
-        it.tok[j] = NMAT == 2 ? (uint32_t)sgpr(lds_read_u32(base + 16 + row * 4))
+        it.tok[j] = GATHER ? (uint32_t)sgpr(lds_read_u32(base + 16 + row * 4))
                               : (uint32_t)(r0 + (row < nr ? row : 0));
         it.live[j] = row < nr ? 1u : 0u;
     }
     const int row = lane & 15;
-    it.gtok = NMAT == 2 ? lds_read_u32(base + 16 + row * 4) : (uint32_t)(r0 + (row < nr ? row : 0));
+    it.gtok = GATHER ? lds_read_u32(base + 16 + row * 4) : (uint32_t)(r0 + (row < nr ? row : 0));
     return it;
 }
 
@@ -787,8 +792,15 @@ __device__ __forceinline__ void s_compute(const SOps& o, const u32x4 (&w)[2], co
     }
 }
 
-template <int NMAT>
+// MODE 0: gate/up (two matrices, SiLU epilogue). MODE 2: down, two 16-row
+// blocks per wave (a 256-row item), the same two-stream shape as gate/up,
+// which halves the batches, barriers and item switches per weight byte
+// against one block per wave (MODE 1, kept for shapes the layer does not
+// pass).
+template <int MODE>
 __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
+    constexpr int NMAT = MODE == 1 ? 1 : 2;
+    constexpr bool GU = MODE == 0, PAIR = MODE == 2;
     using LY = SLay<NMAT>;
     constexpr int P = LY::P;
     extern __shared__ __align__(16) char lds[];
@@ -796,15 +808,15 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int r = lane & 15, q = lane >> 4;
-    const int K = NMAT == 2 ? a.H : a.I;
+    const int K = GU ? a.H : a.I;
     const int KG = K / 128;
     const int BPI = KG / kSGB;                 // activation batches per item
-    const int nfb = (NMAT == 2 ? a.I : a.H) / 16;
-    const int ngrp = nfb / 8;
+    const int nfb = (GU ? a.I : a.H) / 16;
+    const int ngrp = nfb / (PAIR ? 16 : 8);
     const int total = *a.ntiles * ngrp;
     const int nwg = (int)gridDim.x;
     const int base = (int)blockIdx.x;
-    const SSched sch = s_sched(total, nwg, base, NMAT == 2 ? BPI : 1);
+    const SSched sch = s_sched(total, nwg, base, GU ? BPI : 1);
     const int nitems = sch.nunits;
     int* table = reinterpret_cast<int*>(lds + LY::kTab);
     char* junk = lds + LY::kJunk;
@@ -815,7 +827,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
     auto finish = [&](const f32x4 (&T)[NMAT], int r0, int nr, int fb) {
         const bool valid = r < nr;
         const size_t row = (size_t)r0 + r;
-        if constexpr (NMAT == 2) {
+        if constexpr (GU) {
             const uint32_t h01 = pack_bf16x2(silu_fast(T[0][0]) * T[1][0],
                                              silu_fast(T[0][1]) * T[1][1]);
             const uint32_t h23 = pack_bf16x2(silu_fast(T[0][2]) * T[1][2],
@@ -838,15 +850,17 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
             }
             __builtin_amdgcn_s_barrier();
         } else {
-            if (valid)
-                *reinterpret_cast<float4*>(a.dpart + row * a.H + fb * 16 + 4 * q) =
-                    make_float4(T[0][0], T[0][1], T[0][2], T[0][3]);
+#pragma unroll
+            for (int m = 0; m < NMAT; ++m)
+                if (valid)
+                    *reinterpret_cast<float4*>(a.dpart + row * a.H + (fb + 8 * m) * 16 + 4 * q) =
+                        make_float4(T[m][0], T[m][1], T[m][2], T[m][3]);
         }
     };
 
     for (int k0 = 0; k0 < nitems; k0 += kTable) {
         const int cnt = min(kTable, nitems - k0);
-        fill_stream_table(a, table, sch, base, nwg, ngrp, NMAT == 2 ? BPI : 1, k0, cnt);
+        fill_stream_table(a, table, sch, base, nwg, ngrp, GU ? BPI : 1, k0, cnt);
         __syncthreads();
         // Activation batches of the chunk: whole items BPI each, parts 1.
         const int nwhole = sch.split ? max(0, min(cnt, sch.R - k0)) : cnt;
@@ -854,7 +868,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
 
         // Weight stream, P groups ahead (crosses items).
         int wk = 0, wkg = 0;
-        SWItem wit = sw_item<NMAT>(a, table, 0, wave, nfb, KG);
+        SWItem wit = sw_item<NMAT, PAIR>(a, table, 0, wave, nfb, KG);
         u32x4 W[P][2];
         u32x2 Sc[P][2];
         // Past the chunk's last group both streams re-issue their final
@@ -867,12 +881,12 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
             } else if (wk + 1 < cnt) {
                 ++wk;
                 wkg = 0;
-                wit = sw_item<NMAT>(a, table, wk, wave, nfb, KG);
+                wit = sw_item<NMAT, PAIR>(a, table, wk, wave, nfb, KG);
             }
         };
         // Activation stream, one batch ahead.
         int ak = 0, abi = 0;
-        SAItem ait = sa_item<NMAT>(table, 0, wave, lane);
+        SAItem ait = sa_item<GU>(table, 0, wave, lane);
         auto issue_act = [&](int b) {
             s_issue_act<NMAT>(a, ait, ait.kb0 + abi, K, KG, lds + (b & 1) * LY::kBuf, junk, wave,
                               lane);
@@ -881,7 +895,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
             } else if (ak + 1 < cnt) {
                 ++ak;
                 abi = 0;
-                ait = sa_item<NMAT>(table, ak, wave, lane);
+                ait = sa_item<GU>(table, ak, wave, lane);
             }
         };
 
@@ -898,7 +912,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
         auto load_cur = [&]() {
             const uint4 h = lds_bcast16(lds_addr(table + cur_k * kSTabInts));
             const uint4 u = lds_bcast16(lds_addr(table + cur_k * kSTabInts + 20));
-            cr0 = sgpr(h.y); cnr = sgpr(h.z); cfb = sgpr(h.w) * 8 + wave;
+            cr0 = sgpr(h.y); cnr = sgpr(h.z); cfb = sgpr(h.w) * (PAIR ? 16 : 8) + wave;
             ckb = sgpr(u.x); cnb = sgpr(u.y); ctail = sgpr(u.z);
         };
         load_cur();
@@ -966,7 +980,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
     }
-    if constexpr (NMAT == 2) {
+    if constexpr (GU) {
         // Parts: every wave's stores have completed (vmcnt(0) above); the
         // workgroup with an item's last ticket finishes it.
         int* flag = reinterpret_cast<int*>(junk);
@@ -997,12 +1011,12 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
     }
 }
 
-template <int NMAT>
+template <int MODE>
 static int launch_stream(const ExpArgs& a, long max_work, hipStream_t s) {
-    using LY = SLay<NMAT>;
+    using LY = SLay<MODE == 1 ? 1 : 2>;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4_stream_kernel<NMAT>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4_stream_kernel<MODE>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, LY::kTotal) != hipSuccess)
             return -4;
         attr_set = true;
@@ -1013,7 +1027,7 @@ static int launch_stream(const ExpArgs& a, long max_work, hipStream_t s) {
     long blocks = max_work;
     if (blocks > (long)cus) blocks = cus;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL((w4_stream_kernel<NMAT>), dim3((unsigned)blocks), dim3(512), LY::kTotal, s, a);
+    hipLaunchKernelGGL((w4_stream_kernel<MODE>), dim3((unsigned)blocks), dim3(512), LY::kTotal, s, a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
@@ -1111,7 +1125,7 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, co
     const long work = (long)max_tiles * (I / 16 / kNWGU);
 #ifndef GLMMOE_NO_STREAM
     if ((H / 128) % kSGB == 0)
-        return launch_stream<2>(a, (long)max_tiles * (I / 128) * (H / 128 / kSGB), s);
+        return launch_stream<0>(a, (long)max_tiles * (I / 128) * (H / 128 / kSGB), s);
 #endif
     if ((H / 128) % kPFGU == 0) return launch_expert<2, kPFGU, kRingGU, kNWGU>(a, work, s);
     return launch_expert<2, 1, 6, kNWGU>(a, work, s);   // odd K-group count
@@ -1128,7 +1142,8 @@ int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const
     a.dpart = dpart; a.H = H; a.I = I; a.E = E;
     const long work = (long)max_tiles * (H / 16 / kNWDown);
 #ifndef GLMMOE_NO_STREAM
-    if ((I / 128) % kSGB == 0) return launch_stream<1>(a, (long)max_tiles * (H / 128), s);
+    // Two 16-row blocks per wave (the layer's hidden size is a multiple of 256).
+    if ((I / 128) % kSGB == 0 && H % 256 == 0) return launch_stream<2>(a, (long)max_tiles * (H / 256), s);
 #endif
     if ((I / 128) % kPFDown == 0) return launch_expert<1, kPFDown, kRingDown, kNWDown>(a, work, s);
     return launch_expert<1, 1, 6, kNWDown>(a, work, s);   // odd K-group count
