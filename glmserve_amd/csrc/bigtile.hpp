@@ -20,6 +20,7 @@ constexpr int kBigTabInts = 4 + kBigRows; // {expert, row0, nrows, feature group
 
 struct BigItem {
     int e, r0, nr, g;
+    int hs;                    // 64-row item (a half tile): twice the features
     uint32_t tab;              // LDS address of the item's table entry
 };
 
@@ -31,7 +32,8 @@ __device__ __forceinline__ BigItem big_item(const char* table, int k) {
     it.e = sgpr(hd.x);
     it.r0 = sgpr(hd.y);
     it.nr = sgpr(hd.z);
-    it.g = sgpr(hd.w);
+    it.g = sgpr(hd.w & 0xffffu);
+    it.hs = sgpr(hd.w >> 16);
     it.tab = base;
     return it;
 }
@@ -78,6 +80,49 @@ __device__ __forceinline__ void big_fill_table(const int4* tiles, const int* row
         else if (f == 1) v = tile.y;
         else if (f == 2) v = tile.z;
         else if (f == 3) v = (int)(item % nfg);
+        else {
+            const int row = f - 4;
+            const int rr = row < tile.z ? row : 0;
+            v = GATHER ? rows_tok[tile.y + rr] : tile.y + rr;
+        }
+        table[i] = v;
+    }
+}
+
+// Items of a tile list with half tiles (W4A16 kernels): the first n128 tiles
+// take nfg 128-row items each, the half tiles after them nfg / 2 64-row items
+// (each twice as many features wide).
+__device__ __forceinline__ long big2_total(int ntiles, int n128, int nfg) {
+    return (long)n128 * nfg + (long)(ntiles - n128) * (nfg / 2);
+}
+
+__device__ __forceinline__ void big2_locate(long id, int n128, int nfg, int& tile, int& g, int& hs) {
+    const long full = (long)n128 * nfg;
+    if (id < full) {
+        tile = (int)(id / nfg);
+        g = (int)(id % nfg);
+        hs = 0;
+    } else {
+        const long j = id - full;
+        tile = n128 + (int)(j / (nfg / 2));
+        g = (int)(j % (nfg / 2));
+        hs = 1;
+    }
+}
+
+template <bool GATHER>
+__device__ __forceinline__ void big2_fill_table(const int4* tiles, const int* rows_tok, int* table,
+                                                long k0, int cnt, int nfg, int n128) {
+    for (int i = threadIdx.x; i < cnt * kBigTabInts; i += blockDim.x) {
+        const int k = i / kBigTabInts, f = i % kBigTabInts;
+        int ti, g, hs;
+        big2_locate(big_item_id(k0 + k), n128, nfg, ti, g, hs);
+        const int4 tile = tiles[ti];
+        int v;
+        if (f == 0) v = tile.x;
+        else if (f == 1) v = tile.y;
+        else if (f == 2) v = tile.z;
+        else if (f == 3) v = g | (hs << 16);
         else {
             const int row = f - 4;
             const int rr = row < tile.z ? row : 0;

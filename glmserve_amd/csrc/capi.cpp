@@ -28,6 +28,13 @@ int max_tiles_for(int n, int topk, int E, int with_shared) {
     return max_tiles_for(n, topk, E, with_shared, tile_rows_for(n, topk, with_shared));
 }
 
+// Half-tile rows of the W4A16 tile list: with 128-row tiles, an expert's last
+// tile of at most 64 rows runs as a 64-row item of twice the features, which
+// needs an even number of feature groups in both projections.
+int half_rows_w4(int T, int H, int I) {
+    return T == kBigRows && I % 256 == 0 && H % 512 == 0 ? kBigRows / 2 : 0;
+}
+
 // Shape and pointer checks shared by the W4A16 and FP8 layer descriptors.
 template <class Layer>
 int check_layer(const Layer* L, int n) {
@@ -172,7 +179,7 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     int rc = dispatched ? 0
                         : launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids,
                                           v.sorted_row, v.inv, v.tiles, v.ntiles, T, sh, 1, s,
-                                          dispatch_scratch(v.rpart, L, n));
+                                          dispatch_scratch(v.rpart, L, n), half_rows_w4(T, H, I));
     if (rc) return rc;
     const ExpertPtrs P = ptrs(L);
     mark(GLMMOE_STAGE_GATE_UP, s);
@@ -310,8 +317,10 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     // The router pass also writes the activation group sums the expert
     // kernels use to remove the int4 decode offset.
     const int sh = has_shared(L) ? 1 : 0;
+    const int T = tile_rows_for(n, k, sh);
     const DispOut disp{v.expert_offsets, v.sorted_token_ids, v.sorted_row, v.inv,
-                       reinterpret_cast<int4*>(v.tiles), v.ntiles, tile_rows_for(n, k, sh), sh, 1};
+                       reinterpret_cast<int4*>(v.tiles), v.ntiles, T, sh, 1,
+                       half_rows_w4(T, H, L->moe_inter)};
     bool dispatched = false;
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
                               L->routed_scale, v.logits, v.xsum, v.rpart, v.topk_ids, v.topk_w, s,
@@ -396,7 +405,7 @@ int glmmoe_moe_layer_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, fl
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
     const int sh = has_shared(L) ? 1 : 0;
     const DispOut disp{v.expert_offsets, v.sorted_token_ids, v.sorted_row, v.inv,
-                       reinterpret_cast<int4*>(v.tiles), v.ntiles, kBigRows, sh, 1};
+                       reinterpret_cast<int4*>(v.tiles), v.ntiles, kBigRows, sh, 1, 0};
     bool dispatched = false;
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
                               L->routed_scale, v.logits, nullptr, v.rpart, v.topk_ids, v.topk_w, s,

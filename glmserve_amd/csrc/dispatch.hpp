@@ -22,18 +22,19 @@ namespace glmmoe {
 
 constexpr int kDispMaxE = 512;
 
-// Exclusive prefix of vals[0..count) (count <= 512) into pre[0..count], pre[count] =
-// total, by wave 0 alone: each lane sums 8 consecutive entries, then a wave
-// scan of the lane sums. Callers synchronize before and after.
+// Exclusive prefix of vals[0..count) (count <= 576: 512 experts and the
+// shared one) into pre[0..count], pre[count] = total, by wave 0 alone: each
+// lane sums 9 consecutive entries, then a wave scan of the lane sums. Callers
+// synchronize before and after.
 __device__ inline void wave0_exclusive_scan(const int* vals, int count, int* pre) {
-
+    constexpr int kPer = 9;
     const int lane = threadIdx.x & 63;
     if (threadIdx.x >= 64) return;
-    int local[8];
+    int local[kPer];
     int sum = 0;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int i = lane * 8 + j;
+    for (int j = 0; j < kPer; ++j) {
+        const int i = lane * kPer + j;
         local[j] = i < count ? vals[i] : 0;
         sum += local[j];
     }
@@ -45,8 +46,8 @@ __device__ inline void wave0_exclusive_scan(const int* vals, int count, int* pre
     }
     int run = incl - sum;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-        const int i = lane * 8 + j;
+    for (int j = 0; j < kPer; ++j) {
+        const int i = lane * kPer + j;
         if (i < count) pre[i] = run;
         run += local[j];
     }
@@ -169,22 +170,43 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
 
     // Tile list: expert e (e == E is the shared expert) contributes
     // ceil(count / d.tile_rows) tiles of at most d.tile_rows consecutive rows.
+    // With d.half_rows, an expert's last tile of at most half_rows rows is a
+    // "half" tile: all the other tiles come first (ntiles[1] of them, in
+    // expert order), then the half tiles (in expert order). With
+    // half_rows == 0, ntiles[1] = ntiles[0]; below 0, only ntiles[0] is written.
+    static_assert(NT / 64 >= 4, "two scan arrays in the per-wave count area");
     const int nexp = E + (d.with_shared ? 1 : 0);
+    const int T = d.tile_rows, HR = d.half_rows;
+    // nexp <= 513 counts and nexp + 1 prefixes: each may run into the next row.
+    int* nhalf = &wc[0][0];
+    int* prehalf = &wc[2][0];
     for (int e = tid; e < nexp; e += NT) {
         const int ce = e < E ? cnt[e] : n;
-        ntl[e] = (ce + d.tile_rows - 1) / d.tile_rows;
+        const int full = ce / T, rem = ce - full * T;
+        const bool half = HR > 0 && rem > 0 && rem <= HR;
+        ntl[e] = full + (rem > 0 && !half ? 1 : 0);
+        nhalf[e] = half ? 1 : 0;
     }
     __syncthreads();
     wave0_exclusive_scan(ntl, nexp, pre);
+    __syncthreads();
+    if (HR > 0) wave0_exclusive_scan(nhalf, nexp, prehalf);
     __syncthreads();
     for (int e = tid; e < nexp; e += NT) {
         const int ce = e < E ? cnt[e] : n;
         const int row0 = e < E ? cursor[e] - ce : total;  // cursor ended at offset + count
         const int tbase = pre[e];
         for (int j = 0; j < ntl[e]; ++j)
-            d.tiles[tbase + j] = make_int4(e, row0 + j * d.tile_rows, min(d.tile_rows, ce - j * d.tile_rows), 0);
+            d.tiles[tbase + j] = make_int4(e, row0 + j * T, min(T, ce - j * T), 0);
+        if (nhalf[e]) {
+            const int full = ce / T;
+            d.tiles[pre[nexp] + prehalf[e]] = make_int4(e, row0 + full * T, ce - full * T, 0);
+        }
     }
-    if (tid == 0) *d.ntiles = pre[nexp];
+    if (tid == 0) {
+        d.ntiles[0] = pre[nexp] + (HR > 0 ? prehalf[nexp] : 0);
+        if (HR >= 0) d.ntiles[1] = pre[nexp];   // HR < 0: the caller's ntiles holds one int
+    }
 }
 
 }  // namespace glmmoe

@@ -453,6 +453,7 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
         __builtin_amdgcn_s_barrier();
         F8Ops ops;
         f8_load_ops(lds, wave, lane, NMAT, ops);
+        f8_wait_ops(ops);
 
         int cur_k = 0, cur_g = 0;
         BigItem cur = big_item(lds + RG::kTab, 0);
@@ -465,7 +466,6 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
             for (int tb = 0; tb < 2; ++tb) acc[jb][tb] = f32x16{};
 
         for (int step = 0; step < nsteps; ++step) {
-            f8_wait_ops(ops);
             f32x16 p[2][2];
 #ifndef GLMMOE_F8_NOCOMPUTE
             if (live) f8_compute(ops, p);
@@ -492,6 +492,10 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
                     live = cur.nr > wm * 64;
                 }
             }
+            // Last in the iteration: the next step's operands have arrived before
+            // anything (including copies the compiler makes for the loop) reads
+            // their registers.
+            f8_wait_ops(ops);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();

@@ -44,6 +44,7 @@ struct DispOut {
     int tile_rows;
     int with_shared;
     int mode;
+    int half_rows;   // > 0: tail tiles of at most this many rows listed last; < 0: ntiles has one int
 };
 
 // Scratch (bytes) the router-logit launch needs for n tokens; 0 for large n.
@@ -65,7 +66,8 @@ int launch_router_topk(const float* logits, const float* e_bias, int n, int E, i
 size_t dispatch_scratch_bytes(int n, int topk, int E);
 int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,
                     int* sorted_slot, int* inv, int* tiles, int* ntiles, int tile_rows,
-                    int with_shared, int mode, hipStream_t s, int* scratch = nullptr);
+                    int with_shared, int mode, hipStream_t s, int* scratch = nullptr,
+                    int half_rows = -1);
 int launch_pack_w4(const uint8_t* q, const void* sc, int sc_bf16, int n_mats, int rows, int K,
                    uint8_t* pq, uint16_t* ps, hipStream_t s);
 int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,

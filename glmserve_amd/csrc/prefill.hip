@@ -58,71 +58,87 @@ struct BigArgs {
 
 constexpr int kBigD = 3;
 
+// Two item shapes share the ring and the per-group DMA count. A 128-row item
+// (8 waves as 4 features x 2 rows) covers 128 rows x 16 weight tiles; a
+// 64-row item (an expert's last tile of at most 64 rows, 8 waves x 1 row
+// block) covers 64 rows x 32 weight tiles, twice the features. Per group both
+// move 48 KiB: 16 KiB of weights + 32 KiB of activation rows, or 32 + 16.
 struct BigRing {
-    static constexpr int kWBytes = 16 * 1024;           // 16 weight tiles of 1 KiB
-    static constexpr int kSOff = kWBytes;               // scales: tile t at 32 t (512 B)
-    static constexpr int kGOff = kSOff + 512;           // group sums: row r at 4 r (512 B)
+    // Slot: weight tile t at 1 KiB t; activation row r at kX128 + 256 r
+    // (128-row item) or kX64 + 256 r (64-row item); scales of tile t at
+    // kSOff + 32 t; row group sums at kGOff + 4 r.
+    static constexpr int kX128 = 16 * 1024;
+    static constexpr int kX64 = 32 * 1024;
+    static constexpr int kSOff = 48 * 1024;             // 32 tiles x 32 B
+    static constexpr int kGOff = kSOff + 1024;          // 128 rows x 4 B
     static constexpr int kJunk = kGOff + 512;           // target of the placeholder DMAs
-    static constexpr int kXOff = kJunk + 256;
     static constexpr int kQuad = 1024;                  // one DMA = 4 rows x 256 B
-    static constexpr int kSlot = kXOff + (kBigRows / 4) * kQuad;
+    static constexpr int kSlot = kJunk + 256;
     static constexpr int kBytes = kBigD * kSlot;
-    static constexpr int kRed = kBytes;                 // [4][128] floats: h group-sum partials
+    static constexpr int kRed = kBytes;                 // [4][128] or [8][64] floats: h group-sum partials
     static constexpr int kTab = kRed + 4 * kBigRows * 4;
     static constexpr int kTotal = kTab + kBigTable * kBigTabInts * 4;
     static_assert(kTotal <= 160 * 1024, "one workgroup's LDS");
 #ifdef GLMMOE_BIG_NODMA
     static constexpr int kDma = 0;   // diagnostics: compute on stale LDS, no streaming
-#elif defined(GLMMOE_BIG_NOXDMA)
-    static constexpr int kDma = 2 + 1 + 1;   // diagnostics: no activation streaming
-#elif defined(GLMMOE_BIG_NOWDMA)
-    static constexpr int kDma = 1 + 1 + 4;   // diagnostics: no weight-tile streaming
 #else
-    static constexpr int kDma = 2 + 1 + 1 + 4;          // per wave per group
+    static constexpr int kDma = 6 + 1 + 1;              // per wave per group
 #endif
-    // Activation rows are 256 B each, row r at 256 r, so one DMA of 64 lanes
-    // reads 4 whole rows, 16 consecutive lanes per row (lanes that share
-    // cache lines are adjacent, which the address coalescer needs for full
-    // L2 bandwidth). Inside a row, 16-byte chunk c sits at slot c ^ (r & 15):
-    // the 16 rows an MFMA fragment pass reads at one chunk land on 16
-    // distinct bank groups.
+    // Activation rows are 256 B each, so one DMA of 64 lanes reads 4 whole
+    // rows, 16 consecutive lanes per row (lanes that share cache lines are
+    // adjacent, which the address coalescer needs for full L2 bandwidth).
+    // Inside a row, 16-byte chunk c sits at slot c ^ (r & 15): the 16 rows an
+    // MFMA fragment pass reads at one chunk land on 16 distinct bank groups.
     static __device__ __forceinline__ int row_off(int r) { return r * 256; }
 };
 
 template <int NMAT>
 struct BigShape {
-    static constexpr int kFeat = NMAT == 2 ? 128 : 256;   // features per item
+    static constexpr int kFeat = NMAT == 2 ? 128 : 256;   // features per 128-row item
 };
 
-// Tile t (0..15) of an item: weight matrix and 16-row feature block. Tiles
+// Wave geometry of an item: feature block wn, row half wm, activation area.
+struct BigGeo {
+    int wn, wm, xoff;
+};
+__device__ __forceinline__ BigGeo big_geo(int hs, int wave) {
+    return hs ? BigGeo{wave, 0, BigRing::kX64} : BigGeo{wave >> 1, wave & 1, BigRing::kX128};
+}
+
+// Tile t of an item: weight matrix and 16-row feature block. Tiles
 // 4 wn .. 4 wn + 3 belong to feature wave wn: for gate/up, 2 gate tiles then
 // the 2 up tiles of the same 32 features; for down, 4 consecutive tiles.
 template <int NMAT>
-__device__ __forceinline__ void tile_of(int t, int g, int& m, int& fb) {
+__device__ __forceinline__ void tile_of(int t, int g, int hs, int& m, int& fb) {
     if (NMAT == 2) {
         m = (t & 3) >> 1;
-        fb = g * 8 + (t >> 2) * 2 + (t & 1);
+        fb = g * (hs ? 16 : 8) + (t >> 2) * 2 + (t & 1);
     } else {
         m = 0;
-        fb = g * 16 + t;
+        fb = g * (hs ? 32 : 16) + t;
     }
 }
 
 // DMA sources of one item at K-group 0; group kg adds kg times the per-group
-// stride of each stream. The weight-tile bases are wave-uniform (SGPRs); the
-// per-lane parts are 32-bit element offsets to keep the loop's VGPRs low.
+// stride of each stream. The weight-tile bases and LDS targets are
+// wave-uniform (SGPRs); the per-lane parts are 32-bit element offsets to keep
+// the loop's VGPRs low.
 struct IssuePtrs {
-    const uint4* w[2];       // this wave's weight tiles 2 wave, 2 wave + 1 (lane added at issue)
-    const uint16_t* s;       // scale dword of this lane (waves 0, 1)
-    uint32_t g;              // gsum offset of one row (waves 2, 3)
-    uint32_t x[4];           // src offset of 16 B of one activation row, per row DMA
+    const uint4* w[4];       // this wave's weight tiles (2 or 4; lane added at issue)
+    const uint16_t* s;       // scale dword of this lane
+    uint32_t g;              // gsum offset of one row
+    uint32_t x[4];           // src offset of 16 B of one activation row, per row DMA (4 or 2)
+    int hs, sdst, gdst;      // shape; LDS targets of the scale and group-sum DMAs
 };
 
 template <int NMAT>
 __device__ __forceinline__ IssuePtrs issue_ptrs(const BigArgs& a, const BigItem& it, int K, int KG,
                                                 int wave, int lane) {
+    using RG = BigRing;
     IssuePtrs p;
     const bool sh = it.e == a.E;
+    const int hs = it.hs;
+    p.hs = hs;
     const int frows = NMAT == 2 ? a.I : a.H;
     const size_t mstride_q = (size_t)(frows / 16) * KG * 64;
     const size_t mstride_s = (size_t)(frows / 16) * KG * 16;
@@ -134,50 +150,69 @@ __device__ __forceinline__ IssuePtrs issue_ptrs(const BigArgs& a, const BigItem&
         wbase[m] = sh ? a.swq[mm] : a.wq[mm] + (size_t)it.e * mstride_q;
         sbase[m] = sh ? a.sws[mm] : a.ws[mm] + (size_t)it.e * mstride_s;
     }
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-        int m, fb;
-        tile_of<NMAT>(wave * 2 + j, it.g, m, fb);
-        p.w[j] = wbase[m] + (size_t)fb * KG * 64;
-    }
-    {
-        int m, fb;
-        tile_of<NMAT>((wave & 1) * 8 + (lane >> 3), it.g, m, fb);
-        p.s = sbase[m] + (size_t)fb * KG * 16 + (lane & 7) * 2;
-    }
-    // The table's row map holds the token (gate/up) or the grouped row (down)
-    // of each tile row; rows past the tile's end repeat row 0.
-    p.g = lds_read32(it.tab + 16 + ((wave & 1) * 64 + lane) * 4) * (uint32_t)KG;
-    // DMA j of this wave fills rows 16 wave + 4 j + lane / 16; lane's LDS slot
-    // lane % 16 holds chunk (lane % 16) ^ (row & 15) of its row.
+    // Weight DMA j of this wave fills tile nw * wave + j (nw = 2 or 4).
+    const int nw = hs ? 4 : 2;
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-        const int row = wave * 16 + j * 4 + (lane >> 4);
+        int m, fb;
+        tile_of<NMAT>(wave * nw + (j < nw ? j : 0), it.g, hs, m, fb);
+        p.w[j] = wbase[m] + (size_t)fb * KG * 64;
+    }
+    // Scales: lane l of waves < ns fetches dword l % 8 of tile
+    // 8 (wave % ns) + l / 8 (ns = 2 or 4 waves cover the 16 or 32 tiles).
+    const int ns = hs ? 4 : 2;
+    {
+        int m, fb;
+        tile_of<NMAT>((wave % ns) * 8 + (lane >> 3), it.g, hs, m, fb);
+        p.s = sbase[m] + (size_t)fb * KG * 16 + (lane & 7) * 2;
+    }
+    p.sdst = wave < ns ? RG::kSOff + (wave % ns) * 256 : RG::kJunk;
+    // Row group sums: waves 2, 3 (rows 64 (wave & 1) + lane) or wave 4 (row lane).
+    p.g = lds_read32(it.tab + 16 + ((hs ? 0 : (wave & 1) * 64) + lane) * 4) * (uint32_t)KG;
+    p.gdst = hs ? (wave == 4 ? RG::kGOff : RG::kJunk)
+                : ((wave >> 1) == 1 ? RG::kGOff + (wave & 1) * 256 : RG::kJunk);
+    // Activation DMA j fills rows rpw * wave + 4 j + lane / 16 (rpw = 16 or 8
+    // rows per wave); lane's LDS slot lane % 16 holds chunk (lane % 16) ^
+    // (row & 15) of its row. The table's row map holds the token (gate/up) or
+    // the grouped row (down) of each tile row; rows past the tile's end
+    // repeat row 0.
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+        const int row = (hs ? wave * 8 : wave * 16) + j * 4 + (lane >> 4);
         p.x[j] = lds_read32(it.tab + 16 + row * 4) * (uint32_t)K +
                  (uint32_t)((lane & 15) ^ (row & 15)) * 8;
     }
     return p;
 }
 
-// Exactly kDma DMAs per wave: group kg of the item into `slot`.
+// Exactly kDma DMAs per wave: group kg of the item into `slot`. DMAs 0-1
+// are weight tiles and 2-3 activation rows in both shapes; 4-5 are weight
+// tiles 2-3 (64-row item) or activation DMAs 2-3 (128-row item), picked by a
+// uniform select so that no DMA source is indexed dynamically.
 __device__ __forceinline__ void big_issue(const BigArgs& a, const IssuePtrs& p, int kg, char* slot,
                                           int wave, int lane) {
     using RG = BigRing;
 #ifdef GLMMOE_BIG_NODMA
     return;
 #endif
-#ifndef GLMMOE_BIG_NOWDMA
+    const int hs = p.hs;
+    const int nw = hs ? 4 : 2, nx = hs ? 2 : 4;
+    const int xoff = hs ? RG::kX64 : RG::kX128;
 #pragma unroll
     for (int j = 0; j < 2; ++j)
-        dma16(p.w[j] + (size_t)kg * 64 + lane, slot + (wave * 2 + j) * 1024);
-#endif
-    dma4(p.s + (size_t)kg * 16, slot + (wave < 2 ? RG::kSOff + (wave & 1) * 256 : RG::kJunk));
-    dma4(a.gsum + (p.g + (uint32_t)kg), slot + ((wave >> 1) == 1 ? RG::kGOff + (wave & 1) * 256 : RG::kJunk));
-#ifndef GLMMOE_BIG_NOXDMA
+        dma16(p.w[j] + (size_t)kg * 64 + lane, slot + (wave * nw + j) * 1024);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-        dma16(a.src + (p.x[j] + (uint32_t)kg * 128), slot + RG::kXOff + (wave * 4 + j) * RG::kQuad);
-#endif
+    for (int j = 0; j < 2; ++j)
+        dma16(a.src + (p.x[j] + (uint32_t)kg * 128), slot + xoff + (wave * nx + j) * RG::kQuad);
+#pragma unroll
+    for (int j = 2; j < 4; ++j) {
+        const void* wsrc = p.w[j] + (size_t)kg * 64 + lane;
+        const void* xsrc = a.src + (p.x[j] + (uint32_t)kg * 128);
+        const int dst = hs ? (wave * 4 + j) * 1024 : RG::kX128 + (wave * 4 + j) * RG::kQuad;
+        dma16(hs ? wsrc : xsrc, slot + dst);
+    }
+    dma4(p.s + (size_t)kg * 16, slot + p.sdst);
+    dma4(a.gsum + (p.g + (uint32_t)kg), slot + p.gdst);
 }
 
 // bf16 pair {hi(X), bf16(X - hi(X))} in the low dword of an MFMA A fragment
@@ -202,16 +237,16 @@ struct BigOps {
 // stored at slot (8h + s) ^ (R & 15) = (8h ^ (col & 15)) ^ s. Rows are 256 B
 // and the area is 256-B aligned, so step s's address is step 0's with bits
 // 4-6 flipped by s; token block 1 is 32 rows (8 KiB) further.
-__device__ __forceinline__ uint32_t big_xa0(const char* slot, int wave, int lane) {
-    const int wm = wave & 1, col = lane & 31, h = lane >> 5;
-    return lds_addr(slot + BigRing::kXOff) + (uint32_t)BigRing::row_off(wm * 64 + col) +
+__device__ __forceinline__ uint32_t big_xa0(const char* slot, const BigGeo& gm, int lane) {
+    const int col = lane & 31, h = lane >> 5;
+    return lds_addr(slot + gm.xoff) + (uint32_t)BigRing::row_off(gm.wm * 64 + col) +
            ((uint32_t)((8 * h) ^ (col & 15)) << 4);
 }
 
 // Issues the reads of BigOps (no wait).
-__device__ __forceinline__ void big_load_ops(const char* slot, int wave, int lane, BigOps& o) {
+__device__ __forceinline__ void big_load_ops(const char* slot, const BigGeo& gm, int lane, BigOps& o) {
     using RG = BigRing;
-    const int wn = wave >> 1, wm = wave & 1;
+    const int wn = gm.wn, wm = gm.wm;
     const int col = lane & 31, h = lane >> 5;
     // B (weights): block jb = tiles 4 wn + 2 jb (+1 for features 16-31); the
     // lane's feature row col & 15 holds K chunks 8h .. 8h + 7 = packed-tile
@@ -229,12 +264,25 @@ __device__ __forceinline__ void big_load_ops(const char* slot, int wave, int lan
     asm volatile("ds_read_b32 %0, %2\n ds_read_b32 %1, %2 offset:128"
                  : "=&v"(o.xs[0]), "=&v"(o.xs[1]) : "v"(ga));
     asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:8192"
-                 : "=&v"(o.av0[0]), "=&v"(o.av0[1]) : "v"(big_xa0(slot, wave, lane)));
+                 : "=&v"(o.av0[0]), "=&v"(o.av0[1]) : "v"(big_xa0(slot, gm, lane)));
+}
+
+// Waits for the reads of big_load_ops and consumes their registers. Every
+// step calls it, whether or not the wave computes: an LDS read returns
+// asynchronously, so a register the compiler thinks free after an unused
+// read could be handed to another value and then overwritten by the late
+// return (for example a store address), and a copy the compiler makes of an
+// operand before the wait would read it too early.
+__device__ __forceinline__ void big_wait_ops(BigOps& o) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(o.bw[0][0]), "+v"(o.bw[0][1]), "+v"(o.bw[1][0]), "+v"(o.bw[1][1]),
+                   "+v"(o.sc[0]), "+v"(o.sc[1]), "+v"(o.xs[0]), "+v"(o.xs[1]), "+v"(o.av0[0]),
+                   "+v"(o.av0[1]));
 }
 
 // One 128-K group of the wave's 64 x 64 tile: p = sum_k (128 + c) x - 136 X
 // per 32 x 32 block (the caller applies the group's scales).
-__device__ __forceinline__ void big_compute(const char* slot, int wave, int lane,
+__device__ __forceinline__ void big_compute(const char* slot, const BigGeo& gm, int lane,
                                             const DqConst& dqc, BigOps& o, f32x16 (&p)[2][2]) {
     const int h = lane >> 5;
     asm volatile("s_waitcnt lgkmcnt(0)"
@@ -247,7 +295,7 @@ __device__ __forceinline__ void big_compute(const char* slot, int wave, int lane
 #pragma unroll
     for (int tb = 0; tb < 2; ++tb) seed[tb] = mfma32x32x16(corr_a(o.xs[tb], h), bneg, f32x16{});
 
-    const uint32_t xa0 = big_xa0(slot, wave, lane);
+    const uint32_t xa0 = big_xa0(slot, gm, lane);
     u32x4 av[2][2];
     av[0][0] = o.av0[0];
     av[0][1] = o.av0[1];
@@ -317,8 +365,9 @@ __device__ __forceinline__ void halve(float (&v)[32], int col) {
 
 template <int NMAT>
 __device__ __forceinline__ void big_epilogue(const BigArgs& a, const BigItem& cur, char* lds,
-                                             int wave, int lane, f32x16 (&acc)[2][2]) {
-    const int wn = wave >> 1, wm = wave & 1;
+                                             const BigGeo& gm, int lane, f32x16 (&acc)[2][2]) {
+    const int wn = gm.wn, wm = gm.wm;
+    const int hs = cur.hs;
     // Laundered lane index: keeps the compiler from hoisting the per-row
     // addresses below out of the streaming loop (they would stay live across
     // it and spill).
@@ -329,8 +378,9 @@ __device__ __forceinline__ void big_epilogue(const BigArgs& a, const BigItem& cu
         // h = silu(g) * u (bf16) for this lane's feature and 32 rows; then the
         // sum of the rounded h over the workgroup's 128 features (one group of
         // I) per row: a fixed butterfly over the 32 lanes of the wave that
-        // share rows, then the 4 feature waves in order.
-        uint16_t* hbase = a.h + (size_t)cur.r0 * a.I + cur.g * 128 + wn * 32;
+        // share rows, then the 4 feature waves in order. A 64-row item's 8
+        // waves cover two such groups, waves 0-3 and 4-7.
+        uint16_t* hbase = a.h + (size_t)cur.r0 * a.I + cur.g * (hs ? 256 : 128) + wn * 32;
         float v[32];
 #pragma unroll
         for (int tb = 0; tb < 2; ++tb)
@@ -356,14 +406,16 @@ __device__ __forceinline__ void big_epilogue(const BigArgs& a, const BigItem& cu
         halve<1>(v, col);
         const uint32_t red = lds_addr(lds + BigRing::kRed);
         const int myrow = acc_row(wm, col >> 4, col & 15, h);
-        lds_write32(red + (uint32_t)((wn * kBigRows + myrow) * 4), v[0]);
+        const int rstride = hs ? 64 : kBigRows;   // rows of the item
+        lds_write32(red + (uint32_t)((wn * rstride + myrow) * 4), v[0]);
         __builtin_amdgcn_s_barrier();
-        if (wn == 0) {
+        if ((wn & 3) == 0) {
             float s = 0.0f;
 #pragma unroll
             for (int w = 0; w < 4; ++w)
-                s += __uint_as_float(lds_read32(red + (uint32_t)((w * kBigRows + myrow) * 4)));
-            if (myrow < cur.nr) a.hsum[((size_t)cur.r0 + myrow) * (a.I / 128) + cur.g] = s;
+                s += __uint_as_float(lds_read32(red + (uint32_t)(((wn + w) * rstride + myrow) * 4)));
+            const int grp = hs ? cur.g * 2 + (wn >> 2) : cur.g;
+            if (myrow < cur.nr) a.hsum[((size_t)cur.r0 + myrow) * (a.I / 128) + grp] = s;
         }
         __builtin_amdgcn_s_barrier();   // partials consumed before the next item reuses them
     } else {
@@ -372,7 +424,7 @@ __device__ __forceinline__ void big_epilogue(const BigArgs& a, const BigItem& cu
         uint16_t* d16 = reinterpret_cast<uint16_t*>(a.dpart);
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb) {
-            uint16_t* dbase = d16 + (size_t)cur.r0 * a.H + cur.g * 256 + wn * 64 + jb * 32;
+            uint16_t* dbase = d16 + (size_t)cur.r0 * a.H + cur.g * (hs ? 512 : 256) + wn * 64 + jb * 32;
 #pragma unroll
             for (int tb = 0; tb < 2; ++tb)
 #pragma unroll
@@ -392,16 +444,17 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
     int* table = reinterpret_cast<int*>(lds + RG::kTab);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int wm = wave & 1;
     const int K = NMAT == 2 ? a.H : a.I;
     const int KG = K / 128;
     const int nfg = (NMAT == 2 ? a.I : a.H) / BigShape<NMAT>::kFeat;
-    const long total = (long)(*a.ntiles) * nfg;
+    // ntiles[1]: tiles taken as 128-row items; the rest are half tiles.
+    const int ntiles = a.ntiles[0], n128 = a.ntiles[1];
+    const long total = big2_total(ntiles, n128, nfg);
     const long nitems = big_rounds(total);
 
     for (long k0 = 0; k0 < nitems; k0 += kBigTable) {
         const int cnt = (int)min((long)kBigTable, nitems - k0);
-        big_fill_table<NMAT == 2>(a.tiles, a.rows_tok, table, k0, cnt, nfg);
+        big2_fill_table<NMAT == 2>(a.tiles, a.rows_tok, table, k0, cnt, nfg, n128);
         __syncthreads();
         const long nsteps = (long)cnt * KG;
 
@@ -426,13 +479,14 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
         else if (nsteps == 2) wait_vmcnt<RG::kDma>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        BigOps ops;
-        big_load_ops(lds, wave, lane, ops);
-
         int cur_k = 0, cur_g = 0;
         BigItem cur = big_item(lds + RG::kTab, 0);
+        BigGeo gc = big_geo(cur.hs, wave);
+        BigOps ops;
+        big_load_ops(lds, gc, lane, ops);
+        big_wait_ops(ops);
         // Whether this wave's 64 rows hold any live row (wave-uniform per item).
-        bool live = cur.nr > wm * 64;
+        bool live = cur.nr > gc.wm * 64;
         f32x16 acc[2][2];
 #pragma unroll
         for (int jb = 0; jb < 2; ++jb)
@@ -445,7 +499,7 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
             // A wave whose 64 rows are all past the tile's end skips the group;
             // a half-live wave computes both 32-row blocks (one branch-free body
             // keeps the accumulators in fixed registers).
-            if (live) big_compute(lds + (step % kBigD) * RG::kSlot, wave, lane, dqc, ops, p);
+            if (live) big_compute(lds + (step % kBigD) * RG::kSlot, gc, lane, dqc, ops, p);
 #endif
             if (step + 2 < nsteps) wait_vmcnt<RG::kDma>();
             else wait_vmcnt<0>();
@@ -454,12 +508,16 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
 #endif
             if (step + kBigD < nsteps) issue_next(step + kBigD);
             const uint32_t sc[2] = {ops.sc[0], ops.sc[1]};
-            if (step + 1 < nsteps) big_load_ops(lds + ((step + 1) % kBigD) * RG::kSlot, wave, lane, ops);
+            if (step + 1 < nsteps) {
+                // Group step + 1 may start the next item, of the other shape.
+                const BigGeo gn = cur_g + 1 < KG ? gc : big_geo(big_item(lds + RG::kTab, cur_k + 1).hs, wave);
+                big_load_ops(lds + ((step + 1) % kBigD) * RG::kSlot, gn, lane, ops);
+            }
 #ifndef GLMMOE_BIG_NOCOMPUTE
             if (live) big_rescale(sc, p, acc);
 #endif
             if (++cur_g == KG) {
-                big_epilogue<NMAT>(a, cur, lds, wave, lane, acc);
+                big_epilogue<NMAT>(a, cur, lds, gc, lane, acc);
 #pragma unroll
                 for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
@@ -467,9 +525,14 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
                 cur_g = 0;
                 if (++cur_k < cnt) {
                     cur = big_item(lds + RG::kTab, cur_k);
-                    live = cur.nr > wm * 64;
+                    gc = big_geo(cur.hs, wave);
+                    live = cur.nr > gc.wm * 64;
                 }
             }
+            // Last in the iteration: the next step's operands have arrived
+            // before anything (including copies the compiler makes for the
+            // loop) reads their registers.
+            big_wait_ops(ops);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();

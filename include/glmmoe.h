@@ -133,7 +133,7 @@ typedef struct glmmoe_layer_ws {
     int* sorted_row;      /* [R] slot, -1 for shared rows */
     int* inv;             /* [n*topk]: grouped row of (t, s) */
     int* tiles;           /* [max_tiles * 4]: {expert, row0, nrows, 0} */
-    int* ntiles;          /* [1] */
+    int* ntiles;          /* [2]: tiles; tiles before the half tiles (128-row layout) */
     uint16_t* h;          /* [R, I] bf16 SiLU(gate) * up */
     float* hsum;          /* [R, I/128] group sums of h (large-group path) */
     float* dpart;         /* [R, H] per-row expert outputs (unweighted): fp32 below 1024 grouped

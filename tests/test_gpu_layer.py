@@ -94,6 +94,46 @@ def test_prefill_full_shape(oracle):
     assert rel_err(out[tok], ref) < TOL_W4A16
 
 
+def test_prefill_half_tiles(oracle):
+    # Large-group tile list: tiles of more than 64 rows first (ntiles[1] of
+    # them), then each expert's last tile of at most 64 rows, both in expert
+    # order; together they cover every expert's rows exactly once. Half tiles
+    # run as 64-row items of twice the features: tokens with rows in them
+    # match the oracle.
+    L = SynthLayer(6144, 256, 8, 2048, seed=1)
+    n = 3000
+    x = L.x(n, 31)
+    ws = L.layer.alloc_workspace(n)
+    out = torch.empty(n, L.H, dtype=torch.float32, device="cuda")
+    L.layer.forward(x, out, ws)
+    torch.cuda.synchronize()
+    v = L.layer.workspace_view(n, ws)
+    nt = _ws_i32(ws, v.ntiles, 2).cpu().numpy()
+    ntiles, n128 = int(nt[0]), int(nt[1])
+    tiles = _ws_i32(ws, v.tiles, 4 * ntiles).view(ntiles, 4).cpu().numpy()
+    offs = _ws_i32(ws, v.expert_offsets, L.E + 2).cpu().numpy()
+    st = _ws_i32(ws, v.sorted_token_ids, n * L.k + n).cpu().numpy()
+    assert 0 < n128 < ntiles
+    full, half = tiles[:n128], tiles[n128:]
+    assert np.all(full[:, 2] > 64) and np.all(full[:, 2] <= 128)
+    assert np.all(half[:, 2] >= 1) and np.all(half[:, 2] <= 64)
+    assert np.all(np.diff(full[:, 0]) >= 0) and np.all(np.diff(half[:, 0]) > 0)
+    covered = np.zeros(n * L.k + n, np.int32)
+    for e, r0, nr, _ in tiles:
+        lo, hi = (offs[e], offs[e + 1]) if e < L.E else (n * L.k, n * L.k + n)
+        assert lo <= r0 and r0 + nr <= hi, (e, r0, nr)
+        covered[r0:r0 + nr] += 1
+    assert np.all(covered == 1)
+    # Tokens with a row in a half tile, of the routed and the shared expert.
+    picks = []
+    for e, r0, nr, _ in half[:: max(1, len(half) // 3)][:3]:
+        picks.append(int(st[r0 + nr - 1]))
+    tok = np.array(sorted(set(picks)))
+    logits = _ws_f32(ws, v.logits, n * L.E).view(n, L.E).cpu().numpy()
+    ref, _, _ = L.oracle_forward(oracle, x, tok, logits)
+    assert rel_err(out.cpu().numpy()[tok], ref) < TOL_W4A16
+
+
 def test_spec_verify_zipf(oracle):
     # 8 x 65 tokens, routing skewed by a Zipf(1.1) log-prior.
     L = SynthLayer(6144, 256, 8, 2048, seed=4, zipf_s=1.1)
