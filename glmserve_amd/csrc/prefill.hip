@@ -71,9 +71,8 @@ struct BigRing {
     static constexpr int kX64 = 32 * 1024;
     static constexpr int kSOff = 48 * 1024;             // 32 tiles x 32 B
     static constexpr int kGOff = kSOff + 1024;          // 128 rows x 4 B
-    static constexpr int kJunk = kGOff + 512;           // target of the placeholder DMAs
     static constexpr int kQuad = 1024;                  // one DMA = 4 rows x 256 B
-    static constexpr int kSlot = kJunk + 256;
+    static constexpr int kSlot = kGOff + 512;
     static constexpr int kBytes = kBigD * kSlot;
     static constexpr int kRed = kBytes;                 // [4][128] or [8][64] floats: h group-sum partials
     static constexpr int kTab = kRed + 4 * kBigRows * 4;
@@ -82,8 +81,13 @@ struct BigRing {
 #ifdef GLMMOE_BIG_NODMA
     static constexpr int kDma = 0;   // diagnostics: compute on stale LDS, no streaming
 #else
-    static constexpr int kDma = 6 + 1 + 1;              // per wave per group
+    static constexpr int kDma = 6;   // weight / activation DMAs per wave per group
 #endif
+    // Plus one small DMA in waves 0-2: the scales of all the item's tiles
+    // (wave 0, 16 B per lane) and the row group sums (waves 1, 2: rows 0-63,
+    // 64-127). Every DMA instruction holds a slot of the CU's memory queue,
+    // so there are no placeholder DMAs to even the counts out; the waits
+    // count per wave.
     // Activation rows are 256 B each, so one DMA of 64 lanes reads 4 whole
     // rows, 16 consecutive lanes per row (lanes that share cache lines are
     // adjacent, which the address coalescer needs for full L2 bandwidth).
@@ -125,10 +129,10 @@ __device__ __forceinline__ void tile_of(int t, int g, int hs, int& m, int& fb) {
 // the loop's VGPRs low.
 struct IssuePtrs {
     const uint4* w[4];       // this wave's weight tiles (2 or 4; lane added at issue)
-    const uint16_t* s;       // scale dword of this lane
-    uint32_t g;              // gsum offset of one row
+    const uint16_t* s;       // wave 0: 16 B of scales of this lane
+    uint32_t g;              // waves 1, 2: gsum offset of one row
     uint32_t x[4];           // src offset of 16 B of one activation row, per row DMA (4 or 2)
-    int hs, sdst, gdst;      // shape; LDS targets of the scale and group-sum DMAs
+    int hs;
 };
 
 template <int NMAT>
@@ -158,19 +162,16 @@ __device__ __forceinline__ IssuePtrs issue_ptrs(const BigArgs& a, const BigItem&
         tile_of<NMAT>(wave * nw + (j < nw ? j : 0), it.g, hs, m, fb);
         p.w[j] = wbase[m] + (size_t)fb * KG * 64;
     }
-    // Scales: lane l of waves < ns fetches dword l % 8 of tile
-    // 8 (wave % ns) + l / 8 (ns = 2 or 4 waves cover the 16 or 32 tiles).
-    const int ns = hs ? 4 : 2;
+    // Scales (wave 0): lane l fetches half l % 2 (16 B) of tile l / 2's 32 B;
+    // a 128-row item has 16 tiles, so lanes 32-63 fetch them a second time.
     {
         int m, fb;
-        tile_of<NMAT>((wave % ns) * 8 + (lane >> 3), it.g, hs, m, fb);
-        p.s = sbase[m] + (size_t)fb * KG * 16 + (lane & 7) * 2;
+        tile_of<NMAT>((lane >> 1) & (hs ? 31 : 15), it.g, hs, m, fb);
+        p.s = sbase[m] + (size_t)fb * KG * 16 + (lane & 1) * 8;
     }
-    p.sdst = wave < ns ? RG::kSOff + (wave % ns) * 256 : RG::kJunk;
-    // Row group sums: waves 2, 3 (rows 64 (wave & 1) + lane) or wave 4 (row lane).
-    p.g = lds_read32(it.tab + 16 + ((hs ? 0 : (wave & 1) * 64) + lane) * 4) * (uint32_t)KG;
-    p.gdst = hs ? (wave == 4 ? RG::kGOff : RG::kJunk)
-                : ((wave >> 1) == 1 ? RG::kGOff + (wave & 1) * 256 : RG::kJunk);
+    // Row group sums (waves 1, 2): row 64 (wave - 1) + lane (a 64-row item
+    // uses rows 0-63; rows past the tile's end repeat row 0).
+    p.g = lds_read32(it.tab + 16 + (((wave - 1) & 1) * 64 + lane) * 4) * (uint32_t)KG;
     // Activation DMA j fills rows rpw * wave + 4 j + lane / 16 (rpw = 16 or 8
     // rows per wave); lane's LDS slot lane % 16 holds chunk (lane % 16) ^
     // (row & 15) of its row. The table's row map holds the token (gate/up) or
@@ -211,8 +212,16 @@ __device__ __forceinline__ void big_issue(const BigArgs& a, const IssuePtrs& p, 
         const int dst = hs ? (wave * 4 + j) * 1024 : RG::kX128 + (wave * 4 + j) * RG::kQuad;
         dma16(hs ? wsrc : xsrc, slot + dst);
     }
-    dma4(p.s + (size_t)kg * 16, slot + p.sdst);
-    dma4(a.gsum + (p.g + (uint32_t)kg), slot + p.gdst);
+    if (wave == 0) dma16(p.s + (size_t)kg * 16, slot + RG::kSOff);
+    else if (wave < 3) dma4(a.gsum + (p.g + (uint32_t)kg), slot + RG::kGOff + (wave - 1) * 256);
+}
+
+// Waits until at most N groups of this wave's DMAs are pending (the waves
+// with a small DMA issue kDma + 1 per group).
+template <int N>
+__device__ __forceinline__ void big_wait_groups(bool small) {
+    if (small) wait_vmcnt<N * (BigRing::kDma + 1)>();
+    else wait_vmcnt<N * BigRing::kDma>();
 }
 
 // bf16 pair {hi(X), bf16(X - hi(X))} in the low dword of an MFMA A fragment
@@ -436,14 +445,33 @@ __device__ __forceinline__ void big_epilogue(const BigArgs& a, const BigItem& cu
     }
 }
 
+#ifdef GLMMOE_BIG_TRACE
+// Diagnostics: per-wave shader-clock totals of the main-loop phases (compute,
+// DMA wait, barrier, issue + operand reads, rescale, epilogue), printed for
+// the first workgroups.
+#define BIG_T(i)                                                        \
+    do {                                                                \
+        const unsigned long long t_ = __builtin_amdgcn_s_memtime();     \
+        bt_[(i)] += t_ - bt_last_;                                      \
+        bt_last_ = t_;                                                  \
+    } while (0)
+#else
+#define BIG_T(i) do {} while (0)
+#endif
+
 template <int NMAT>
 __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
     using RG = BigRing;
+#ifdef GLMMOE_BIG_TRACE
+    unsigned long long bt_[6] = {0, 0, 0, 0, 0, 0};
+    unsigned long long bt_last_ = __builtin_amdgcn_s_memtime();
+#endif
     extern __shared__ __align__(16) char lds[];
     const DqConst dqc = dq_const();
     int* table = reinterpret_cast<int*>(lds + RG::kTab);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const bool small = wave < 3;   // issues one small DMA per group
     const int K = NMAT == 2 ? a.H : a.I;
     const int KG = K / 128;
     const int nfg = (NMAT == 2 ? a.I : a.H) / BigShape<NMAT>::kFeat;
@@ -475,8 +503,8 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
         };
         for (int j = 0; j < kBigD; ++j)
             if (j < nsteps) issue_next(j);
-        if (nsteps >= 3) wait_vmcnt<RG::kDma * 2>();
-        else if (nsteps == 2) wait_vmcnt<RG::kDma>();
+        if (nsteps >= 3) big_wait_groups<2>(small);
+        else if (nsteps == 2) big_wait_groups<1>(small);
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
         int cur_k = 0, cur_g = 0;
@@ -501,11 +529,14 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
             // keeps the accumulators in fixed registers).
             if (live) big_compute(lds + (step % kBigD) * RG::kSlot, gc, lane, dqc, ops, p);
 #endif
-            if (step + 2 < nsteps) wait_vmcnt<RG::kDma>();
+            BIG_T(0);
+            if (step + 2 < nsteps) big_wait_groups<1>(small);
             else wait_vmcnt<0>();
+            BIG_T(1);
 #ifndef GLMMOE_BIG_NOBARRIER
             __builtin_amdgcn_s_barrier();
 #endif
+            BIG_T(2);
             if (step + kBigD < nsteps) issue_next(step + kBigD);
             const uint32_t sc[2] = {ops.sc[0], ops.sc[1]};
             if (step + 1 < nsteps) {
@@ -513,9 +544,11 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
                 const BigGeo gn = cur_g + 1 < KG ? gc : big_geo(big_item(lds + RG::kTab, cur_k + 1).hs, wave);
                 big_load_ops(lds + ((step + 1) % kBigD) * RG::kSlot, gn, lane, ops);
             }
+            BIG_T(3);
 #ifndef GLMMOE_BIG_NOCOMPUTE
             if (live) big_rescale(sc, p, acc);
 #endif
+            BIG_T(4);
             if (++cur_g == KG) {
                 big_epilogue<NMAT>(a, cur, lds, gc, lane, acc);
 #pragma unroll
@@ -533,10 +566,16 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
             // before anything (including copies the compiler makes for the
             // loop) reads their registers.
             big_wait_ops(ops);
+            BIG_T(5);
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
     }
+#ifdef GLMMOE_BIG_TRACE
+    if (lane == 0 && blockIdx.x < 3)
+        printf("BIGT %d wg %d w %d: comp %llu vmw %llu bar %llu iss %llu resc %llu epi %llu\n", NMAT,
+               (int)blockIdx.x, wave, bt_[0], bt_[1], bt_[2], bt_[3], bt_[4], bt_[5]);
+#endif
 }
 
 template <int NMAT>
