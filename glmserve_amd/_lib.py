@@ -10,7 +10,7 @@ LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), "_lib", "lib
 LIB_PATH = os.environ.get("GLMMOE_LIB_PATH", LIB_PATH)
 
 # Every exported symbol of include/glmmoe.h, with its ctypes signature.
-_vp, _i, _f, _sz = C.c_void_p, C.c_int, C.c_float, C.c_size_t
+_vp, _i, _f, _sz, _i64 = C.c_void_p, C.c_int, C.c_float, C.c_size_t, C.c_int64
 SIGNATURES = {
     "glmmoe_version": (C.c_char_p, []),
     "glmmoe_router_logits_workspace_bytes": (_sz, [_i, _i, _i]),
@@ -34,6 +34,18 @@ SIGNATURES = {
     "glmmoe_expert_ffn_fp8": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "glmmoe_profile_enable": (_i, [_i]),
     "glmmoe_profile_read": (_i, [_vp, _vp]),
+    "glmmoe_ref_register_w4a16": (_i, [_vp, _vp, _vp, _vp]),
+    "glmmoe_ref_unregister_w4a16": (_i, [_vp, _vp, _vp]),
+    "glmmoe_ref_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "glmmoe_ref_set_workspace": (_i, [_vp, _sz]),
+    "glmmoe_ref_moe_expert_ffn_w4a16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,
+                                             _i, _i, _i, _i, _i, _i, _vp, _vp]),
+    "glmmoe_ref_moe_expert_ffn": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp,
+                                       _vp]),
+    "glmmoe_ref_gemm_w4a16": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "glmmoe_ref_gemm_fp8": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
+    "glmmoe_ref_silu_mul": (_i, [_vp, _vp, _vp, _i64, _vp]),
+    "glmmoe_ref_add_inplace": (_i, [_vp, _vp, _i64, _vp]),
 }
 
 STAGES = ["router_logits", "router_topk", "dispatch", "gate_up", "down", "combine"]

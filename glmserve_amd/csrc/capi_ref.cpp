@@ -1,0 +1,189 @@
+// Reference-signature C-ABI: the cuda/kernels.cuh launchers of the MoE branch
+// (src/model_gpu.cpp:1448-1494) with the reference's arguments and fp32
+// activations. Declarations and contracts: include/glmmoe.h.
+#include <hip/hip_runtime.h>
+
+#include <map>
+#include <mutex>
+#include <vector>
+
+#include "../../include/glmmoe.h"
+#include "kernels.hpp"
+
+using namespace glmmoe;
+
+namespace {
+
+inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
+inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Packed copies of reference-layout weight sets, keyed by the reference's
+// qweight pointers (host state; the lock covers lookups and updates).
+struct Registered {
+    const uint8_t *gate_q, *up_q, *down_q;
+    glmmoe_w4a16_layer packed;
+};
+std::mutex g_mu;
+std::vector<Registered> g_sets;
+std::map<int, std::pair<void*, size_t>> g_ws;   // device -> caller workspace
+
+// Routed-only layer descriptor of the given shape whose pointers are
+// placeholders: used to size the workspace.
+glmmoe_w4a16_layer shape_layer(int topk, int hidden, int moe_inter, int E) {
+    glmmoe_w4a16_layer L{};
+    L.hidden = hidden;
+    L.moe_inter = moe_inter;
+    L.n_experts = E;
+    L.topk = topk;
+    L.norm_topk = 1;
+    L.routed_scale = 1.0f;
+    const void* p = reinterpret_cast<const void*>(static_cast<uintptr_t>(256));
+    L.gate_q = L.up_q = L.down_q = static_cast<const uint8_t*>(p);
+    L.gate_s = L.up_s = L.down_s = static_cast<const uint16_t*>(p);
+    return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+int glmmoe_ref_register_w4a16(const uint8_t* gate_q, const uint8_t* up_q, const uint8_t* down_q,
+                              const glmmoe_w4a16_layer* packed) {
+    if (!gate_q || !up_q || !down_q || !packed) return GLMMOE_ERR_ARG;
+    if (!packed->gate_q || !packed->gate_s || !packed->up_q || !packed->up_s ||
+        !packed->down_q || !packed->down_s)
+        return GLMMOE_ERR_ARG;
+    Registered r{gate_q, up_q, down_q, *packed};
+    // Routed experts only: the reference's moe_expert_ffn_w4a16 has no shared
+    // expert and no router.
+    r.packed.sh_gate_q = r.packed.sh_up_q = r.packed.sh_down_q = nullptr;
+    r.packed.sh_gate_s = r.packed.sh_up_s = r.packed.sh_down_s = nullptr;
+    r.packed.router_w = nullptr;
+    r.packed.e_bias = nullptr;
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (auto& e : g_sets)
+        if (e.gate_q == gate_q && e.up_q == up_q && e.down_q == down_q) {
+            e = r;
+            return GLMMOE_OK;
+        }
+    g_sets.push_back(r);
+    return GLMMOE_OK;
+}
+
+int glmmoe_ref_unregister_w4a16(const uint8_t* gate_q, const uint8_t* up_q,
+                                const uint8_t* down_q) {
+    std::lock_guard<std::mutex> lk(g_mu);
+    for (size_t i = 0; i < g_sets.size(); ++i)
+        if (g_sets[i].gate_q == gate_q && g_sets[i].up_q == up_q && g_sets[i].down_q == down_q) {
+            g_sets.erase(g_sets.begin() + (long)i);
+            return GLMMOE_OK;
+        }
+    return GLMMOE_ERR_ARG;
+}
+
+size_t glmmoe_ref_workspace_bytes(int n, int topk, int hidden, int moe_inter, int E) {
+    if (n <= 0 || topk <= 0 || hidden <= 0 || moe_inter <= 0 || E <= 0) return 0;
+    const glmmoe_w4a16_layer L = shape_layer(topk, hidden, moe_inter, E);
+    const size_t lw = glmmoe_layer_workspace_bytes(&L, n);
+    if (!lw) return 0;
+    return align256((size_t)n * hidden * 2) + lw;
+}
+
+int glmmoe_ref_set_workspace(void* workspace, size_t bytes) {
+    int dev = 0;
+    if (hipGetDevice(&dev) != hipSuccess) return GLMMOE_ERR_LAUNCH;
+    std::lock_guard<std::mutex> lk(g_mu);
+    if (!workspace || !bytes) g_ws.erase(dev);
+    else g_ws[dev] = {workspace, bytes};
+    return GLMMOE_OK;
+}
+
+int glmmoe_ref_moe_expert_ffn_w4a16(const float* x, const int* topk_ids, const float* topk_weights,
+                                    const uint8_t* gate_q, const float* gate_sc,
+                                    const uint8_t* up_q, const float* up_sc,
+                                    const uint8_t* down_q, const float* down_sc, int n, int topk,
+                                    int hidden, int moe_inter, int E, int group_size, float* out,
+                                    void* stream) {
+    (void)gate_sc;
+    (void)up_sc;
+    (void)down_sc;
+    if (!x || !topk_ids || !topk_weights || !out || n <= 0) return GLMMOE_ERR_ARG;
+    if (group_size != 128) return GLMMOE_ERR_SHAPE;
+    glmmoe_w4a16_layer L;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    {
+        std::lock_guard<std::mutex> lk(g_mu);
+        const Registered* hit = nullptr;
+        for (const auto& e : g_sets)
+            if (e.gate_q == gate_q && e.up_q == up_q && e.down_q == down_q) hit = &e;
+        if (!hit) return GLMMOE_ERR_ARG;
+        L = hit->packed;
+        int dev = 0;
+        if (hipGetDevice(&dev) != hipSuccess) return GLMMOE_ERR_LAUNCH;
+        const auto w = g_ws.find(dev);
+        if (w == g_ws.end()) return GLMMOE_ERR_WORKSPACE;
+        ws = w->second.first;
+        ws_bytes = w->second.second;
+    }
+    if (L.hidden != hidden || L.moe_inter != moe_inter || L.n_experts != E) return GLMMOE_ERR_SHAPE;
+    L.topk = topk;
+    L.norm_topk = 1;        // unused: the weights come from the caller
+    L.routed_scale = 1.0f;
+    const size_t xb = align256((size_t)n * hidden * 2);
+    const size_t need = glmmoe_ref_workspace_bytes(n, topk, hidden, moe_inter, E);
+    if (!need) return GLMMOE_ERR_SHAPE;
+    if (ws_bytes < need) return GLMMOE_ERR_WORKSPACE;
+    uint16_t* xbf = static_cast<uint16_t*>(ws);
+    int rc = launch_f32_to_bf16(x, xbf, (long)n * hidden, S(stream));
+    if (rc) return GLMMOE_ERR_LAUNCH;
+    return glmmoe_expert_ffn_w4a16(&L, xbf, n, topk_ids, topk_weights, out,
+                                   static_cast<char*>(ws) + xb, ws_bytes - xb, stream);
+}
+
+int glmmoe_ref_moe_expert_ffn(const float* x, const int* topk_ids, const float* topk_weights,
+                              const float* gate_w, const float* up_w, const float* down_w, int n,
+                              int topk, int hidden, int moe_inter, int E, float* out,
+                              void* stream) {
+    (void)E;
+    if (!x || !topk_ids || !topk_weights || !gate_w || !up_w || !down_w || !out || n <= 0 ||
+        topk <= 0 || hidden <= 0 || moe_inter <= 0)
+        return GLMMOE_ERR_ARG;
+    const int rc = launch_ref_expert_f32(x, topk_ids, topk_weights, gate_w, up_w, down_w, n, topk,
+                                         hidden, moe_inter, out, S(stream));
+    return rc == -2 ? GLMMOE_ERR_SHAPE : rc ? GLMMOE_ERR_LAUNCH : GLMMOE_OK;
+}
+
+int glmmoe_ref_gemm_w4a16(const float* x, const uint8_t* qW, const float* scales,
+                          const float* bias, float* y, int64_t n, int64_t in, int64_t out,
+                          int64_t group_size, void* stream) {
+    if (!x || !qW || !scales || !y || n <= 0 || in <= 0 || out <= 0 || group_size <= 0)
+        return GLMMOE_ERR_ARG;
+    if (n > INT32_MAX || in > INT32_MAX || out > INT32_MAX) return GLMMOE_ERR_SHAPE;
+    return launch_ref_gemm_w4(x, qW, scales, bias, y, (int)n, (int)in, (int)out, (int)group_size,
+                              S(stream))
+               ? GLMMOE_ERR_LAUNCH
+               : GLMMOE_OK;
+}
+
+int glmmoe_ref_gemm_fp8(const float* x, const uint8_t* fp8W, const float* w_scale,
+                        const float* bias, float* y, int64_t n, int64_t in, int64_t out,
+                        void* stream) {
+    if (!x || !fp8W || !y || n <= 0 || in <= 0 || out <= 0) return GLMMOE_ERR_ARG;
+    if (n > INT32_MAX || in > INT32_MAX || out > INT32_MAX) return GLMMOE_ERR_SHAPE;
+    return launch_ref_gemm_fp8(x, fp8W, w_scale, bias, y, (int)n, (int)in, (int)out, S(stream))
+               ? GLMMOE_ERR_LAUNCH
+               : GLMMOE_OK;
+}
+
+int glmmoe_ref_silu_mul(const float* g, const float* u, float* out, int64_t n, void* stream) {
+    if (!g || !u || !out || n <= 0) return GLMMOE_ERR_ARG;
+    return launch_ref_silu_mul(g, u, out, (long)n, S(stream)) ? GLMMOE_ERR_LAUNCH : GLMMOE_OK;
+}
+
+int glmmoe_ref_add_inplace(float* y, const float* x, int64_t n, void* stream) {
+    if (!y || !x || n <= 0) return GLMMOE_ERR_ARG;
+    return launch_ref_add_inplace(y, x, (long)n, S(stream)) ? GLMMOE_ERR_LAUNCH : GLMMOE_OK;
+}
+
+}  // extern "C"

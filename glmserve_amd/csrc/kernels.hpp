@@ -97,4 +97,17 @@ int launch_down_fp8(const Fp8Ptrs& P, const uint8_t* hq, const float* hscale, co
                     const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
                     hipStream_t s);
 
+
+// Reference-signature kernels (compat.hip).
+int launch_ref_gemm_w4(const float* x, const uint8_t* qw, const float* sc, const float* bias,
+                       float* y, int n, int in, int out, int g, hipStream_t s);
+int launch_ref_gemm_fp8(const float* x, const uint8_t* w, const float* sc, const float* bias,
+                        float* y, int n, int in, int out, hipStream_t s);
+int launch_ref_expert_f32(const float* x, const int* ids, const float* w, const float* gw,
+                          const float* uw, const float* dw, int n, int topk, int H, int I,
+                          float* out, hipStream_t s);
+int launch_ref_silu_mul(const float* g, const float* u, float* o, long n, hipStream_t s);
+int launch_ref_add_inplace(float* y, const float* x, long n, hipStream_t s);
+int launch_f32_to_bf16(const float* x, uint16_t* y, long n, hipStream_t s);
+
 }  // namespace glmmoe

@@ -202,3 +202,90 @@ def ws_tensor(ws_base, view_ptr, ws, dtype, numel):
     off = view_ptr - ws.data_ptr()
     nbytes = numel * torch.empty((), dtype=dtype).element_size()
     return ws[off:off + nbytes].view(dtype)
+
+
+# ---- Reference signatures (cuda/kernels.cuh argument lists, fp32 activations) ----
+
+def ref_gemm_w4a16(x, qweight, scales, bias, y, group_size=128, stream=None):
+    """gemm_w4a16 (cuda/kernels.cuh:50-52): y[n, out] = x[n, in] . W^T (+ bias), W from
+    qweight [out, ceil(in/2)] u8 and fp32 scales [out, ceil(in/g)]."""
+    n, in_ = x.shape
+    out = qweight.shape[0]
+    _need(x, torch.float32, n * in_, "x")
+    _need(qweight, torch.uint8, out * ((in_ + 1) // 2), "qweight")
+    _need(scales, torch.float32, out * ((in_ + group_size - 1) // group_size), "scales")
+    _need(y, torch.float32, n * out, "y")
+    check(lib().glmmoe_ref_gemm_w4a16(_p(x), _p(qweight), _p(scales), _p(bias), _p(y), n, in_, out,
+                                      group_size, _s(stream)), "ref_gemm_w4a16")
+
+
+def ref_gemm_fp8(x, w, w_scale, bias, y, stream=None):
+    """gemm_fp8 (cuda/kernels.cuh:55-57): e4m3 W [out, in], optional fp32 scale per row."""
+    n, in_ = x.shape
+    out = w.shape[0]
+    _need(x, torch.float32, n * in_, "x")
+    _need(w, torch.uint8, out * in_, "w")
+    _need(y, torch.float32, n * out, "y")
+    check(lib().glmmoe_ref_gemm_fp8(_p(x), _p(w), _p(w_scale), _p(bias), _p(y), n, in_, out,
+                                    _s(stream)), "ref_gemm_fp8")
+
+
+def ref_silu_mul(g, u, out, stream=None):
+    check(lib().glmmoe_ref_silu_mul(_p(g), _p(u), _p(out), g.numel(), _s(stream)), "ref_silu_mul")
+
+
+def ref_add_inplace(y, x, stream=None):
+    check(lib().glmmoe_ref_add_inplace(_p(y), _p(x), y.numel(), _s(stream)), "ref_add_inplace")
+
+
+def ref_moe_expert_ffn(x, topk_ids, topk_weights, gate_w, up_w, down_w, out, stream=None):
+    """moe_expert_ffn (cuda/kernels.cuh:252-257): fp32 experts gate/up [E, I, H], down
+    [E, H, I]; out [n, H] overwritten."""
+    n, H = x.shape
+    E, I, _ = gate_w.shape
+    k = topk_ids.shape[1]
+    check(lib().glmmoe_ref_moe_expert_ffn(_p(x), _p(topk_ids), _p(topk_weights), _p(gate_w),
+                                          _p(up_w), _p(down_w), n, k, H, I, E, _p(out),
+                                          _s(stream)), "ref_moe_expert_ffn")
+
+
+class RefW4Experts:
+    """Reference-layout W4A16 routed experts registered with their packed copy, for
+    glmmoe_ref_moe_expert_ffn_w4a16 (cuda/kernels.cuh:259-268 argument list)."""
+
+    def __init__(self, gate_q, gate_s, up_q, up_s, down_q, down_s, hidden, moe_inter,
+                 group_size=128):
+        E = gate_q.shape[0]
+        self.raw = (gate_q, gate_s, up_q, up_s, down_q, down_s)
+        self.hidden, self.moe_inter, self.E, self.group_size = hidden, moe_inter, E, group_size
+        self.packed = (pack_w4a16(gate_q, gate_s, E, moe_inter, hidden, group_size),
+                       pack_w4a16(up_q, up_s, E, moe_inter, hidden, group_size),
+                       pack_w4a16(down_q, down_s, E, hidden, moe_inter, group_size))
+        st = Layer()
+        st.hidden, st.moe_inter, st.n_experts, st.topk = hidden, moe_inter, E, 1
+        st.gate_q, st.gate_s = _p(self.packed[0][0]), _p(self.packed[0][1])
+        st.up_q, st.up_s = _p(self.packed[1][0]), _p(self.packed[1][1])
+        st.down_q, st.down_s = _p(self.packed[2][0]), _p(self.packed[2][1])
+        self.struct = st
+        check(lib().glmmoe_ref_register_w4a16(_p(gate_q), _p(up_q), _p(down_q),
+                                              ctypes.byref(st)), "ref_register_w4a16")
+
+    def release(self):
+        gq, _, uq, _, dq, _ = self.raw
+        check(lib().glmmoe_ref_unregister_w4a16(_p(gq), _p(uq), _p(dq)), "ref_unregister_w4a16")
+
+    def workspace_bytes(self, n, topk):
+        return lib().glmmoe_ref_workspace_bytes(n, topk, self.hidden, self.moe_inter, self.E)
+
+    @staticmethod
+    def set_workspace(ws):
+        check(lib().glmmoe_ref_set_workspace(_p(ws), 0 if ws is None else ws.numel()),
+              "ref_set_workspace")
+
+    def ffn(self, x, topk_ids, topk_weights, out, stream=None):
+        n = x.shape[0]
+        gq, gs, uq, us, dq, ds = self.raw
+        check(lib().glmmoe_ref_moe_expert_ffn_w4a16(
+            _p(x), _p(topk_ids), _p(topk_weights), _p(gq), _p(gs), _p(uq), _p(us), _p(dq), _p(ds),
+            n, topk_ids.shape[1], self.hidden, self.moe_inter, self.E, self.group_size, _p(out),
+            _s(stream)), "ref_moe_expert_ffn_w4a16")

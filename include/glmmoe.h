@@ -3,7 +3,8 @@
  *
  * Every pointer argument is a DEVICE pointer owned by the caller unless noted;
  * `stream` is a hipStream_t passed as void* (NULL = the null stream). No entry
- * point allocates, frees or synchronizes; work is enqueued on `stream`.
+ * point allocates device memory, frees or synchronizes; work is enqueued on
+ * `stream`.
  * Return value: GLMMOE_OK (0) or a negative GLMMOE_ERR_* code; nothing throws
  * across this boundary (the reference's wrappers return void and print launch
  * errors, cuda/moe_expert.cu:126-129; callers here get a code instead).
@@ -260,6 +261,80 @@ int glmmoe_expert_ffn_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n,
 #define GLMMOE_PROF_MAX_CALLS 512
 int glmmoe_profile_enable(int on);
 int glmmoe_profile_read(float* stage_ms, int* n_calls);
+
+/* ---- Reference-signature entry points ---------------------------------------
+ * The cuda/kernels.cuh launchers that the MoE branch of the forward calls
+ * (src/model_gpu.cpp:1448-1494), with the reference's arguments, weight
+ * layouts and fp32 activations, for callers that keep the reference's call
+ * sites; include/glmmoe/kernels.hpp exposes them under the reference's names
+ * and argument lists. */
+
+/* Routed W4A16 experts, replacing moe_expert_ffn_w4a16 (cuda/kernels.cuh:259-268,
+ * cuda/moe_expert.cu:143-244) argument for argument: x fp32 [n, hidden];
+ * gate/up qweight [E, moe_inter, hidden/2] u8 (low nibble = even column,
+ * value nibble - 8) with fp32 scales [E, moe_inter, hidden/group_size]; down
+ * [E, hidden, moe_inter/2] with [E, hidden, moe_inter/group_size]; out fp32
+ * [n, hidden] overwritten with sum_s topk_weights[t,s] * y_{t,s} in slot
+ * order (no shared expert, as in the reference).
+ * The work runs the grouped kernels of glmmoe_expert_ffn_w4a16 on the native
+ * packed copy of those weights (glmmoe_pack_w4a16, once at load time) that
+ * glmmoe_ref_register_w4a16 associated with (gate_q, up_q, down_q), in the
+ * workspace glmmoe_ref_set_workspace registered for the current device, so
+ * the call allocates nothing. x is rounded to bf16 (RNE) for those kernels and
+ * the scales were rounded to bf16 when packed: results are within the W4A16
+ * tolerance of the reference, not bit-identical. The scale pointers are not
+ * read. Errors: GLMMOE_ERR_ARG when the weights are not registered,
+ * GLMMOE_ERR_WORKSPACE when no workspace of glmmoe_ref_workspace_bytes is
+ * registered, GLMMOE_ERR_SHAPE for a shape other than the registered one.
+ * Limits: group_size 128, hidden % 256 == 0, moe_inter % 128 == 0,
+ * topk <= 8, E <= 512. The registry is a host-side table behind a lock;
+ * registering or releasing while a call of the same weights is being
+ * enqueued on another thread is the caller's race. */
+int glmmoe_ref_register_w4a16(const uint8_t* gate_q, const uint8_t* up_q, const uint8_t* down_q,
+                              const glmmoe_w4a16_layer* packed);
+int glmmoe_ref_unregister_w4a16(const uint8_t* gate_q, const uint8_t* up_q,
+                                const uint8_t* down_q);
+size_t glmmoe_ref_workspace_bytes(int n, int topk, int hidden, int moe_inter, int E);
+int glmmoe_ref_set_workspace(void* workspace, size_t bytes);
+int glmmoe_ref_moe_expert_ffn_w4a16(const float* x, const int* topk_ids, const float* topk_weights,
+                                    const uint8_t* gate_q, const float* gate_sc,
+                                    const uint8_t* up_q, const float* up_sc,
+                                    const uint8_t* down_q, const float* down_sc, int n, int topk,
+                                    int hidden, int moe_inter, int E, int group_size, float* out,
+                                    void* stream);
+
+/* Routed experts with fp32 weights, replacing moe_expert_ffn (cuda/kernels.cuh:
+ * 252-257, cuda/moe_expert.cu:32-130): gate/up [E, moe_inter, hidden], down
+ * [E, hidden, moe_inter] fp32; out [n, hidden] overwritten with
+ * sum_s w[t,s] * down_e(silu(gate_e x) * up_e x) in slot order. One workgroup
+ * per token, fp32 throughout (the reference's per-token structure; fp32
+ * experts are not a served format). Limit: topk * moe_inter <= 40960. */
+int glmmoe_ref_moe_expert_ffn(const float* x, const int* topk_ids, const float* topk_weights,
+                              const float* gate_w, const float* up_w, const float* down_w, int n,
+                              int topk, int hidden, int moe_inter, int E, float* out,
+                              void* stream);
+
+/* y[n, out] = x[n, in] . W[out, in]^T (+ bias), fp32 in and out, replacing
+ * gemm_w4a16 (cuda/kernels.cuh:50-52, cuda/int4_gemm.cu:15-48): qW [out,
+ * ceil(in/2)] u8, scales [out, ceil(in/group_size)] fp32, bias nullable; the
+ * shared expert's linears. Any shape; in % 8 == 0 with group_size % 8 == 0
+ * takes the staged path (a workgroup per 16 rows, tokens in blocks of 8). */
+int glmmoe_ref_gemm_w4a16(const float* x, const uint8_t* qW, const float* scales,
+                          const float* bias, float* y, int64_t n, int64_t in, int64_t out,
+                          int64_t group_size, void* stream);
+
+/* The same product with e4m3 weights [out, in] and an optional fp32 scale per
+ * row, replacing gemm_fp8 (cuda/kernels.cuh:55-57, cuda/fp8_gemm.cu:14-44).
+ * e4m3 is the OCP "fn" encoding: codes 0x7f / 0xff decode to NaN (as the
+ * reference's device conversion does). */
+int glmmoe_ref_gemm_fp8(const float* x, const uint8_t* fp8W, const float* w_scale,
+                        const float* bias, float* y, int64_t n, int64_t in, int64_t out,
+                        void* stream);
+
+/* out = silu(g) * u and y += x over n floats, replacing silu_mul and
+ * add_inplace (cuda/kernels.cuh:281-282, cuda/mla_glue.cu:10-28). */
+int glmmoe_ref_silu_mul(const float* g, const float* u, float* out, int64_t n, void* stream);
+int glmmoe_ref_add_inplace(float* y, const float* x, int64_t n, void* stream);
 
 #ifdef __cplusplus
 }

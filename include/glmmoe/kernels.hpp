@@ -11,10 +11,12 @@
 //   * the router logits come from glmmoe_router_logits (bf16 in, fixed
 //     reduction order) rather than gemm_fp32 on fp32 activations;
 //   * expert weights live in the native packed W4A16 layout produced once at
-//     load time by pack_w4a16 (from the reference's qweight/scales layout), and
-//     the routed + shared expert stage is one call (moe_expert_ffn_w4a16 with a
-//     glmmoe_w4a16_layer) instead of moe_expert_ffn_w4a16 + 3 gemm_w4a16 +
-//     silu_mul + add_inplace.
+//     load time by pack_w4a16 (from the reference's qweight/scales layout). The
+//     fast form of the routed + shared expert stage is one call
+//     (moe_expert_ffn_w4a16 with a glmmoe_w4a16_layer) instead of
+//     moe_expert_ffn_w4a16 + 3 gemm_w4a16 + silu_mul + add_inplace; those
+//     launchers also exist with the reference's argument lists (below), the
+//     W4A16 experts after a one-time registration of the packed copy.
 // Define GLMMOE_GLMSERVE_NAMESPACE to also make these visible as
 // glmserve::cuda::* (only when kernels.cuh is not included in the same unit).
 #pragma once
@@ -84,6 +86,52 @@ inline int moe_layer_w4a16(const glmmoe_w4a16_layer& layer, const uint16_t* x_bf
 
 inline size_t moe_layer_workspace_bytes(const glmmoe_w4a16_layer& layer, int n) {
     return glmmoe_layer_workspace_bytes(&layer, n);
+}
+
+// ---- The reference's own argument lists (fp32 activations, reference weight
+// layouts). moe_expert_ffn_w4a16 needs the weights registered once at load
+// time (glmmoe_ref_register_w4a16 with their packed copy) and a workspace
+// registered per device (glmmoe_ref_set_workspace); the rest need nothing.
+
+// cuda/kernels.cuh:263-268
+inline int moe_expert_ffn_w4a16(const float* x, const int* topk_ids, const float* topk_weights,
+                                const uint8_t* gate_q, const float* gate_sc, const uint8_t* up_q,
+                                const float* up_sc, const uint8_t* down_q, const float* down_sc,
+                                int n, int topk, int hidden, int moe_inter, int E, int group_size,
+                                float* out, void* s = nullptr) {
+    return glmmoe_ref_moe_expert_ffn_w4a16(x, topk_ids, topk_weights, gate_q, gate_sc, up_q,
+                                           up_sc, down_q, down_sc, n, topk, hidden, moe_inter, E,
+                                           group_size, out, s);
+}
+
+// cuda/kernels.cuh:254-257
+inline int moe_expert_ffn(const float* x, const int* topk_ids, const float* topk_weights,
+                          const float* gate_w, const float* up_w, const float* down_w, int n,
+                          int topk, int hidden, int moe_inter, int E, float* out,
+                          void* s = nullptr) {
+    return glmmoe_ref_moe_expert_ffn(x, topk_ids, topk_weights, gate_w, up_w, down_w, n, topk,
+                                     hidden, moe_inter, E, out, s);
+}
+
+// cuda/kernels.cuh:50-52
+inline int gemm_w4a16(const float* x, const uint8_t* qW, const float* scales, const float* bias,
+                      float* y, int64_t n, int64_t in, int64_t out, int64_t group_size,
+                      void* s = nullptr) {
+    return glmmoe_ref_gemm_w4a16(x, qW, scales, bias, y, n, in, out, group_size, s);
+}
+
+// cuda/kernels.cuh:55-57
+inline int gemm_fp8(const float* x, const uint8_t* fp8W, const float* w_scale, const float* bias,
+                    float* y, int64_t n, int64_t in, int64_t out, void* s = nullptr) {
+    return glmmoe_ref_gemm_fp8(x, fp8W, w_scale, bias, y, n, in, out, s);
+}
+
+// cuda/kernels.cuh:281-282
+inline int add_inplace(float* y, const float* x, int64_t n, void* s = nullptr) {
+    return glmmoe_ref_add_inplace(y, x, n, s);
+}
+inline int silu_mul(const float* g, const float* u, float* out, int64_t n, void* s = nullptr) {
+    return glmmoe_ref_silu_mul(g, u, out, n, s);
 }
 
 }  // namespace compat

@@ -55,6 +55,35 @@ def test_host_argument_checks():
     assert L.glmmoe_pack_w4a16(dummy, dummy, 2, 1, 16, 128, 128, dummy, dummy, None) == -1
 
 
+def test_reference_signature_host_checks():
+    L = _lib.lib()
+    dummy = C.c_void_p(16)   # never dereferenced: the checks below reject first
+    assert L.glmmoe_ref_moe_expert_ffn_w4a16(None, dummy, dummy, dummy, dummy, dummy, dummy, dummy,
+                                             dummy, 1, 8, 6144, 2048, 256, 128, dummy, None) == -1
+    # group sizes other than 128 are outside the packed format
+    assert L.glmmoe_ref_moe_expert_ffn_w4a16(dummy, dummy, dummy, dummy, dummy, dummy, dummy,
+                                             dummy, dummy, 1, 8, 6144, 2048, 256, 64, dummy,
+                                             None) == -2
+    assert L.glmmoe_ref_gemm_w4a16(None, dummy, dummy, None, dummy, 1, 6144, 2048, 128, None) == -1
+    assert L.glmmoe_ref_gemm_w4a16(dummy, dummy, dummy, None, dummy, 0, 6144, 2048, 128, None) == -1
+    assert L.glmmoe_ref_gemm_fp8(dummy, None, None, None, dummy, 1, 64, 64, None) == -1
+    assert L.glmmoe_ref_silu_mul(dummy, dummy, None, 8, None) == -1
+    assert L.glmmoe_ref_add_inplace(dummy, dummy, 0, None) == -1
+    assert L.glmmoe_ref_moe_expert_ffn(dummy, dummy, dummy, None, dummy, dummy, 1, 8, 64, 64, 16,
+                                       dummy, None) == -1
+    # x in bf16 plus the routed-only layer workspace
+    lw = L.glmmoe_layer_workspace_bytes(C.byref(_layer(shared=False)), 64)
+    assert L.glmmoe_ref_workspace_bytes(64, 8, 6144, 2048, 256) == 64 * 6144 * 2 + lw
+    assert L.glmmoe_ref_workspace_bytes(0, 8, 6144, 2048, 256) == 0
+    # registry: host-side table keyed by the reference's qweight pointers
+    packed = _layer(shared=False)
+    a, b, c = C.c_void_p(0x1000), C.c_void_p(0x2000), C.c_void_p(0x3000)
+    assert L.glmmoe_ref_register_w4a16(None, b, c, C.byref(packed)) == -1
+    assert L.glmmoe_ref_register_w4a16(a, b, c, C.byref(packed)) == 0
+    assert L.glmmoe_ref_unregister_w4a16(a, b, c) == 0
+    assert L.glmmoe_ref_unregister_w4a16(a, b, c) == -1
+
+
 def _layer(H=6144, I=2048, E=256, k=8, shared=True):
     st = _lib.Layer()
     st.hidden, st.moe_inter, st.n_experts, st.topk = H, I, E, k
@@ -105,6 +134,15 @@ def test_cpp_header_compiles_against_the_library(tmp_path):
         '  // reference call sites, unchanged apart from the include\n'
         '  glmserve::cuda::moe_router(nullptr, nullptr, 1, 256, 8, true, 2.5f, nullptr, nullptr);\n'
         '  glmserve::cuda::moe_dispatch(nullptr, 1, 8, 256, nullptr, nullptr, nullptr);\n'
+        '  const float* x = nullptr; float* y = nullptr; const uint8_t* q = nullptr;\n'
+        '  const float* sc = nullptr; const int* ids = nullptr; const float* w = nullptr;\n'
+        '  glmserve::cuda::moe_expert_ffn_w4a16(x, ids, w, q, sc, q, sc, q, sc, 1, 8, 6144, 2048,\n'
+        '                                       256, 128, y);\n'
+        '  glmserve::cuda::moe_expert_ffn(x, ids, w, sc, sc, sc, 1, 8, 6144, 2048, 256, y);\n'
+        '  glmserve::cuda::gemm_w4a16(x, q, sc, nullptr, y, 1, 6144, 2048, 128);\n'
+        '  glmserve::cuda::gemm_fp8(x, q, sc, nullptr, y, 1, 6144, 2048);\n'
+        '  glmserve::cuda::silu_mul(x, x, y, 2048);\n'
+        '  glmserve::cuda::add_inplace(y, x, 6144);\n'
         '  glmmoe_w4a16_layer L{};\n'
         '  return (int)glmserve::cuda::moe_layer_workspace_bytes(L, 1);\n'
         '}\n')
