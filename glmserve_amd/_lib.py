@@ -46,6 +46,10 @@ SIGNATURES = {
     "glmmoe_ref_gemm_fp8": (_i, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "glmmoe_ref_silu_mul": (_i, [_vp, _vp, _vp, _i64, _vp]),
     "glmmoe_ref_add_inplace": (_i, [_vp, _vp, _i64, _vp]),
+    "glmmoe_ref_gemm_q": (_i, [C.c_uint32, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64, _vp]),
+    "glmmoe_ref_moe_expert_ffn_q": (_i, [C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp, _vp,
+                                         _vp, _vp, _i, _i, _i, _i, _i, _i64, _i64, _i64, _vp,
+                                         _vp, _vp, _vp, _vp, _vp]),
 }
 
 STAGES = ["router_logits", "router_topk", "dispatch", "gate_up", "down", "combine"]

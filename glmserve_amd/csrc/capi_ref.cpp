@@ -186,4 +186,44 @@ int glmmoe_ref_add_inplace(float* y, const float* x, int64_t n, void* stream) {
     return launch_ref_add_inplace(y, x, (long)n, S(stream)) ? GLMMOE_ERR_LAUNCH : GLMMOE_OK;
 }
 
+// Rows of `in` elements of GGUF type t fit row_bytes and decode 8 at a time.
+static bool gguf_rows_ok(uint32_t t, int64_t in, int64_t row_bytes) {
+    const int be = gguf_block_elems(t), bb = gguf_block_bytes(t);
+    return be && in % be == 0 && in % 8 == 0 && row_bytes >= in / be * bb;
+}
+
+int glmmoe_ref_gemm_q(uint32_t qtype, const float* x, const uint8_t* qW, const float* bias,
+                      float* y, int64_t n, int64_t in, int64_t out, int64_t row_bytes,
+                      void* stream) {
+    if (!x || !qW || !y || n <= 0 || in <= 0 || out <= 0) return GLMMOE_ERR_ARG;
+    if (n > INT32_MAX || in > INT32_MAX || out > INT32_MAX || !gguf_rows_ok(qtype, in, row_bytes))
+        return GLMMOE_ERR_SHAPE;
+    return launch_gg_gemm(qtype, x, qW, bias, y, (int)n, (int)in, (int)out, (long)row_bytes,
+                          S(stream))
+               ? GLMMOE_ERR_LAUNCH
+               : GLMMOE_OK;
+}
+
+int glmmoe_ref_moe_expert_ffn_q(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
+                                const float* x, const int* topk_ids, const float* topk_w,
+                                const uint8_t* gate_q, const uint8_t* up_q, const uint8_t* down_q,
+                                int n, int topk, int hidden, int moe_inter, int E,
+                                int64_t gate_row_bytes, int64_t up_row_bytes,
+                                int64_t down_row_bytes, float* h_act, float* dpart, float* out,
+                                int* dispatch, float* gu_part, void* stream) {
+    (void)gu_part;   // split-K partials of the reference's decode path; not needed here
+    if (!x || !topk_ids || !topk_w || !gate_q || !up_q || !down_q || !h_act || !dpart || !out ||
+        n <= 0 || topk <= 0 || hidden <= 0 || moe_inter <= 0 || E <= 0)
+        return GLMMOE_ERR_ARG;
+    if (E > 4096 || (int64_t)n * topk > INT32_MAX / 2 || !gguf_rows_ok(gate_type, hidden, gate_row_bytes) ||
+        !gguf_rows_ok(up_type, hidden, up_row_bytes) ||
+        !gguf_rows_ok(down_type, moe_inter, down_row_bytes))
+        return GLMMOE_ERR_SHAPE;
+    return launch_gg_moe(gate_type, up_type, down_type, x, topk_ids, topk_w, gate_q, up_q, down_q,
+                         n, topk, hidden, moe_inter, E, (long)gate_row_bytes, (long)up_row_bytes,
+                         (long)down_row_bytes, h_act, dpart, out, dispatch, S(stream))
+               ? GLMMOE_ERR_LAUNCH
+               : GLMMOE_OK;
+}
+
 }  // extern "C"

@@ -1,0 +1,550 @@
+// GGUF block-quantized weights (ggml block formats) on the reference's
+// launcher signatures:
+//   gg_gemv_kernel      gemm_q (cuda/kernels.cuh:63-66): y[n,out] = x[n,in] . W^T (+ bias),
+//                       W [out, in] rows of GGUF blocks at qW + o * row_bytes.
+//   gg_moe_kernel       moe_expert_ffn_q (cuda/kernels.cuh:117-123, cuda/qgemm.cu:1505-1639):
+//                       gate/up rows [E, moe_inter, hidden], down [E, hidden, moe_inter],
+//                       row o of expert e at base + (e * out + o) * row_bytes.
+//                       Phase 1: h_act[r, f] = silu(gate_e[f] . x_t) * (up_e[f] . x_t) for
+//                       every routed row r = t * topk + s; phase 2: dpart[r, o] =
+//                       down_e[o] . h_act[r]; then out[t] = sum_s w[t, s] * dpart[t*topk+s]
+//                       in slot order (the reference's fixed-order reduce,
+//                       cuda/qgemm.cu:943-955).
+// Element decode restates src/gguf_quant.cpp:98-262 per 8 consecutive elements
+// with the same float operations in the same order, so the dequantized
+// weights equal the reference's bit for bit; products and sums are fp32.
+//
+// Work: a workgroup (4 waves) owns 16 output rows (4 per wave) and a tile of
+// up to 8 input rows. With the caller's `dispatch` scratch the routed rows are
+// first grouped by expert (counting pass, one workgroup), so a tile is 8 rows
+// of one expert and each weight row is read once per tile; without it every
+// routed row is a tile of its own (the reference's token-major path). Each
+// 512-wide K chunk of the tile's input rows is staged in LDS; each lane
+// decodes 8 consecutive K of its 4 weight rows and accumulates 4 x 8 dot
+// products; lane partials are added by a fixed xor butterfly.
+#include <type_traits>
+
+#include "common.hpp"
+#include "kernels.hpp"
+
+namespace glmmoe {
+
+// ggml's IQ3_XXS codebook (256 entries of 4 magnitudes, one byte each) and
+// IQ4_NL values: format data, identical to the reference's tables
+// (src/gguf_quant.cpp:53-90).
+__constant__ uint32_t c_iq3xxs_grid[256] = {
+    0x04040404u, 0x04040414u, 0x04040424u, 0x04040c0cu, 0x04040c1cu, 0x04040c3eu, 0x04041404u, 0x04041414u,
+    0x04041c0cu, 0x04042414u, 0x04043e1cu, 0x04043e2cu, 0x040c040cu, 0x040c041cu, 0x040c0c04u, 0x040c0c14u,
+    0x040c140cu, 0x040c142cu, 0x040c1c04u, 0x040c1c14u, 0x040c240cu, 0x040c2c24u, 0x040c3e04u, 0x04140404u,
+    0x04140414u, 0x04140424u, 0x04140c0cu, 0x04141404u, 0x04141414u, 0x04141c0cu, 0x04141c1cu, 0x04141c3eu,
+    0x04142c0cu, 0x04142c3eu, 0x04143e2cu, 0x041c040cu, 0x041c043eu, 0x041c0c04u, 0x041c0c14u, 0x041c142cu,
+    0x041c3e04u, 0x04240c1cu, 0x04241c3eu, 0x04242424u, 0x04242c3eu, 0x04243e1cu, 0x04243e2cu, 0x042c040cu,
+    0x042c043eu, 0x042c1c14u, 0x042c2c14u, 0x04341c2cu, 0x04343424u, 0x043e0c04u, 0x043e0c24u, 0x043e0c34u,
+    0x043e241cu, 0x043e340cu, 0x0c04040cu, 0x0c04041cu, 0x0c040c04u, 0x0c040c14u, 0x0c04140cu, 0x0c04141cu,
+    0x0c041c04u, 0x0c041c14u, 0x0c041c24u, 0x0c04243eu, 0x0c042c04u, 0x0c0c0404u, 0x0c0c0414u, 0x0c0c0c0cu,
+    0x0c0c1404u, 0x0c0c1414u, 0x0c14040cu, 0x0c14041cu, 0x0c140c04u, 0x0c140c14u, 0x0c14140cu, 0x0c141c04u,
+    0x0c143e14u, 0x0c1c0404u, 0x0c1c0414u, 0x0c1c1404u, 0x0c1c1c0cu, 0x0c1c2434u, 0x0c1c3434u, 0x0c24040cu,
+    0x0c24042cu, 0x0c242c04u, 0x0c2c1404u, 0x0c2c1424u, 0x0c2c2434u, 0x0c2c3e0cu, 0x0c34042cu, 0x0c3e1414u,
+    0x0c3e2404u, 0x14040404u, 0x14040414u, 0x14040c0cu, 0x14040c1cu, 0x14041404u, 0x14041414u, 0x14041434u,
+    0x14041c0cu, 0x14042414u, 0x140c040cu, 0x140c041cu, 0x140c042cu, 0x140c0c04u, 0x140c0c14u, 0x140c140cu,
+    0x140c1c04u, 0x140c341cu, 0x140c343eu, 0x140c3e04u, 0x14140404u, 0x14140414u, 0x14140c0cu, 0x14140c3eu,
+    0x14141404u, 0x14141414u, 0x14141c3eu, 0x14142404u, 0x14142c2cu, 0x141c040cu, 0x141c0c04u, 0x141c0c24u,
+    0x141c3e04u, 0x141c3e24u, 0x14241c2cu, 0x14242c1cu, 0x142c041cu, 0x142c143eu, 0x142c240cu, 0x142c3e24u,
+    0x143e040cu, 0x143e041cu, 0x143e0c34u, 0x143e242cu, 0x1c04040cu, 0x1c040c04u, 0x1c040c14u, 0x1c04140cu,
+    0x1c04141cu, 0x1c042c04u, 0x1c04342cu, 0x1c043e14u, 0x1c0c0404u, 0x1c0c0414u, 0x1c0c1404u, 0x1c0c1c0cu,
+    0x1c0c2424u, 0x1c0c2434u, 0x1c14040cu, 0x1c14041cu, 0x1c140c04u, 0x1c14142cu, 0x1c142c14u, 0x1c143e14u,
+    0x1c1c0c0cu, 0x1c1c1c1cu, 0x1c241c04u, 0x1c24243eu, 0x1c243e14u, 0x1c2c0404u, 0x1c2c0434u, 0x1c2c1414u,
+    0x1c2c2c2cu, 0x1c340c24u, 0x1c341c34u, 0x1c34341cu, 0x1c3e1c1cu, 0x1c3e3404u, 0x24040424u, 0x24040c3eu,
+    0x24041c2cu, 0x24041c3eu, 0x24042c1cu, 0x24042c3eu, 0x240c3e24u, 0x24141404u, 0x24141c3eu, 0x24142404u,
+    0x24143404u, 0x24143434u, 0x241c043eu, 0x241c242cu, 0x24240424u, 0x24242c0cu, 0x24243424u, 0x242c142cu,
+    0x242c241cu, 0x242c3e04u, 0x243e042cu, 0x243e0c04u, 0x243e0c14u, 0x243e1c04u, 0x2c040c14u, 0x2c04240cu,
+    0x2c043e04u, 0x2c0c0404u, 0x2c0c0434u, 0x2c0c1434u, 0x2c0c2c2cu, 0x2c140c24u, 0x2c141c14u, 0x2c143e14u,
+    0x2c1c0414u, 0x2c1c2c1cu, 0x2c240c04u, 0x2c24141cu, 0x2c24143eu, 0x2c243e14u, 0x2c2c0414u, 0x2c2c1c0cu,
+    0x2c342c04u, 0x2c3e1424u, 0x2c3e2414u, 0x34041424u, 0x34042424u, 0x34042434u, 0x34043424u, 0x340c140cu,
+    0x340c340cu, 0x34140c3eu, 0x34143424u, 0x341c1c04u, 0x341c1c34u, 0x34242424u, 0x342c042cu, 0x342c2c14u,
+    0x34341c1cu, 0x343e041cu, 0x343e140cu, 0x3e04041cu, 0x3e04042cu, 0x3e04043eu, 0x3e040c04u, 0x3e041c14u,
+    0x3e042c14u, 0x3e0c1434u, 0x3e0c2404u, 0x3e140c14u, 0x3e14242cu, 0x3e142c14u, 0x3e1c0404u, 0x3e1c0c2cu,
+    0x3e1c1c1cu, 0x3e1c3404u, 0x3e24140cu, 0x3e24240cu, 0x3e2c0404u, 0x3e2c0414u, 0x3e2c1424u, 0x3e341c04u,
+};
+__constant__ int8_t c_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                                   1,    13,   25,  38,  53,  69,  89,  113};
+
+__device__ __forceinline__ float gg_f16(const uint8_t* p) {
+    const uint16_t h = (uint16_t)(p[0] | (p[1] << 8));
+    return (float)__builtin_bit_cast(_Float16, h);
+}
+
+int gguf_block_elems(uint32_t t) {
+    switch (t) {
+        case 0: case 1: return 1;
+        case 8: return 32;
+        case 11: case 12: case 13: case 14: case 18: case 23: return 256;
+        default: return 0;
+    }
+}
+
+int gguf_block_bytes(uint32_t t) {
+    switch (t) {
+        case 0: return 4;
+        case 1: return 2;
+        case 8: return 34;
+        case 11: return 110;
+        case 12: return 144;
+        case 13: return 176;
+        case 14: return 210;
+        case 18: return 98;
+        case 23: return 136;
+        default: return 0;
+    }
+}
+
+// Elements k .. k + 7 (k % 8 == 0) of a row of GGUF type t.
+__device__ __forceinline__ void gg_dec8_any(uint32_t t, const uint8_t* __restrict__ row, int k,
+                                            float (&y)[8]) {
+    switch (t) {
+        case 0: {
+            const float4* p = reinterpret_cast<const float4*>(row + 4 * (size_t)k);
+            const float4 a = p[0], b = p[1];
+            y[0] = a.x; y[1] = a.y; y[2] = a.z; y[3] = a.w;
+            y[4] = b.x; y[5] = b.y; y[6] = b.z; y[7] = b.w;
+            return;
+        }
+        case 1: {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) y[j] = gg_f16(row + 2 * ((size_t)k + j));
+            return;
+        }
+        case 8: {   // d, 32 x int8
+            const uint8_t* b = row + (size_t)(k / 32) * 34;
+            const int p = k % 32;
+            const float d = gg_f16(b);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) y[j] = d * (float)(int8_t)b[2 + p + j];
+            return;
+        }
+        case 11: {  // hmask[32] q[64] scales[12] d
+            const uint8_t* b = row + (size_t)(k / 256) * 110;
+            const int p = k % 256, half = p / 128, r = p % 128, j = r / 32, sub = (r % 32) / 16;
+            const int l0 = r % 16, i = 8 * half + 2 * j + sub;
+            const int lo = (b[96 + i % 8] >> (4 * (i / 8))) & 15;
+            const int hi = (b[104 + i % 4] >> (2 * (i / 4))) & 3;
+            const int sc = (int)(int8_t)(uint8_t)(lo | (hi << 4));
+            const float dl = gg_f16(b + 108) * (float)(sc - 32);
+            const int hm = 1 << (4 * half + j);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int idx = 16 * sub + l0 + e;
+                const int v = (b[32 + 32 * half + idx] >> (2 * j)) & 3;
+                y[e] = dl * (float)(v - ((b[idx] & hm) ? 0 : 4));
+            }
+            return;
+        }
+        case 12:
+        case 13: {  // d dmin scales[12] (qh[32]) q[128]
+            const int bb = t == 12 ? 144 : 176;
+            const uint8_t* b = row + (size_t)(k / 256) * bb;
+            const int p = k % 256, c64 = p / 64, c = p % 64, l0 = c % 32, hi = c / 32;
+            const int js = 2 * c64 + hi;
+            const uint8_t* s = b + 4;
+            int sc, mn;
+            if (js < 4) {
+                sc = s[js] & 63;
+                mn = s[js + 4] & 63;
+            } else {
+                sc = (s[js + 4] & 15) | ((s[js - 4] >> 6) << 4);
+                mn = (s[js + 4] >> 4) | ((s[js] >> 6) << 4);
+            }
+            const float d1 = gg_f16(b) * (float)sc, m1 = gg_f16(b + 2) * (float)mn;
+            const uint8_t* q = b + (t == 12 ? 16 : 48);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                int v = (q[32 * c64 + l0 + e] >> (4 * hi)) & 15;
+                if (t == 13) v += (b[16 + l0 + e] & (1 << js)) ? 16 : 0;
+                y[e] = d1 * (float)v - m1;
+            }
+            return;
+        }
+        case 14: {  // ql[128] qh[64] scales[16] d
+            const uint8_t* b = row + (size_t)(k / 256) * 210;
+            const int p = k % 256, nn = p / 128, r = p % 128, quarter = r / 32, l0 = r % 32;
+            const uint8_t* ql = b + 64 * nn + 32 * (quarter & 1);
+            const uint8_t* qh = b + 128 + 32 * nn;
+            const float dsc = gg_f16(b + 208) * (float)(int8_t)b[192 + 8 * nn + l0 / 16 + 2 * quarter];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int lo = (ql[l0 + e] >> (4 * (quarter >> 1))) & 15;
+                const int q6 = (int)(int8_t)(uint8_t)(lo | (((qh[l0 + e] >> (2 * quarter)) & 3) << 4)) - 32;
+                y[e] = dsc * (float)q6;
+            }
+            return;
+        }
+        case 18: {  // d qs[64] signs+scales[32]
+            const uint8_t* b = row + (size_t)(k / 256) * 98;
+            const int p = k % 256, ib = p / 32, l = (p % 32) / 8;
+            const uint8_t* w = b + 66 + 4 * ib;
+            const uint32_t aux = (uint32_t)w[0] | ((uint32_t)w[1] << 8) | ((uint32_t)w[2] << 16) |
+                                 ((uint32_t)w[3] << 24);
+            const float db = gg_f16(b) * (0.5f + (float)(aux >> 28)) * 0.5f;
+            const uint32_t i7 = (aux >> (7 * l)) & 127u;
+            const uint32_t signs = i7 | ((uint32_t)(__builtin_popcount(i7) & 1) << 7);
+            const uint32_t g0 = c_iq3xxs_grid[b[2 + 8 * ib + 2 * l]];
+            const uint32_t g1 = c_iq3xxs_grid[b[2 + 8 * ib + 2 * l + 1]];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float mag = (float)(((e < 4 ? g0 : g1) >> (8 * (e & 3))) & 255u);
+                y[e] = db * mag * ((signs & (1u << e)) ? -1.0f : 1.0f);
+            }
+            return;
+        }
+        case 23: {  // d scales_h scales_l[4] qs[128]
+            const uint8_t* b = row + (size_t)(k / 256) * 136;
+            const int p = k % 256, ib = p / 32, c = p % 32;
+            const int sh = b[2] | (b[3] << 8);
+            const int lo = (b[4 + ib / 2] >> (4 * (ib & 1))) & 15;
+            const int hi = (sh >> (2 * ib)) & 3;
+            const float dl = gg_f16(b) * (float)((int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int cc = c + e;
+                const int code = (b[8 + 16 * ib + (cc % 16)] >> (4 * (cc / 16))) & 15;
+                y[e] = dl * (float)c_iq4nl[code];
+            }
+            return;
+        }
+        default:
+#pragma unroll
+            for (int e = 0; e < 8; ++e) y[e] = 0.0f;
+    }
+}
+
+// The type as a compile-time constant (one decode body per kernel
+// instantiation); kGgAny decodes by a runtime switch on t.
+constexpr uint32_t kGgAny = 0xffffffffu;
+template <uint32_t T>
+__device__ __forceinline__ void gg_dec8(uint32_t t, const uint8_t* __restrict__ row, int k,
+                                        float (&y)[8]) {
+    gg_dec8_any(T == kGgAny ? t : T, row, k, y);
+}
+
+constexpr int kGgRows = 16;   // weight rows per workgroup (4 per wave)
+constexpr int kGgTile = 8;    // input rows per tile
+constexpr int kGgKC = 512;    // K per staged chunk
+
+__device__ __forceinline__ float gg_wave_sum(float v) {
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m);
+    return v;
+}
+
+__device__ __forceinline__ float gg_silu(float v) { return v / (1.0f + expf(-v)); }
+
+// The input rows of a tile (up to kGgTile, indices into src) and its expert.
+struct GgTile {
+    int e, nr;
+    int row[kGgTile];    // output row index (routed row r, or the token for gemm_q)
+    int src[kGgTile];    // input row index into src
+};
+
+// Stages rows srcs[0..nr) x [k0, k0 + kc) of a [*, K] fp32 matrix into xs
+// (srcs: the tile's input rows, in LDS so that they index dynamically).
+__device__ __forceinline__ void gg_stage(float (*xs)[kGgKC], const float* __restrict__ src, int K,
+                                         const int* srcs, int nr, int k0, int kc) {
+    for (int i = threadIdx.x; i < kGgTile * (kGgKC / 4); i += blockDim.x) {
+        const int t = i / (kGgKC / 4), c4 = i % (kGgKC / 4);
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (t < nr && 4 * c4 < kc)
+            v = *reinterpret_cast<const float4*>(src + (size_t)srcs[t] * K + k0 + 4 * c4);
+        *reinterpret_cast<float4*>(&xs[t][4 * c4]) = v;
+    }
+}
+
+// Dot products of NM weight matrices' rows o0 .. o0 + 3 with the tile's input
+// rows over K: acc[m][r][t].
+template <uint32_t T, int NM>
+__device__ __forceinline__ void gg_dots(float (*xs)[kGgKC], int* srcs, const float* __restrict__ src,
+                                        int K, const GgTile& tl, const uint32_t (&type)[NM],
+                                        const uint8_t* const (&wrow)[NM][4],
+                                        float (&acc)[NM][4][kGgTile]) {
+    const int lane = threadIdx.x & 63;
+    __syncthreads();   // srcs and xs of a previous tile are consumed
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int t = 0; t < kGgTile; ++t) srcs[t] = tl.src[t];
+    }
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < kGgTile; ++t) acc[m][r][t] = 0.0f;
+    for (int k0 = 0; k0 < K; k0 += kGgKC) {
+        const int kc = min(kGgKC, K - k0);
+        __syncthreads();
+        gg_stage(xs, src, K, srcs, tl.nr, k0, kc);
+        __syncthreads();
+        const int kk = lane * 8;
+        if (kk >= kc) continue;
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                float w[8];
+                gg_dec8<T>(type[m], wrow[m][r], k0 + kk, w);
+#pragma unroll
+                for (int j = 0; j < 8; ++j)
+#pragma unroll
+                    for (int t = 0; t < kGgTile; ++t)
+                        acc[m][r][t] = __builtin_fmaf(w[j], xs[t][kk + j], acc[m][r][t]);
+            }
+    }
+}
+
+// gemm_q: tiles are 8 consecutive tokens.
+template <uint32_t T>
+__global__ __launch_bounds__(256) void gg_gemv_kernel(uint32_t qtype, const float* __restrict__ x,
+                                                      const uint8_t* __restrict__ qw,
+                                                      const float* __restrict__ bias,
+                                                      float* __restrict__ y, int n, int in, int out,
+                                                      long row_bytes) {
+    __shared__ __align__(16) float xs[kGgTile][kGgKC];
+    __shared__ int srcs[kGgTile];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int o0 = blockIdx.x * kGgRows + wave * 4;
+    const uint32_t type[1] = {qtype};
+    const uint8_t* wrow[1][4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) wrow[0][r] = qw + (size_t)min(o0 + r, out - 1) * row_bytes;
+    for (int t0 = 0; t0 < n; t0 += kGgTile) {
+        GgTile tl;
+        tl.e = 0;
+        tl.nr = min(kGgTile, n - t0);
+#pragma unroll
+        for (int t = 0; t < kGgTile; ++t) tl.row[t] = tl.src[t] = t0 + t;
+        float acc[1][4][kGgTile];
+        gg_dots<T, 1>(xs, srcs, x, in, tl, type, wrow, acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < kGgTile; ++t) {
+                const float v = gg_wave_sum(acc[0][r][t]);
+                const int o = o0 + r;
+                if (lane == 0 && t < tl.nr && o < out)
+                    y[(size_t)(t0 + t) * out + o] = bias ? v + bias[o] : v;
+            }
+    }
+}
+
+// Tile g of the routed rows. grouped: d = [offsets E+1 | tile prefix E+1 |
+// rows n*topk] from gg_group_kernel; otherwise routed row g alone.
+__device__ __forceinline__ bool gg_tile(int g, const int* __restrict__ ids,
+                                        const int* __restrict__ d, int nk, int E, int topk,
+                                        bool down, GgTile& tl) {
+    if (!d) {
+        if (g >= nk) return false;
+        tl.e = ids[g];
+        tl.nr = 1;
+        tl.row[0] = g;
+        tl.src[0] = down ? g : g / topk;
+        return true;
+    }
+    const int* off = d;
+    const int* tp = d + E + 1;
+    const int* rows = d + 2 * (E + 1);
+    if (g >= tp[E]) return false;
+    int lo = 0, hi = E;   // the expert e with tp[e] <= g < tp[e + 1]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (tp[mid] <= g) lo = mid;
+        else hi = mid;
+    }
+    tl.e = lo;
+    const int r0 = off[lo] + (g - tp[lo]) * kGgTile;
+    tl.nr = min(kGgTile, off[lo + 1] - r0);
+#pragma unroll
+    for (int t = 0; t < kGgTile; ++t) {
+        const int r = rows[r0 + (t < tl.nr ? t : 0)];
+        tl.row[t] = r;
+        tl.src[t] = down ? r : r / topk;
+    }
+    return true;
+}
+
+struct GgMoeArgs {
+    uint32_t gate_type, up_type, down_type;
+    const float* x;
+    const int* ids;
+    const float* w;
+    const uint8_t *gate_q, *up_q, *down_q;
+    long gate_rb, up_rb, down_rb;
+    int n, topk, H, I, E;
+    float* h_act;
+    float* dpart;
+    const int* d;   // grouping (nullable)
+};
+
+// DOWN = false: phase 1 (gate/up, output rows = I features); true: phase 2.
+// T: the weight type (gate and up share it in phase 1), or kGgAny.
+template <bool DOWN, uint32_t T>
+__global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
+    __shared__ __align__(16) float xs[kGgTile][kGgKC];
+    __shared__ int srcs[kGgTile];
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nk = a.n * a.topk;
+    GgTile tl;
+    if (!gg_tile((int)blockIdx.x, a.ids, a.d, nk, a.E, a.topk, DOWN, tl)) return;
+    const int out = DOWN ? a.H : a.I;
+    const int o0 = blockIdx.y * kGgRows + wave * 4;
+    const size_t e = (size_t)tl.e;
+    if constexpr (!DOWN) {
+        const uint32_t type[2] = {a.gate_type, a.up_type};
+        const uint8_t* wrow[2][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const size_t o = (size_t)min(o0 + r, out - 1);
+            wrow[0][r] = a.gate_q + (e * a.I + o) * a.gate_rb;
+            wrow[1][r] = a.up_q + (e * a.I + o) * a.up_rb;
+        }
+        float acc[2][4][kGgTile];
+        gg_dots<T, 2>(xs, srcs, a.x, a.H, tl, type, wrow, acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < kGgTile; ++t) {
+                const float g = gg_wave_sum(acc[0][r][t]);
+                const float u = gg_wave_sum(acc[1][r][t]);
+                const int o = o0 + r;
+                if (lane == 0 && t < tl.nr && o < out)
+                    a.h_act[(size_t)tl.row[t] * a.I + o] = gg_silu(g) * u;
+            }
+    } else {
+        const uint32_t type[1] = {a.down_type};
+        const uint8_t* wrow[1][4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const size_t o = (size_t)min(o0 + r, out - 1);
+            wrow[0][r] = a.down_q + (e * a.H + o) * a.down_rb;
+        }
+        float acc[1][4][kGgTile];
+        gg_dots<T, 1>(xs, srcs, a.h_act, a.I, tl, type, wrow, acc);
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < kGgTile; ++t) {
+                const float v = gg_wave_sum(acc[0][r][t]);
+                const int o = o0 + r;
+                if (lane == 0 && t < tl.nr && o < out) a.dpart[(size_t)tl.row[t] * a.H + o] = v;
+            }
+    }
+}
+
+// out[t] = ((0 + w0 y0) + w1 y1) + ... over the slots (cuda/qgemm.cu:943-955).
+__global__ __launch_bounds__(256) void gg_reduce_kernel(const float* __restrict__ dpart,
+                                                        const float* __restrict__ w, int n,
+                                                        int topk, int H, float* __restrict__ out) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= (long)n * H) return;
+    const long t = i / H, o = i % H;
+    float acc = 0.0f;
+    for (int s = 0; s < topk; ++s) acc = acc + w[t * topk + s] * dpart[(t * topk + s) * H + o];
+    out[i] = acc;
+}
+
+// Groups the routed rows by expert (one workgroup): d = [offsets E+1 | tile
+// prefix E+1 | rows n*topk]; rows of an expert are in any order (each row's
+// result depends only on its own inputs).
+__global__ __launch_bounds__(1024) void gg_group_kernel(const int* __restrict__ ids, int nk, int E,
+                                                        int* __restrict__ d) {
+    extern __shared__ int gl[];   // cnt[E] | cursor[E]
+    int* cnt = gl;
+    int* cur = gl + E;
+    int* off = d;
+    int* tp = d + E + 1;
+    int* rows = d + 2 * (E + 1);
+    for (int e = threadIdx.x; e < E; e += blockDim.x) cnt[e] = 0;
+    __syncthreads();
+    for (int i = threadIdx.x; i < nk; i += blockDim.x) {
+        const int e = ids[i];
+        if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        int o = 0, t = 0;
+        for (int e = 0; e < E; ++e) {
+            off[e] = o;
+            tp[e] = t;
+            cur[e] = o;
+            o += cnt[e];
+            t += (cnt[e] + kGgTile - 1) / kGgTile;
+        }
+        off[E] = o;
+        tp[E] = t;
+    }
+    __syncthreads();
+    for (int i = threadIdx.x; i < nk; i += blockDim.x) {
+        const int e = ids[i];
+        if (e >= 0 && e < E) rows[atomicAdd(&cur[e], 1)] = i;
+    }
+}
+
+// Calls f(std::integral_constant<uint32_t, t>) for a supported type t,
+// f(kGgAny constant) otherwise.
+template <class F>
+static void gg_by_type(uint32_t t, F&& f) {
+    switch (t) {
+        case 0: f(std::integral_constant<uint32_t, 0>{}); break;
+        case 1: f(std::integral_constant<uint32_t, 1>{}); break;
+        case 8: f(std::integral_constant<uint32_t, 8>{}); break;
+        case 11: f(std::integral_constant<uint32_t, 11>{}); break;
+        case 12: f(std::integral_constant<uint32_t, 12>{}); break;
+        case 13: f(std::integral_constant<uint32_t, 13>{}); break;
+        case 14: f(std::integral_constant<uint32_t, 14>{}); break;
+        case 18: f(std::integral_constant<uint32_t, 18>{}); break;
+        case 23: f(std::integral_constant<uint32_t, 23>{}); break;
+        default: f(std::integral_constant<uint32_t, kGgAny>{}); break;
+    }
+}
+
+int launch_gg_gemm(uint32_t qtype, const float* x, const uint8_t* qw, const float* bias, float* y,
+                   int n, int in, int out, long row_bytes, hipStream_t s) {
+    gg_by_type(qtype, [&](auto tc) {
+        hipLaunchKernelGGL((gg_gemv_kernel<decltype(tc)::value>),
+                           dim3((unsigned)((out + kGgRows - 1) / kGgRows)), dim3(256), 0, s, qtype,
+                           x, qw, bias, y, n, in, out, row_bytes);
+    });
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int launch_gg_moe(uint32_t gt, uint32_t ut, uint32_t dt, const float* x, const int* ids,
+                  const float* w, const uint8_t* gq, const uint8_t* uq, const uint8_t* dq, int n,
+                  int topk, int H, int I, int E, long grb, long urb, long drb, float* h_act,
+                  float* dpart, float* out, int* dispatch, hipStream_t s) {
+    const int nk = n * topk;
+    GgMoeArgs a{gt, ut, dt, x, ids, w, gq, uq, dq, grb, urb, drb, n, topk, H, I, E, h_act, dpart,
+                dispatch};
+    unsigned tiles = (unsigned)nk;
+    if (dispatch) {
+        hipLaunchKernelGGL(gg_group_kernel, dim3(1), dim3(1024), (size_t)2 * E * 4, s, ids, nk, E,
+                           dispatch);
+        if (hipGetLastError() != hipSuccess) return -4;
+        tiles = (unsigned)((nk + kGgTile - 1) / kGgTile + E);
+    }
+    const dim3 g1(tiles, (unsigned)((I + kGgRows - 1) / kGgRows));
+    if (gt == ut)
+        gg_by_type(gt, [&](auto tc) {
+            hipLaunchKernelGGL((gg_moe_kernel<false, decltype(tc)::value>), g1, dim3(256), 0, s, a);
+        });
+    else
+        hipLaunchKernelGGL((gg_moe_kernel<false, kGgAny>), g1, dim3(256), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return -4;
+    const dim3 g2(tiles, (unsigned)((H + kGgRows - 1) / kGgRows));
+    gg_by_type(dt, [&](auto tc) {
+        hipLaunchKernelGGL((gg_moe_kernel<true, decltype(tc)::value>), g2, dim3(256), 0, s, a);
+    });
+    if (hipGetLastError() != hipSuccess) return -4;
+    const long total = (long)n * H;
+    hipLaunchKernelGGL(gg_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       dpart, w, n, topk, H, out);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+}  // namespace glmmoe

@@ -110,4 +110,15 @@ int launch_ref_silu_mul(const float* g, const float* u, float* o, long n, hipStr
 int launch_ref_add_inplace(float* y, const float* x, long n, hipStream_t s);
 int launch_f32_to_bf16(const float* x, uint16_t* y, long n, hipStream_t s);
 
+// GGUF block formats (gguf.hip): block geometry (0 if unsupported) and the
+// gemm_q / moe_expert_ffn_q launches.
+int gguf_block_elems(uint32_t type);
+int gguf_block_bytes(uint32_t type);
+int launch_gg_gemm(uint32_t qtype, const float* x, const uint8_t* qw, const float* bias, float* y,
+                   int n, int in, int out, long row_bytes, hipStream_t s);
+int launch_gg_moe(uint32_t gt, uint32_t ut, uint32_t dt, const float* x, const int* ids,
+                  const float* w, const uint8_t* gq, const uint8_t* uq, const uint8_t* dq, int n,
+                  int topk, int H, int I, int E, long grb, long urb, long drb, float* h_act,
+                  float* dpart, float* out, int* dispatch, hipStream_t s);
+
 }  // namespace glmmoe

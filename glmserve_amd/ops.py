@@ -289,3 +289,24 @@ class RefW4Experts:
             _p(x), _p(topk_ids), _p(topk_weights), _p(gq), _p(gs), _p(uq), _p(us), _p(dq), _p(ds),
             n, topk_ids.shape[1], self.hidden, self.moe_inter, self.E, self.group_size, _p(out),
             _s(stream)), "ref_moe_expert_ffn_w4a16")
+
+
+def ref_gemm_q(qtype, x, qweight, bias, y, row_bytes, stream=None):
+    """gemm_q (cuda/kernels.cuh:63-66): GGUF rows of W [out, in] at qweight + o * row_bytes."""
+    n, in_ = x.shape
+    out = y.shape[1]
+    _need(x, torch.float32, n * in_, "x")
+    _need(y, torch.float32, n * out, "y")
+    check(lib().glmmoe_ref_gemm_q(qtype, _p(x), _p(qweight), _p(bias), _p(y), n, in_, out,
+                                  row_bytes, _s(stream)), "ref_gemm_q")
+
+
+def ref_moe_expert_ffn_q(types, x, topk_ids, topk_w, gate_q, up_q, down_q, moe_inter, E,
+                         row_bytes, h_act, dpart, out, dispatch=None, stream=None):
+    """moe_expert_ffn_q (cuda/kernels.cuh:117-123). types / row_bytes: (gate, up, down)."""
+    n, H = x.shape
+    k = topk_ids.shape[1]
+    check(lib().glmmoe_ref_moe_expert_ffn_q(
+        types[0], types[1], types[2], _p(x), _p(topk_ids), _p(topk_w), _p(gate_q), _p(up_q),
+        _p(down_q), n, k, H, moe_inter, E, row_bytes[0], row_bytes[1], row_bytes[2], _p(h_act),
+        _p(dpart), _p(out), _p(dispatch), None, _s(stream)), "ref_moe_expert_ffn_q")

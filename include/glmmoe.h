@@ -336,6 +336,35 @@ int glmmoe_ref_gemm_fp8(const float* x, const uint8_t* fp8W, const float* w_scal
 int glmmoe_ref_silu_mul(const float* g, const float* u, float* out, int64_t n, void* stream);
 int glmmoe_ref_add_inplace(float* y, const float* x, int64_t n, void* stream);
 
+/* GGUF block-quantized weights (the ggml block formats of src/gguf_quant.cpp:
+ * qtype 0 F32, 1 F16, 8 Q8_0, 11 Q3_K, 12 Q4_K, 13 Q5_K, 14 Q6_K, 18 IQ3_XXS,
+ * 23 IQ4_XS), dequantized inside the kernels bit-identically to the
+ * reference's CPU dequantizer; products and sums in fp32.
+ * glmmoe_ref_gemm_q replaces gemm_q (cuda/kernels.cuh:63-66): y[n,out] =
+ * x[n,in] . W^T (+ bias), row o of W at qW + o * row_bytes.
+ * glmmoe_ref_moe_expert_ffn_q replaces moe_expert_ffn_q (cuda/kernels.cuh:
+ * 117-123, cuda/qgemm.cu:1505-1639) argument for argument: gate/up rows
+ * [E, moe_inter, hidden], down [E, hidden, moe_inter], row o of expert e at
+ * base + (e * out + o) * row_bytes; h_act [n, topk, moe_inter] and dpart
+ * [n * topk, hidden] are caller scratch; out [n, hidden] is overwritten with
+ * sum_s topk_w[t,s] * y_{t,s} in slot order. With `dispatch` (int scratch of
+ * 3E + 1 + n*topk, nullable) the routed rows are grouped by expert first so
+ * each weight row is read once per 8 rows of its expert; without it every
+ * routed row reads its expert's rows (the reference's token-major path).
+ * gu_part (the reference's split-K partials) is accepted and not used.
+ * Limits: every row length a multiple of its type's block and of 8,
+ * row_bytes at least the blocks of a row, E <= 4096. */
+int glmmoe_ref_gemm_q(uint32_t qtype, const float* x, const uint8_t* qW, const float* bias,
+                      float* y, int64_t n, int64_t in, int64_t out, int64_t row_bytes,
+                      void* stream);
+int glmmoe_ref_moe_expert_ffn_q(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
+                                const float* x, const int* topk_ids, const float* topk_w,
+                                const uint8_t* gate_q, const uint8_t* up_q, const uint8_t* down_q,
+                                int n, int topk, int hidden, int moe_inter, int E,
+                                int64_t gate_row_bytes, int64_t up_row_bytes,
+                                int64_t down_row_bytes, float* h_act, float* dpart, float* out,
+                                int* dispatch, float* gu_part, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

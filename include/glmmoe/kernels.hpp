@@ -134,6 +134,26 @@ inline int silu_mul(const float* g, const float* u, float* out, int64_t n, void*
     return glmmoe_ref_silu_mul(g, u, out, n, s);
 }
 
+// cuda/kernels.cuh:63-66
+inline int gemm_q(uint32_t qtype, const float* x, const uint8_t* qW, const float* bias, float* y,
+                  int64_t n, int64_t in, int64_t out, int64_t row_bytes, void* s = nullptr) {
+    return glmmoe_ref_gemm_q(qtype, x, qW, bias, y, n, in, out, row_bytes, s);
+}
+
+// cuda/kernels.cuh:117-123
+inline int moe_expert_ffn_q(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
+                            const float* x, const int* topk_ids, const float* topk_w,
+                            const uint8_t* gate_q, const uint8_t* up_q, const uint8_t* down_q,
+                            int n, int topk, int hidden, int moe_inter, int E,
+                            int64_t gate_row_bytes, int64_t up_row_bytes, int64_t down_row_bytes,
+                            float* h_act, float* dpart, float* out, int* dispatch = nullptr,
+                            float* gu_part = nullptr, void* s = nullptr) {
+    return glmmoe_ref_moe_expert_ffn_q(gate_type, up_type, down_type, x, topk_ids, topk_w, gate_q,
+                                       up_q, down_q, n, topk, hidden, moe_inter, E, gate_row_bytes,
+                                       up_row_bytes, down_row_bytes, h_act, dpart, out, dispatch,
+                                       gu_part, s);
+}
+
 }  // namespace compat
 }  // namespace glmmoe
 

@@ -456,3 +456,196 @@ int orc_moe_forward_ex(const float* x, int64_t n, int64_t H, int E, int topk, in
     free(logits);
     return status;
 }
+
+/* ---------------------------------------------------------------------------
+ * GGUF block formats (src/gguf_quant.cpp:98-262, the reference's CPU
+ * dequantizers of the ggml block layouts; types 0 F32, 1 F16, 8 Q8_0, 11 Q3_K,
+ * 12 Q4_K, 13 Q5_K, 14 Q6_K, 18 IQ3_XXS, 23 IQ4_XS). Restated per element:
+ * orc_gguf_value(type, block, p) decodes element p of one block with the same
+ * float operations, in the same order, as the reference's block loops, so
+ * rows dequantize bit-identically (pinned against oracle/_ref).
+ * The two codebooks are format data and must hold exactly ggml's values: the
+ * IQ3_XXS grid (256 entries of 4 magnitudes) and the IQ4_NL values; the
+ * IQ2 sign table is the 7-bit index with an even-parity eighth bit.
+ * ------------------------------------------------------------------------- */
+static const uint32_t orc_iq3xxs_grid[256] = {
+    0x04040404u, 0x04040414u, 0x04040424u, 0x04040c0cu, 0x04040c1cu, 0x04040c3eu, 0x04041404u, 0x04041414u,
+    0x04041c0cu, 0x04042414u, 0x04043e1cu, 0x04043e2cu, 0x040c040cu, 0x040c041cu, 0x040c0c04u, 0x040c0c14u,
+    0x040c140cu, 0x040c142cu, 0x040c1c04u, 0x040c1c14u, 0x040c240cu, 0x040c2c24u, 0x040c3e04u, 0x04140404u,
+    0x04140414u, 0x04140424u, 0x04140c0cu, 0x04141404u, 0x04141414u, 0x04141c0cu, 0x04141c1cu, 0x04141c3eu,
+    0x04142c0cu, 0x04142c3eu, 0x04143e2cu, 0x041c040cu, 0x041c043eu, 0x041c0c04u, 0x041c0c14u, 0x041c142cu,
+    0x041c3e04u, 0x04240c1cu, 0x04241c3eu, 0x04242424u, 0x04242c3eu, 0x04243e1cu, 0x04243e2cu, 0x042c040cu,
+    0x042c043eu, 0x042c1c14u, 0x042c2c14u, 0x04341c2cu, 0x04343424u, 0x043e0c04u, 0x043e0c24u, 0x043e0c34u,
+    0x043e241cu, 0x043e340cu, 0x0c04040cu, 0x0c04041cu, 0x0c040c04u, 0x0c040c14u, 0x0c04140cu, 0x0c04141cu,
+    0x0c041c04u, 0x0c041c14u, 0x0c041c24u, 0x0c04243eu, 0x0c042c04u, 0x0c0c0404u, 0x0c0c0414u, 0x0c0c0c0cu,
+    0x0c0c1404u, 0x0c0c1414u, 0x0c14040cu, 0x0c14041cu, 0x0c140c04u, 0x0c140c14u, 0x0c14140cu, 0x0c141c04u,
+    0x0c143e14u, 0x0c1c0404u, 0x0c1c0414u, 0x0c1c1404u, 0x0c1c1c0cu, 0x0c1c2434u, 0x0c1c3434u, 0x0c24040cu,
+    0x0c24042cu, 0x0c242c04u, 0x0c2c1404u, 0x0c2c1424u, 0x0c2c2434u, 0x0c2c3e0cu, 0x0c34042cu, 0x0c3e1414u,
+    0x0c3e2404u, 0x14040404u, 0x14040414u, 0x14040c0cu, 0x14040c1cu, 0x14041404u, 0x14041414u, 0x14041434u,
+    0x14041c0cu, 0x14042414u, 0x140c040cu, 0x140c041cu, 0x140c042cu, 0x140c0c04u, 0x140c0c14u, 0x140c140cu,
+    0x140c1c04u, 0x140c341cu, 0x140c343eu, 0x140c3e04u, 0x14140404u, 0x14140414u, 0x14140c0cu, 0x14140c3eu,
+    0x14141404u, 0x14141414u, 0x14141c3eu, 0x14142404u, 0x14142c2cu, 0x141c040cu, 0x141c0c04u, 0x141c0c24u,
+    0x141c3e04u, 0x141c3e24u, 0x14241c2cu, 0x14242c1cu, 0x142c041cu, 0x142c143eu, 0x142c240cu, 0x142c3e24u,
+    0x143e040cu, 0x143e041cu, 0x143e0c34u, 0x143e242cu, 0x1c04040cu, 0x1c040c04u, 0x1c040c14u, 0x1c04140cu,
+    0x1c04141cu, 0x1c042c04u, 0x1c04342cu, 0x1c043e14u, 0x1c0c0404u, 0x1c0c0414u, 0x1c0c1404u, 0x1c0c1c0cu,
+    0x1c0c2424u, 0x1c0c2434u, 0x1c14040cu, 0x1c14041cu, 0x1c140c04u, 0x1c14142cu, 0x1c142c14u, 0x1c143e14u,
+    0x1c1c0c0cu, 0x1c1c1c1cu, 0x1c241c04u, 0x1c24243eu, 0x1c243e14u, 0x1c2c0404u, 0x1c2c0434u, 0x1c2c1414u,
+    0x1c2c2c2cu, 0x1c340c24u, 0x1c341c34u, 0x1c34341cu, 0x1c3e1c1cu, 0x1c3e3404u, 0x24040424u, 0x24040c3eu,
+    0x24041c2cu, 0x24041c3eu, 0x24042c1cu, 0x24042c3eu, 0x240c3e24u, 0x24141404u, 0x24141c3eu, 0x24142404u,
+    0x24143404u, 0x24143434u, 0x241c043eu, 0x241c242cu, 0x24240424u, 0x24242c0cu, 0x24243424u, 0x242c142cu,
+    0x242c241cu, 0x242c3e04u, 0x243e042cu, 0x243e0c04u, 0x243e0c14u, 0x243e1c04u, 0x2c040c14u, 0x2c04240cu,
+    0x2c043e04u, 0x2c0c0404u, 0x2c0c0434u, 0x2c0c1434u, 0x2c0c2c2cu, 0x2c140c24u, 0x2c141c14u, 0x2c143e14u,
+    0x2c1c0414u, 0x2c1c2c1cu, 0x2c240c04u, 0x2c24141cu, 0x2c24143eu, 0x2c243e14u, 0x2c2c0414u, 0x2c2c1c0cu,
+    0x2c342c04u, 0x2c3e1424u, 0x2c3e2414u, 0x34041424u, 0x34042424u, 0x34042434u, 0x34043424u, 0x340c140cu,
+    0x340c340cu, 0x34140c3eu, 0x34143424u, 0x341c1c04u, 0x341c1c34u, 0x34242424u, 0x342c042cu, 0x342c2c14u,
+    0x34341c1cu, 0x343e041cu, 0x343e140cu, 0x3e04041cu, 0x3e04042cu, 0x3e04043eu, 0x3e040c04u, 0x3e041c14u,
+    0x3e042c14u, 0x3e0c1434u, 0x3e0c2404u, 0x3e140c14u, 0x3e14242cu, 0x3e142c14u, 0x3e1c0404u, 0x3e1c0c2cu,
+    0x3e1c1c1cu, 0x3e1c3404u, 0x3e24140cu, 0x3e24240cu, 0x3e2c0404u, 0x3e2c0414u, 0x3e2c1424u, 0x3e341c04u,
+};
+static const int8_t orc_iq4nl_values[16] = {
+    -127, -104, -83, -65, -49, -35, -22, -10, 1, 13, 25, 38, 53, 69, 89, 113,
+};
+
+static uint8_t orc_iq2_signs(uint32_t i7) {
+    return (uint8_t)(i7 | ((uint32_t)(__builtin_popcount(i7) & 1) << 7));
+}
+
+/* IEEE half -> float (exact). */
+static float orc_f16(const uint8_t* p) {
+    const uint32_t h = (uint32_t)p[0] | ((uint32_t)p[1] << 8);
+    const uint32_t s = (h & 0x8000u) << 16, e = (h >> 10) & 31u, m = h & 1023u;
+    uint32_t b;
+    if (e == 31u) b = s | 0x7f800000u | (m << 13);
+    else if (e != 0u) b = s | ((e + 112u) << 23) | (m << 13);
+    else if (m == 0u) b = s;
+    else {
+        int ee = 113;
+        uint32_t mm = m;
+        while (!(mm & 1024u)) { mm <<= 1; --ee; }
+        b = s | ((uint32_t)ee << 23) | ((mm & 1023u) << 13);
+    }
+    float f;
+    memcpy(&f, &b, 4);
+    return f;
+}
+
+int64_t orc_gguf_block_elems(uint32_t type) {
+    switch (type) {
+        case 0: case 1: return 1;
+        case 8: return 32;
+        case 11: case 12: case 13: case 14: case 18: case 23: return 256;
+        default: return 0;
+    }
+}
+
+int64_t orc_gguf_block_bytes(uint32_t type) {
+    switch (type) {
+        case 0: return 4;
+        case 1: return 2;
+        case 8: return 34;
+        case 11: return 110;
+        case 12: return 144;
+        case 13: return 176;
+        case 14: return 210;
+        case 18: return 98;
+        case 23: return 136;
+        default: return 0;
+    }
+}
+
+/* 6-bit scale and min j (0..7) of a Q4_K / Q5_K block (12 packed bytes):
+ * src/gguf_quant.cpp:29-37. */
+static void orc_k4_scale_min(const uint8_t* q, int j, int* sc, int* mn) {
+    if (j < 4) {
+        *sc = q[j] & 63;
+        *mn = q[j + 4] & 63;
+    } else {
+        *sc = (q[j + 4] & 15) | ((q[j - 4] >> 6) << 4);
+        *mn = (q[j + 4] >> 4) | ((q[j] >> 6) << 4);
+    }
+}
+
+/* Signed 6-bit scale i (0..15) of a Q3_K block: low 4 bits from bytes 0-7
+ * (nibble i / 8 of byte i % 8), high 2 bits from bytes 8-11 (bits 2 (i / 4)
+ * of byte 8 + i % 4); src/gguf_quant.cpp:109-121. */
+static int orc_q3k_scale(const uint8_t* s12, int i) {
+    const int lo = (s12[i % 8] >> (4 * (i / 8))) & 15;
+    const int hi = (s12[8 + i % 4] >> (2 * (i / 4))) & 3;
+    return (int)(int8_t)(uint8_t)(lo | (hi << 4));
+}
+
+float orc_gguf_value(uint32_t type, const uint8_t* b, int p) {
+    switch (type) {
+        case 0: { float f; memcpy(&f, b, 4); return f; }
+        case 1: return orc_f16(b);
+        case 8: /* d, 32 x int8 (src/gguf_quant.cpp:102-106) */
+            return orc_f16(b) * (float)(int8_t)b[2 + p];
+        case 11: { /* hmask[32] q[64] scales[12] d (src/gguf_quant.cpp:108-142) */
+            const uint8_t* hmask = b;
+            const uint8_t* q = b + 32;
+            const int half = p / 128, r = p % 128, j = r / 32, sub = (r % 32) / 16, l = r % 16;
+            const int idx = 16 * sub + l;
+            const float d_all = orc_f16(b + 108);
+            const float dl = d_all * (float)(orc_q3k_scale(b + 96, 8 * half + 2 * j + sub) - 32);
+            const int v = (q[32 * half + idx] >> (2 * j)) & 3;
+            const int hbit = hmask[idx] & (1 << (4 * half + j));
+            return dl * (float)(v - (hbit ? 0 : 4));
+        }
+        case 12: case 13: { /* d dmin scales[12] (qh[32]) q[128] (src/gguf_quant.cpp:144-191) */
+            const float d = orc_f16(b), dmin = orc_f16(b + 2);
+            const int c64 = p / 64, c = p % 64, l = c % 32, hi = c / 32;
+            int sc, mn;
+            orc_k4_scale_min(b + 4, 2 * c64 + hi, &sc, &mn);
+            const float d1 = d * (float)sc, m1 = dmin * (float)mn;
+            const uint8_t* q = b + (type == 12 ? 16 : 48);
+            int v = (q[32 * c64 + l] >> (4 * hi)) & 15;
+            if (type == 13) v += (b[16 + l] & (1 << (2 * c64 + hi))) ? 16 : 0;
+            return d1 * (float)v - m1;
+        }
+        case 14: { /* ql[128] qh[64] scales[16] d (src/gguf_quant.cpp:193-218) */
+            const int n = p / 128, r = p % 128, quarter = r / 32, l = r % 32;
+            const uint8_t* ql = b + 64 * n;
+            const uint8_t* qh = b + 128 + 32 * n;
+            const int8_t* sc = (const int8_t*)(b + 192) + 8 * n;
+            const int lo = (ql[l + 32 * (quarter & 1)] >> (4 * (quarter >> 1))) & 15;
+            const int q6 = (int)(int8_t)(uint8_t)(lo | (((qh[l] >> (2 * quarter)) & 3) << 4)) - 32;
+            const float d = orc_f16(b + 208);
+            return d * (float)sc[l / 16 + 2 * quarter] * (float)q6;
+        }
+        case 18: { /* d qs[64] signs+scales[32] (src/gguf_quant.cpp:220-239) */
+            const int ib = p / 32, l = (p % 32) / 8, j = p % 8;
+            const uint8_t* w = b + 66 + 4 * ib;
+            const uint32_t aux = (uint32_t)w[0] | ((uint32_t)w[1] << 8) | ((uint32_t)w[2] << 16) |
+                                 ((uint32_t)w[3] << 24);
+            const float db = orc_f16(b) * (0.5f + (float)(aux >> 28)) * 0.5f;
+            const uint8_t signs = orc_iq2_signs((aux >> (7 * l)) & 127u);
+            const uint32_t g = orc_iq3xxs_grid[b[2 + 8 * ib + 2 * l + (j >> 2)]];
+            const float mag = (float)((g >> (8 * (j & 3))) & 255u);
+            return db * mag * ((signs & (1u << j)) ? -1.0f : 1.0f);
+        }
+        case 23: { /* d scales_h scales_l[4] qs[128] (src/gguf_quant.cpp:241-257) */
+            const int ib = p / 32, c = p % 32;
+            const uint16_t sh = (uint16_t)(b[2] | (b[3] << 8));
+            const int lo = (b[4 + ib / 2] >> (4 * (ib & 1))) & 15;
+            const int hi = (sh >> (2 * ib)) & 3;
+            const int scale = (int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32;
+            const float dl = orc_f16(b) * (float)scale;
+            const int code = (b[8 + 16 * ib + (c % 16)] >> (4 * (c / 16))) & 15;
+            return dl * (float)orc_iq4nl_values[code];
+        }
+        default: return 0.0f;
+    }
+}
+
+int orc_gguf_dequant_row(uint32_t type, const uint8_t* src, int64_t n, float* dst) {
+    const int64_t be = orc_gguf_block_elems(type), bb = orc_gguf_block_bytes(type);
+    if (!be || n % be) return -1;
+    for (int64_t i = 0; i < n; ++i)
+        dst[i] = orc_gguf_value(type, src + (i / be) * bb, (int)(i % be));
+    return 0;
+}
+
+void orc_gguf_tables(const uint32_t** iq3xxs_grid, const int8_t** iq4nl_values) {
+    *iq3xxs_grid = orc_iq3xxs_grid;
+    *iq4nl_values = orc_iq4nl_values;
+}

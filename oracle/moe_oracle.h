@@ -34,6 +34,10 @@
  *   orc_quant_act_e4m3       : vs torch's float8_e4m3fn conversion of x/scale,
  *                             scale = amax/448 closed form, |x - deq| bound.
  *   orc_dequant_e4m3_blocks  : closed form per element, block index mapping.
+ *   orc_gguf_*               : bit-exact vs the reference's gguf_dequantize_row
+ *                             (oracle/_ref) on random blocks of every type,
+ *                             codebooks byte-identical to the reference's,
+ *                             and hand-built known-answer blocks.
  */
 #ifndef GLMMOE_ORACLE_H
 #define GLMMOE_ORACLE_H
@@ -93,6 +97,16 @@ int orc_moe_forward_ex(const float* x, int64_t n, int64_t H, int E, int topk, in
                        const float* const* down, const float* sh_gate, const float* sh_up,
                        const float* sh_down, int norm_topk, float routed_scale, int h_fp8,
                        int nthreads, float* out, int* ids_out, float* w_out);
+
+
+/* GGUF block formats (src/gguf_quant.cpp:98-262): element p of one block, a
+ * whole row of n elements (n a multiple of the block size; -1 otherwise), the
+ * block geometry, and the two codebooks (for pinning against the reference's). */
+int64_t orc_gguf_block_elems(uint32_t type);
+int64_t orc_gguf_block_bytes(uint32_t type);
+float orc_gguf_value(uint32_t type, const uint8_t* block, int p);
+int orc_gguf_dequant_row(uint32_t type, const uint8_t* src, int64_t n, float* dst);
+void orc_gguf_tables(const uint32_t** iq3xxs_grid, const int8_t** iq4nl_values);
 
 #ifdef __cplusplus
 }

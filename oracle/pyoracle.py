@@ -69,6 +69,16 @@ class Oracle:
             _f32p, _i64, _i64, C.c_int, C.c_int, _i64, _i64, C.c_void_p, C.c_void_p,
             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
             C.c_void_p, C.c_int, C.c_float, C.c_int, C.c_int, _f32p, _i32p, _f32p]
+        L.orc_gguf_block_elems.restype = _i64
+        L.orc_gguf_block_elems.argtypes = [C.c_uint32]
+        L.orc_gguf_block_bytes.restype = _i64
+        L.orc_gguf_block_bytes.argtypes = [C.c_uint32]
+        L.orc_gguf_value.restype = C.c_float
+        L.orc_gguf_value.argtypes = [C.c_uint32, _u8p, C.c_int]
+        L.orc_gguf_dequant_row.restype = C.c_int
+        L.orc_gguf_dequant_row.argtypes = [C.c_uint32, _u8p, _i64, _f32p]
+        L.orc_gguf_tables.argtypes = [C.POINTER(C.POINTER(C.c_uint32)),
+                                      C.POINTER(C.POINTER(C.c_int8))]
 
     # scalar helpers
     def expf(self, x):
@@ -153,6 +163,27 @@ class Oracle:
             raise ValueError("orc_dispatch: expert id out of range")
         return off, st, sr
 
+    def gguf_block(self, qtype):
+        """(elements, bytes) of one block of a GGUF type (0, 0 if unsupported)."""
+        return self.L.orc_gguf_block_elems(qtype), self.L.orc_gguf_block_bytes(qtype)
+
+    def gguf_dequant_rows(self, qtype, data, rows, n):
+        """rows x n fp32 from GGUF rows stored back to back (uint8 array)."""
+        be, bb = self.gguf_block(qtype)
+        rb = n // be * bb
+        data = np.ascontiguousarray(data, np.uint8).reshape(-1)
+        out = np.empty((rows, n), np.float32)
+        for r in range(rows):
+            if self.L.orc_gguf_dequant_row(qtype, data[r * rb:(r + 1) * rb], n, out[r]):
+                raise ValueError(f"orc_gguf_dequant_row: type {qtype}")
+        return out
+
+    def gguf_tables(self):
+        g = C.POINTER(C.c_uint32)()
+        k = C.POINTER(C.c_int8)()
+        self.L.orc_gguf_tables(C.byref(g), C.byref(k))
+        return (np.ctypeslib.as_array(g, (256,)).copy(), np.ctypeslib.as_array(k, (16,)).copy())
+
     def dequant_int4_rows(self, q, scales, in_features, group_size):
         q = np.ascontiguousarray(q, np.uint8)
         s = np.ascontiguousarray(scales, np.float32)
@@ -210,6 +241,11 @@ class RefLib:
         L.ref_hardware_concurrency.restype = C.c_int
         L.ref_dequant_int4.argtypes = [_u8p, _f32p, _i64, _i64, _f32p]
         L.ref_moe_mlp.restype = C.c_int
+        L.ref_gguf_dequant_row.restype = C.c_int
+        L.ref_gguf_dequant_row.argtypes = [C.c_uint32, _u8p, _i64, _f32p]
+        L.ref_gguf_tables.argtypes = [C.POINTER(C.POINTER(C.c_uint8)),
+                                      C.POINTER(C.POINTER(C.c_uint8)),
+                                      C.POINTER(C.POINTER(C.c_int8))]
         L.ref_moe_mlp.argtypes = [
             _f32p, _i64, _i64, C.c_int, C.c_int, _i64, _i64, _f32p, C.c_void_p,
             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
@@ -217,6 +253,20 @@ class RefLib:
 
     def hw_threads(self):
         return self.L.ref_hw_threads()
+
+    def gguf_dequant_row(self, qtype, data, n):
+        out = np.empty(n, np.float32)
+        if self.L.ref_gguf_dequant_row(qtype, np.ascontiguousarray(data, np.uint8), n, out):
+            raise ValueError(f"ref_gguf_dequant_row: type {qtype}")
+        return out
+
+    def gguf_tables(self):
+        g = C.POINTER(C.c_uint8)()
+        s = C.POINTER(C.c_uint8)()
+        k = C.POINTER(C.c_int8)()
+        self.L.ref_gguf_tables(C.byref(g), C.byref(s), C.byref(k))
+        return (np.ctypeslib.as_array(g, (1024,)).copy().view(np.uint32),
+                np.ctypeslib.as_array(s, (128,)).copy(), np.ctypeslib.as_array(k, (16,)).copy())
 
     def hardware_concurrency(self):
         return self.L.ref_hardware_concurrency()

@@ -25,6 +25,7 @@
 #include "model.hpp"
 #undef private
 #include "tensor.hpp"
+#include "gguf_quant.hpp"
 
 using glmserve::GLM52Config;
 using glmserve::GLM52Model;
@@ -95,6 +96,22 @@ int ref_moe_mlp(const float* x, int64_t n, int64_t H, int E, int topk, int64_t I
     } catch (...) {
         return -1;
     }
+}
+
+// src/gguf_quant.cpp: one row of n elements of a GGUF tensor (row 0 of data).
+// Returns 0, -1 for a type it cannot dequantize.
+int ref_gguf_dequant_row(uint32_t type, const uint8_t* data, int64_t n, float* out) {
+    if (!glmserve::gguf_type_can_dequantize(type)) return -1;
+    const std::vector<float> v = glmserve::gguf_dequantize_row(type, data, (uint64_t)n, 0);
+    std::memcpy(out, v.data(), (size_t)n * sizeof(float));
+    return 0;
+}
+
+// The reference's dequant codebooks (src/gguf_quant.cpp:363-381).
+void ref_gguf_tables(const uint8_t** iq3xxs_grid, const uint8_t** ksigns, const int8_t** iq4nl) {
+    *iq3xxs_grid = glmserve::gguf_iq3xxs_grid_table();
+    *ksigns = glmserve::gguf_ksigns_iq2xs_table();
+    *iq4nl = glmserve::gguf_kvalues_iq4nl_table();
 }
 
 }  // extern "C"

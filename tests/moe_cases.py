@@ -203,3 +203,27 @@ class SynthFp8Layer:
         return oracle.moe_forward(xd, self.E, self.k, gate, up, down, sh, logits=lg, e_bias=eb,
                                   norm_topk=self.norm_topk, routed_scale=self.routed_scale,
                                   nthreads=nthreads, h_fp8=True)
+
+
+# GGUF types with block geometry (elements, bytes) and the byte offsets of
+# their fp16 scale fields (src/gguf_quant.cpp:98-262; 0 = F32, 1 = F16).
+GGUF_TYPES = {0: (1, 4, ()), 1: (1, 2, ()), 8: (32, 34, (0,)), 11: (256, 110, (108,)),
+              12: (256, 144, (0, 2)), 13: (256, 176, (0, 2)), 14: (256, 210, (208,)),
+              18: (256, 98, (0,)), 23: (256, 136, (0,))}
+
+
+def random_gguf_rows(qtype, rows, n, rng, scale=1e-2):
+    """rows x n elements of GGUF type qtype as uint8 [rows, row_bytes]: random
+    codes with finite fp16 scales of about `scale` (random bytes there could be
+    Inf / NaN)."""
+    be, bb, dofs = GGUF_TYPES[qtype]
+    nb = n // be
+    if qtype == 0:
+        return rng.standard_normal((rows, n)).astype(np.float32).view(np.uint8)
+    if qtype == 1:
+        return (rng.standard_normal((rows, n)) * 0.1).astype(np.float16).view(np.uint8)
+    data = rng.integers(0, 256, (rows, nb, bb), dtype=np.uint8)
+    d = (rng.uniform(0.5, 1.5, (rows, nb, len(dofs))) * scale).astype(np.float16).view(np.uint8)
+    for i, o in enumerate(dofs):
+        data[:, :, o:o + 2] = d[:, :, 2 * i:2 * i + 2]
+    return data.reshape(rows, nb * bb)

@@ -82,6 +82,17 @@ def test_reference_signature_host_checks():
     assert L.glmmoe_ref_register_w4a16(a, b, c, C.byref(packed)) == 0
     assert L.glmmoe_ref_unregister_w4a16(a, b, c) == 0
     assert L.glmmoe_ref_unregister_w4a16(a, b, c) == -1
+    # GGUF: supported types, row lengths a multiple of the block, row_bytes large enough
+    assert L.glmmoe_ref_gemm_q(18, None, dummy, None, dummy, 1, 6144, 64, 2352, None) == -1
+    assert L.glmmoe_ref_gemm_q(99, dummy, dummy, None, dummy, 1, 6144, 64, 2352, None) == -2
+    assert L.glmmoe_ref_gemm_q(18, dummy, dummy, None, dummy, 1, 6100, 64, 2352, None) == -2
+    assert L.glmmoe_ref_gemm_q(18, dummy, dummy, None, dummy, 1, 6144, 64, 2351, None) == -2
+    assert L.glmmoe_ref_moe_expert_ffn_q(18, 18, 23, dummy, dummy, dummy, dummy, dummy, dummy,
+                                         1, 8, 6144, 2048, 256, 2352, 2352, 1088, None, dummy,
+                                         dummy, None, None, None) == -1
+    assert L.glmmoe_ref_moe_expert_ffn_q(18, 18, 23, dummy, dummy, dummy, dummy, dummy, dummy,
+                                         1, 8, 6144, 2048, 256, 2352, 2352, 1087, dummy, dummy,
+                                         dummy, None, None, None) == -2
 
 
 def _layer(H=6144, I=2048, E=256, k=8, shared=True):
@@ -143,6 +154,10 @@ def test_cpp_header_compiles_against_the_library(tmp_path):
         '  glmserve::cuda::gemm_fp8(x, q, sc, nullptr, y, 1, 6144, 2048);\n'
         '  glmserve::cuda::silu_mul(x, x, y, 2048);\n'
         '  glmserve::cuda::add_inplace(y, x, 6144);\n'
+        '  float* hbuf = nullptr; int* disp = nullptr;\n'
+        '  glmserve::cuda::gemm_q(18, x, q, nullptr, y, 1, 6144, 2048, 6144 / 256 * 98);\n'
+        '  glmserve::cuda::moe_expert_ffn_q(18, 18, 23, x, ids, w, q, q, q, 1, 8, 6144, 2048, 256,\n'
+        '                                   2352, 2352, 1088, hbuf, hbuf, y, disp);\n'
         '  glmmoe_w4a16_layer L{};\n'
         '  return (int)glmserve::cuda::moe_layer_workspace_bytes(L, 1);\n'
         '}\n')

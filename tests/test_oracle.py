@@ -343,3 +343,69 @@ def test_moe_forward_h_fp8(oracle):
         assert np.array_equal(q8[t], ref)
     # e4m3 keeps 3 mantissa bits: the layer moves by a few percent, not more.
     assert np.max(np.abs(q8 - plain)) <= 0.08 * np.max(np.abs(plain))
+
+
+# ---- GGUF block formats ----------------------------------------------------
+
+from moe_cases import GGUF_TYPES, random_gguf_rows  # noqa: E402
+
+
+def test_gguf_tables_match_reference(oracle, ref):
+    grid, iq4 = oracle.gguf_tables()
+    rgrid, rsigns, riq4 = ref.gguf_tables()
+    assert np.array_equal(grid, rgrid)
+    assert np.array_equal(iq4, riq4)
+    # the IQ2 sign table is the 7-bit index with an even-parity bit 7
+    parity = np.array([i | ((bin(i).count("1") & 1) << 7) for i in range(128)], np.uint8)
+    assert np.array_equal(parity, rsigns)
+
+
+@pytest.mark.parametrize("qtype", sorted(GGUF_TYPES))
+def test_gguf_dequant_bit_exact_vs_reference(oracle, ref, qtype):
+    rng = np.random.default_rng(100 + qtype)
+    n = 1024
+    rows = random_gguf_rows(qtype, 6, n, rng)
+    got = oracle.gguf_dequant_rows(qtype, rows, 6, n)
+    for r in range(6):
+        want = ref.gguf_dequant_row(qtype, rows[r], n)
+        assert np.array_equal(got[r].view(np.uint32), want.view(np.uint32)), r
+
+
+def _f16(v):
+    return np.array([v], np.float16).view(np.uint8)
+
+
+def test_gguf_known_answers(oracle):
+    # Q8_0: d = 1 -> the int8 codes themselves.
+    b = np.zeros(34, np.uint8)
+    b[0:2] = _f16(1.0)
+    b[2:] = np.arange(-16, 16, dtype=np.int8).view(np.uint8)
+    assert np.array_equal(oracle.gguf_dequant_rows(8, b, 1, 32)[0], np.arange(-16, 16))
+    # IQ4_XS: d = 1, every 6-bit scale 33 (lo 1, hi 2) -> scale 1, so element
+    # values are the IQ4_NL table entries of their codes.
+    _, iq4 = oracle.gguf_tables()
+    b = np.zeros(136, np.uint8)
+    b[0:2] = _f16(1.0)
+    b[2:4] = np.array([0xAA, 0xAA], np.uint8)          # hi = 2 for all 8 sub-blocks
+    b[4:8] = 0x11                                       # lo = 1 for all 8 sub-blocks
+    codes = np.arange(256) % 16
+    b[8:] = (codes[0::2][:128] | (codes[1::2][:128] << 4)).astype(np.uint8)
+    y = oracle.gguf_dequant_rows(23, b, 1, 256)[0]
+    for ib in range(8):
+        q = b[8 + 16 * ib: 24 + 16 * ib]
+        want = np.concatenate([iq4[q & 15], iq4[q >> 4]]).astype(np.float32)
+        assert np.array_equal(y[32 * ib:32 * ib + 32], want)
+    # Q6_K: d = 1, scales 1, ql / qh codes c -> c - 32.
+    b = np.zeros(210, np.uint8)
+    b[192:208] = 1
+    b[208:210] = _f16(1.0)
+    b[0:128] = 0x53        # low nibbles 3, high nibbles 5
+    b[128:192] = 0b10010011   # 2-bit fields 3, 0, 1, 2
+    y = oracle.gguf_dequant_rows(14, b, 1, 256)[0]
+    assert np.all(y[0:32] == (3 | (3 << 4)) - 32)      # quarter 0: low nibble, bits 0-1
+    assert np.all(y[32:64] == (3 | (0 << 4)) - 32)     # quarter 1: low nibble, bits 2-3
+    assert np.all(y[64:96] == (5 | (1 << 4)) - 32)     # quarter 2: high nibble, bits 4-5
+    assert np.all(y[96:128] == (5 | (2 << 4)) - 32)    # quarter 3: high nibble, bits 6-7
+    # F16 / F32 rows are the values themselves.
+    v = np.array([0.5, -2.0, 65504.0, 6.1e-5], np.float16)
+    assert np.array_equal(oracle.gguf_dequant_rows(1, v.view(np.uint8), 1, 4)[0], v.astype(np.float32))
