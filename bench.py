@@ -190,6 +190,55 @@ def main():
         torch.cuda.synchronize()
         print(json.dumps({"copy_calib_bytes": src.numel() * 4, "reps": 3}))
         return
+    gguf_state = {}
+
+    def measure_gguf(n, steps, warmup):
+        # The served checkpoint's expert formats (IQ3_XXS gate/up, IQ4_XS down) at the
+        # configs[1] layer shape, through moe_expert_ffn_q's signature with the
+        # expert-grouping scratch; routing from the synthetic layer's router.
+        from glmserve_amd import ops
+        if not gguf_state:
+            def rows(nrows, K, bb):
+                nb = K // 256
+                q = torch.randint(0, 256, (nrows, nb, bb), dtype=torch.uint8, device="cuda")
+                d = (torch.rand(nrows, nb, device="cuda") * 0.01 + 0.005).half()
+                q[:, :, 0:2] = d.view(torch.uint8).view(nrows, nb, 2)
+                return q.view(nrows, nb * bb)
+            gguf_state["w"] = (rows(E * I, H, 98), rows(E * I, H, 98), rows(E * H, I, 136))
+        gq, uq, dq = gguf_state["w"]
+        rb = (H // 256 * 98, H // 256 * 98, I // 256 * 136)
+        x = L.x(n, 100 + n)
+        ws = L.layer.alloc_workspace(n)
+        ids = torch.empty(n, K, dtype=torch.int32, device="cuda")
+        w = torch.empty(n, K, dtype=torch.float32, device="cuda")
+        L.layer.route(x, ids, w, ws)
+        xf = x.float()
+        h_act = torch.empty(n * K * I, device="cuda")
+        dpart = torch.empty(n * K * H, device="cuda")
+        out = torch.empty(n, H, device="cuda")
+        disp = torch.empty(3 * E + 1 + n * K, dtype=torch.int32, device="cuda")
+        call = lambda: ops.ref_moe_expert_ffn_q((18, 18, 23), xf, ids, w, gq, uq, dq, I, E, rb,
+                                                h_act, dpart, out, disp)
+        for _ in range(warmup):
+            call()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            call()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        U = int(torch.unique(ids).numel())
+        per_expert = (2 * I * rb[0] + H * rb[2])
+        alg = U * per_expert + n * H * 4 * 2
+        return {"n": n, "ms": ms, "tokens_per_s": n / (ms * 1e-3), "distinct_experts": U,
+                "alg_bytes": alg, "GBps": alg / (ms * 1e-3) / 1e9,
+                "hbm_frac_layer": alg / (ms * 1e-3) / HBM_PEAK,
+                "expert_bytes": per_expert,
+                "note": "routed experts only (the reference's moe_expert_ffn_q has no shared "
+                        "expert); fp32 activations and arithmetic as in the reference"}
+
     def measure_fp8(n, steps, warmup):
         from moe_cases import SynthFp8Layer
         log("bench: building synthetic FP8 layer (configs[4] format)")
@@ -309,6 +358,11 @@ def main():
         LZ = SynthLayer(H, E, K, I, seed=2, zipf_s=1.1)
         sweep["verify_520_zipf"] = measure(520, max(5, args.steps // 5), 3, layer=LZ)
         del LZ
+        torch.cuda.empty_cache()
+    if not args.no_sweep:
+        for n in (1, 64):
+            log(f"bench: sweep GGUF decode B={n} (IQ3_XXS gate/up, IQ4_XS down)")
+            sweep[f"gguf_decode_B{n}"] = measure_gguf(n, args.steps, args.warmup)
         torch.cuda.empty_cache()
     if not args.no_sweep and not args.no_fp8:
         log("bench: sweep FP8 prefill 8192")
