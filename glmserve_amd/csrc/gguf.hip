@@ -227,8 +227,9 @@ __device__ __forceinline__ void gg_dec8(uint32_t t, const uint8_t* __restrict__ 
 }
 
 constexpr int kGgRows = 16;   // weight rows per workgroup (4 per wave)
-constexpr int kGgTile = 8;    // input rows per tile
 constexpr int kGgKC = 512;    // K per staged chunk
+// Input rows per tile (TT): 8 for prefill-sized groups, fewer when an expert
+// holds a row or a few (decode), so no FMAs go to empty rows.
 
 __device__ __forceinline__ float gg_wave_sum(float v) {
 #pragma unroll
@@ -238,18 +239,20 @@ __device__ __forceinline__ float gg_wave_sum(float v) {
 
 __device__ __forceinline__ float gg_silu(float v) { return v / (1.0f + expf(-v)); }
 
-// The input rows of a tile (up to kGgTile, indices into src) and its expert.
+// The input rows of a tile (up to TT, indices into src) and its expert.
+template <int TT>
 struct GgTile {
     int e, nr;
-    int row[kGgTile];    // output row index (routed row r, or the token for gemm_q)
-    int src[kGgTile];    // input row index into src
+    int row[TT];    // output row index (routed row r, or the token for gemm_q)
+    int src[TT];    // input row index into src
 };
 
 // Stages rows srcs[0..nr) x [k0, k0 + kc) of a [*, K] fp32 matrix into xs
 // (srcs: the tile's input rows, in LDS so that they index dynamically).
+template <int TT>
 __device__ __forceinline__ void gg_stage(float (*xs)[kGgKC], const float* __restrict__ src, int K,
                                          const int* srcs, int nr, int k0, int kc) {
-    for (int i = threadIdx.x; i < kGgTile * (kGgKC / 4); i += blockDim.x) {
+    for (int i = threadIdx.x; i < TT * (kGgKC / 4); i += blockDim.x) {
         const int t = i / (kGgKC / 4), c4 = i % (kGgKC / 4);
         float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
         if (t < nr && 4 * c4 < kc)
@@ -260,27 +263,27 @@ __device__ __forceinline__ void gg_stage(float (*xs)[kGgKC], const float* __rest
 
 // Dot products of NM weight matrices' rows o0 .. o0 + 3 with the tile's input
 // rows over K: acc[m][r][t].
-template <uint32_t T, int NM>
+template <uint32_t T, int NM, int TT>
 __device__ __forceinline__ void gg_dots(float (*xs)[kGgKC], int* srcs, const float* __restrict__ src,
-                                        int K, const GgTile& tl, const uint32_t (&type)[NM],
+                                        int K, const GgTile<TT>& tl, const uint32_t (&type)[NM],
                                         const uint8_t* const (&wrow)[NM][4],
-                                        float (&acc)[NM][4][kGgTile]) {
+                                        float (&acc)[NM][4][TT]) {
     const int lane = threadIdx.x & 63;
     __syncthreads();   // srcs and xs of a previous tile are consumed
     if (threadIdx.x == 0) {
 #pragma unroll
-        for (int t = 0; t < kGgTile; ++t) srcs[t] = tl.src[t];
+        for (int t = 0; t < TT; ++t) srcs[t] = tl.src[t];
     }
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int t = 0; t < kGgTile; ++t) acc[m][r][t] = 0.0f;
+            for (int t = 0; t < TT; ++t) acc[m][r][t] = 0.0f;
     for (int k0 = 0; k0 < K; k0 += kGgKC) {
         const int kc = min(kGgKC, K - k0);
         __syncthreads();
-        gg_stage(xs, src, K, srcs, tl.nr, k0, kc);
+        gg_stage<TT>(xs, src, K, srcs, tl.nr, k0, kc);
         __syncthreads();
         const int kk = lane * 8;
         if (kk >= kc) continue;
@@ -293,39 +296,39 @@ __device__ __forceinline__ void gg_dots(float (*xs)[kGgKC], int* srcs, const flo
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
 #pragma unroll
-                    for (int t = 0; t < kGgTile; ++t)
+                    for (int t = 0; t < TT; ++t)
                         acc[m][r][t] = __builtin_fmaf(w[j], xs[t][kk + j], acc[m][r][t]);
             }
     }
 }
 
 // gemm_q: tiles are 8 consecutive tokens.
-template <uint32_t T>
+template <uint32_t T, int TT>
 __global__ __launch_bounds__(256) void gg_gemv_kernel(uint32_t qtype, const float* __restrict__ x,
                                                       const uint8_t* __restrict__ qw,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ y, int n, int in, int out,
                                                       long row_bytes) {
-    __shared__ __align__(16) float xs[kGgTile][kGgKC];
-    __shared__ int srcs[kGgTile];
+    __shared__ __align__(16) float xs[TT][kGgKC];
+    __shared__ int srcs[TT];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int o0 = blockIdx.x * kGgRows + wave * 4;
     const uint32_t type[1] = {qtype};
     const uint8_t* wrow[1][4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) wrow[0][r] = qw + (size_t)min(o0 + r, out - 1) * row_bytes;
-    for (int t0 = 0; t0 < n; t0 += kGgTile) {
-        GgTile tl;
+    for (int t0 = 0; t0 < n; t0 += TT) {
+        GgTile<TT> tl;
         tl.e = 0;
-        tl.nr = min(kGgTile, n - t0);
+        tl.nr = min(TT, n - t0);
 #pragma unroll
-        for (int t = 0; t < kGgTile; ++t) tl.row[t] = tl.src[t] = t0 + t;
-        float acc[1][4][kGgTile];
-        gg_dots<T, 1>(xs, srcs, x, in, tl, type, wrow, acc);
+        for (int t = 0; t < TT; ++t) tl.row[t] = tl.src[t] = min(t0 + t, n - 1);
+        float acc[1][4][TT];
+        gg_dots<T, 1, TT>(xs, srcs, x, in, tl, type, wrow, acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int t = 0; t < kGgTile; ++t) {
+            for (int t = 0; t < TT; ++t) {
                 const float v = gg_wave_sum(acc[0][r][t]);
                 const int o = o0 + r;
                 if (lane == 0 && t < tl.nr && o < out)
@@ -336,15 +339,19 @@ __global__ __launch_bounds__(256) void gg_gemv_kernel(uint32_t qtype, const floa
 
 // Tile g of the routed rows. grouped: d = [offsets E+1 | tile prefix E+1 |
 // rows n*topk] from gg_group_kernel; otherwise routed row g alone.
+template <int TT>
 __device__ __forceinline__ bool gg_tile(int g, const int* __restrict__ ids,
                                         const int* __restrict__ d, int nk, int E, int topk,
-                                        bool down, GgTile& tl) {
+                                        bool down, GgTile<TT>& tl) {
     if (!d) {
         if (g >= nk) return false;
         tl.e = ids[g];
         tl.nr = 1;
-        tl.row[0] = g;
-        tl.src[0] = down ? g : g / topk;
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            tl.row[t] = g;
+            tl.src[t] = down ? g : g / topk;
+        }
         return true;
     }
     const int* off = d;
@@ -358,10 +365,10 @@ __device__ __forceinline__ bool gg_tile(int g, const int* __restrict__ ids,
         else hi = mid;
     }
     tl.e = lo;
-    const int r0 = off[lo] + (g - tp[lo]) * kGgTile;
-    tl.nr = min(kGgTile, off[lo + 1] - r0);
+    const int r0 = off[lo] + (g - tp[lo]) * TT;
+    tl.nr = min(TT, off[lo + 1] - r0);
 #pragma unroll
-    for (int t = 0; t < kGgTile; ++t) {
+    for (int t = 0; t < TT; ++t) {
         const int r = rows[r0 + (t < tl.nr ? t : 0)];
         tl.row[t] = r;
         tl.src[t] = down ? r : r / topk;
@@ -384,13 +391,13 @@ struct GgMoeArgs {
 
 // DOWN = false: phase 1 (gate/up, output rows = I features); true: phase 2.
 // T: the weight type (gate and up share it in phase 1), or kGgAny.
-template <bool DOWN, uint32_t T>
+template <bool DOWN, uint32_t T, int TT>
 __global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
-    __shared__ __align__(16) float xs[kGgTile][kGgKC];
-    __shared__ int srcs[kGgTile];
+    __shared__ __align__(16) float xs[TT][kGgKC];
+    __shared__ int srcs[TT];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nk = a.n * a.topk;
-    GgTile tl;
+    GgTile<TT> tl;
     if (!gg_tile((int)blockIdx.x, a.ids, a.d, nk, a.E, a.topk, DOWN, tl)) return;
     const int out = DOWN ? a.H : a.I;
     const int o0 = blockIdx.y * kGgRows + wave * 4;
@@ -404,12 +411,12 @@ __global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
             wrow[0][r] = a.gate_q + (e * a.I + o) * a.gate_rb;
             wrow[1][r] = a.up_q + (e * a.I + o) * a.up_rb;
         }
-        float acc[2][4][kGgTile];
-        gg_dots<T, 2>(xs, srcs, a.x, a.H, tl, type, wrow, acc);
+        float acc[2][4][TT];
+        gg_dots<T, 2, TT>(xs, srcs, a.x, a.H, tl, type, wrow, acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int t = 0; t < kGgTile; ++t) {
+            for (int t = 0; t < TT; ++t) {
                 const float g = gg_wave_sum(acc[0][r][t]);
                 const float u = gg_wave_sum(acc[1][r][t]);
                 const int o = o0 + r;
@@ -424,12 +431,12 @@ __global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
             const size_t o = (size_t)min(o0 + r, out - 1);
             wrow[0][r] = a.down_q + (e * a.H + o) * a.down_rb;
         }
-        float acc[1][4][kGgTile];
-        gg_dots<T, 1>(xs, srcs, a.h_act, a.I, tl, type, wrow, acc);
+        float acc[1][4][TT];
+        gg_dots<T, 1, TT>(xs, srcs, a.h_act, a.I, tl, type, wrow, acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
-            for (int t = 0; t < kGgTile; ++t) {
+            for (int t = 0; t < TT; ++t) {
                 const float v = gg_wave_sum(acc[0][r][t]);
                 const int o = o0 + r;
                 if (lane == 0 && t < tl.nr && o < out) a.dpart[(size_t)tl.row[t] * a.H + o] = v;
@@ -453,7 +460,7 @@ __global__ __launch_bounds__(256) void gg_reduce_kernel(const float* __restrict_
 // prefix E+1 | rows n*topk]; rows of an expert are in any order (each row's
 // result depends only on its own inputs).
 __global__ __launch_bounds__(1024) void gg_group_kernel(const int* __restrict__ ids, int nk, int E,
-                                                        int* __restrict__ d) {
+                                                        int tile_rows, int* __restrict__ d) {
     extern __shared__ int gl[];   // cnt[E] | cursor[E]
     int* cnt = gl;
     int* cur = gl + E;
@@ -474,7 +481,7 @@ __global__ __launch_bounds__(1024) void gg_group_kernel(const int* __restrict__ 
             tp[e] = t;
             cur[e] = o;
             o += cnt[e];
-            t += (cnt[e] + kGgTile - 1) / kGgTile;
+            t += (cnt[e] + tile_rows - 1) / tile_rows;
         }
         off[E] = o;
         tp[E] = t;
@@ -506,10 +513,34 @@ static void gg_by_type(uint32_t t, F&& f) {
 
 int launch_gg_gemm(uint32_t qtype, const float* x, const uint8_t* qw, const float* bias, float* y,
                    int n, int in, int out, long row_bytes, hipStream_t s) {
+    const dim3 grid((unsigned)((out + kGgRows - 1) / kGgRows));
     gg_by_type(qtype, [&](auto tc) {
-        hipLaunchKernelGGL((gg_gemv_kernel<decltype(tc)::value>),
-                           dim3((unsigned)((out + kGgRows - 1) / kGgRows)), dim3(256), 0, s, qtype,
-                           x, qw, bias, y, n, in, out, row_bytes);
+        constexpr uint32_t T = decltype(tc)::value;
+        if (n == 1)
+            hipLaunchKernelGGL((gg_gemv_kernel<T, 1>), grid, dim3(256), 0, s, qtype, x, qw, bias,
+                               y, n, in, out, row_bytes);
+        else
+            hipLaunchKernelGGL((gg_gemv_kernel<T, 8>), grid, dim3(256), 0, s, qtype, x, qw, bias,
+                               y, n, in, out, row_bytes);
+    });
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+template <int TT>
+static int gg_moe_phases(uint32_t gt, uint32_t ut, uint32_t dt, const GgMoeArgs& a, unsigned tiles,
+                         hipStream_t s) {
+    const dim3 g1(tiles, (unsigned)((a.I + kGgRows - 1) / kGgRows));
+    if (gt == ut)
+        gg_by_type(gt, [&](auto tc) {
+            hipLaunchKernelGGL((gg_moe_kernel<false, decltype(tc)::value, TT>), g1, dim3(256), 0, s,
+                               a);
+        });
+    else
+        hipLaunchKernelGGL((gg_moe_kernel<false, kGgAny, TT>), g1, dim3(256), 0, s, a);
+    if (hipGetLastError() != hipSuccess) return -4;
+    const dim3 g2(tiles, (unsigned)((a.H + kGgRows - 1) / kGgRows));
+    gg_by_type(dt, [&](auto tc) {
+        hipLaunchKernelGGL((gg_moe_kernel<true, decltype(tc)::value, TT>), g2, dim3(256), 0, s, a);
     });
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
@@ -521,26 +552,19 @@ int launch_gg_moe(uint32_t gt, uint32_t ut, uint32_t dt, const float* x, const i
     const int nk = n * topk;
     GgMoeArgs a{gt, ut, dt, x, ids, w, gq, uq, dq, grb, urb, drb, n, topk, H, I, E, h_act, dpart,
                 dispatch};
+    // Rows per tile: about the rows an expert holds (decode: one or a few).
+    const int tt = !dispatch || nk <= E ? 1 : nk <= 4 * E ? 4 : 8;
     unsigned tiles = (unsigned)nk;
     if (dispatch) {
         hipLaunchKernelGGL(gg_group_kernel, dim3(1), dim3(1024), (size_t)2 * E * 4, s, ids, nk, E,
-                           dispatch);
+                           tt, dispatch);
         if (hipGetLastError() != hipSuccess) return -4;
-        tiles = (unsigned)((nk + kGgTile - 1) / kGgTile + E);
+        tiles = (unsigned)((nk + tt - 1) / tt + E);
     }
-    const dim3 g1(tiles, (unsigned)((I + kGgRows - 1) / kGgRows));
-    if (gt == ut)
-        gg_by_type(gt, [&](auto tc) {
-            hipLaunchKernelGGL((gg_moe_kernel<false, decltype(tc)::value>), g1, dim3(256), 0, s, a);
-        });
-    else
-        hipLaunchKernelGGL((gg_moe_kernel<false, kGgAny>), g1, dim3(256), 0, s, a);
-    if (hipGetLastError() != hipSuccess) return -4;
-    const dim3 g2(tiles, (unsigned)((H + kGgRows - 1) / kGgRows));
-    gg_by_type(dt, [&](auto tc) {
-        hipLaunchKernelGGL((gg_moe_kernel<true, decltype(tc)::value>), g2, dim3(256), 0, s, a);
-    });
-    if (hipGetLastError() != hipSuccess) return -4;
+    const int rc = tt == 1 ? gg_moe_phases<1>(gt, ut, dt, a, tiles, s)
+                 : tt == 4 ? gg_moe_phases<4>(gt, ut, dt, a, tiles, s)
+                           : gg_moe_phases<8>(gt, ut, dt, a, tiles, s);
+    if (rc) return rc;
     const long total = (long)n * H;
     hipLaunchKernelGGL(gg_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
                        dpart, w, n, topk, H, out);
