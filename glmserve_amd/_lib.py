@@ -50,6 +50,13 @@ SIGNATURES = {
     "glmmoe_ref_moe_expert_ffn_q": (_i, [C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp, _vp,
                                          _vp, _vp, _i, _i, _i, _i, _i, _i64, _i64, _i64, _vp,
                                          _vp, _vp, _vp, _vp, _vp]),
+    "glmmoe_ref_qtype_has_i8": (_i, [C.c_uint32]),
+    "glmmoe_ref_quantize_act_q8": (_i, [_vp, _i64, _i64, _vp, _vp, _vp]),
+    "glmmoe_ref_gemm_q_i8": (_i, [C.c_uint32, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _i64,
+                                  _vp]),
+    "glmmoe_ref_moe_expert_ffn_q_i8": (_i, [C.c_uint32, C.c_uint32, C.c_uint32, _vp, _vp, _vp,
+                                            _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i64, _i64,
+                                            _i64, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp]),
 }
 
 STAGES = ["router_logits", "router_topk", "dispatch", "gate_up", "down", "combine"]

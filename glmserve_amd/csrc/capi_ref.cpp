@@ -226,4 +226,59 @@ int glmmoe_ref_moe_expert_ffn_q(uint32_t gate_type, uint32_t up_type, uint32_t d
                : GLMMOE_OK;
 }
 
+int glmmoe_ref_qtype_has_i8(uint32_t qtype) { return gguf_has_i8(qtype) ? 1 : 0; }
+
+int glmmoe_ref_quantize_act_q8(const float* x, int64_t n, int64_t in, int8_t* xq, float* xs,
+                               void* stream) {
+    if (!x || !xq || !xs || n <= 0 || in <= 0) return GLMMOE_ERR_ARG;
+    if (in % 32 || n > INT32_MAX || in > INT32_MAX) return GLMMOE_ERR_SHAPE;
+    return launch_gg_quant_q8(x, (long)(n * in), xq, xs, S(stream)) ? GLMMOE_ERR_LAUNCH
+                                                                   : GLMMOE_OK;
+}
+
+// int8 activation rows are read four bytes at a time.
+static bool i8_rows_ok(const int8_t* q, int64_t in) {
+    return in % 32 == 0 && ((uintptr_t)q & 3) == 0;
+}
+
+int glmmoe_ref_gemm_q_i8(uint32_t qtype, const int8_t* xq, const float* xs, const uint8_t* qW,
+                         const float* bias, float* y, int64_t n, int64_t in, int64_t out,
+                         int64_t row_bytes, void* stream) {
+    if (!xq || !xs || !qW || !y || n <= 0 || in <= 0 || out <= 0) return GLMMOE_ERR_ARG;
+    if (n > INT32_MAX || in > INT32_MAX || out > INT32_MAX || !gguf_has_i8(qtype) ||
+        !gguf_rows_ok(qtype, in, row_bytes) || !i8_rows_ok(xq, in))
+        return GLMMOE_ERR_SHAPE;
+    return launch_gg_gemm_i8(qtype, xq, xs, qW, bias, y, (int)n, (int)in, (int)out,
+                             (long)row_bytes, S(stream))
+               ? GLMMOE_ERR_LAUNCH
+               : GLMMOE_OK;
+}
+
+int glmmoe_ref_moe_expert_ffn_q_i8(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
+                                   const int8_t* xq, const float* xs, const int* topk_ids,
+                                   const float* topk_w, const uint8_t* gate_q,
+                                   const uint8_t* up_q, const uint8_t* down_q, int n, int topk,
+                                   int hidden, int moe_inter, int E, int64_t gate_row_bytes,
+                                   int64_t up_row_bytes, int64_t down_row_bytes, float* h_act,
+                                   int8_t* hq, float* hs, float* dpart, float* out, int* dispatch,
+                                   float* gu_part, void* stream) {
+    (void)gu_part;
+    if (!xq || !xs || !topk_ids || !topk_w || !gate_q || !up_q || !down_q || !h_act || !hq ||
+        !hs || !dpart || !out || n <= 0 || topk <= 0 || hidden <= 0 || moe_inter <= 0 || E <= 0)
+        return GLMMOE_ERR_ARG;
+    if (E > 4096 || (int64_t)n * topk > INT32_MAX / 2 || !gguf_has_i8(gate_type) ||
+        !gguf_has_i8(up_type) || !gguf_has_i8(down_type) ||
+        !gguf_rows_ok(gate_type, hidden, gate_row_bytes) ||
+        !gguf_rows_ok(up_type, hidden, up_row_bytes) ||
+        !gguf_rows_ok(down_type, moe_inter, down_row_bytes) || !i8_rows_ok(xq, hidden) ||
+        !i8_rows_ok(hq, moe_inter))
+        return GLMMOE_ERR_SHAPE;
+    return launch_gg_moe_i8(gate_type, up_type, down_type, xq, xs, topk_ids, topk_w, gate_q, up_q,
+                            down_q, n, topk, hidden, moe_inter, E, (long)gate_row_bytes,
+                            (long)up_row_bytes, (long)down_row_bytes, h_act, hq, hs, dpart, out,
+                            dispatch, S(stream))
+               ? GLMMOE_ERR_LAUNCH
+               : GLMMOE_OK;
+}
+
 }  // extern "C"

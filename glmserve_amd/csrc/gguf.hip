@@ -302,14 +302,240 @@ __device__ __forceinline__ void gg_dots(float (*xs)[kGgKC], int* srcs, const flo
     }
 }
 
+// ---- int8 activations (gemm_q_i8 / moe_expert_ffn_q_i8, cuda/qgemm.cu:104-303,
+// 556-587). Weights k .. k + 7 as integers with one affine pair,
+// weight[j] = ds * wq[j] - dm (dm != 0 for Q4_K / Q5_K only), packed four
+// per int32 for v_dot4c_i32_i8. The same bits give exactly the decode above.
+__device__ __forceinline__ int gg_pk4(int a, int b, int c, int d) {
+    return (a & 255) | ((b & 255) << 8) | ((c & 255) << 16) | (int)((unsigned)d << 24);
+}
+
+__device__ __forceinline__ uint32_t gg_ld32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+__device__ __forceinline__ void gg_dec8i_any(uint32_t t, const uint8_t* __restrict__ row, int k,
+                                             int& w0, int& w1, float& ds, float& dm) {
+    int v[8];
+    dm = 0.0f;
+    switch (t) {
+        case 8: {
+            const uint8_t* b = row + (size_t)(k / 32) * 34;
+            ds = gg_f16(b);
+            w0 = (int)gg_ld32(b + 2 + k % 32);
+            w1 = (int)gg_ld32(b + 6 + k % 32);
+            return;
+        }
+        case 11: {
+            const uint8_t* b = row + (size_t)(k / 256) * 110;
+            const int p = k % 256, half = p / 128, r = p % 128, j = r / 32, sub = (r % 32) / 16;
+            const int l0 = r % 16, i = 8 * half + 2 * j + sub;
+            const int lo = (b[96 + i % 8] >> (4 * (i / 8))) & 15;
+            const int hi = (b[104 + i % 4] >> (2 * (i / 4))) & 3;
+            ds = gg_f16(b + 108) * (float)((int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32);
+            const int hm = 1 << (4 * half + j);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int idx = 16 * sub + l0 + e;
+                v[e] = ((b[32 + 32 * half + idx] >> (2 * j)) & 3) - ((b[idx] & hm) ? 0 : 4);
+            }
+            break;
+        }
+        case 12:
+        case 13: {
+            const int bb = t == 12 ? 144 : 176;
+            const uint8_t* b = row + (size_t)(k / 256) * bb;
+            const int p = k % 256, c64 = p / 64, c = p % 64, l0 = c % 32, hi = c / 32;
+            const int js = 2 * c64 + hi;
+            const uint8_t* s = b + 4;
+            int sc, mn;
+            if (js < 4) {
+                sc = s[js] & 63;
+                mn = s[js + 4] & 63;
+            } else {
+                sc = (s[js + 4] & 15) | ((s[js - 4] >> 6) << 4);
+                mn = (s[js + 4] >> 4) | ((s[js] >> 6) << 4);
+            }
+            ds = gg_f16(b) * (float)sc;
+            dm = gg_f16(b + 2) * (float)mn;
+            const uint8_t* q = b + (t == 12 ? 16 : 48) + 32 * c64 + l0;
+            uint32_t a0 = (gg_ld32(q) >> (4 * hi)) & 0x0f0f0f0fu;
+            uint32_t a1 = (gg_ld32(q + 4) >> (4 * hi)) & 0x0f0f0f0fu;
+            if (t == 13) {
+                a0 |= ((gg_ld32(b + 16 + l0) >> js) & 0x01010101u) << 4;
+                a1 |= ((gg_ld32(b + 20 + l0) >> js) & 0x01010101u) << 4;
+            }
+            w0 = (int)a0;
+            w1 = (int)a1;
+            return;
+        }
+        case 14: {
+            const uint8_t* b = row + (size_t)(k / 256) * 210;
+            const int p = k % 256, nn = p / 128, r = p % 128, quarter = r / 32, l0 = r % 32;
+            const uint8_t* ql = b + 64 * nn + 32 * (quarter & 1) + l0;
+            const uint8_t* qh = b + 128 + 32 * nn + l0;
+            ds = gg_f16(b + 208) * (float)(int8_t)b[192 + 8 * nn + l0 / 16 + 2 * quarter];
+            const int sl = 4 * (quarter >> 1), sh = 2 * quarter;
+            // q6 - 32 per byte: (lo | hi << 4) in 0..63, minus 32 by a bytewise
+            // subtract with no borrow across bytes (each byte >= 0, result -32..31).
+            const uint32_t u0 = ((gg_ld32(ql) >> sl) & 0x0f0f0f0fu) | (((gg_ld32(qh) >> sh) & 0x03030303u) << 4);
+            const uint32_t u1 = ((gg_ld32(ql + 4) >> sl) & 0x0f0f0f0fu) | (((gg_ld32(qh + 4) >> sh) & 0x03030303u) << 4);
+            w0 = (int)((u0 | 0x80808080u) - 0x20202020u) ^ (int)0x80808080u;
+            w1 = (int)((u1 | 0x80808080u) - 0x20202020u) ^ (int)0x80808080u;
+            return;
+        }
+        case 18: {
+            const uint8_t* b = row + (size_t)(k / 256) * 98;
+            const int p = k % 256, ib = p / 32, l = (p % 32) / 8;
+            const uint32_t aux = gg_ld32(b + 66 + 4 * ib);
+            ds = gg_f16(b) * (0.5f + (float)(aux >> 28)) * 0.5f;
+            const uint32_t i7 = (aux >> (7 * l)) & 127u;
+            const uint32_t signs = i7 | ((uint32_t)(__builtin_popcount(i7) & 1) << 7);
+            const uint32_t g0 = c_iq3xxs_grid[b[2 + 8 * ib + 2 * l]];
+            const uint32_t g1 = c_iq3xxs_grid[b[2 + 8 * ib + 2 * l + 1]];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int mag = (int)(((e < 4 ? g0 : g1) >> (8 * (e & 3))) & 255u);
+                v[e] = (signs & (1u << e)) ? -mag : mag;
+            }
+            break;
+        }
+        case 23: {
+            const uint8_t* b = row + (size_t)(k / 256) * 136;
+            const int p = k % 256, ib = p / 32, c = p % 32;
+            const int sh = b[2] | (b[3] << 8);
+            const int lo = (b[4 + ib / 2] >> (4 * (ib & 1))) & 15;
+            const int hi = (sh >> (2 * ib)) & 3;
+            ds = gg_f16(b) * (float)((int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const int cc = c + e;
+                v[e] = c_iq4nl[(b[8 + 16 * ib + (cc % 16)] >> (4 * (cc / 16))) & 15];
+            }
+            break;
+        }
+        default:
+            ds = 0.0f;
+            w0 = w1 = 0;
+            return;
+    }
+    w0 = gg_pk4(v[0], v[1], v[2], v[3]);
+    w1 = gg_pk4(v[4], v[5], v[6], v[7]);
+}
+
+template <uint32_t T>
+__device__ __forceinline__ void gg_dec8i(uint32_t t, const uint8_t* __restrict__ row, int k,
+                                         int& w0, int& w1, float& ds, float& dm) {
+    gg_dec8i_any(T == kGgAny ? t : T, row, k, w0, w1, ds, dm);
+}
+
+// LDS tile of int8 activations: TT rows x kGgKC bytes and their per-32 scales.
+template <int TT>
+struct GgI8Tile {
+    int q[TT][kGgKC / 4];
+    float s[TT][kGgKC / 32];
+};
+
+// The int8 twin of gg_dots: xq [*, K] int8 and xsc [*, K / 32] scales; per
+// 8-element fragment r = ds * dot(wq, xq) - dm * sum(xq), acc += sx * r.
+template <uint32_t T, int NM, int TT>
+__device__ __forceinline__ void gg_dots_i8(GgI8Tile<TT>& xt, int* srcs, const int8_t* __restrict__ xq,
+                                           const float* __restrict__ xsc, int K,
+                                           const GgTile<TT>& tl, const uint32_t (&type)[NM],
+                                           const uint8_t* const (&wrow)[NM][4],
+                                           float (&acc)[NM][4][TT]) {
+    const int lane = threadIdx.x & 63;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t) srcs[t] = tl.src[t];
+    }
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < TT; ++t) acc[m][r][t] = 0.0f;
+    const int K32 = K / 32;
+    for (int k0 = 0; k0 < K; k0 += kGgKC) {
+        const int kc = min(kGgKC, K - k0);
+        __syncthreads();
+        for (int i = threadIdx.x; i < TT * (kGgKC / 4); i += blockDim.x) {
+            const int t = i / (kGgKC / 4), c = i % (kGgKC / 4);
+            int v = 0;
+            if (t < tl.nr && 4 * c < kc)
+                v = *reinterpret_cast<const int*>(xq + (size_t)srcs[t] * K + k0 + 4 * c);
+            xt.q[t][c] = v;
+        }
+        for (int i = threadIdx.x; i < TT * (kGgKC / 32); i += blockDim.x) {
+            const int t = i / (kGgKC / 32), c = i % (kGgKC / 32);
+            xt.s[t][c] = (t < tl.nr && 32 * c < kc) ? xsc[(size_t)srcs[t] * K32 + k0 / 32 + c] : 0.0f;
+        }
+        __syncthreads();
+        const int kk = lane * 8;
+        if (kk >= kc) continue;
+        int x0[TT], x1[TT], sx1[TT];
+        float sx[TT];
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+            const int2 q = *reinterpret_cast<const int2*>(&xt.q[t][kk / 4]);
+            x0[t] = q.x;
+            x1[t] = q.y;
+            sx[t] = xt.s[t][kk / 32];
+            sx1[t] = __builtin_amdgcn_sdot4(0x01010101, q.y, __builtin_amdgcn_sdot4(0x01010101, q.x, 0, false), false);
+        }
+#pragma unroll
+        for (int m = 0; m < NM; ++m)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                int w0, w1;
+                float ds, dm;
+                gg_dec8i<T>(type[m], wrow[m][r], k0 + kk, w0, w1, ds, dm);
+#pragma unroll
+                for (int t = 0; t < TT; ++t) {
+                    const int si = __builtin_amdgcn_sdot4(w1, x1[t], __builtin_amdgcn_sdot4(w0, x0[t], 0, false), false);
+                    float v = ds * (float)si;
+                    if (T == 12 || T == 13 || (T == kGgAny && dm != 0.0f)) v = v - dm * (float)sx1[t];
+                    acc[m][r][t] = __builtin_fmaf(sx[t], v, acc[m][r][t]);
+                }
+            }
+    }
+}
+
+// quantize_act_q8 (cuda/qgemm.cu:556-587): per 32-element block (one half
+// wave), sx = absmax / 127, q = round-half-even(v * (1 / sx)), 0 when sx = 0.
+__global__ __launch_bounds__(256) void gg_quant_q8_kernel(const float* __restrict__ x, long total,
+                                                          int8_t* __restrict__ xq,
+                                                          float* __restrict__ xs) {
+    const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
+    const float v = i < total ? x[i] : 0.0f;
+    float a = fabsf(v);
+#pragma unroll
+    for (int m = 16; m >= 1; m >>= 1) a = fmaxf(a, __shfl_xor(a, m));
+    if (i >= total) return;
+    const float sx = a / 127.0f;
+    const float id = sx > 0.0f ? 1.0f / sx : 0.0f;
+    xq[i] = (int8_t)(int)rintf(v * id);
+    if ((i & 31) == 0) xs[i / 32] = sx;
+}
+
 // gemm_q: tiles are 8 consecutive tokens.
-template <uint32_t T, int TT>
+// LDS bytes of a tile's staged activations.
+template <int TT, bool I8>
+constexpr size_t gg_lds_bytes() {
+    return I8 ? sizeof(GgI8Tile<TT>) : sizeof(float) * TT * kGgKC;
+}
+
+// I8: activations are (xq, xsc) from quantize_act_q8 instead of x (gemm_q_i8).
+template <uint32_t T, int TT, bool I8>
 __global__ __launch_bounds__(256) void gg_gemv_kernel(uint32_t qtype, const float* __restrict__ x,
+                                                      const int8_t* __restrict__ xq,
+                                                      const float* __restrict__ xsc,
                                                       const uint8_t* __restrict__ qw,
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ y, int n, int in, int out,
                                                       long row_bytes) {
-    __shared__ __align__(16) float xs[TT][kGgKC];
+    __shared__ __align__(16) char lds[gg_lds_bytes<TT, I8>()];
     __shared__ int srcs[TT];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int o0 = blockIdx.x * kGgRows + wave * 4;
@@ -324,7 +550,12 @@ __global__ __launch_bounds__(256) void gg_gemv_kernel(uint32_t qtype, const floa
 #pragma unroll
         for (int t = 0; t < TT; ++t) tl.row[t] = tl.src[t] = min(t0 + t, n - 1);
         float acc[1][4][TT];
-        gg_dots<T, 1, TT>(xs, srcs, x, in, tl, type, wrow, acc);
+        if constexpr (I8)
+            gg_dots_i8<T, 1, TT>(*reinterpret_cast<GgI8Tile<TT>*>(lds), srcs, xq, xsc, in, tl, type,
+                                 wrow, acc);
+        else
+            gg_dots<T, 1, TT>(reinterpret_cast<float (*)[kGgKC]>(lds), srcs, x, in, tl, type, wrow,
+                              acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -387,13 +618,18 @@ struct GgMoeArgs {
     float* h_act;
     float* dpart;
     const int* d;   // grouping (nullable)
+    // int8 activations (moe_expert_ffn_q_i8): x as (xq, xs), h_act as (hq, hs)
+    const int8_t* xq;
+    const float* xs;
+    const int8_t* hq;
+    const float* hs;
 };
 
 // DOWN = false: phase 1 (gate/up, output rows = I features); true: phase 2.
 // T: the weight type (gate and up share it in phase 1), or kGgAny.
-template <bool DOWN, uint32_t T, int TT>
+template <bool DOWN, uint32_t T, int TT, bool I8>
 __global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
-    __shared__ __align__(16) float xs[TT][kGgKC];
+    __shared__ __align__(16) char lds[gg_lds_bytes<TT, I8>()];
     __shared__ int srcs[TT];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nk = a.n * a.topk;
@@ -412,7 +648,12 @@ __global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
             wrow[1][r] = a.up_q + (e * a.I + o) * a.up_rb;
         }
         float acc[2][4][TT];
-        gg_dots<T, 2, TT>(xs, srcs, a.x, a.H, tl, type, wrow, acc);
+        if constexpr (I8)
+            gg_dots_i8<T, 2, TT>(*reinterpret_cast<GgI8Tile<TT>*>(lds), srcs, a.xq, a.xs, a.H, tl,
+                                 type, wrow, acc);
+        else
+            gg_dots<T, 2, TT>(reinterpret_cast<float (*)[kGgKC]>(lds), srcs, a.x, a.H, tl, type,
+                              wrow, acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -432,7 +673,12 @@ __global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
             wrow[0][r] = a.down_q + (e * a.H + o) * a.down_rb;
         }
         float acc[1][4][TT];
-        gg_dots<T, 1, TT>(xs, srcs, a.h_act, a.I, tl, type, wrow, acc);
+        if constexpr (I8)
+            gg_dots_i8<T, 1, TT>(*reinterpret_cast<GgI8Tile<TT>*>(lds), srcs, a.hq, a.hs, a.I, tl,
+                                 type, wrow, acc);
+        else
+            gg_dots<T, 1, TT>(reinterpret_cast<float (*)[kGgKC]>(lds), srcs, a.h_act, a.I, tl, type,
+                              wrow, acc);
 #pragma unroll
         for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -511,47 +757,100 @@ static void gg_by_type(uint32_t t, F&& f) {
     }
 }
 
-int launch_gg_gemm(uint32_t qtype, const float* x, const uint8_t* qw, const float* bias, float* y,
-                   int n, int in, int out, long row_bytes, hipStream_t s) {
+// The int8-capable types (qtype_has_i8, cuda/qgemm.cu:556-567).
+bool gguf_has_i8(uint32_t t) {
+    return t == 8 || t == 11 || t == 12 || t == 13 || t == 14 || t == 18 || t == 23;
+}
+
+// gg_by_type over the int8-capable types (kGgAny for anything else).
+template <class F>
+static void gg_by_type_i8(uint32_t t, F&& f) {
+    switch (t) {
+        case 8: f(std::integral_constant<uint32_t, 8>{}); break;
+        case 11: f(std::integral_constant<uint32_t, 11>{}); break;
+        case 12: f(std::integral_constant<uint32_t, 12>{}); break;
+        case 13: f(std::integral_constant<uint32_t, 13>{}); break;
+        case 14: f(std::integral_constant<uint32_t, 14>{}); break;
+        case 18: f(std::integral_constant<uint32_t, 18>{}); break;
+        case 23: f(std::integral_constant<uint32_t, 23>{}); break;
+        default: f(std::integral_constant<uint32_t, kGgAny>{}); break;
+    }
+}
+
+template <bool I8, class F>
+static void gg_by_type_t(uint32_t t, F&& f) {
+    if constexpr (I8) gg_by_type_i8(t, f);
+    else gg_by_type(t, f);
+}
+
+template <bool I8>
+static int gg_gemm(uint32_t qtype, const float* x, const int8_t* xq, const float* xsc,
+                   const uint8_t* qw, const float* bias, float* y, int n, int in, int out,
+                   long row_bytes, hipStream_t s) {
     const dim3 grid((unsigned)((out + kGgRows - 1) / kGgRows));
-    gg_by_type(qtype, [&](auto tc) {
+    gg_by_type_t<I8>(qtype, [&](auto tc) {
         constexpr uint32_t T = decltype(tc)::value;
         if (n == 1)
-            hipLaunchKernelGGL((gg_gemv_kernel<T, 1>), grid, dim3(256), 0, s, qtype, x, qw, bias,
-                               y, n, in, out, row_bytes);
+            hipLaunchKernelGGL((gg_gemv_kernel<T, 1, I8>), grid, dim3(256), 0, s, qtype, x, xq,
+                               xsc, qw, bias, y, n, in, out, row_bytes);
         else
-            hipLaunchKernelGGL((gg_gemv_kernel<T, 8>), grid, dim3(256), 0, s, qtype, x, qw, bias,
-                               y, n, in, out, row_bytes);
+            hipLaunchKernelGGL((gg_gemv_kernel<T, 8, I8>), grid, dim3(256), 0, s, qtype, x, xq,
+                               xsc, qw, bias, y, n, in, out, row_bytes);
     });
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-template <int TT>
+int launch_gg_gemm(uint32_t qtype, const float* x, const uint8_t* qw, const float* bias, float* y,
+                   int n, int in, int out, long row_bytes, hipStream_t s) {
+    return gg_gemm<false>(qtype, x, nullptr, nullptr, qw, bias, y, n, in, out, row_bytes, s);
+}
+
+int launch_gg_gemm_i8(uint32_t qtype, const int8_t* xq, const float* xs, const uint8_t* qw,
+                      const float* bias, float* y, int n, int in, int out, long row_bytes,
+                      hipStream_t s) {
+    return gg_gemm<true>(qtype, nullptr, xq, xs, qw, bias, y, n, in, out, row_bytes, s);
+}
+
+int launch_gg_quant_q8(const float* x, long total, int8_t* xq, float* xs, hipStream_t s) {
+    hipLaunchKernelGGL(gg_quant_q8_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                       x, total, xq, xs);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+// I8: h_act is quantized into (hq, hs) between the phases.
+template <int TT, bool I8>
 static int gg_moe_phases(uint32_t gt, uint32_t ut, uint32_t dt, const GgMoeArgs& a, unsigned tiles,
                          hipStream_t s) {
     const dim3 g1(tiles, (unsigned)((a.I + kGgRows - 1) / kGgRows));
     if (gt == ut)
-        gg_by_type(gt, [&](auto tc) {
-            hipLaunchKernelGGL((gg_moe_kernel<false, decltype(tc)::value, TT>), g1, dim3(256), 0, s,
-                               a);
+        gg_by_type_t<I8>(gt, [&](auto tc) {
+            hipLaunchKernelGGL((gg_moe_kernel<false, decltype(tc)::value, TT, I8>), g1, dim3(256),
+                               0, s, a);
         });
     else
-        hipLaunchKernelGGL((gg_moe_kernel<false, kGgAny, TT>), g1, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((gg_moe_kernel<false, kGgAny, TT, I8>), g1, dim3(256), 0, s, a);
     if (hipGetLastError() != hipSuccess) return -4;
+    if constexpr (I8) {
+        if (launch_gg_quant_q8(a.h_act, (long)a.n * a.topk * a.I, const_cast<int8_t*>(a.hq),
+                               const_cast<float*>(a.hs), s))
+            return -4;
+    }
     const dim3 g2(tiles, (unsigned)((a.H + kGgRows - 1) / kGgRows));
-    gg_by_type(dt, [&](auto tc) {
-        hipLaunchKernelGGL((gg_moe_kernel<true, decltype(tc)::value, TT>), g2, dim3(256), 0, s, a);
+    gg_by_type_t<I8>(dt, [&](auto tc) {
+        hipLaunchKernelGGL((gg_moe_kernel<true, decltype(tc)::value, TT, I8>), g2, dim3(256), 0, s,
+                           a);
     });
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
-int launch_gg_moe(uint32_t gt, uint32_t ut, uint32_t dt, const float* x, const int* ids,
-                  const float* w, const uint8_t* gq, const uint8_t* uq, const uint8_t* dq, int n,
-                  int topk, int H, int I, int E, long grb, long urb, long drb, float* h_act,
-                  float* dpart, float* out, int* dispatch, hipStream_t s) {
+template <bool I8>
+static int gg_moe(const GgMoeArgs& a, float* out, int* dispatch, hipStream_t s) {
+    const uint32_t gt = a.gate_type, ut = a.up_type, dt = a.down_type;
+    const int n = a.n, topk = a.topk, H = a.H, E = a.E;
+    const float* ids_w = a.w;
+    const float* dpart = a.dpart;
+    const int* ids = a.ids;
     const int nk = n * topk;
-    GgMoeArgs a{gt, ut, dt, x, ids, w, gq, uq, dq, grb, urb, drb, n, topk, H, I, E, h_act, dpart,
-                dispatch};
     // Rows per tile: about the rows an expert holds (decode: one or a few).
     const int tt = !dispatch || nk <= E ? 1 : nk <= 4 * E ? 4 : 8;
     unsigned tiles = (unsigned)nk;
@@ -561,14 +860,33 @@ int launch_gg_moe(uint32_t gt, uint32_t ut, uint32_t dt, const float* x, const i
         if (hipGetLastError() != hipSuccess) return -4;
         tiles = (unsigned)((nk + tt - 1) / tt + E);
     }
-    const int rc = tt == 1 ? gg_moe_phases<1>(gt, ut, dt, a, tiles, s)
-                 : tt == 4 ? gg_moe_phases<4>(gt, ut, dt, a, tiles, s)
-                           : gg_moe_phases<8>(gt, ut, dt, a, tiles, s);
+    const int rc = tt == 1 ? gg_moe_phases<1, I8>(gt, ut, dt, a, tiles, s)
+                 : tt == 4 ? gg_moe_phases<4, I8>(gt, ut, dt, a, tiles, s)
+                           : gg_moe_phases<8, I8>(gt, ut, dt, a, tiles, s);
     if (rc) return rc;
     const long total = (long)n * H;
     hipLaunchKernelGGL(gg_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                       dpart, w, n, topk, H, out);
+                       dpart, ids_w, n, topk, H, out);
     return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
+int launch_gg_moe(uint32_t gt, uint32_t ut, uint32_t dt, const float* x, const int* ids,
+                  const float* w, const uint8_t* gq, const uint8_t* uq, const uint8_t* dq, int n,
+                  int topk, int H, int I, int E, long grb, long urb, long drb, float* h_act,
+                  float* dpart, float* out, int* dispatch, hipStream_t s) {
+    GgMoeArgs a{gt, ut, dt, x, ids, w, gq, uq, dq, grb, urb, drb, n, topk, H, I, E, h_act, dpart,
+                dispatch, nullptr, nullptr, nullptr, nullptr};
+    return gg_moe<false>(a, out, dispatch, s);
+}
+
+int launch_gg_moe_i8(uint32_t gt, uint32_t ut, uint32_t dt, const int8_t* xq, const float* xs,
+                     const int* ids, const float* w, const uint8_t* gq, const uint8_t* uq,
+                     const uint8_t* dq, int n, int topk, int H, int I, int E, long grb, long urb,
+                     long drb, float* h_act, int8_t* hq, float* hs, float* dpart, float* out,
+                     int* dispatch, hipStream_t s) {
+    GgMoeArgs a{gt, ut, dt, nullptr, ids, w, gq, uq, dq, grb, urb, drb, n, topk, H, I, E, h_act,
+                dpart, dispatch, xq, xs, hq, hs};
+    return gg_moe<true>(a, out, dispatch, s);
 }
 
 }  // namespace glmmoe

@@ -120,5 +120,16 @@ int launch_gg_moe(uint32_t gt, uint32_t ut, uint32_t dt, const float* x, const i
                   const float* w, const uint8_t* gq, const uint8_t* uq, const uint8_t* dq, int n,
                   int topk, int H, int I, int E, long grb, long urb, long drb, float* h_act,
                   float* dpart, float* out, int* dispatch, hipStream_t s);
+// int8-activation twins (quantize_act_q8, gemm_q_i8, moe_expert_ffn_q_i8).
+bool gguf_has_i8(uint32_t type);
+int launch_gg_quant_q8(const float* x, long total, int8_t* xq, float* xs, hipStream_t s);
+int launch_gg_gemm_i8(uint32_t qtype, const int8_t* xq, const float* xs, const uint8_t* qw,
+                      const float* bias, float* y, int n, int in, int out, long row_bytes,
+                      hipStream_t s);
+int launch_gg_moe_i8(uint32_t gt, uint32_t ut, uint32_t dt, const int8_t* xq, const float* xs,
+                     const int* ids, const float* w, const uint8_t* gq, const uint8_t* uq,
+                     const uint8_t* dq, int n, int topk, int H, int I, int E, long grb, long urb,
+                     long drb, float* h_act, int8_t* hq, float* hs, float* dpart, float* out,
+                     int* dispatch, hipStream_t s);
 
 }  // namespace glmmoe

@@ -310,3 +310,44 @@ def ref_moe_expert_ffn_q(types, x, topk_ids, topk_w, gate_q, up_q, down_q, moe_i
         types[0], types[1], types[2], _p(x), _p(topk_ids), _p(topk_w), _p(gate_q), _p(up_q),
         _p(down_q), n, k, H, moe_inter, E, row_bytes[0], row_bytes[1], row_bytes[2], _p(h_act),
         _p(dpart), _p(out), _p(dispatch), None, _s(stream)), "ref_moe_expert_ffn_q")
+
+
+def ref_qtype_has_i8(qtype):
+    """qtype_has_i8 (cuda/kernels.cuh:74)."""
+    return bool(lib().glmmoe_ref_qtype_has_i8(qtype))
+
+
+def ref_quantize_act_q8(x, xq, xs, stream=None):
+    """quantize_act_q8 (cuda/kernels.cuh:77-78): x [n, in] fp32 -> xq int8, xs [n, in/32]."""
+    n, in_ = x.shape
+    _need(x, torch.float32, n * in_, "x")
+    _need(xq, torch.int8, n * in_, "xq")
+    _need(xs, torch.float32, n * in_ // 32, "xs")
+    check(lib().glmmoe_ref_quantize_act_q8(_p(x), n, in_, _p(xq), _p(xs), _s(stream)),
+          "ref_quantize_act_q8")
+
+
+def ref_gemm_q_i8(qtype, xq, xs, qweight, bias, y, row_bytes, stream=None):
+    """gemm_q_i8 (cuda/kernels.cuh:81-83)."""
+    n, in_ = xq.shape
+    out = y.shape[1]
+    _need(xq, torch.int8, n * in_, "xq")
+    _need(xs, torch.float32, n * in_ // 32, "xs")
+    _need(y, torch.float32, n * out, "y")
+    check(lib().glmmoe_ref_gemm_q_i8(qtype, _p(xq), _p(xs), _p(qweight), _p(bias), _p(y), n, in_,
+                                     out, row_bytes, _s(stream)), "ref_gemm_q_i8")
+
+
+def ref_moe_expert_ffn_q_i8(types, xq, xs, topk_ids, topk_w, gate_q, up_q, down_q, moe_inter, E,
+                            row_bytes, h_act, hq, hs, dpart, out, dispatch=None, stream=None):
+    """moe_expert_ffn_q_i8 (cuda/kernels.cuh:128-135). types / row_bytes: (gate, up, down)."""
+    n, H = xq.shape
+    k = topk_ids.shape[1]
+    _need(xq, torch.int8, n * H, "xq")
+    _need(hq, torch.int8, n * k * moe_inter, "hq")
+    _need(hs, torch.float32, n * k * moe_inter // 32, "hs")
+    check(lib().glmmoe_ref_moe_expert_ffn_q_i8(
+        types[0], types[1], types[2], _p(xq), _p(xs), _p(topk_ids), _p(topk_w), _p(gate_q),
+        _p(up_q), _p(down_q), n, k, H, moe_inter, E, row_bytes[0], row_bytes[1], row_bytes[2],
+        _p(h_act), _p(hq), _p(hs), _p(dpart), _p(out), _p(dispatch), None, _s(stream)),
+        "ref_moe_expert_ffn_q_i8")

@@ -365,6 +365,37 @@ int glmmoe_ref_moe_expert_ffn_q(uint32_t gate_type, uint32_t up_type, uint32_t d
                                 int64_t down_row_bytes, float* h_act, float* dpart, float* out,
                                 int* dispatch, float* gu_part, void* stream);
 
+/* int8-activation twins (cuda/kernels.cuh:68-83, 124-135; cuda/qgemm.cu:
+ * 104-303, 556-587, 775-779, 1656-1670).
+ * glmmoe_ref_qtype_has_i8 replaces qtype_has_i8: 1 for Q8_0, Q3_K, Q4_K,
+ * Q5_K, Q6_K, IQ3_XXS and IQ4_XS, 0 otherwise.
+ * glmmoe_ref_quantize_act_q8 replaces quantize_act_q8: xq [n, in] int8 and
+ * xs [n, in/32] fp32 with, per 32-element block, xs = absmax / 127 and
+ * xq = round-half-even(x * (1 / xs)) (0 for an all-zero block); in % 32 == 0.
+ * glmmoe_ref_gemm_q_i8 replaces gemm_q_i8: gemm_q with pre-quantized
+ * activations; each 8-weight fragment is an int8 dot,
+ * y += xs * (ds * dot(wq, xq) - dm * sum(xq)).
+ * glmmoe_ref_moe_expert_ffn_q_i8 replaces moe_expert_ffn_q_i8 argument for
+ * argument: moe_expert_ffn_q with x as (xq, xs); h_act (fp32) is quantized
+ * into hq [n*topk, moe_inter] and hs [n*topk, moe_inter/32] between the
+ * gate/up and down phases.
+ * Limits: as gemm_q / moe_expert_ffn_q, every type int8-capable, in / hidden /
+ * moe_inter multiples of 32, xq and hq 4-byte aligned (else GLMMOE_ERR_SHAPE). */
+int glmmoe_ref_qtype_has_i8(uint32_t qtype);
+int glmmoe_ref_quantize_act_q8(const float* x, int64_t n, int64_t in, int8_t* xq, float* xs,
+                               void* stream);
+int glmmoe_ref_gemm_q_i8(uint32_t qtype, const int8_t* xq, const float* xs, const uint8_t* qW,
+                         const float* bias, float* y, int64_t n, int64_t in, int64_t out,
+                         int64_t row_bytes, void* stream);
+int glmmoe_ref_moe_expert_ffn_q_i8(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
+                                   const int8_t* xq, const float* xs, const int* topk_ids,
+                                   const float* topk_w, const uint8_t* gate_q,
+                                   const uint8_t* up_q, const uint8_t* down_q, int n, int topk,
+                                   int hidden, int moe_inter, int E, int64_t gate_row_bytes,
+                                   int64_t up_row_bytes, int64_t down_row_bytes, float* h_act,
+                                   int8_t* hq, float* hs, float* dpart, float* out, int* dispatch,
+                                   float* gu_part, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

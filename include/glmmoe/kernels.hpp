@@ -154,6 +154,33 @@ inline int moe_expert_ffn_q(uint32_t gate_type, uint32_t up_type, uint32_t down_
                                        gu_part, s);
 }
 
+// cuda/kernels.cuh:74-83
+inline bool qtype_has_i8(uint32_t qtype) { return glmmoe_ref_qtype_has_i8(qtype) != 0; }
+inline int quantize_act_q8(const float* x, int64_t n, int64_t in, int8_t* xq, float* xs,
+                           void* s = nullptr) {
+    return glmmoe_ref_quantize_act_q8(x, n, in, xq, xs, s);
+}
+inline int gemm_q_i8(uint32_t qtype, const int8_t* xq, const float* xs, const uint8_t* qW,
+                     const float* bias, float* y, int64_t n, int64_t in, int64_t out,
+                     int64_t row_bytes, void* s = nullptr) {
+    return glmmoe_ref_gemm_q_i8(qtype, xq, xs, qW, bias, y, n, in, out, row_bytes, s);
+}
+
+// cuda/kernels.cuh:124-135
+inline int moe_expert_ffn_q_i8(uint32_t gate_type, uint32_t up_type, uint32_t down_type,
+                               const int8_t* xq, const float* xs, const int* topk_ids,
+                               const float* topk_w, const uint8_t* gate_q, const uint8_t* up_q,
+                               const uint8_t* down_q, int n, int topk, int hidden, int moe_inter,
+                               int E, int64_t gate_row_bytes, int64_t up_row_bytes,
+                               int64_t down_row_bytes, float* h_act, int8_t* hq, float* hs,
+                               float* dpart, float* out, int* dispatch = nullptr,
+                               float* gu_part = nullptr, void* s = nullptr) {
+    return glmmoe_ref_moe_expert_ffn_q_i8(gate_type, up_type, down_type, xq, xs, topk_ids, topk_w,
+                                          gate_q, up_q, down_q, n, topk, hidden, moe_inter, E,
+                                          gate_row_bytes, up_row_bytes, down_row_bytes, h_act, hq,
+                                          hs, dpart, out, dispatch, gu_part, s);
+}
+
 }  // namespace compat
 }  // namespace glmmoe
 

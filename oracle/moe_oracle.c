@@ -649,3 +649,123 @@ void orc_gguf_tables(const uint32_t** iq3xxs_grid, const int8_t** iq4nl_values) 
     *iq3xxs_grid = orc_iq3xxs_grid;
     *iq4nl_values = orc_iq4nl_values;
 }
+
+/* ---------------------------------------------------------------------------
+ * GGUF int8-activation path (cuda/qgemm.cu:104-303, 556-587).
+ * quantize_act_q8: per 32-element block, sx = absmax / 127 and
+ * q = round-to-nearest-even(v * (1 / sx)) (q = 0 for an all-zero block).
+ * A weight fragment of 8 elements is integers with one affine pair,
+ * weight[j] = ds * wq[j] - dm (dm != 0 only for Q4_K / Q5_K); the dot of a
+ * fragment with activations (xq, sx) is sx * (ds * sum(wq * xq) - dm * sum(xq)).
+ * ------------------------------------------------------------------------- */
+void orc_quant_act_q8(const float* x, int64_t n, int64_t in, int8_t* xq, float* xs) {
+    for (int64_t t = 0; t < n; ++t)
+        for (int64_t b = 0; b < in / 32; ++b) {
+            const float* v = x + t * in + 32 * b;
+            float amax = 0.0f;
+            for (int j = 0; j < 32; ++j) amax = fmaxf(amax, fabsf(v[j]));
+            const float sx = amax / 127.0f;
+            const float id = sx > 0.0f ? 1.0f / sx : 0.0f;
+            for (int j = 0; j < 32; ++j) xq[t * in + 32 * b + j] = (int8_t)lrintf(v[j] * id);
+            xs[t * (in / 32) + b] = sx;
+        }
+}
+
+int orc_gguf_frag_i8(uint32_t type, const uint8_t* row, int64_t k, int8_t* wq, float* ds,
+                     float* dm) {
+    const int64_t be = orc_gguf_block_elems(type), bb = orc_gguf_block_bytes(type);
+    if (!be || be == 1 || k % 8) return -1;
+    const uint8_t* b = row + (k / be) * bb;
+    const int p = (int)(k % be);
+    *dm = 0.0f;
+    switch (type) {
+        case 8:
+            *ds = orc_f16(b);
+            for (int j = 0; j < 8; ++j) wq[j] = (int8_t)b[2 + p + j];
+            return 0;
+        case 11: {
+            const int half = p / 128, r = p % 128, j = r / 32, sub = (r % 32) / 16, l = r % 16;
+            *ds = orc_f16(b + 108) * (float)(orc_q3k_scale(b + 96, 8 * half + 2 * j + sub) - 32);
+            for (int e = 0; e < 8; ++e) {
+                const int idx = 16 * sub + l + e;
+                const int v = (b[32 + 32 * half + idx] >> (2 * j)) & 3;
+                wq[e] = (int8_t)(v - ((b[idx] & (1 << (4 * half + j))) ? 0 : 4));
+            }
+            return 0;
+        }
+        case 12: case 13: {
+            const int c64 = p / 64, c = p % 64, l = c % 32, hi = c / 32;
+            int sc, mn;
+            orc_k4_scale_min(b + 4, 2 * c64 + hi, &sc, &mn);
+            *ds = orc_f16(b) * (float)sc;
+            *dm = orc_f16(b + 2) * (float)mn;
+            const uint8_t* q = b + (type == 12 ? 16 : 48);
+            for (int e = 0; e < 8; ++e) {
+                int v = (q[32 * c64 + l + e] >> (4 * hi)) & 15;
+                if (type == 13) v += (b[16 + l + e] & (1 << (2 * c64 + hi))) ? 16 : 0;
+                wq[e] = (int8_t)v;
+            }
+            return 0;
+        }
+        case 14: {
+            const int nn = p / 128, r = p % 128, quarter = r / 32, l = r % 32;
+            const uint8_t* ql = b + 64 * nn;
+            const uint8_t* qh = b + 128 + 32 * nn;
+            *ds = orc_f16(b + 208) * (float)((const int8_t*)(b + 192))[8 * nn + l / 16 + 2 * quarter];
+            for (int e = 0; e < 8; ++e) {
+                const int lo = (ql[l + e + 32 * (quarter & 1)] >> (4 * (quarter >> 1))) & 15;
+                wq[e] = (int8_t)((int)(lo | (((qh[l + e] >> (2 * quarter)) & 3) << 4)) - 32);
+            }
+            return 0;
+        }
+        case 18: {
+            const int ib = p / 32, l = (p % 32) / 8;
+            const uint8_t* w = b + 66 + 4 * ib;
+            const uint32_t aux = (uint32_t)w[0] | ((uint32_t)w[1] << 8) | ((uint32_t)w[2] << 16) |
+                                 ((uint32_t)w[3] << 24);
+            *ds = orc_f16(b) * (0.5f + (float)(aux >> 28)) * 0.5f;
+            const uint8_t signs = orc_iq2_signs((aux >> (7 * l)) & 127u);
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t g = orc_iq3xxs_grid[b[2 + 8 * ib + 2 * l + (e >> 2)]];
+                const int mag = (int)((g >> (8 * (e & 3))) & 255u);
+                wq[e] = (int8_t)((signs & (1u << e)) ? -mag : mag);
+            }
+            return 0;
+        }
+        case 23: {
+            const int ib = p / 32, c = p % 32;
+            const uint16_t sh = (uint16_t)(b[2] | (b[3] << 8));
+            const int lo = (b[4 + ib / 2] >> (4 * (ib & 1))) & 15;
+            const int hi = (sh >> (2 * ib)) & 3;
+            *ds = orc_f16(b) * (float)((int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32);
+            for (int e = 0; e < 8; ++e) {
+                const int cc = c + e;
+                wq[e] = orc_iq4nl_values[(b[8 + 16 * ib + (cc % 16)] >> (4 * (cc / 16))) & 15];
+            }
+            return 0;
+        }
+        default: return -1;
+    }
+}
+
+int orc_gemm_q_i8(uint32_t type, const int8_t* xq, const float* xs, const uint8_t* w, int64_t n,
+                  int64_t in, int64_t out, int64_t row_bytes, double* y) {
+    for (int64_t o = 0; o < out; ++o)
+        for (int64_t t = 0; t < n; ++t) {
+            double acc = 0.0;
+            for (int64_t k = 0; k < in; k += 8) {
+                int8_t wq[8];
+                float ds, dm;
+                if (orc_gguf_frag_i8(type, w + o * row_bytes, k, wq, &ds, &dm)) return -1;
+                int sumi = 0, sumx = 0;
+                for (int j = 0; j < 8; ++j) {
+                    sumi += (int)wq[j] * (int)xq[t * in + k + j];
+                    sumx += (int)xq[t * in + k + j];
+                }
+                acc += (double)xs[t * (in / 32) + k / 32] *
+                       ((double)ds * (double)sumi - (double)dm * (double)sumx);
+            }
+            y[t * out + o] = acc;
+        }
+    return 0;
+}

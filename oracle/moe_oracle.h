@@ -34,6 +34,10 @@
  *   orc_quant_act_e4m3       : vs torch's float8_e4m3fn conversion of x/scale,
  *                             scale = amax/448 closed form, |x - deq| bound.
  *   orc_dequant_e4m3_blocks  : closed form per element, block index mapping.
+ *   orc_quant_act_q8         : numpy float32 closed form (sx = amax / 127,
+ *                             RNE of v * (1 / sx)) and |x - sx * q| <= sx / 2.
+ *   orc_gguf_frag_i8         : ds * wq - dm equals orc_gguf_value for every
+ *                             element of random blocks of every int8 type.
  *   orc_gguf_*               : bit-exact vs the reference's gguf_dequantize_row
  *                             (oracle/_ref) on random blocks of every type,
  *                             codebooks byte-identical to the reference's,
@@ -107,6 +111,16 @@ int64_t orc_gguf_block_bytes(uint32_t type);
 float orc_gguf_value(uint32_t type, const uint8_t* block, int p);
 int orc_gguf_dequant_row(uint32_t type, const uint8_t* src, int64_t n, float* dst);
 void orc_gguf_tables(const uint32_t** iq3xxs_grid, const int8_t** iq4nl_values);
+
+
+/* GGUF int8-activation path (cuda/qgemm.cu:104-303, 556-587): the activation
+ * quantizer, the integer fragment form of 8 weights (weight = ds * wq - dm),
+ * and gemm_q_i8's products summed per fragment in fp64. */
+void orc_quant_act_q8(const float* x, int64_t n, int64_t in, int8_t* xq, float* xs);
+int orc_gguf_frag_i8(uint32_t type, const uint8_t* row, int64_t k, int8_t* wq, float* ds,
+                     float* dm);
+int orc_gemm_q_i8(uint32_t type, const int8_t* xq, const float* xs, const uint8_t* w, int64_t n,
+                  int64_t in, int64_t out, int64_t row_bytes, double* y);
 
 #ifdef __cplusplus
 }

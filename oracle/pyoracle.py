@@ -79,6 +79,14 @@ class Oracle:
         L.orc_gguf_dequant_row.argtypes = [C.c_uint32, _u8p, _i64, _f32p]
         L.orc_gguf_tables.argtypes = [C.POINTER(C.POINTER(C.c_uint32)),
                                       C.POINTER(C.POINTER(C.c_int8))]
+        _i8p = np.ctypeslib.ndpointer(np.int8, flags="C_CONTIGUOUS")
+        _f64p = np.ctypeslib.ndpointer(np.float64, flags="C_CONTIGUOUS")
+        L.orc_quant_act_q8.argtypes = [_f32p, _i64, _i64, _i8p, _f32p]
+        L.orc_gguf_frag_i8.restype = C.c_int
+        L.orc_gguf_frag_i8.argtypes = [C.c_uint32, _u8p, _i64, _i8p, C.POINTER(C.c_float),
+                                       C.POINTER(C.c_float)]
+        L.orc_gemm_q_i8.restype = C.c_int
+        L.orc_gemm_q_i8.argtypes = [C.c_uint32, _i8p, _f32p, _u8p, _i64, _i64, _i64, _i64, _f64p]
 
     # scalar helpers
     def expf(self, x):
@@ -177,6 +185,34 @@ class Oracle:
             if self.L.orc_gguf_dequant_row(qtype, data[r * rb:(r + 1) * rb], n, out[r]):
                 raise ValueError(f"orc_gguf_dequant_row: type {qtype}")
         return out
+
+    def quant_act_q8(self, x):
+        """x [n, in] fp32 -> (xq [n, in] int8, xs [n, in/32] fp32)."""
+        x = np.ascontiguousarray(x, np.float32)
+        n, i = x.shape
+        q = np.empty((n, i), np.int8)
+        s = np.empty((n, i // 32), np.float32)
+        self.L.orc_quant_act_q8(x, n, i, q, s)
+        return q, s
+
+    def gguf_frag_i8(self, qtype, row, k):
+        wq = np.empty(8, np.int8)
+        ds, dm = C.c_float(), C.c_float()
+        if self.L.orc_gguf_frag_i8(qtype, np.ascontiguousarray(row, np.uint8), k, wq,
+                                   C.byref(ds), C.byref(dm)):
+            raise ValueError(f"orc_gguf_frag_i8: type {qtype}")
+        return wq, ds.value, dm.value
+
+    def gemm_q_i8(self, qtype, xq, xs, w, out, row_bytes):
+        """gemm_q_i8's sums in fp64: y [n, out]."""
+        xq = np.ascontiguousarray(xq, np.int8)
+        n, i = xq.shape
+        y = np.empty((n, out), np.float64)
+        if self.L.orc_gemm_q_i8(qtype, xq, np.ascontiguousarray(xs, np.float32),
+                                np.ascontiguousarray(w, np.uint8).reshape(-1), n, i, out,
+                                row_bytes, y):
+            raise ValueError(f"orc_gemm_q_i8: type {qtype}")
+        return y
 
     def gguf_tables(self):
         g = C.POINTER(C.c_uint32)()

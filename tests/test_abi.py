@@ -93,6 +93,22 @@ def test_reference_signature_host_checks():
     assert L.glmmoe_ref_moe_expert_ffn_q(18, 18, 23, dummy, dummy, dummy, dummy, dummy, dummy,
                                          1, 8, 6144, 2048, 256, 2352, 2352, 1087, dummy, dummy,
                                          dummy, None, None, None) == -2
+    # int8 twins: int8-capable types only, rows a multiple of 32, 4-byte aligned int8 rows
+    assert [t for t in range(32) if L.glmmoe_ref_qtype_has_i8(t)] == [8, 11, 12, 13, 14, 18, 23]
+    assert L.glmmoe_ref_quantize_act_q8(dummy, 2, 48, dummy, dummy, None) == -2
+    assert L.glmmoe_ref_quantize_act_q8(None, 2, 64, dummy, dummy, None) == -1
+    assert L.glmmoe_ref_gemm_q_i8(1, dummy, dummy, dummy, None, dummy, 1, 256, 8, 512, None) == -2
+    assert L.glmmoe_ref_gemm_q_i8(8, C.c_void_p(18), dummy, dummy, None, dummy, 1, 256, 8, 272,
+                                  None) == -2
+    assert L.glmmoe_ref_gemm_q_i8(8, dummy, None, dummy, None, dummy, 1, 256, 8, 272, None) == -1
+    i8 = [18, 18, 23, dummy, dummy, dummy, dummy, dummy, dummy, dummy, 1, 8, 6144, 2048, 256,
+          2352, 2352, 1088, dummy, dummy, dummy, dummy, dummy, None, None, None]
+    bad = list(i8); bad[2] = 0                    # F32 down: no int8 form
+    assert L.glmmoe_ref_moe_expert_ffn_q_i8(*bad) == -2
+    bad = list(i8); bad[19] = None                # hq
+    assert L.glmmoe_ref_moe_expert_ffn_q_i8(*bad) == -1
+    bad = list(i8); bad[13] = 2040                # moe_inter % 32
+    assert L.glmmoe_ref_moe_expert_ffn_q_i8(*bad) == -2
 
 
 def _layer(H=6144, I=2048, E=256, k=8, shared=True):
@@ -158,6 +174,14 @@ def test_cpp_header_compiles_against_the_library(tmp_path):
         '  glmserve::cuda::gemm_q(18, x, q, nullptr, y, 1, 6144, 2048, 6144 / 256 * 98);\n'
         '  glmserve::cuda::moe_expert_ffn_q(18, 18, 23, x, ids, w, q, q, q, 1, 8, 6144, 2048, 256,\n'
         '                                   2352, 2352, 1088, hbuf, hbuf, y, disp);\n'
+        '  int8_t* xq = nullptr; float* xs = nullptr;\n'
+        '  if (glmserve::cuda::qtype_has_i8(18)) {\n'
+        '    glmserve::cuda::quantize_act_q8(x, 1, 6144, xq, xs);\n'
+        '    glmserve::cuda::gemm_q_i8(18, xq, xs, q, nullptr, y, 1, 6144, 2048, 2352);\n'
+        '    glmserve::cuda::moe_expert_ffn_q_i8(18, 18, 23, xq, xs, ids, w, q, q, q, 1, 8, 6144,\n'
+        '                                        2048, 256, 2352, 2352, 1088, hbuf, xq, xs, hbuf,\n'
+        '                                        y, disp);\n'
+        '  }\n'
         '  glmmoe_w4a16_layer L{};\n'
         '  return (int)glmserve::cuda::moe_layer_workspace_bytes(L, 1);\n'
         '}\n')

@@ -409,3 +409,37 @@ def test_gguf_known_answers(oracle):
     # F16 / F32 rows are the values themselves.
     v = np.array([0.5, -2.0, 65504.0, 6.1e-5], np.float16)
     assert np.array_equal(oracle.gguf_dequant_rows(1, v.view(np.uint8), 1, 4)[0], v.astype(np.float32))
+
+
+I8_TYPES = [8, 11, 12, 13, 14, 18, 23]
+
+
+@pytest.mark.parametrize("qtype", I8_TYPES)
+def test_gguf_int8_fragments_equal_the_decode(oracle, qtype):
+    # weight = ds * wq - dm (the integer form the int8 path dots) reproduces the
+    # block decode exactly, element by element.
+    rng = np.random.default_rng(500 + qtype)
+    n = 512
+    rows = random_gguf_rows(qtype, 3, n, rng)
+    W = oracle.gguf_dequant_rows(qtype, rows, 3, n)
+    for r in range(3):
+        for k in range(0, n, 8):
+            wq, ds, dm = oracle.gguf_frag_i8(qtype, rows[r], k)
+            w = np.float32(ds) * wq.astype(np.float32) - np.float32(dm)
+            assert np.array_equal(w, W[r, k:k + 8]), (r, k)
+
+
+def test_quant_act_q8_closed_form(oracle):
+    rng = np.random.default_rng(7)
+    x = (rng.standard_normal((5, 256)) * rng.uniform(0.01, 10, (5, 1))).astype(np.float32)
+    x[2, 32:64] = 0.0                                  # an all-zero block
+    q, s = oracle.quant_act_q8(x)
+    xb = x.reshape(5, 8, 32)
+    sx = (np.abs(xb).max(axis=2) / np.float32(127)).astype(np.float32)
+    assert np.array_equal(s, sx)
+    inv = np.where(sx > 0, np.float32(1) / np.where(sx > 0, sx, 1), 0).astype(np.float32)
+    want = np.rint((xb * inv[:, :, None]).astype(np.float32)).astype(np.int8).reshape(5, 256)
+    assert np.array_equal(q, want)
+    assert np.all(q[2, 32:64] == 0) and s[2, 1] == 0
+    err = np.abs(x.reshape(5, 8, 32) - s[:, :, None] * q.reshape(5, 8, 32).astype(np.float32))
+    assert np.all(err <= s[:, :, None] * 0.5 * (1 + 1e-5))
