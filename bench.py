@@ -192,7 +192,7 @@ def main():
         return
     gguf_state = {}
 
-    def measure_gguf(n, steps, warmup):
+    def measure_gguf(n, steps, warmup, i8=False):
         # The served checkpoint's expert formats (IQ3_XXS gate/up, IQ4_XS down) at the
         # configs[1] layer shape, through moe_expert_ffn_q's signature with the
         # expert-grouping scratch; routing from the synthetic layer's router.
@@ -219,6 +219,18 @@ def main():
         disp = torch.empty(3 * E + 1 + n * K, dtype=torch.int32, device="cuda")
         call = lambda: ops.ref_moe_expert_ffn_q((18, 18, 23), xf, ids, w, gq, uq, dq, I, E, rb,
                                                 h_act, dpart, out, disp)
+        if i8:
+            # int8 twin: quantize_act_q8 of x inside the timed call, then
+            # moe_expert_ffn_q_i8 (h_act requantized between its phases)
+            xq = torch.empty(n, H, dtype=torch.int8, device="cuda")
+            xs = torch.empty(n, H // 32, device="cuda")
+            hq = torch.empty(n * K, I, dtype=torch.int8, device="cuda")
+            hs = torch.empty(n * K, I // 32, device="cuda")
+
+            def call():
+                ops.ref_quantize_act_q8(xf, xq, xs)
+                ops.ref_moe_expert_ffn_q_i8((18, 18, 23), xq, xs, ids, w, gq, uq, dq, I, E, rb,
+                                            h_act, hq, hs, dpart, out, disp)
         for _ in range(warmup):
             call()
         torch.cuda.synchronize()
@@ -237,7 +249,8 @@ def main():
                 "hbm_frac_layer": alg / (ms * 1e-3) / HBM_PEAK,
                 "expert_bytes": per_expert,
                 "note": "routed experts only (the reference's moe_expert_ffn_q has no shared "
-                        "expert); fp32 activations and arithmetic as in the reference"}
+                        "expert); " + ("int8 activations, int32 fragment dots" if i8 else
+                                       "fp32 activations and arithmetic as in the reference")}
 
     def measure_fp8(n, steps, warmup):
         from moe_cases import SynthFp8Layer
@@ -363,6 +376,7 @@ def main():
         for n in (1, 64):
             log(f"bench: sweep GGUF decode B={n} (IQ3_XXS gate/up, IQ4_XS down)")
             sweep[f"gguf_decode_B{n}"] = measure_gguf(n, args.steps, args.warmup)
+            sweep[f"gguf_i8_decode_B{n}"] = measure_gguf(n, args.steps, args.warmup, i8=True)
         torch.cuda.empty_cache()
     if not args.no_sweep and not args.no_fp8:
         log("bench: sweep FP8 prefill 8192")
