@@ -66,8 +66,22 @@ __constant__ uint32_t c_iq3xxs_grid[256] = {
     0x3e042c14u, 0x3e0c1434u, 0x3e0c2404u, 0x3e140c14u, 0x3e14242cu, 0x3e142c14u, 0x3e1c0404u, 0x3e1c0c2cu,
     0x3e1c1c1cu, 0x3e1c3404u, 0x3e24140cu, 0x3e24240cu, 0x3e2c0404u, 0x3e2c0414u, 0x3e2c1424u, 0x3e341c04u,
 };
-__constant__ int8_t c_iq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
-                                   1,    13,   25,  38,  53,  69,  89,  113};
+constexpr int8_t kIq4nl[16] = {-127, -104, -83, -65, -49, -35, -22, -10,
+                               1,    13,   25,  38,  53,  69,  89,  113};
+constexpr uint32_t iq4nl_word(int i) {
+    return (uint32_t)(uint8_t)kIq4nl[4 * i] | ((uint32_t)(uint8_t)kIq4nl[4 * i + 1] << 8) |
+           ((uint32_t)(uint8_t)kIq4nl[4 * i + 2] << 16) | ((uint32_t)(uint8_t)kIq4nl[4 * i + 3] << 24);
+}
+
+// IQ4_NL values of four 4-bit codes (one per byte of `codes`), packed as int8:
+// two byte selects (v_perm_b32) from the table held in four constant words.
+__device__ __forceinline__ uint32_t gg_iq4nl4(uint32_t codes) {
+    const uint32_t sel = codes & 0x07070707u;
+    const uint32_t lo = __builtin_amdgcn_perm(iq4nl_word(1), iq4nl_word(0), sel);
+    const uint32_t hi = __builtin_amdgcn_perm(iq4nl_word(3), iq4nl_word(2), sel);
+    const uint32_t m = ((codes >> 3) & 0x01010101u) * 0xffu;
+    return (lo & ~m) | (hi & m);
+}
 
 __device__ __forceinline__ float gg_f16(const uint8_t* p) {
     const uint16_t h = (uint16_t)(p[0] | (p[1] << 8));
@@ -98,9 +112,23 @@ int gguf_block_bytes(uint32_t t) {
     }
 }
 
-// Elements k .. k + 7 (k % 8 == 0) of a row of GGUF type t.
+__device__ __forceinline__ uint32_t gg_ld32(const uint8_t* p) {
+    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+// The codes of IQ4_XS elements k .. k + 7 of a block (k % 8 == 0), one per byte.
+__device__ __forceinline__ void gg_iq4xs_codes(const uint8_t* b, int ib, int c, uint32_t& c0,
+                                               uint32_t& c1) {
+    const uint8_t* q = b + 8 + 16 * ib + (c % 16);
+    const int sh = 4 * (c / 16);
+    c0 = (gg_ld32(q) >> sh) & 0x0f0f0f0fu;
+    c1 = (gg_ld32(q + 4) >> sh) & 0x0f0f0f0fu;
+}
+
+// Elements k .. k + 7 (k % 8 == 0) of a row of GGUF type t; grid: the IQ3_XXS
+// codebook (constant memory or an LDS copy).
 __device__ __forceinline__ void gg_dec8_any(uint32_t t, const uint8_t* __restrict__ row, int k,
-                                            float (&y)[8]) {
+                                            const uint32_t* __restrict__ grid, float (&y)[8]) {
     switch (t) {
         case 0: {
             const float4* p = reinterpret_cast<const float4*>(row + 4 * (size_t)k);
@@ -187,8 +215,8 @@ __device__ __forceinline__ void gg_dec8_any(uint32_t t, const uint8_t* __restric
             const float db = gg_f16(b) * (0.5f + (float)(aux >> 28)) * 0.5f;
             const uint32_t i7 = (aux >> (7 * l)) & 127u;
             const uint32_t signs = i7 | ((uint32_t)(__builtin_popcount(i7) & 1) << 7);
-            const uint32_t g0 = c_iq3xxs_grid[b[2 + 8 * ib + 2 * l]];
-            const uint32_t g1 = c_iq3xxs_grid[b[2 + 8 * ib + 2 * l + 1]];
+            const uint32_t g0 = grid[b[2 + 8 * ib + 2 * l]];
+            const uint32_t g1 = grid[b[2 + 8 * ib + 2 * l + 1]];
 #pragma unroll
             for (int e = 0; e < 8; ++e) {
                 const float mag = (float)(((e < 4 ? g0 : g1) >> (8 * (e & 3))) & 255u);
@@ -203,12 +231,12 @@ __device__ __forceinline__ void gg_dec8_any(uint32_t t, const uint8_t* __restric
             const int lo = (b[4 + ib / 2] >> (4 * (ib & 1))) & 15;
             const int hi = (sh >> (2 * ib)) & 3;
             const float dl = gg_f16(b) * (float)((int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32);
+            uint32_t c0, c1;
+            gg_iq4xs_codes(b, ib, c, c0, c1);
+            const uint32_t v0 = gg_iq4nl4(c0), v1 = gg_iq4nl4(c1);
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int cc = c + e;
-                const int code = (b[8 + 16 * ib + (cc % 16)] >> (4 * (cc / 16))) & 15;
-                y[e] = dl * (float)c_iq4nl[code];
-            }
+            for (int e = 0; e < 8; ++e)
+                y[e] = dl * (float)(int8_t)(((e < 4 ? v0 : v1) >> (8 * (e & 3))) & 255u);
             return;
         }
         default:
@@ -222,8 +250,8 @@ __device__ __forceinline__ void gg_dec8_any(uint32_t t, const uint8_t* __restric
 constexpr uint32_t kGgAny = 0xffffffffu;
 template <uint32_t T>
 __device__ __forceinline__ void gg_dec8(uint32_t t, const uint8_t* __restrict__ row, int k,
-                                        float (&y)[8]) {
-    gg_dec8_any(T == kGgAny ? t : T, row, k, y);
+                                        const uint32_t* __restrict__ grid, float (&y)[8]) {
+    gg_dec8_any(T == kGgAny ? t : T, row, k, grid, y);
 }
 
 constexpr int kGgRows = 16;   // weight rows per workgroup (4 per wave)
@@ -292,7 +320,7 @@ __device__ __forceinline__ void gg_dots(float (*xs)[kGgKC], int* srcs, const flo
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 float w[8];
-                gg_dec8<T>(type[m], wrow[m][r], k0 + kk, w);
+                gg_dec8<T>(type[m], wrow[m][r], k0 + kk, c_iq3xxs_grid, w);
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
 #pragma unroll
@@ -310,20 +338,43 @@ __device__ __forceinline__ int gg_pk4(int a, int b, int c, int d) {
     return (a & 255) | ((b & 255) << 8) | ((c & 255) << 16) | (int)((unsigned)d << 24);
 }
 
-__device__ __forceinline__ uint32_t gg_ld32(const uint8_t* p) {
-    return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+
+// A2: every 2- and 4-byte field is read as 16-bit halves (the caller's rows
+// are 2-byte aligned, as in the LDS copies; block sizes are even); otherwise
+// byte by byte.
+template <bool A2>
+__device__ __forceinline__ uint32_t gg_rd32(const uint8_t* p) {
+    if constexpr (A2) {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(p);
+        return (uint32_t)h[0] | ((uint32_t)h[1] << 16);
+    } else {
+        return gg_ld32(p);
+    }
+}
+template <bool A2>
+__device__ __forceinline__ float gg_rdf16(const uint8_t* p) {
+    if constexpr (A2)
+        return (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(p));
+    else
+        return gg_f16(p);
 }
 
+// Byte i of the result is 0xff where bit i of s (i < 4) is set.
+__device__ __forceinline__ uint32_t gg_bytemask4(uint32_t s) {
+    return (((s & 15u) * 0x00204081u) & 0x01010101u) * 0xffu;
+}
+
+template <bool A2>
 __device__ __forceinline__ void gg_dec8i_any(uint32_t t, const uint8_t* __restrict__ row, int k,
-                                             int& w0, int& w1, float& ds, float& dm) {
-    int v[8];
+                                             const uint32_t* __restrict__ grid, int& w0, int& w1,
+                                             float& ds, float& dm) {
     dm = 0.0f;
     switch (t) {
         case 8: {
             const uint8_t* b = row + (size_t)(k / 32) * 34;
-            ds = gg_f16(b);
-            w0 = (int)gg_ld32(b + 2 + k % 32);
-            w1 = (int)gg_ld32(b + 6 + k % 32);
+            ds = gg_rdf16<A2>(b);
+            w0 = (int)gg_rd32<A2>(b + 2 + k % 32);
+            w1 = (int)gg_rd32<A2>(b + 6 + k % 32);
             return;
         }
         case 11: {
@@ -332,14 +383,17 @@ __device__ __forceinline__ void gg_dec8i_any(uint32_t t, const uint8_t* __restri
             const int l0 = r % 16, i = 8 * half + 2 * j + sub;
             const int lo = (b[96 + i % 8] >> (4 * (i / 8))) & 15;
             const int hi = (b[104 + i % 4] >> (2 * (i / 4))) & 3;
-            ds = gg_f16(b + 108) * (float)((int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32);
-            const int hm = 1 << (4 * half + j);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int idx = 16 * sub + l0 + e;
-                v[e] = ((b[32 + 32 * half + idx] >> (2 * j)) & 3) - ((b[idx] & hm) ? 0 : 4);
-            }
-            break;
+            ds = gg_rdf16<A2>(b + 108) * (float)((int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32);
+            const int idx = 16 * sub + l0, hb = 4 * half + j;
+            // q - (hmask bit ? 0 : 4) per byte, q in 0..3: biased by 0x80 so no
+            // byte borrows from its neighbour
+            const uint32_t q0 = (gg_rd32<A2>(b + 32 + 32 * half + idx) >> (2 * j)) & 0x03030303u;
+            const uint32_t q1 = (gg_rd32<A2>(b + 36 + 32 * half + idx) >> (2 * j)) & 0x03030303u;
+            const uint32_t m0 = ((gg_rd32<A2>(b + idx) >> hb) & 0x01010101u) ^ 0x01010101u;
+            const uint32_t m1 = ((gg_rd32<A2>(b + idx + 4) >> hb) & 0x01010101u) ^ 0x01010101u;
+            w0 = (int)(((q0 | 0x80808080u) - (m0 << 2)) ^ 0x80808080u);
+            w1 = (int)(((q1 | 0x80808080u) - (m1 << 2)) ^ 0x80808080u);
+            return;
         }
         case 12:
         case 13: {
@@ -356,14 +410,14 @@ __device__ __forceinline__ void gg_dec8i_any(uint32_t t, const uint8_t* __restri
                 sc = (s[js + 4] & 15) | ((s[js - 4] >> 6) << 4);
                 mn = (s[js + 4] >> 4) | ((s[js] >> 6) << 4);
             }
-            ds = gg_f16(b) * (float)sc;
-            dm = gg_f16(b + 2) * (float)mn;
+            ds = gg_rdf16<A2>(b) * (float)sc;
+            dm = gg_rdf16<A2>(b + 2) * (float)mn;
             const uint8_t* q = b + (t == 12 ? 16 : 48) + 32 * c64 + l0;
-            uint32_t a0 = (gg_ld32(q) >> (4 * hi)) & 0x0f0f0f0fu;
-            uint32_t a1 = (gg_ld32(q + 4) >> (4 * hi)) & 0x0f0f0f0fu;
+            uint32_t a0 = (gg_rd32<A2>(q) >> (4 * hi)) & 0x0f0f0f0fu;
+            uint32_t a1 = (gg_rd32<A2>(q + 4) >> (4 * hi)) & 0x0f0f0f0fu;
             if (t == 13) {
-                a0 |= ((gg_ld32(b + 16 + l0) >> js) & 0x01010101u) << 4;
-                a1 |= ((gg_ld32(b + 20 + l0) >> js) & 0x01010101u) << 4;
+                a0 |= ((gg_rd32<A2>(b + 16 + l0) >> js) & 0x01010101u) << 4;
+                a1 |= ((gg_rd32<A2>(b + 20 + l0) >> js) & 0x01010101u) << 4;
             }
             w0 = (int)a0;
             w1 = (int)a1;
@@ -374,12 +428,14 @@ __device__ __forceinline__ void gg_dec8i_any(uint32_t t, const uint8_t* __restri
             const int p = k % 256, nn = p / 128, r = p % 128, quarter = r / 32, l0 = r % 32;
             const uint8_t* ql = b + 64 * nn + 32 * (quarter & 1) + l0;
             const uint8_t* qh = b + 128 + 32 * nn + l0;
-            ds = gg_f16(b + 208) * (float)(int8_t)b[192 + 8 * nn + l0 / 16 + 2 * quarter];
+            ds = gg_rdf16<A2>(b + 208) * (float)(int8_t)b[192 + 8 * nn + l0 / 16 + 2 * quarter];
             const int sl = 4 * (quarter >> 1), sh = 2 * quarter;
             // q6 - 32 per byte: (lo | hi << 4) in 0..63, minus 32 by a bytewise
             // subtract with no borrow across bytes (each byte >= 0, result -32..31).
-            const uint32_t u0 = ((gg_ld32(ql) >> sl) & 0x0f0f0f0fu) | (((gg_ld32(qh) >> sh) & 0x03030303u) << 4);
-            const uint32_t u1 = ((gg_ld32(ql + 4) >> sl) & 0x0f0f0f0fu) | (((gg_ld32(qh + 4) >> sh) & 0x03030303u) << 4);
+            const uint32_t u0 = ((gg_rd32<A2>(ql) >> sl) & 0x0f0f0f0fu) |
+                                (((gg_rd32<A2>(qh) >> sh) & 0x03030303u) << 4);
+            const uint32_t u1 = ((gg_rd32<A2>(ql + 4) >> sl) & 0x0f0f0f0fu) |
+                                (((gg_rd32<A2>(qh + 4) >> sh) & 0x03030303u) << 4);
             w0 = (int)((u0 | 0x80808080u) - 0x20202020u) ^ (int)0x80808080u;
             w1 = (int)((u1 | 0x80808080u) - 0x20202020u) ^ (int)0x80808080u;
             return;
@@ -387,46 +443,45 @@ __device__ __forceinline__ void gg_dec8i_any(uint32_t t, const uint8_t* __restri
         case 18: {
             const uint8_t* b = row + (size_t)(k / 256) * 98;
             const int p = k % 256, ib = p / 32, l = (p % 32) / 8;
-            const uint32_t aux = gg_ld32(b + 66 + 4 * ib);
-            ds = gg_f16(b) * (0.5f + (float)(aux >> 28)) * 0.5f;
+            const uint32_t aux = gg_rd32<A2>(b + 66 + 4 * ib);
+            ds = gg_rdf16<A2>(b) * (0.5f + (float)(aux >> 28)) * 0.5f;
             const uint32_t i7 = (aux >> (7 * l)) & 127u;
             const uint32_t signs = i7 | ((uint32_t)(__builtin_popcount(i7) & 1) << 7);
-            const uint32_t g0 = c_iq3xxs_grid[b[2 + 8 * ib + 2 * l]];
-            const uint32_t g1 = c_iq3xxs_grid[b[2 + 8 * ib + 2 * l + 1]];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int mag = (int)(((e < 4 ? g0 : g1) >> (8 * (e & 3))) & 255u);
-                v[e] = (signs & (1u << e)) ? -mag : mag;
-            }
-            break;
+            const uint32_t qs = A2 ? *reinterpret_cast<const uint16_t*>(b + 2 + 8 * ib + 2 * l)
+                                   : (uint32_t)(b[2 + 8 * ib + 2 * l] | (b[3 + 8 * ib + 2 * l] << 8));
+            const uint32_t g0 = grid[qs & 255u], g1 = grid[qs >> 8];
+            // negate the flagged bytes: (g ^ 0xff) + 1 per byte, with no carry
+            // out of a byte since every grid magnitude is at least 4
+            const uint32_t n0 = gg_bytemask4(signs), n1 = gg_bytemask4(signs >> 4);
+            w0 = (int)((g0 ^ n0) + (n0 & 0x01010101u));
+            w1 = (int)((g1 ^ n1) + (n1 & 0x01010101u));
+            return;
         }
         case 23: {
             const uint8_t* b = row + (size_t)(k / 256) * 136;
             const int p = k % 256, ib = p / 32, c = p % 32;
-            const int sh = b[2] | (b[3] << 8);
+            const int sh = A2 ? *reinterpret_cast<const uint16_t*>(b + 2) : (b[2] | (b[3] << 8));
             const int lo = (b[4 + ib / 2] >> (4 * (ib & 1))) & 15;
             const int hi = (sh >> (2 * ib)) & 3;
-            ds = gg_f16(b) * (float)((int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const int cc = c + e;
-                v[e] = c_iq4nl[(b[8 + 16 * ib + (cc % 16)] >> (4 * (cc / 16))) & 15];
-            }
-            break;
+            ds = gg_rdf16<A2>(b) * (float)((int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32);
+            const uint8_t* q = b + 8 + 16 * ib + (c % 16);
+            const int shq = 4 * (c / 16);
+            w0 = (int)gg_iq4nl4((gg_rd32<A2>(q) >> shq) & 0x0f0f0f0fu);
+            w1 = (int)gg_iq4nl4((gg_rd32<A2>(q + 4) >> shq) & 0x0f0f0f0fu);
+            return;
         }
         default:
             ds = 0.0f;
             w0 = w1 = 0;
             return;
     }
-    w0 = gg_pk4(v[0], v[1], v[2], v[3]);
-    w1 = gg_pk4(v[4], v[5], v[6], v[7]);
 }
 
-template <uint32_t T>
+template <uint32_t T, bool A2 = false>
 __device__ __forceinline__ void gg_dec8i(uint32_t t, const uint8_t* __restrict__ row, int k,
-                                         int& w0, int& w1, float& ds, float& dm) {
-    gg_dec8i_any(T == kGgAny ? t : T, row, k, w0, w1, ds, dm);
+                                         const uint32_t* __restrict__ grid, int& w0, int& w1,
+                                         float& ds, float& dm) {
+    gg_dec8i_any<A2>(T == kGgAny ? t : T, row, k, grid, w0, w1, ds, dm);
 }
 
 // LDS tile of int8 activations: TT rows x kGgKC bytes and their per-32 scales.
@@ -490,7 +545,7 @@ __device__ __forceinline__ void gg_dots_i8(GgI8Tile<TT>& xt, int* srcs, const in
             for (int r = 0; r < 4; ++r) {
                 int w0, w1;
                 float ds, dm;
-                gg_dec8i<T>(type[m], wrow[m][r], k0 + kk, w0, w1, ds, dm);
+                gg_dec8i<T>(type[m], wrow[m][r], k0 + kk, c_iq3xxs_grid, w0, w1, ds, dm);
 #pragma unroll
                 for (int t = 0; t < TT; ++t) {
                     const int si = __builtin_amdgcn_sdot4(w1, x1[t], __builtin_amdgcn_sdot4(w0, x0[t], 0, false), false);
@@ -499,6 +554,223 @@ __device__ __forceinline__ void gg_dots_i8(GgI8Tile<TT>& xt, int* srcs, const in
                     acc[m][r][t] = __builtin_fmaf(sx[t], v, acc[m][r][t]);
                 }
             }
+    }
+}
+
+// Diagnostic builds only: 1 skips the decode, 2 the weight loads after the first chunk.
+#ifndef GLMMOE_GG_DIAG
+#define GLMMOE_GG_DIAG 0
+#endif
+
+// ---- Streamed weights (the block types, one type per matrix set). Each wave
+// owns 4 weight rows per matrix; per K chunk it loads those rows' block bytes
+// with coalesced dword loads (lane l: dwords l, l + 64, ...) one chunk ahead
+// into registers, parks them in a private LDS buffer and decodes from there,
+// so every weight byte is one wide load and a chunk is in flight while the
+// previous one is decoded. The tile's activations are staged the same way
+// (shared by the four waves, one barrier per chunk).
+constexpr int gg_be(uint32_t t) { return t == 8 ? 32 : 256; }
+constexpr int gg_bb(uint32_t t) {
+    return t == 8 ? 34 : t == 11 ? 110 : t == 12 ? 144 : t == 13 ? 176 : t == 14 ? 210
+         : t == 18 ? 98 : t == 23 ? 136 : 0;
+}
+// K per chunk: at most 3 dwords per lane per row, and 512 for 8-row tiles (LDS).
+// Lane l always takes K elements 512 f + 8 l of each 512, so the sums do not
+// depend on the chunk size.
+constexpr int gg_kc(uint32_t t, int tt) { return (t == 8 || t == 14 || tt > 1) ? 512 : 1024; }
+constexpr bool gg_streamed(uint32_t t) { return gg_bb(t) != 0; }
+
+template <uint32_t T, int NM, int TT, bool I8>
+struct GgStream {
+    static constexpr int KC = gg_kc(T, TT);
+    static constexpr int CB = KC / gg_be(T) * gg_bb(T);   // bytes of a row's chunk
+    static constexpr int ND = CB / 4;
+    static constexpr int LPR = (ND + 63) / 64;            // dword loads per lane per row
+    static constexpr int XV = I8 ? TT * KC / 4 : TT * KC / 4;   // int / float4 items of x
+    static constexpr int XR = (XV + 255) / 256;           // per thread
+    static constexpr int SR = TT * KC / 32;               // scales (I8)
+    uint32_t w[2][4][NM * 4][ND];
+    uint32_t grid[T == 18 ? 256 : 1];   // the IQ3_XXS codebook
+    float x[I8 ? 1 : 2][I8 ? 1 : TT][I8 ? 4 : KC];
+    struct {
+        int q[I8 ? 2 : 1][I8 ? TT : 1][I8 ? KC / 4 : 1];
+        float s[I8 ? 2 : 1][I8 ? TT : 1][I8 ? KC / 32 : 1];
+    } i8;
+};
+
+template <uint32_t T, int NM, int TT, bool I8>
+__device__ __forceinline__ void gg_dots_stream(GgStream<T, NM, TT, I8>& L, int* srcs,
+                                               const float* __restrict__ x,
+                                               const int8_t* __restrict__ xq,
+                                               const float* __restrict__ xsc, int K,
+                                               const GgTile<TT>& tl,
+                                               const uint8_t* const (&wrow)[NM][4],
+                                               float (&acc)[NM][4][TT]) {
+    using S = GgStream<T, NM, TT, I8>;
+    constexpr int KC = S::KC, ND = S::ND, LPR = S::LPR, XR = S::XR;
+    const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int tid = threadIdx.x;
+    __syncthreads();   // srcs and the buffers of a previous tile are consumed
+    if (tid == 0) {
+#pragma unroll
+        for (int t = 0; t < TT; ++t) srcs[t] = tl.src[t];
+    }
+    if constexpr (T == 18) L.grid[tid] = c_iq3xxs_grid[tid];
+#pragma unroll
+    for (int m = 0; m < NM; ++m)
+#pragma unroll
+        for (int r = 0; r < 4; ++r)
+#pragma unroll
+            for (int t = 0; t < TT; ++t) acc[m][r][t] = 0.0f;
+    __syncthreads();
+    const int nch = (K + KC - 1) / KC;
+    const int rowb = K / gg_be(T) * gg_bb(T);   // block bytes of a whole row
+    uint32_t wr[NM * 4][LPR];
+    float4 xr[XR];
+    int qr[XR];
+    float sr = 0.0f;
+    auto load = [&](int c) {
+        const int k0 = c * KC, kc = min(KC, K - k0);
+        const int nd = min(ND, (rowb - c * S::CB) / 4);
+#pragma unroll
+        for (int i = 0; i < NM * 4; ++i)
+#pragma unroll
+            for (int j = 0; j < LPR; ++j) {
+                const int d = j * 64 + lane;
+                if (d < nd)
+                    wr[i][j] = *reinterpret_cast<const uint32_t*>(wrow[i / 4][i % 4] +
+                                                                  (size_t)c * S::CB + 4 * d);
+            }
+#pragma unroll
+        for (int j = 0; j < XR; ++j) {
+            const int v = tid + 256 * j;
+            const int t = v / (KC / 4), c4 = v % (KC / 4);
+            if (v < S::XV && t < tl.nr && 4 * c4 < kc) {
+                if constexpr (I8)
+                    qr[j] = *reinterpret_cast<const int*>(xq + (size_t)srcs[t] * K + k0 + 4 * c4);
+                else
+                    xr[j] = *reinterpret_cast<const float4*>(x + (size_t)srcs[t] * K + k0 + 4 * c4);
+            }
+        }
+        if constexpr (I8) {
+            if (tid < S::SR) {
+                const int t = tid / (KC / 32), c32 = tid % (KC / 32);
+                sr = (t < tl.nr && 32 * c32 < kc)
+                         ? xsc[(size_t)srcs[t] * (K / 32) + k0 / 32 + c32] : 0.0f;
+            }
+        }
+    };
+    auto park = [&](int b, int c) {
+        const int k0 = c * KC, kc = min(KC, K - k0);
+        const int nd = min(ND, (rowb - c * S::CB) / 4);
+#pragma unroll
+        for (int i = 0; i < NM * 4; ++i)
+#pragma unroll
+            for (int j = 0; j < LPR; ++j) {
+                const int d = j * 64 + lane;
+                if (d < nd) L.w[b][wave][i][d] = wr[i][j];
+            }
+#pragma unroll
+        for (int j = 0; j < XR; ++j) {
+            const int v = tid + 256 * j;
+            const int t = v / (KC / 4), c4 = v % (KC / 4);
+            if (v < S::XV) {
+                const bool ok = t < tl.nr && 4 * c4 < kc;
+                if constexpr (I8)
+                    L.i8.q[b][t][c4] = ok ? qr[j] : 0;
+                else
+                    *reinterpret_cast<float4*>(&L.x[b][t][4 * c4]) =
+                        ok ? xr[j] : make_float4(0.f, 0.f, 0.f, 0.f);
+            }
+        }
+        if constexpr (I8) {
+            if (tid < S::SR) L.i8.s[b][tid / (KC / 32)][tid % (KC / 32)] = sr;
+        }
+    };
+    load(0);
+    park(0, 0);
+    __syncthreads();
+    for (int c = 0; c < nch; ++c) {
+        const int b = c & 1;
+#if GLMMOE_GG_DIAG != 2
+        if (c + 1 < nch) load(c + 1);
+#endif
+        const int kc = min(KC, K - c * KC);
+#pragma unroll
+        for (int f = 0; f < KC / 512; ++f) {
+            const int kk = f * 512 + lane * 8;
+            if (kk < kc && GLMMOE_GG_DIAG != 1) {
+                if constexpr (I8) {
+                    int x0[TT], x1[TT], sx1[TT];
+                    float sx[TT];
+#pragma unroll
+                    for (int t = 0; t < TT; ++t) {
+                        const int2 q = *reinterpret_cast<const int2*>(&L.i8.q[b][t][kk / 4]);
+                        x0[t] = q.x;
+                        x1[t] = q.y;
+                        sx[t] = L.i8.s[b][t][kk / 32];
+                        sx1[t] = __builtin_amdgcn_sdot4(
+                            0x01010101, q.y, __builtin_amdgcn_sdot4(0x01010101, q.x, 0, false),
+                            false);
+                    }
+#pragma unroll
+                    for (int i = 0; i < NM * 4; ++i) {
+                        int w0, w1;
+                        float ds, dm;
+                        gg_dec8i<T, true>(T, reinterpret_cast<const uint8_t*>(L.w[b][wave][i]),
+                                          kk, L.grid, w0, w1, ds, dm);
+#pragma unroll
+                        for (int t = 0; t < TT; ++t) {
+                            const int si = __builtin_amdgcn_sdot4(
+                                w1, x1[t], __builtin_amdgcn_sdot4(w0, x0[t], 0, false), false);
+                            float v = ds * (float)si;
+                            if (T == 12 || T == 13) v = v - dm * (float)sx1[t];
+                            acc[i / 4][i % 4][t] = __builtin_fmaf(sx[t], v, acc[i / 4][i % 4][t]);
+                        }
+                    }
+                } else {
+                    // The integer fragment (weight = ds * wq - dm, the reference's
+                    // dequantized value exactly), then
+                    // acc += ds * sum(wq * x) - dm * sum(x).
+                    float xv[TT][8], sx[TT];
+#pragma unroll
+                    for (int t = 0; t < TT; ++t) {
+                        const float4 a = *reinterpret_cast<const float4*>(&L.x[b][t][kk]);
+                        const float4 e = *reinterpret_cast<const float4*>(&L.x[b][t][kk + 4]);
+                        xv[t][0] = a.x; xv[t][1] = a.y; xv[t][2] = a.z; xv[t][3] = a.w;
+                        xv[t][4] = e.x; xv[t][5] = e.y; xv[t][6] = e.z; xv[t][7] = e.w;
+                        if (T == 12 || T == 13) {
+                            float v = xv[t][0];
+#pragma unroll
+                            for (int j = 1; j < 8; ++j) v = v + xv[t][j];
+                            sx[t] = v;
+                        }
+                    }
+#pragma unroll
+                    for (int i = 0; i < NM * 4; ++i) {
+                        int w0, w1;
+                        float ds, dm;
+                        gg_dec8i<T, true>(T, reinterpret_cast<const uint8_t*>(L.w[b][wave][i]),
+                                          kk, L.grid, w0, w1, ds, dm);
+                        float wf[8];
+#pragma unroll
+                        for (int j = 0; j < 8; ++j)
+                            wf[j] = (float)(int8_t)((uint32_t)(j < 4 ? w0 : w1) >> (8 * (j & 3)));
+#pragma unroll
+                        for (int t = 0; t < TT; ++t) {
+                            float v = wf[0] * xv[t][0];
+#pragma unroll
+                            for (int j = 1; j < 8; ++j) v = __builtin_fmaf(wf[j], xv[t][j], v);
+                            float& ac = acc[i / 4][i % 4][t];
+                            ac = __builtin_fmaf(ds, v, ac);
+                            if (T == 12 || T == 13) ac = __builtin_fmaf(-dm, sx[t], ac);
+                        }
+                    }
+                }
+            }
+        }
+        if (c + 1 < nch) park(b ^ 1, c + 1);
+        __syncthreads();
     }
 }
 
@@ -535,7 +807,8 @@ __global__ __launch_bounds__(256) void gg_gemv_kernel(uint32_t qtype, const floa
                                                       const float* __restrict__ bias,
                                                       float* __restrict__ y, int n, int in, int out,
                                                       long row_bytes) {
-    __shared__ __align__(16) char lds[gg_lds_bytes<TT, I8>()];
+    constexpr bool ST = gg_streamed(T);
+    __shared__ __align__(16) char lds[ST ? sizeof(GgStream<T, 1, TT, I8>) : gg_lds_bytes<TT, I8>()];
     __shared__ int srcs[TT];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int o0 = blockIdx.x * kGgRows + wave * 4;
@@ -550,7 +823,10 @@ __global__ __launch_bounds__(256) void gg_gemv_kernel(uint32_t qtype, const floa
 #pragma unroll
         for (int t = 0; t < TT; ++t) tl.row[t] = tl.src[t] = min(t0 + t, n - 1);
         float acc[1][4][TT];
-        if constexpr (I8)
+        if constexpr (ST)
+            gg_dots_stream<T, 1, TT, I8>(*reinterpret_cast<GgStream<T, 1, TT, I8>*>(lds), srcs, x,
+                                         xq, xsc, in, tl, wrow, acc);
+        else if constexpr (I8)
             gg_dots_i8<T, 1, TT>(*reinterpret_cast<GgI8Tile<TT>*>(lds), srcs, xq, xsc, in, tl, type,
                                  wrow, acc);
         else
@@ -629,7 +905,9 @@ struct GgMoeArgs {
 // T: the weight type (gate and up share it in phase 1), or kGgAny.
 template <bool DOWN, uint32_t T, int TT, bool I8>
 __global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
-    __shared__ __align__(16) char lds[gg_lds_bytes<TT, I8>()];
+    constexpr bool ST = gg_streamed(T);
+    __shared__ __align__(16) char lds[ST ? sizeof(GgStream<T, DOWN ? 1 : 2, TT, I8>)
+                                         : gg_lds_bytes<TT, I8>()];
     __shared__ int srcs[TT];
     const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int nk = a.n * a.topk;
@@ -648,7 +926,10 @@ __global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
             wrow[1][r] = a.up_q + (e * a.I + o) * a.up_rb;
         }
         float acc[2][4][TT];
-        if constexpr (I8)
+        if constexpr (ST)
+            gg_dots_stream<T, 2, TT, I8>(*reinterpret_cast<GgStream<T, 2, TT, I8>*>(lds), srcs, a.x,
+                                         a.xq, a.xs, a.H, tl, wrow, acc);
+        else if constexpr (I8)
             gg_dots_i8<T, 2, TT>(*reinterpret_cast<GgI8Tile<TT>*>(lds), srcs, a.xq, a.xs, a.H, tl,
                                  type, wrow, acc);
         else
@@ -673,7 +954,10 @@ __global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
             wrow[0][r] = a.down_q + (e * a.H + o) * a.down_rb;
         }
         float acc[1][4][TT];
-        if constexpr (I8)
+        if constexpr (ST)
+            gg_dots_stream<T, 1, TT, I8>(*reinterpret_cast<GgStream<T, 1, TT, I8>*>(lds), srcs,
+                                         a.h_act, a.hq, a.hs, a.I, tl, wrow, acc);
+        else if constexpr (I8)
             gg_dots_i8<T, 1, TT>(*reinterpret_cast<GgI8Tile<TT>*>(lds), srcs, a.hq, a.hs, a.I, tl,
                                  type, wrow, acc);
         else
@@ -720,17 +1004,46 @@ __global__ __launch_bounds__(1024) void gg_group_kernel(const int* __restrict__ 
         if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
     }
     __syncthreads();
-    if (threadIdx.x == 0) {
-        int o = 0, t = 0;
-        for (int e = 0; e < E; ++e) {
-            off[e] = o;
-            tp[e] = t;
-            cur[e] = o;
-            o += cnt[e];
-            t += (cnt[e] + tile_rows - 1) / tile_rows;
+    // Exclusive prefix sums of rows and tiles over the experts: thread i owns
+    // experts [i * per, (i + 1) * per); a shuffle scan per wave, then the 16
+    // wave totals.
+    __shared__ int wsum[2][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int per = (E + 1023) / 1024, e0 = min(E, tid * per), e1 = min(E, e0 + per);
+    int o = 0, t = 0;
+    for (int e = e0; e < e1; ++e) {
+        o += cnt[e];
+        t += (cnt[e] + tile_rows - 1) / tile_rows;
+    }
+    int so = o, st = t;
+#pragma unroll
+    for (int m = 1; m < 64; m <<= 1) {
+        const int a = __shfl_up(so, m), b = __shfl_up(st, m);
+        if (lane >= m) {
+            so += a;
+            st += b;
         }
-        off[E] = o;
-        tp[E] = t;
+    }
+    if (lane == 63) {
+        wsum[0][wave] = so;
+        wsum[1][wave] = st;
+    }
+    __syncthreads();
+    int bo = so - o, bt = st - t;
+    for (int w = 0; w < wave; ++w) {
+        bo += wsum[0][w];
+        bt += wsum[1][w];
+    }
+    for (int e = e0; e < e1; ++e) {
+        off[e] = bo;
+        tp[e] = bt;
+        cur[e] = bo;
+        bo += cnt[e];
+        bt += (cnt[e] + tile_rows - 1) / tile_rows;
+    }
+    if (tid == 1023) {
+        off[E] = bo;
+        tp[E] = bt;
     }
     __syncthreads();
     for (int i = threadIdx.x; i < nk; i += blockDim.x) {
@@ -783,12 +1096,21 @@ static void gg_by_type_t(uint32_t t, F&& f) {
     else gg_by_type(t, f);
 }
 
+// The streamed kernels load weight rows as dwords and fp32 activations as
+// float4: with rows or bases not aligned for that, the type is decoded by the
+// runtime switch (kGgAny) with byte loads instead.
+static bool gg_aligned(const void* w, long row_bytes, const void* x, int xalign) {
+    return ((uintptr_t)w & 3) == 0 && (row_bytes & 3) == 0 &&
+           (x == nullptr || ((uintptr_t)x & (uintptr_t)(xalign - 1)) == 0);
+}
+
 template <bool I8>
 static int gg_gemm(uint32_t qtype, const float* x, const int8_t* xq, const float* xsc,
                    const uint8_t* qw, const float* bias, float* y, int n, int in, int out,
                    long row_bytes, hipStream_t s) {
     const dim3 grid((unsigned)((out + kGgRows - 1) / kGgRows));
-    gg_by_type_t<I8>(qtype, [&](auto tc) {
+    const bool al = gg_aligned(qw, row_bytes, I8 ? (const void*)xq : (const void*)x, I8 ? 4 : 16);
+    gg_by_type_t<I8>(al ? qtype : kGgAny, [&](auto tc) {
         constexpr uint32_t T = decltype(tc)::value;
         if (n == 1)
             hipLaunchKernelGGL((gg_gemv_kernel<T, 1, I8>), grid, dim3(256), 0, s, qtype, x, xq,
@@ -822,7 +1144,12 @@ template <int TT, bool I8>
 static int gg_moe_phases(uint32_t gt, uint32_t ut, uint32_t dt, const GgMoeArgs& a, unsigned tiles,
                          hipStream_t s) {
     const dim3 g1(tiles, (unsigned)((a.I + kGgRows - 1) / kGgRows));
-    if (gt == ut)
+    const bool al1 = gg_aligned(a.gate_q, a.gate_rb, I8 ? (const void*)a.xq : (const void*)a.x,
+                                I8 ? 4 : 16) &&
+                     gg_aligned(a.up_q, a.up_rb, nullptr, 1);
+    const bool al2 = gg_aligned(a.down_q, a.down_rb,
+                                I8 ? (const void*)a.hq : (const void*)a.h_act, I8 ? 4 : 16);
+    if (gt == ut && al1)
         gg_by_type_t<I8>(gt, [&](auto tc) {
             hipLaunchKernelGGL((gg_moe_kernel<false, decltype(tc)::value, TT, I8>), g1, dim3(256),
                                0, s, a);
@@ -836,7 +1163,7 @@ static int gg_moe_phases(uint32_t gt, uint32_t ut, uint32_t dt, const GgMoeArgs&
             return -4;
     }
     const dim3 g2(tiles, (unsigned)((a.H + kGgRows - 1) / kGgRows));
-    gg_by_type_t<I8>(dt, [&](auto tc) {
+    gg_by_type_t<I8>(al2 ? dt : kGgAny, [&](auto tc) {
         hipLaunchKernelGGL((gg_moe_kernel<true, decltype(tc)::value, TT, I8>), g2, dim3(256), 0, s,
                            a);
     });
@@ -844,15 +1171,21 @@ static int gg_moe_phases(uint32_t gt, uint32_t ut, uint32_t dt, const GgMoeArgs&
 }
 
 template <bool I8>
-static int gg_moe(const GgMoeArgs& a, float* out, int* dispatch, hipStream_t s) {
+static int gg_moe(GgMoeArgs a, float* out, int* dispatch, hipStream_t s) {
     const uint32_t gt = a.gate_type, ut = a.up_type, dt = a.down_type;
     const int n = a.n, topk = a.topk, H = a.H, E = a.E;
     const float* ids_w = a.w;
     const float* dpart = a.dpart;
     const int* ids = a.ids;
     const int nk = n * topk;
-    // Rows per tile: about the rows an expert holds (decode: one or a few).
+    // Rows per tile: about the rows an expert holds (decode: one or a few). With
+    // one row per tile, grouping changes nothing but the order of the tiles, so
+    // the routed rows are taken as they come (an exact grid, no counting pass).
     const int tt = !dispatch || nk <= E ? 1 : nk <= 4 * E ? 4 : 8;
+    if (tt == 1) {
+        dispatch = nullptr;
+        a.d = nullptr;
+    }
     unsigned tiles = (unsigned)nk;
     if (dispatch) {
         hipLaunchKernelGGL(gg_group_kernel, dim3(1), dim3(1024), (size_t)2 * E * 4, s, ids, nk, E,

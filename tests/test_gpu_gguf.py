@@ -42,9 +42,10 @@ def test_gemm_q_decode_bit_exact(oracle, qtype):
 
 
 @pytest.mark.parametrize("qtype", TYPES)
-def test_gemm_q_dense(oracle, qtype):
-    rng = np.random.default_rng(400 + qtype)
-    n, in_, out = 11, 1024, 40
+@pytest.mark.parametrize("in_", [1024, 1280])    # 1280: a partial last K chunk
+def test_gemm_q_dense(oracle, qtype, in_):
+    rng = np.random.default_rng(400 + qtype + in_)
+    n, out = 11, 40
     w = random_gguf_rows(qtype, out, in_, rng)
     W = oracle.gguf_dequant_rows(qtype, w, out, in_).astype(np.float64)
     x = rng.standard_normal((n, in_)).astype(np.float32)
@@ -86,3 +87,18 @@ def test_moe_expert_ffn_q(oracle, types, grouped):
                               _row_bytes(types[2], I)), h_act, dpart, out, disp)
     torch.cuda.synchronize()
     assert rel_err(out.cpu().numpy(), ref) < 1e-4
+
+
+def test_gemm_q_unaligned_rows(oracle):
+    # Q8_0 rows of 3 blocks (102 B) are not 4-byte aligned: the byte-load decode
+    # serves them (the streamed kernels need dword-aligned rows).
+    rng = np.random.default_rng(5)
+    n, in_, out = 3, 96, 21
+    w = random_gguf_rows(8, out, in_, rng)
+    W = oracle.gguf_dequant_rows(8, w, out, in_).astype(np.float64)
+    x = rng.standard_normal((n, in_)).astype(np.float32)
+    y = torch.full((n, out), float("nan"), device="cuda")
+    ops.ref_gemm_q(8, torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda(), None, y,
+                   _row_bytes(8, in_))
+    torch.cuda.synchronize()
+    assert rel_err(y.cpu().numpy(), x.astype(np.float64) @ W.T) < 1e-5

@@ -94,9 +94,11 @@ def _silu(v):
     return v / (1.0 + np.exp(-v))
 
 
-@pytest.mark.parametrize("types", [(18, 18, 23), (12, 12, 14), (8, 8, 8), (11, 13, 12)])
-def test_moe_expert_ffn_q_i8(oracle, types):
-    H, I, E, k, n = 512, 256, 8, 4, 6
+@pytest.mark.parametrize("types,n", [((18, 18, 23), 6), ((12, 12, 14), 6), ((8, 8, 8), 6),
+                                     ((11, 13, 12), 6), ((18, 18, 23), 20)])
+def test_moe_expert_ffn_q_i8(oracle, types, n):
+    # n = 20: 80 routed rows over 8 experts, so the grouped run uses 8-row tiles
+    H, I, E, k = 512, 256, 8, 4
     rng = np.random.default_rng(sum(types) + 99)
     gq = random_gguf_rows(types[0], E * I, H, rng)
     uq = random_gguf_rows(types[1], E * I, H, rng)
