@@ -171,6 +171,8 @@ def main():
     ap.add_argument("--no-fp8", action="store_true", help="skip the configs[4] FP8 sweep line")
     ap.add_argument("--fp8-only", action="store_true",
                     help="only time the FP8 8192-token prefill (for profiling)")
+    ap.add_argument("--gguf-only", action="store_true",
+                    help="only time the GGUF expert FFN (fp32 and int8) at B=1 and B=64")
     ap.add_argument("--copy-calib", action="store_true",
                     help="only run a 1 GiB device copy (calibrates rocprof FETCH/WRITE_SIZE)")
     args = ap.parse_args()
@@ -280,6 +282,11 @@ def main():
     log("bench: building synthetic W4A16 layer H=6144 E=256 k=8 I=2048 (+shared)")
     L = SynthLayer(H, E, K, I, seed=1)
     torch.cuda.synchronize()
+    if args.gguf_only:
+        r = {f"gguf{'_i8' if i8 else ''}_decode_B{n}": measure_gguf(n, args.steps, args.warmup, i8)
+             for n in (1, 64) for i8 in (False, True)}
+        print(json.dumps(r), flush=True)
+        return
 
     def summarize(n, ms, U, st):
         bytes_alg = (U + 1) * EXPERT_BYTES + ROUTER_BYTES + n * H * 2 + n * H * 4

@@ -16,12 +16,15 @@
 //
 // Work: a workgroup (4 waves) owns 16 output rows (4 per wave) and a tile of
 // up to 8 input rows. With the caller's `dispatch` scratch the routed rows are
-// first grouped by expert (counting pass, one workgroup), so a tile is 8 rows
-// of one expert and each weight row is read once per tile; without it every
-// routed row is a tile of its own (the reference's token-major path). Each
-// 512-wide K chunk of the tile's input rows is staged in LDS; each lane
-// decodes 8 consecutive K of its 4 weight rows and accumulates 4 x 8 dot
-// products; lane partials are added by a fixed xor butterfly.
+// first grouped by expert (counting pass, one workgroup), so a tile holds up
+// to 8 rows of one expert and each weight row is read once per tile; without
+// it every routed row is a tile of its own (the reference's token-major path).
+// K is walked in chunks: the tile's input rows of a chunk are staged in LDS
+// (shared by the waves); each lane takes 8 consecutive K of the wave's weight
+// rows and accumulates 8-element dot products; lane partials are added by a
+// fixed xor butterfly. For the block types with dword-aligned rows the weight
+// bytes are streamed one chunk ahead (gg_dots_stream); otherwise each lane
+// reads its blocks' bytes directly (gg_dots / gg_dots_i8).
 #include <type_traits>
 
 #include "common.hpp"
@@ -254,7 +257,9 @@ __device__ __forceinline__ void gg_dec8(uint32_t t, const uint8_t* __restrict__ 
     gg_dec8_any(T == kGgAny ? t : T, row, k, grid, y);
 }
 
-constexpr int kGgRows = 16;   // weight rows per workgroup (4 per wave)
+constexpr int kGgWaves = 4;                // waves per workgroup
+constexpr int kGgThreads = 64 * kGgWaves;
+constexpr int kGgRows = 4 * kGgWaves;      // weight rows per workgroup (4 per wave)
 constexpr int kGgKC = 512;    // K per staged chunk
 // Input rows per tile (TT): 8 for prefill-sized groups, fewer when an expert
 // holds a row or a few (decode), so no FMAs go to empty rows.
@@ -587,9 +592,9 @@ struct GgStream {
     static constexpr int ND = CB / 4;
     static constexpr int LPR = (ND + 63) / 64;            // dword loads per lane per row
     static constexpr int XV = I8 ? TT * KC / 4 : TT * KC / 4;   // int / float4 items of x
-    static constexpr int XR = (XV + 255) / 256;           // per thread
+    static constexpr int XR = (XV + kGgThreads - 1) / kGgThreads;   // per thread
     static constexpr int SR = TT * KC / 32;               // scales (I8)
-    uint32_t w[2][4][NM * 4][ND];
+    uint32_t w[2][kGgWaves][NM * 4][ND];
     uint32_t grid[T == 18 ? 256 : 1];   // the IQ3_XXS codebook
     float x[I8 ? 1 : 2][I8 ? 1 : TT][I8 ? 4 : KC];
     struct {
@@ -615,7 +620,9 @@ __device__ __forceinline__ void gg_dots_stream(GgStream<T, NM, TT, I8>& L, int* 
 #pragma unroll
         for (int t = 0; t < TT; ++t) srcs[t] = tl.src[t];
     }
-    if constexpr (T == 18) L.grid[tid] = c_iq3xxs_grid[tid];
+    if constexpr (T == 18) {
+        if (tid < 256) L.grid[tid] = c_iq3xxs_grid[tid];
+    }
 #pragma unroll
     for (int m = 0; m < NM; ++m)
 #pragma unroll
@@ -643,7 +650,7 @@ __device__ __forceinline__ void gg_dots_stream(GgStream<T, NM, TT, I8>& L, int* 
             }
 #pragma unroll
         for (int j = 0; j < XR; ++j) {
-            const int v = tid + 256 * j;
+            const int v = tid + kGgThreads * j;
             const int t = v / (KC / 4), c4 = v % (KC / 4);
             if (v < S::XV && t < tl.nr && 4 * c4 < kc) {
                 if constexpr (I8)
@@ -672,7 +679,7 @@ __device__ __forceinline__ void gg_dots_stream(GgStream<T, NM, TT, I8>& L, int* 
             }
 #pragma unroll
         for (int j = 0; j < XR; ++j) {
-            const int v = tid + 256 * j;
+            const int v = tid + kGgThreads * j;
             const int t = v / (KC / 4), c4 = v % (KC / 4);
             if (v < S::XV) {
                 const bool ok = t < tl.nr && 4 * c4 < kc;
@@ -800,7 +807,7 @@ constexpr size_t gg_lds_bytes() {
 
 // I8: activations are (xq, xsc) from quantize_act_q8 instead of x (gemm_q_i8).
 template <uint32_t T, int TT, bool I8>
-__global__ __launch_bounds__(256) void gg_gemv_kernel(uint32_t qtype, const float* __restrict__ x,
+__global__ __launch_bounds__(kGgThreads) void gg_gemv_kernel(uint32_t qtype, const float* __restrict__ x,
                                                       const int8_t* __restrict__ xq,
                                                       const float* __restrict__ xsc,
                                                       const uint8_t* __restrict__ qw,
@@ -904,7 +911,7 @@ struct GgMoeArgs {
 // DOWN = false: phase 1 (gate/up, output rows = I features); true: phase 2.
 // T: the weight type (gate and up share it in phase 1), or kGgAny.
 template <bool DOWN, uint32_t T, int TT, bool I8>
-__global__ __launch_bounds__(256) void gg_moe_kernel(GgMoeArgs a) {
+__global__ __launch_bounds__(kGgThreads) void gg_moe_kernel(GgMoeArgs a) {
     constexpr bool ST = gg_streamed(T);
     __shared__ __align__(16) char lds[ST ? sizeof(GgStream<T, DOWN ? 1 : 2, TT, I8>)
                                          : gg_lds_bytes<TT, I8>()];
@@ -1113,10 +1120,10 @@ static int gg_gemm(uint32_t qtype, const float* x, const int8_t* xq, const float
     gg_by_type_t<I8>(al ? qtype : kGgAny, [&](auto tc) {
         constexpr uint32_t T = decltype(tc)::value;
         if (n == 1)
-            hipLaunchKernelGGL((gg_gemv_kernel<T, 1, I8>), grid, dim3(256), 0, s, qtype, x, xq,
+            hipLaunchKernelGGL((gg_gemv_kernel<T, 1, I8>), grid, dim3(kGgThreads), 0, s, qtype, x, xq,
                                xsc, qw, bias, y, n, in, out, row_bytes);
         else
-            hipLaunchKernelGGL((gg_gemv_kernel<T, 8, I8>), grid, dim3(256), 0, s, qtype, x, xq,
+            hipLaunchKernelGGL((gg_gemv_kernel<T, 8, I8>), grid, dim3(kGgThreads), 0, s, qtype, x, xq,
                                xsc, qw, bias, y, n, in, out, row_bytes);
     });
     return hipGetLastError() == hipSuccess ? 0 : -4;
@@ -1151,11 +1158,11 @@ static int gg_moe_phases(uint32_t gt, uint32_t ut, uint32_t dt, const GgMoeArgs&
                                 I8 ? (const void*)a.hq : (const void*)a.h_act, I8 ? 4 : 16);
     if (gt == ut && al1)
         gg_by_type_t<I8>(gt, [&](auto tc) {
-            hipLaunchKernelGGL((gg_moe_kernel<false, decltype(tc)::value, TT, I8>), g1, dim3(256),
+            hipLaunchKernelGGL((gg_moe_kernel<false, decltype(tc)::value, TT, I8>), g1, dim3(kGgThreads),
                                0, s, a);
         });
     else
-        hipLaunchKernelGGL((gg_moe_kernel<false, kGgAny, TT, I8>), g1, dim3(256), 0, s, a);
+        hipLaunchKernelGGL((gg_moe_kernel<false, kGgAny, TT, I8>), g1, dim3(kGgThreads), 0, s, a);
     if (hipGetLastError() != hipSuccess) return -4;
     if constexpr (I8) {
         if (launch_gg_quant_q8(a.h_act, (long)a.n * a.topk * a.I, const_cast<int8_t*>(a.hq),
@@ -1164,7 +1171,7 @@ static int gg_moe_phases(uint32_t gt, uint32_t ut, uint32_t dt, const GgMoeArgs&
     }
     const dim3 g2(tiles, (unsigned)((a.H + kGgRows - 1) / kGgRows));
     gg_by_type_t<I8>(al2 ? dt : kGgAny, [&](auto tc) {
-        hipLaunchKernelGGL((gg_moe_kernel<true, decltype(tc)::value, TT, I8>), g2, dim3(256), 0, s,
+        hipLaunchKernelGGL((gg_moe_kernel<true, decltype(tc)::value, TT, I8>), g2, dim3(kGgThreads), 0, s,
                            a);
     });
     return hipGetLastError() == hipSuccess ? 0 : -4;
