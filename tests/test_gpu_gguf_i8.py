@@ -154,3 +154,18 @@ def test_moe_expert_ffn_q_i8(oracle, types, n):
     # grouped tiles: per row the same sums in the same order
     for a, b in zip(outs[0], outs[1]):
         assert np.array_equal(a, b)
+
+
+def test_gemm_q_i8_unaligned_rows(oracle):
+    # Q8_0 rows of 3 blocks (102 B) are not 4-byte aligned: the byte-load decode
+    # serves them.
+    rng = np.random.default_rng(6)
+    n, in_, out = 5, 96, 19
+    w = random_gguf_rows(8, out, in_, rng)
+    x = rng.standard_normal((n, in_)).astype(np.float32)
+    xq, xs = _quant(_dev(x))
+    y = torch.full((n, out), float("nan"), device="cuda")
+    ops.ref_gemm_q_i8(8, xq, xs, _dev(w), None, y, _row_bytes(8, in_))
+    torch.cuda.synchronize()
+    ref = oracle.gemm_q_i8(8, xq.cpu().numpy(), xs.cpu().numpy(), w, out, _row_bytes(8, in_))
+    assert rel_err(y.cpu().numpy(), ref) < 1e-5
