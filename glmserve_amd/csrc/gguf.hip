@@ -369,9 +369,12 @@ __device__ __forceinline__ uint32_t gg_bytemask4(uint32_t s) {
     return (((s & 15u) * 0x00204081u) & 0x01010101u) * 0xffu;
 }
 
+// sgn (used with A2): the IQ3_XXS sign byte masks of the 128 7-bit patterns,
+// two words per pattern (the LDS table of gg_dots_stream).
 template <bool A2>
 __device__ __forceinline__ void gg_dec8i_any(uint32_t t, const uint8_t* __restrict__ row, int k,
-                                             const uint32_t* __restrict__ grid, int& w0, int& w1,
+                                             const uint32_t* __restrict__ grid,
+                                             const uint32_t* __restrict__ sgn, int& w0, int& w1,
                                              float& ds, float& dm) {
     dm = 0.0f;
     switch (t) {
@@ -451,13 +454,21 @@ __device__ __forceinline__ void gg_dec8i_any(uint32_t t, const uint8_t* __restri
             const uint32_t aux = gg_rd32<A2>(b + 66 + 4 * ib);
             ds = gg_rdf16<A2>(b) * (0.5f + (float)(aux >> 28)) * 0.5f;
             const uint32_t i7 = (aux >> (7 * l)) & 127u;
-            const uint32_t signs = i7 | ((uint32_t)(__builtin_popcount(i7) & 1) << 7);
+            uint32_t n0, n1;
+            if constexpr (A2) {
+                const uint2 m = *reinterpret_cast<const uint2*>(sgn + 2 * i7);
+                n0 = m.x;
+                n1 = m.y;
+            } else {
+                const uint32_t signs = i7 | ((uint32_t)(__builtin_popcount(i7) & 1) << 7);
+                n0 = gg_bytemask4(signs);
+                n1 = gg_bytemask4(signs >> 4);
+            }
             const uint32_t qs = A2 ? *reinterpret_cast<const uint16_t*>(b + 2 + 8 * ib + 2 * l)
                                    : (uint32_t)(b[2 + 8 * ib + 2 * l] | (b[3 + 8 * ib + 2 * l] << 8));
             const uint32_t g0 = grid[qs & 255u], g1 = grid[qs >> 8];
             // negate the flagged bytes: (g ^ 0xff) + 1 per byte, with no carry
             // out of a byte since every grid magnitude is at least 4
-            const uint32_t n0 = gg_bytemask4(signs), n1 = gg_bytemask4(signs >> 4);
             w0 = (int)((g0 ^ n0) + (n0 & 0x01010101u));
             w1 = (int)((g1 ^ n1) + (n1 & 0x01010101u));
             return;
@@ -484,9 +495,10 @@ __device__ __forceinline__ void gg_dec8i_any(uint32_t t, const uint8_t* __restri
 
 template <uint32_t T, bool A2 = false>
 __device__ __forceinline__ void gg_dec8i(uint32_t t, const uint8_t* __restrict__ row, int k,
-                                         const uint32_t* __restrict__ grid, int& w0, int& w1,
+                                         const uint32_t* __restrict__ grid,
+                                         const uint32_t* __restrict__ sgn, int& w0, int& w1,
                                          float& ds, float& dm) {
-    gg_dec8i_any<A2>(T == kGgAny ? t : T, row, k, grid, w0, w1, ds, dm);
+    gg_dec8i_any<A2>(T == kGgAny ? t : T, row, k, grid, sgn, w0, w1, ds, dm);
 }
 
 // LDS tile of int8 activations: TT rows x kGgKC bytes and their per-32 scales.
@@ -550,7 +562,7 @@ __device__ __forceinline__ void gg_dots_i8(GgI8Tile<TT>& xt, int* srcs, const in
             for (int r = 0; r < 4; ++r) {
                 int w0, w1;
                 float ds, dm;
-                gg_dec8i<T>(type[m], wrow[m][r], k0 + kk, c_iq3xxs_grid, w0, w1, ds, dm);
+                gg_dec8i<T>(type[m], wrow[m][r], k0 + kk, c_iq3xxs_grid, nullptr, w0, w1, ds, dm);
 #pragma unroll
                 for (int t = 0; t < TT; ++t) {
                     const int si = __builtin_amdgcn_sdot4(w1, x1[t], __builtin_amdgcn_sdot4(w0, x0[t], 0, false), false);
@@ -596,6 +608,7 @@ struct GgStream {
     static constexpr int SR = TT * KC / 32;               // scales (I8)
     uint32_t w[2][kGgWaves][NM * 4][ND];
     uint32_t grid[T == 18 ? 256 : 1];   // the IQ3_XXS codebook
+    uint32_t sgn[T == 18 ? 256 : 1];    // IQ3_XXS: byte masks of the 128 sign patterns
     float x[I8 ? 1 : 2][I8 ? 1 : TT][I8 ? 4 : KC];
     struct {
         int q[I8 ? 2 : 1][I8 ? TT : 1][I8 ? KC / 4 : 1];
@@ -621,7 +634,13 @@ __device__ __forceinline__ void gg_dots_stream(GgStream<T, NM, TT, I8>& L, int* 
         for (int t = 0; t < TT; ++t) srcs[t] = tl.src[t];
     }
     if constexpr (T == 18) {
-        if (tid < 256) L.grid[tid] = c_iq3xxs_grid[tid];
+        if (tid < 256) {
+            L.grid[tid] = c_iq3xxs_grid[tid];
+            // pattern e: 7 sign bits plus their parity bit, as 8 byte masks
+            const uint32_t e = (uint32_t)tid >> 1;
+            const uint32_t sg = e | ((uint32_t)(__builtin_popcount(e) & 1) << 7);
+            L.sgn[tid] = gg_bytemask4(sg >> (4 * (tid & 1)));
+        }
     }
 #pragma unroll
     for (int m = 0; m < NM; ++m)
@@ -725,7 +744,7 @@ __device__ __forceinline__ void gg_dots_stream(GgStream<T, NM, TT, I8>& L, int* 
                         int w0, w1;
                         float ds, dm;
                         gg_dec8i<T, true>(T, reinterpret_cast<const uint8_t*>(L.w[b][wave][i]),
-                                          kk, L.grid, w0, w1, ds, dm);
+                                          kk, L.grid, L.sgn, w0, w1, ds, dm);
 #pragma unroll
                         for (int t = 0; t < TT; ++t) {
                             const int si = __builtin_amdgcn_sdot4(
@@ -758,7 +777,7 @@ __device__ __forceinline__ void gg_dots_stream(GgStream<T, NM, TT, I8>& L, int* 
                         int w0, w1;
                         float ds, dm;
                         gg_dec8i<T, true>(T, reinterpret_cast<const uint8_t*>(L.w[b][wave][i]),
-                                          kk, L.grid, w0, w1, ds, dm);
+                                          kk, L.grid, L.sgn, w0, w1, ds, dm);
                         float wf[8];
 #pragma unroll
                         for (int j = 0; j < 8; ++j)
