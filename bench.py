@@ -254,6 +254,33 @@ def main():
                         "expert); " + ("int8 activations, int32 fragment dots" if i8 else
                                        "fp32 activations and arithmetic as in the reference")}
 
+    def measure_gemm_q(qtype, bb, be, n, steps, warmup):
+        # gemm_q (the reference's GGUF linear) at the configs[1] shared-expert gate shape,
+        # H=6144 -> 2048 outputs: Q8_0 (the served dense / shared type) or IQ3_XXS.
+        from glmserve_amd import ops
+        out, K = 2048, H
+        nb = K // be
+        q = torch.randint(0, 256, (out, nb, bb), dtype=torch.uint8, device="cuda")
+        q[:, :, 0:2] = (torch.rand(out, nb, device="cuda") * 0.01 + 0.005).half() \
+            .view(torch.uint8).view(out, nb, 2)
+        q = q.view(out, nb * bb)
+        x = torch.randn(n, K, device="cuda")
+        y = torch.empty(n, out, device="cuda")
+        call = lambda: ops.ref_gemm_q(qtype, x, q, None, y, nb * bb)
+        for _ in range(warmup):
+            call()
+        torch.cuda.synchronize()
+        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0.record()
+        for _ in range(steps):
+            call()
+        t1.record()
+        torch.cuda.synchronize()
+        ms = t0.elapsed_time(t1) / steps
+        alg = out * nb * bb + n * K * 4 + n * out * 4
+        return {"qtype": qtype, "n": n, "ms": ms, "alg_bytes": alg, "GBps": alg / (ms * 1e-3) / 1e9,
+                "hbm_frac": alg / (ms * 1e-3) / HBM_PEAK}
+
     def measure_fp8(n, steps, warmup):
         from moe_cases import SynthFp8Layer
         log("bench: building synthetic FP8 layer (configs[4] format)")
@@ -285,6 +312,9 @@ def main():
     if args.gguf_only:
         r = {f"gguf{'_i8' if i8 else ''}_decode_B{n}": measure_gguf(n, args.steps, args.warmup, i8)
              for n in (1, 64) for i8 in (False, True)}
+        for name, qt, bb, be in (("q8_0", 8, 34, 32), ("iq3_xxs", 18, 98, 256)):
+            for n in (1, 64):
+                r[f"gguf_gemm_q_{name}_n{n}"] = measure_gemm_q(qt, bb, be, n, args.steps, args.warmup)
         print(json.dumps(r), flush=True)
         return
 
@@ -384,6 +414,7 @@ def main():
             log(f"bench: sweep GGUF decode B={n} (IQ3_XXS gate/up, IQ4_XS down)")
             sweep[f"gguf_decode_B{n}"] = measure_gguf(n, args.steps, args.warmup)
             sweep[f"gguf_i8_decode_B{n}"] = measure_gguf(n, args.steps, args.warmup, i8=True)
+            sweep[f"gguf_gemm_q_q8_0_n{n}"] = measure_gemm_q(8, 34, 32, n, args.steps, args.warmup)
         torch.cuda.empty_cache()
     if not args.no_sweep and not args.no_fp8:
         log("bench: sweep FP8 prefill 8192")

@@ -25,6 +25,7 @@
 // fixed xor butterfly. For the block types with dword-aligned rows the weight
 // bytes are streamed one chunk ahead (gg_dots_stream); otherwise each lane
 // reads its blocks' bytes directly (gg_dots / gg_dots_i8).
+#include <algorithm>
 #include <type_traits>
 
 #include "common.hpp"
@@ -817,7 +818,8 @@ __global__ __launch_bounds__(256) void gg_quant_q8_kernel(const float* __restric
     if ((i & 31) == 0) xs[i / 32] = sx;
 }
 
-// gemm_q: tiles are 8 consecutive tokens.
+// gemm_q: tiles are 8 consecutive tokens (one at n = 1), one tile per
+// workgroup row of the grid.
 // LDS bytes of a tile's staged activations.
 template <int TT, bool I8>
 constexpr size_t gg_lds_bytes() {
@@ -842,7 +844,8 @@ __global__ __launch_bounds__(kGgThreads) void gg_gemv_kernel(uint32_t qtype, con
     const uint8_t* wrow[1][4];
 #pragma unroll
     for (int r = 0; r < 4; ++r) wrow[0][r] = qw + (size_t)min(o0 + r, out - 1) * row_bytes;
-    for (int t0 = 0; t0 < n; t0 += TT) {
+    // token tiles: blockIdx.y, then strided by the grid's height
+    for (int t0 = blockIdx.y * TT; t0 < n; t0 += gridDim.y * TT) {
         GgTile<TT> tl;
         tl.e = 0;
         tl.nr = min(TT, n - t0);
@@ -1134,7 +1137,9 @@ template <bool I8>
 static int gg_gemm(uint32_t qtype, const float* x, const int8_t* xq, const float* xsc,
                    const uint8_t* qw, const float* bias, float* y, int n, int in, int out,
                    long row_bytes, hipStream_t s) {
-    const dim3 grid((unsigned)((out + kGgRows - 1) / kGgRows));
+    const int tt = n == 1 ? 1 : 8;
+    const dim3 grid((unsigned)((out + kGgRows - 1) / kGgRows),
+                    (unsigned)std::min((n + tt - 1) / tt, 65535));
     const bool al = gg_aligned(qw, row_bytes, I8 ? (const void*)xq : (const void*)x, I8 ? 4 : 16);
     gg_by_type_t<I8>(al ? qtype : kGgAny, [&](auto tc) {
         constexpr uint32_t T = decltype(tc)::value;
