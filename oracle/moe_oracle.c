@@ -458,6 +458,125 @@ int orc_moe_forward_ex(const float* x, int64_t n, int64_t H, int E, int topk, in
 }
 
 /* ---------------------------------------------------------------------------
+ * The layer streamed expert by expert, for full-output checks at large n.
+ * orc_expert_rows runs orc_ffn's arithmetic on m rows of one expert at once:
+ * every output element is the same scalar fp32 chain as orc_linear_f32
+ * (ascending i, product rounded before the add), so each row equals orc_ffn on
+ * that row bit for bit. Rows are processed in blocks of ORC_RB, transposed so
+ * that the ORC_RB independent chains of one output sit side by side in memory
+ * (the compiler can keep them in vector registers without reassociating any
+ * chain). orc_combine_slots then adds the per-slot rows in slot order and the
+ * shared row last, exactly as orc_moe_worker does (src/model_glm52.cpp:1133-1152):
+ *   out[t] = ((0 + w0*y0) + w1*y1 + ...) + y_shared.
+ * ------------------------------------------------------------------------- */
+#define ORC_RB 32
+__attribute__((optimize("O3"))) static void orc_linear_block(const float* xT, int64_t in, const float* w, int64_t out,
+                             float* yT /* [out][ORC_RB] */) {
+    for (int64_t o = 0; o < out; ++o) {
+        const float* wo = w + o * in;
+        float acc[ORC_RB];
+        for (int r = 0; r < ORC_RB; ++r) acc[r] = 0.0f;
+        for (int64_t i = 0; i < in; ++i) {
+            const float wi = wo[i];
+            const float* xi = xT + i * ORC_RB;
+            for (int r = 0; r < ORC_RB; ++r) {
+                float p = xi[r] * wi;
+                acc[r] = acc[r] + p;
+            }
+        }
+        for (int r = 0; r < ORC_RB; ++r) yT[o * ORC_RB + r] = acc[r];
+    }
+}
+
+typedef struct {
+    const float *x, *g_w, *u_w, *d_w;
+    int64_t m, H, I;
+    int h_fp8;
+    float* y;
+    int64_t b0, b1; /* row blocks of this worker */
+} orc_rows_job;
+
+static void* orc_rows_worker(void* arg) {
+    orc_rows_job* j = (orc_rows_job*)arg;
+    const int64_t H = j->H, I = j->I;
+    float* xT = (float*)malloc(sizeof(float) * (size_t)(H * ORC_RB));
+    float* gT = (float*)malloc(sizeof(float) * (size_t)(I * ORC_RB));
+    float* uT = (float*)malloc(sizeof(float) * (size_t)(I * ORC_RB));
+    float* yT = (float*)malloc(sizeof(float) * (size_t)(H * ORC_RB));
+    for (int64_t b = j->b0; b < j->b1; ++b) {
+        const int64_t r0 = b * ORC_RB;
+        const int nr = (int)(j->m - r0 < ORC_RB ? j->m - r0 : ORC_RB);
+        for (int64_t i = 0; i < H; ++i)
+            for (int r = 0; r < ORC_RB; ++r)
+                xT[i * ORC_RB + r] = r < nr ? j->x[(r0 + r) * H + i] : 0.0f;
+        orc_linear_block(xT, H, j->g_w, I, gT);
+        orc_linear_block(xT, H, j->u_w, I, uT);
+        for (int64_t i = 0; i < I * ORC_RB; ++i) gT[i] = orc_silu(gT[i]) * uT[i];
+        if (j->h_fp8) {
+            /* per row: quantize h per 128 features (orc_ffn's h_fp8 step) */
+            for (int r = 0; r < nr; ++r)
+                for (int64_t g0 = 0; g0 < I; g0 += 128) {
+                    float hv[128];
+                    uint8_t q[128];
+                    float sc;
+                    for (int i = 0; i < 128; ++i) hv[i] = gT[(g0 + i) * ORC_RB + r];
+                    orc_quant_act_e4m3(hv, 1, 128, q, &sc);
+                    for (int i = 0; i < 128; ++i) gT[(g0 + i) * ORC_RB + r] = orc_e4m3_to_f32(q[i]) * sc;
+                }
+        }
+        orc_linear_block(gT, I, j->d_w, H, yT);
+        for (int r = 0; r < nr; ++r)
+            for (int64_t i = 0; i < H; ++i) j->y[(r0 + r) * H + i] = yT[i * ORC_RB + r];
+    }
+    free(xT);
+    free(gT);
+    free(uT);
+    free(yT);
+    return NULL;
+}
+
+void orc_expert_rows(const float* x, int64_t m, int64_t H, int64_t I, const float* gate,
+                     const float* up, const float* down, int h_fp8, int nthreads, float* y) {
+    const int64_t nb = (m + ORC_RB - 1) / ORC_RB;
+    if (nb == 0) return;
+    if (nthreads < 1) nthreads = 1;
+    if (nthreads > nb) nthreads = (int)nb;
+    orc_rows_job* jobs = (orc_rows_job*)calloc((size_t)nthreads, sizeof(orc_rows_job));
+    pthread_t* th = (pthread_t*)calloc((size_t)nthreads, sizeof(pthread_t));
+    for (int i = 0; i < nthreads; ++i) {
+        orc_rows_job* j = &jobs[i];
+        j->x = x; j->g_w = gate; j->u_w = up; j->d_w = down;
+        j->m = m; j->H = H; j->I = I; j->h_fp8 = h_fp8; j->y = y;
+        j->b0 = nb * i / nthreads;
+        j->b1 = nb * (i + 1) / nthreads;
+    }
+    if (nthreads == 1) {
+        orc_rows_worker(&jobs[0]);
+    } else {
+        for (int i = 0; i < nthreads; ++i) pthread_create(&th[i], NULL, orc_rows_worker, &jobs[i]);
+        for (int i = 0; i < nthreads; ++i) pthread_join(th[i], NULL);
+    }
+    free(jobs);
+    free(th);
+}
+
+void orc_combine_slots(const float* slot_rows /* [n*topk, H], row t*topk+kk */,
+                       const float* topk_w, const float* shared_rows /* [n, H] or NULL */,
+                       int64_t n, int topk, int64_t H, float* out) {
+    for (int64_t t = 0; t < n; ++t) {
+        float* ot = out + t * H;
+        for (int64_t i = 0; i < H; ++i) ot[i] = 0.0f;
+        for (int kk = 0; kk < topk; ++kk) {
+            const float w = topk_w[t * topk + kk];
+            const float* y = slot_rows + (t * topk + kk) * H;
+            for (int64_t i = 0; i < H; ++i) ot[i] = ot[i] + w * y[i];
+        }
+        if (shared_rows)
+            for (int64_t i = 0; i < H; ++i) ot[i] = ot[i] + shared_rows[t * H + i];
+    }
+}
+
+/* ---------------------------------------------------------------------------
  * GGUF block formats (src/gguf_quant.cpp:98-262, the reference's CPU
  * dequantizers of the ggml block layouts; types 0 F32, 1 F16, 8 Q8_0, 11 Q3_K,
  * 12 Q4_K, 13 Q5_K, 14 Q6_K, 18 IQ3_XXS, 23 IQ4_XS). Restated per element:

@@ -106,6 +106,14 @@ int orc_moe_forward_ex(const float* x, int64_t n, int64_t H, int E, int topk, in
 /* GGUF block formats (src/gguf_quant.cpp:98-262): element p of one block, a
  * whole row of n elements (n a multiple of the block size; -1 otherwise), the
  * block geometry, and the two codebooks (for pinning against the reference's). */
+/* Expert FFN of m rows at once (orc_ffn per row, bit for bit) and the
+ * slot-order combine of per-slot rows plus the shared rows; together they
+ * equal orc_moe_forward_ex for the same routing. */
+void orc_expert_rows(const float* x, int64_t m, int64_t H, int64_t I, const float* gate,
+                     const float* up, const float* down, int h_fp8, int nthreads, float* y);
+void orc_combine_slots(const float* slot_rows, const float* topk_w, const float* shared_rows,
+                       int64_t n, int topk, int64_t H, float* out);
+
 int64_t orc_gguf_block_elems(uint32_t type);
 int64_t orc_gguf_block_bytes(uint32_t type);
 float orc_gguf_value(uint32_t type, const uint8_t* block, int p);

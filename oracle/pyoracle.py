@@ -69,6 +69,9 @@ class Oracle:
             _f32p, _i64, _i64, C.c_int, C.c_int, _i64, _i64, C.c_void_p, C.c_void_p,
             C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p, C.c_void_p,
             C.c_void_p, C.c_int, C.c_float, C.c_int, C.c_int, _f32p, _i32p, _f32p]
+        L.orc_expert_rows.argtypes = [_f32p, _i64, _i64, _i64, _f32p, _f32p, _f32p, C.c_int,
+                                      C.c_int, _f32p]
+        L.orc_combine_slots.argtypes = [_f32p, _f32p, C.c_void_p, _i64, C.c_int, _i64, _f32p]
         L.orc_gguf_block_elems.restype = _i64
         L.orc_gguf_block_elems.argtypes = [C.c_uint32]
         L.orc_gguf_block_bytes.restype = _i64
@@ -235,6 +238,57 @@ class Oracle:
         s = np.empty((rows, (i + group_size - 1) // group_size), np.float32)
         self.L.orc_quantize_w4_rows(w, rows, i, group_size, q, s)
         return q, s
+
+    def expert_rows(self, x, gate, up, down, h_fp8=False, nthreads=1, out=None):
+        """One expert's FFN on the rows of x [m, H] (orc_ffn per row, bit for bit)."""
+        x = np.ascontiguousarray(x, np.float32)
+        m, H = x.shape
+        I = gate.shape[0]
+        y = np.empty((m, H), np.float32) if out is None else out
+        assert y.shape == (m, H) and y.dtype == np.float32 and y.flags.c_contiguous
+        self.L.orc_expert_rows(x, m, H, I, np.ascontiguousarray(gate, np.float32),
+                               np.ascontiguousarray(up, np.float32),
+                               np.ascontiguousarray(down, np.float32), int(h_fp8), nthreads, y)
+        return y
+
+    def combine_slots(self, slot_rows, topk_w, shared_rows=None):
+        """out[t] = ((0 + w0*y0) + w1*y1 + ...) + y_shared[t] (orc_moe_worker's order)."""
+        slot_rows = np.ascontiguousarray(slot_rows, np.float32)
+        topk_w = np.ascontiguousarray(topk_w, np.float32)
+        n, topk = topk_w.shape
+        H = slot_rows.shape[-1]
+        assert slot_rows.size == n * topk * H
+        sh = None
+        if shared_rows is not None:
+            sh = np.ascontiguousarray(shared_rows, np.float32)
+            assert sh.shape == (n, H)
+        out = np.empty((n, H), np.float32)
+        self.L.orc_combine_slots(slot_rows, topk_w, None if sh is None else sh.ctypes.data, n,
+                                 topk, H, out)
+        return out
+
+    def moe_forward_streamed(self, x, ids, w, expert, shared=None, h_fp8=False, nthreads=8):
+        """The layer for given routing (ids, w [n, topk]) with the experts
+        materialized one at a time: expert(e) -> (gate, up, down) fp32. Equals
+        moe_forward on the same routing bit for bit, at a fraction of the memory
+        (one expert's weights at a time) and with row-batched arithmetic."""
+        x = np.ascontiguousarray(x, np.float32)
+        n, H = x.shape
+        ids = np.asarray(ids)
+        topk = ids.shape[1]
+        slots = np.empty((n * topk, H), np.float32)
+        flat = ids.ravel()
+        order = np.argsort(flat, kind="stable")
+        bounds = np.searchsorted(flat[order], np.arange(flat.max() + 2 if n else 1))
+        for e in np.unique(flat):
+            rows = order[bounds[e]:bounds[e + 1]]
+            g, u, d = expert(int(e))
+            slots[rows] = self.expert_rows(x[rows // topk], g, u, d, h_fp8, nthreads)
+        sh_rows = None
+        if shared is not None:
+            g, u, d = shared
+            sh_rows = self.expert_rows(x, g, u, d, h_fp8, nthreads)
+        return self.combine_slots(slots, w, sh_rows)
 
     def moe_forward(self, x, E, topk, gate, up, down, sh=None, router_w=None, logits=None,
                     e_bias=None, norm_topk=True, routed_scale=2.5, nthreads=1, h_fp8=False):

@@ -7,8 +7,14 @@ Values follow the benchmark definition: int4 codes uniform over [-8, 7],
 scales |N(0, 0.01)| in bf16, router weights bf16 N(0, 0.02), correction bias
 U(-0.1, 0.1), activations bf16 N(0, 1).
 """
+import os
+
 import numpy as np
 import torch
+
+# Host threads for the oracle's row-batched expert FFN (the GPU box gives a
+# process a 16-CPU share whatever os.cpu_count() reports).
+ORACLE_THREADS = max(1, min(16, os.cpu_count() or 1))
 
 
 def bf16_bits(a):
@@ -60,6 +66,7 @@ class SynthLayer:
         self.up = mat(E, I, H)
         self.down = mat(E, H, I)
         self.shared = (mat(1, I, H), mat(1, I, H), mat(1, H, I)) if shared else None
+        self.has_shared_expert = shared
         pk = lambda m, rows, K: pack_w4a16(m[0], m[1], m[0].shape[0], rows, K)
         sh_packed = None
         if shared:
@@ -105,6 +112,20 @@ class SynthLayer:
                                   nthreads=nthreads)
 
 
+def _oracle_full(L, oracle, xf, ids, w, h_fp8):
+    """Every token's oracle output for the given routing, experts materialized
+    one at a time (oracle.moe_forward_streamed)."""
+    sh = L.dequant_expert(oracle, L.E) if L.has_shared_expert else None
+    return oracle.moe_forward_streamed(xf, ids, w, lambda e: L.dequant_expert(oracle, e), sh,
+                                       h_fp8=h_fp8, nthreads=ORACLE_THREADS)
+
+
+def oracle_full_w4(L, oracle, x_bf16, ids, w):
+    """Oracle output of every token of a W4A16 layer for routing (ids, w)."""
+    xf = bits_to_f32(x_bf16.view(torch.int16).cpu().numpy().view(np.uint16))
+    return _oracle_full(L, oracle, xf, ids, w, h_fp8=False)
+
+
 def rel_err(got, ref):
     """max|got - ref| / max|ref|: the reference's tests/test_qgemm.cpp:17-26
     check() without its max(1, .) floor, which would make small-magnitude
@@ -130,6 +151,7 @@ class SynthFp8Layer:
         self.H, self.E, self.k, self.I, self.seed = H, E, k, I, seed
         self.norm_topk, self.routed_scale = norm_topk, routed_scale
         self.has_shared = shared
+        self.has_shared_expert = shared
         g = torch.Generator(device=device)
         g.manual_seed(seed)
         gc = torch.Generator(device="cpu")
@@ -203,6 +225,18 @@ class SynthFp8Layer:
         return oracle.moe_forward(xd, self.E, self.k, gate, up, down, sh, logits=lg, e_bias=eb,
                                   norm_topk=self.norm_topk, routed_scale=self.routed_scale,
                                   nthreads=nthreads, h_fp8=True)
+
+
+def oracle_full_fp8(L, oracle, x_bf16, ids, w):
+    """Oracle output of every token of an FP8 layer for routing (ids, w): x
+    quantized per token and 128 channels and dequantized, h quantized the
+    same way (SynthFp8Layer.oracle_forward's rule)."""
+    xf = bits_to_f32(x_bf16.view(torch.int16).cpu().numpy().view(np.uint16))
+    q, s = oracle.quant_act_e4m3(xf)
+    dec = np.array([oracle.e4m3_to_f32(c) for c in range(256)], np.float32)
+    n = xf.shape[0]
+    xd = (dec[q].reshape(n, -1, 128) * s[:, :, None]).reshape(n, L.H)
+    return _oracle_full(L, oracle, xd, ids, w, h_fp8=True)
 
 
 # GGUF types with block geometry (elements, bytes) and the byte offsets of

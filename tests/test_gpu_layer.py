@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from moe_cases import SynthLayer, rel_err
+from moe_cases import SynthLayer, oracle_full_w4, rel_err
 
 pytestmark = pytest.mark.gpu
 TOL_W4A16 = 2e-2
@@ -24,10 +24,25 @@ def _ws_f32(ws, ptr, numel):
     return ws[off:off + 4 * numel].view(torch.float32)
 
 
+def _nan_out(n, H):
+    """Output buffer pre-filled with NaN: a row the layer fails to write shows."""
+    return torch.full((n, H), float("nan"), dtype=torch.float32, device="cuda")
+
+
+def _check_full(out, ref):
+    assert np.isfinite(out).all(), "every output element written and finite"
+    assert rel_err(out, ref) < TOL_W4A16
+
+
+@pytest.fixture(scope="module")
+def full_layer():
+    return SynthLayer(6144, 256, 8, 2048, seed=1)
+
+
 def _run(L, n, seed):
     x = L.x(n, seed)
     ws = L.layer.alloc_workspace(n)
-    out = torch.empty(n, L.H, dtype=torch.float32, device="cuda")
+    out = _nan_out(n, L.H)
     L.layer.forward(x, out, ws)
     torch.cuda.synchronize()
     v = L.layer.workspace_view(n, ws)
@@ -69,42 +84,61 @@ def test_tiny_config(oracle, n):
     x, out, logits, ids, w, offs, st, sr = _run(L, n, seed=5)
     ref_logits = _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
     ref, _, _ = L.oracle_forward(oracle, x, np.arange(n), ref_logits)
-    assert rel_err(out, ref) < TOL_W4A16
+    _check_full(out, ref)
 
 
-@pytest.mark.parametrize("n", [1, 8, 64])
-def test_decode_full_shape(oracle, n):
-    # configs[1] geometry: H 6144, 256 experts, top-8, I = S = 2048.
-    L = SynthLayer(6144, 256, 8, 2048, seed=1)
+@pytest.mark.parametrize("n", [1, 8, 32, 64])
+def test_decode_full_shape(oracle, full_layer, n):
+    # configs[1] geometry: H 6144, 256 experts, top-8, I = S = 2048; every
+    # token's output against the oracle.
+    L = full_layer
     x, out, logits, ids, w, offs, st, sr = _run(L, n, seed=2)
-    ref_logits = _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
-    tok = np.arange(min(n, 4))
-    ref, _, _ = L.oracle_forward(oracle, x, tok, ref_logits)
-    assert rel_err(out[tok], ref) < TOL_W4A16
+    _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
+    _check_full(out, oracle_full_w4(L, oracle, x, ids, w))
 
 
-def test_prefill_full_shape(oracle):
-    # 4096 tokens through the large-group kernels.
-    L = SynthLayer(6144, 256, 8, 2048, seed=1)
+def test_prefill_full_shape(oracle, full_layer):
+    # configs[2] size through the large-group kernels, router-chosen routing:
+    # all 4096 tokens against the oracle.
+    L = full_layer
     n = 4096
     x, out, logits, ids, w, offs, st, sr = _run(L, n, seed=3)
-    ref_logits = _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
-    tok = np.array([0, 1, 2047, 4095])
-    ref, _, _ = L.oracle_forward(oracle, x, tok, ref_logits)
-    assert rel_err(out[tok], ref) < TOL_W4A16
+    _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
+    _check_full(out, oracle_full_w4(L, oracle, x, ids, w))
 
 
-def test_prefill_half_tiles(oracle):
+def test_prefill_uniform_routing(oracle, full_layer):
+    # configs[2] as specified: 4096 tokens with uniform-random routing (k
+    # distinct experts per token, ~128 rows per expert, every expert hit),
+    # through the expert-FFN entry on given ids and weights; every token.
+    L = full_layer
+    n = 4096
+    x = L.x(n, 13)
+    g = torch.Generator(device="cuda")
+    g.manual_seed(17)
+    ids = torch.rand(n, L.E, generator=g, device="cuda").topk(L.k, dim=1).indices
+    ids = ids.to(torch.int32).contiguous()
+    w = (torch.rand(n, L.k, generator=g, device="cuda") * 0.5).contiguous()
+    ws = L.layer.alloc_workspace(n)
+    out = _nan_out(n, L.H)
+    L.layer.expert_ffn(x, ids, w, out, ws)
+    torch.cuda.synchronize()
+    idn = ids.cpu().numpy()
+    assert len(np.unique(idn)) == L.E
+    _check_full(out.cpu().numpy(), oracle_full_w4(L, oracle, x, idn, w.cpu().numpy()))
+
+
+def test_prefill_half_tiles(oracle, full_layer):
     # Large-group tile list: tiles of more than 64 rows first (ntiles[1] of
     # them), then each expert's last tile of at most 64 rows, both in expert
     # order; together they cover every expert's rows exactly once. Half tiles
     # run as 64-row items of twice the features: tokens with rows in them
     # match the oracle.
-    L = SynthLayer(6144, 256, 8, 2048, seed=1)
+    L = full_layer
     n = 3000
     x = L.x(n, 31)
     ws = L.layer.alloc_workspace(n)
-    out = torch.empty(n, L.H, dtype=torch.float32, device="cuda")
+    out = _nan_out(n, L.H)
     L.layer.forward(x, out, ws)
     torch.cuda.synchronize()
     v = L.layer.workspace_view(n, ws)
@@ -124,14 +158,10 @@ def test_prefill_half_tiles(oracle):
         assert lo <= r0 and r0 + nr <= hi, (e, r0, nr)
         covered[r0:r0 + nr] += 1
     assert np.all(covered == 1)
-    # Tokens with a row in a half tile, of the routed and the shared expert.
-    picks = []
-    for e, r0, nr, _ in half[:: max(1, len(half) // 3)][:3]:
-        picks.append(int(st[r0 + nr - 1]))
-    tok = np.array(sorted(set(picks)))
-    logits = _ws_f32(ws, v.logits, n * L.E).view(n, L.E).cpu().numpy()
-    ref, _, _ = L.oracle_forward(oracle, x, tok, logits)
-    assert rel_err(out.cpu().numpy()[tok], ref) < TOL_W4A16
+    # Every token (rows in full tiles and in half tiles) against the oracle.
+    ids = _ws_i32(ws, v.topk_ids, n * L.k).view(n, L.k).cpu().numpy()
+    w = _ws_f32(ws, v.topk_w, n * L.k).view(n, L.k).cpu().numpy()
+    _check_full(out.cpu().numpy(), oracle_full_w4(L, oracle, x, ids, w))
 
 
 def test_spec_verify_zipf(oracle):
@@ -142,18 +172,16 @@ def test_spec_verify_zipf(oracle):
     ref_logits = _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
     counts = np.diff(offs)
     assert counts.max() > 100   # the skew really produces large groups
-    tok = np.array([0, 64, 65, 519])
-    ref, _, _ = L.oracle_forward(oracle, x, tok, ref_logits)
-    assert rel_err(out[tok], ref) < TOL_W4A16
+    _check_full(out, oracle_full_w4(L, oracle, x, ids, w))
 
 
-def test_decode_poisoned_workspace_deterministic():
+def test_decode_poisoned_workspace_deterministic(full_layer):
     # Decode batches whose expert work splits items across workgroups (the
     # last round of a launch) and whose routing runs the fused small-batch
     # kernel: with every workspace byte 0xFF (NaN patterns) beforehand and
     # batch sizes alternating, the output is finite and bit-identical to a
     # run on a zeroed workspace -- no state leaks between launches.
-    L = SynthLayer(6144, 256, 8, 2048, seed=1)
+    L = full_layer
     for n in (8, 1, 33, 8, 64, 1):
         x = L.x(n, 10 + n)
         outs = []
@@ -168,13 +196,13 @@ def test_decode_poisoned_workspace_deterministic():
         assert torch.equal(outs[0], outs[1]), n
 
 
-def test_batch_composition_bit_identical():
+def test_batch_composition_bit_identical(full_layer):
     # A token's routing, expert outputs and combine do not depend on the other
     # tokens of the batch (MFMA columns are independent, the combine adds in
     # slot order then the shared expert), so the same tokens give
     # bit-identical outputs at batch 1, 16 and 17 -- across different tile
     # layouts, workgroup assignments and ticket groupings.
-    L = SynthLayer(6144, 256, 8, 2048, seed=1)
+    L = full_layer
     x = L.x(17, 21)
     outs = {}
     for n in (17, 16, 1):

@@ -252,6 +252,28 @@ def test_moe_forward_vs_compiled_reference(oracle, ref):
     assert np.max(np.abs(out - rout)) <= 1e-6 * max(1.0, np.max(np.abs(rout)))
 
 
+@pytest.mark.parametrize("h_fp8", [False, True])
+def test_moe_forward_streamed_equals_per_token(oracle, ref, h_fp8):
+    # The expert-streamed form used for full-output GPU checks at large n
+    # (row-batched expert FFN, then the slot-order combine) is the per-token
+    # layer bit for bit: ragged expert groups (1 .. many rows, row blocks of
+    # 32 with partial tails), empty experts, and the shared expert. Without
+    # h quantization it also matches the compiled reference's moe_mlp.
+    L, rng = _tiny_layer(3)
+    n = 75
+    x = rng.standard_normal((n, 256)).astype(np.float32)
+    out, ids, w = oracle.moe_forward(x, 16, 4, L["g"], L["u"], L["d"], L["sh"], router_w=L["rw"],
+                                     e_bias=L["bias"], nthreads=3, h_fp8=h_fp8)
+    counts = np.bincount(ids.ravel(), minlength=16)
+    assert counts.max() > 32 and counts.min() <= 16
+    st = oracle.moe_forward_streamed(x, ids, w, lambda e: (L["g"][e], L["u"][e], L["d"][e]),
+                                     L["sh"], h_fp8=h_fp8, nthreads=3)
+    assert np.array_equal(st.view(np.uint32), out.view(np.uint32))
+    if not h_fp8:
+        rout, _ = ref.moe_mlp(x, L["rw"], L["bias"], L["g"], L["u"], L["d"], L["sh"], topk=4)
+        assert np.max(np.abs(st - rout)) <= 1e-6 * max(1.0, np.max(np.abs(rout)))
+
+
 def test_moe_forward_vs_fp64_bruteforce(oracle):
     L, rng = _tiny_layer(1)
     x = rng.standard_normal((8, 256)).astype(np.float32)
