@@ -179,11 +179,7 @@ struct F8Ring {
     static constexpr int kTab = kRed + 4 * kBigRows * 4;
     static constexpr int kTotal = kTab + kBigTable * kBigTabInts * 4;
     static_assert(kTotal <= 160 * 1024, "one workgroup's LDS");
-#ifdef GLMMOE_F8_NODMA
-    static constexpr int kDma = 0;   // diagnostics: compute on stale LDS, no streaming
-#else
     static constexpr int kDma = 4 + 2 + 1;                       // per wave per group
-#endif
     static __device__ __forceinline__ int swz(int r) { return (r >> 1) & 7; }
 };
 
@@ -243,9 +239,6 @@ __device__ __forceinline__ F8Issue f8_issue_ptrs(const F8Args& a, const BigItem&
 __device__ __forceinline__ void f8_issue(const F8Args& a, const F8Issue& p, int kg, char* slot,
                                          int wave) {
     using RG = F8Ring;
-#ifdef GLMMOE_F8_NODMA
-    return;
-#endif
     const uint8_t* src = p.w + (size_t)kg * 4096;
     char* dst = slot + wave * 4096;
 #pragma unroll
@@ -467,9 +460,7 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
 
         for (int step = 0; step < nsteps; ++step) {
             f32x16 p[2][2];
-#ifndef GLMMOE_F8_NOCOMPUTE
             if (live) f8_compute(ops, p);
-#endif
             if (step + 2 < nsteps) wait_vmcnt<RG::kDma>();
             else wait_vmcnt<0>();
             __builtin_amdgcn_s_barrier();
@@ -477,9 +468,7 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
             const float xs[2] = {ops.xs[0], ops.xs[1]};
             const float ws[2] = {ops.ws[0], ops.ws[1]};
             if (step + 1 < nsteps) f8_load_ops(lds + ((step + 1) % kF8D) * RG::kSlot, wave, lane, NMAT, ops);
-#ifndef GLMMOE_F8_NOCOMPUTE
             if (live) f8_rescale(xs, ws, p, acc);
-#endif
             if (++cur_g == KG) {
                 f8_epilogue<NMAT>(a, cur, lds, wave, lane, acc);
 #pragma unroll

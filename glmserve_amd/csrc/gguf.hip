@@ -575,11 +575,6 @@ __device__ __forceinline__ void gg_dots_i8(GgI8Tile<TT>& xt, int* srcs, const in
     }
 }
 
-// Diagnostic builds only: 1 skips the decode, 2 the weight loads after the first chunk.
-#ifndef GLMMOE_GG_DIAG
-#define GLMMOE_GG_DIAG 0
-#endif
-
 // ---- Streamed weights (the block types, one type per matrix set). Each wave
 // owns 4 weight rows per matrix; per K chunk it loads those rows' block bytes
 // with coalesced dword loads (lane l: dwords l, l + 64, ...) one chunk ahead
@@ -719,14 +714,12 @@ __device__ __forceinline__ void gg_dots_stream(GgStream<T, NM, TT, I8>& L, int* 
     __syncthreads();
     for (int c = 0; c < nch; ++c) {
         const int b = c & 1;
-#if GLMMOE_GG_DIAG != 2
         if (c + 1 < nch) load(c + 1);
-#endif
         const int kc = min(KC, K - c * KC);
 #pragma unroll
         for (int f = 0; f < KC / 512; ++f) {
             const int kk = f * 512 + lane * 8;
-            if (kk < kc && GLMMOE_GG_DIAG != 1) {
+            if (kk < kc) {
                 if constexpr (I8) {
                     int x0[TT], x1[TT], sx1[TT];
                     float sx[TT];

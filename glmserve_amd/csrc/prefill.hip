@@ -78,11 +78,7 @@ struct BigRing {
     static constexpr int kTab = kRed + 4 * kBigRows * 4;
     static constexpr int kTotal = kTab + kBigTable * kBigTabInts * 4;
     static_assert(kTotal <= 160 * 1024, "one workgroup's LDS");
-#ifdef GLMMOE_BIG_NODMA
-    static constexpr int kDma = 0;   // diagnostics: compute on stale LDS, no streaming
-#else
     static constexpr int kDma = 6;   // weight / activation DMAs per wave per group
-#endif
     // Plus one small DMA in waves 0-2: the scales of all the item's tiles
     // (wave 0, 16 B per lane) and the row group sums (waves 1, 2: rows 0-63,
     // 64-127). Every DMA instruction holds a slot of the CU's memory queue,
@@ -193,9 +189,6 @@ __device__ __forceinline__ IssuePtrs issue_ptrs(const BigArgs& a, const BigItem&
 __device__ __forceinline__ void big_issue(const BigArgs& a, const IssuePtrs& p, int kg, char* slot,
                                           int wave, int lane) {
     using RG = BigRing;
-#ifdef GLMMOE_BIG_NODMA
-    return;
-#endif
     const int hs = p.hs;
     const int nw = hs ? 4 : 2, nx = hs ? 2 : 4;
     const int xoff = hs ? RG::kX64 : RG::kX128;
@@ -319,11 +312,7 @@ __device__ __forceinline__ void big_compute(const char* slot, const BigGeo& gm, 
     for (int s = 0; s < 8; ++s) {
         const int cb = s & 1, nb = cb ^ 1;
         if (s > 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(av[cb][0]), "+v"(av[cb][1]));
-#ifdef GLMMOE_BIG_NOAREAD
-        if (false) {
-#else
         if (s < 7) {
-#endif
             const uint32_t xs_addr = xa0 ^ (uint32_t)((s + 1) << 4);
             asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:8192"
                          : "=&v"(av[nb][0]), "=&v"(av[nb][1]) : "v"(xs_addr));
@@ -445,27 +434,11 @@ __device__ __forceinline__ void big_epilogue(const BigArgs& a, const BigItem& cu
     }
 }
 
-#ifdef GLMMOE_BIG_TRACE
-// Diagnostics: per-wave shader-clock totals of the main-loop phases (compute,
-// DMA wait, barrier, issue + operand reads, rescale, epilogue), printed for
-// the first workgroups.
-#define BIG_T(i)                                                        \
-    do {                                                                \
-        const unsigned long long t_ = __builtin_amdgcn_s_memtime();     \
-        bt_[(i)] += t_ - bt_last_;                                      \
-        bt_last_ = t_;                                                  \
-    } while (0)
-#else
 #define BIG_T(i) do {} while (0)
-#endif
 
 template <int NMAT>
 __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
     using RG = BigRing;
-#ifdef GLMMOE_BIG_TRACE
-    unsigned long long bt_[6] = {0, 0, 0, 0, 0, 0};
-    unsigned long long bt_last_ = __builtin_amdgcn_s_memtime();
-#endif
     extern __shared__ __align__(16) char lds[];
     const DqConst dqc = dq_const();
     int* table = reinterpret_cast<int*>(lds + RG::kTab);
@@ -523,19 +496,15 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
 
         for (long step = 0; step < nsteps; ++step) {
             f32x16 p[2][2];
-#ifndef GLMMOE_BIG_NOCOMPUTE
             // A wave whose 64 rows are all past the tile's end skips the group;
             // a half-live wave computes both 32-row blocks (one branch-free body
             // keeps the accumulators in fixed registers).
             if (live) big_compute(lds + (step % kBigD) * RG::kSlot, gc, lane, dqc, ops, p);
-#endif
             BIG_T(0);
             if (step + 2 < nsteps) big_wait_groups<1>(small);
             else wait_vmcnt<0>();
             BIG_T(1);
-#ifndef GLMMOE_BIG_NOBARRIER
             __builtin_amdgcn_s_barrier();
-#endif
             BIG_T(2);
             if (step + kBigD < nsteps) issue_next(step + kBigD);
             const uint32_t sc[2] = {ops.sc[0], ops.sc[1]};
@@ -545,9 +514,7 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
                 big_load_ops(lds + ((step + 1) % kBigD) * RG::kSlot, gn, lane, ops);
             }
             BIG_T(3);
-#ifndef GLMMOE_BIG_NOCOMPUTE
             if (live) big_rescale(sc, p, acc);
-#endif
             BIG_T(4);
             if (++cur_g == KG) {
                 big_epilogue<NMAT>(a, cur, lds, gc, lane, acc);
@@ -571,11 +538,6 @@ __global__ __launch_bounds__(512) void w4_big_kernel(BigArgs a) {
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();
     }
-#ifdef GLMMOE_BIG_TRACE
-    if (lane == 0 && blockIdx.x < 3)
-        printf("BIGT %d wg %d w %d: comp %llu vmw %llu bar %llu iss %llu resc %llu epi %llu\n", NMAT,
-               (int)blockIdx.x, wave, bt_[0], bt_[1], bt_[2], bt_[3], bt_[4], bt_[5]);
-#endif
 }
 
 template <int NMAT>

@@ -691,20 +691,6 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
 // use this path together.
 // ---------------------------------------------------------------------------
 constexpr int kSmallThreads = 512;
-#ifdef GLMMOE_SMALL_TRACE
-// Diagnostics: shader-clock stamps of each workgroup's phases (one row per
-// workgroup: start, staged, logits stored, top-k start/end, dispatch
-// start/end).
-__device__ unsigned long long g_small_trace[8192][8];
-#define SMALL_STAMP(i)                                                               \
-    do {                                                                             \
-        const unsigned long long ts_ = __builtin_amdgcn_s_memtime();                 \
-        if (threadIdx.x == 0)                                                        \
-            g_small_trace[blockIdx.y * gridDim.x + blockIdx.x][(i)] = ts_;           \
-    } while (0)
-#else
-#define SMALL_STAMP(i) do {} while (0)
-#endif
 constexpr int kSmallMaxChunks = 64;
 // Staged activation bytes: 8 tokens x nchunks rows of 256 B, whole 1 KiB DMAs.
 __host__ __device__ constexpr int small_x_bytes(int nchunks) {
@@ -777,7 +763,6 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     uint32_t* __restrict__ cs) {
     extern __shared__ __align__(16) char small_lds[];
     __shared__ int last;
-    SMALL_STAMP(0);
     const int nchunks = H / kRouterKC;
     const int tid = threadIdx.x;
     const int eb = blockIdx.x, tg = blockIdx.y;
@@ -818,7 +803,6 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     }
     wait_vmcnt<0>();
     __syncthreads();
-    SMALL_STAMP(1);
     if (active) {
         float* out = part + pair * kRouterTG;
         if (tcnt == 1) small_chunk_dots<1>(xl, wv, c, nchunks, tb, tcnt, out);
@@ -863,7 +847,6 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
             st_dev(reinterpret_cast<float*>(cs) + (size_t)n * E + o, sc);
         }
     }
-    SMALL_STAMP(2);
     // This workgroup's logits are complete in memory; take the group ticket.
     drain_vm();
     __syncthreads();
@@ -872,15 +855,13 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
         if (last) reset_dev(&g_small_tick[tg]);
     }
     __syncthreads();
-    if (!last || do_disp < 0) return;
-    SMALL_STAMP(3);
+    if (!last) return;
     __shared__ uint32_t tscratch[kSmallThreads / 64][kTopkScratch];
     for (int t = tid >> 6; t < nt; t += kSmallThreads / 64)
         topk_wave<true>(logits + (size_t)(t0 + t) * E, e_bias, E, topk, norm_topk, routed_scale,
                         ids + (size_t)(t0 + t) * topk, w + (size_t)(t0 + t) * topk,
                         tscratch[tid >> 6], cs + (size_t)(t0 + t) * E,
                         reinterpret_cast<const float*>(cs) + (size_t)n * E + (size_t)(t0 + t) * E);
-    SMALL_STAMP(4);
     if (do_disp <= 0) return;
     drain_vm();
     __syncthreads();
@@ -890,9 +871,7 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     }
     __syncthreads();
     if (!last) return;
-    SMALL_STAMP(5);
     dispatch_block<kSmallThreads, true>(ids, n, topk, E, d, reinterpret_cast<int*>(small_lds));
-    SMALL_STAMP(6);
 }
 
 size_t router_select_scratch_bytes(int n, int H, int E) {
@@ -907,7 +886,6 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
                          const DispOut* disp, bool* dispatched) {
     const int nchunks = H / kRouterKC;
     if (dispatched) *dispatched = false;
-#ifndef GLMMOE_NO_SMALL_ROUTER
     if (n < kTiledMinTokens && H % kRouterKC == 0 && nchunks <= kSmallMaxChunks &&
         E <= 64 * kMaxPerLane && topk <= 8) {
         // scratch: the order codes and scores [2][n][E] handed to the top-k.
@@ -932,11 +910,8 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         while (slices < kRouterTG && 2 * slices * epw * nchunks <= kSmallThreads) slices *= 2;
         const bool dd = disp && E <= kDispMaxE;
         dim3 grid((unsigned)((E + epw - 1) / epw), (unsigned)((n + kRouterTG - 1) / kRouterTG));
-#ifndef GLMMOE_SMALL_MODE
-#define GLMMOE_SMALL_MODE 2
-#endif
-        // mode: -1 logits only, 0 + top-k, 1 + top-k and dispatch.
-        const int mode = GLMMOE_SMALL_MODE == 0 ? -1 : GLMMOE_SMALL_MODE == 1 ? 0 : (dd ? 1 : 0);
+        // mode: 0 logits and top-k, 1 logits, top-k and dispatch.
+        const int mode = dd ? 1 : 0;
         // The dispatch reuses the staging area.
         size_t lds = (size_t)small_x_bytes(nchunks) + (size_t)epw * nchunks * kRouterTG * 4;
         if (lds < (size_t)dispatch_lds_ints<kSmallThreads>() * 4) lds = dispatch_lds_ints<kSmallThreads>() * 4;
@@ -953,11 +928,9 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
                            H, E, epw, topk, norm_topk, routed_scale, logits, xsum, ids, w,
                            dd ? *disp : DispOut{}, mode, slices, reinterpret_cast<uint32_t*>(scratch));
         if (hipGetLastError() != hipSuccess) return -4;
-        if (mode < 0) return launch_router_topk(logits, e_bias, n, E, topk, norm_topk, routed_scale, ids, w, s);
         if (dispatched) *dispatched = mode == 1;
         return 0;
     }
-#endif
     if (n >= kTiledMinTokens && H % kMfmaK == 0 && H % kRouterKC == 0 && nchunks <= 64 &&
         E <= 64 * kMaxPerLane) {
         if (!scratch) return -3;

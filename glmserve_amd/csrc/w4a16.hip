@@ -146,11 +146,7 @@ struct Ring {
     static constexpr int kRed = kBytes;                               // [NW][16] h group-sum partials
     static constexpr int kTotal = kRed + NW * 64 + kTable * kTabInts * 4;   // + the item table
     static_assert(kTotal * (8 / NW) <= 160 * 1024, "8 / NW workgroups per CU");
-#ifdef GLMMOE_EXP_NODMA
-    static constexpr int kDma = 0;   // diagnostics: compute on stale LDS, no streaming
-#else
     static constexpr int kDma = NMAT * PF + 2 + kXDma;            // DMA instructions per batch per wave
-#endif
 };
 
 // Work items of a workgroup come in steps k: WG-item base + k * nwg is
@@ -230,9 +226,6 @@ template <int NMAT, int PF, int D, int NW>
 __device__ __forceinline__ void issue_batch(const ExpArgs& a, const Item& it, int bb, int K,
                                             int KG, char* slot, int wave, int lane) {
     using RG = Ring<NMAT, PF, D, NW>;
-#ifdef GLMMOE_EXP_NODMA
-    return;
-#endif
     const int kg0 = bb * PF;
     // Weight tiles: [wave][m][i] 1 KiB each, lane-contiguous like the global tile.
 #pragma unroll
@@ -440,9 +433,7 @@ __global__ __launch_bounds__(NW * 64) void w4_expert_kernel(ExpArgs a) {
             if (step + 1 < nsteps)
                 exp_load_batch<NMAT, PF, D, NW>(ring + ((u + 1) % D) * RG::kSlot, wave, lane,
                                                 ops[(u + 1) & 1]);
-#ifndef GLMMOE_EXP_NOCOMPUTE
             exp_compute_batch<NMAT, PF>(now, dqc, acc);
-#endif
             if (++cur_b == nbatch) {
                 const bool valid = r < cur.nr;
                 const size_t row = (size_t)cur.r0 + r;
@@ -520,14 +511,8 @@ __device__ __forceinline__ void static_for(F&& f) {
     static_for_impl(f, std::make_integer_sequence<int, N>{});
 }     // K-groups per activation batch
 constexpr int kSActDma = 9;  // activation + group-sum DMAs per wave per batch
-#ifndef GLMMOE_SP_GU
-#define GLMMOE_SP_GU 4
-#endif
-#ifndef GLMMOE_SP_DOWN
-#define GLMMOE_SP_DOWN 8
-#endif
-constexpr int kSPGU = GLMMOE_SP_GU;
-constexpr int kSPDown = GLMMOE_SP_DOWN;
+constexpr int kSPGU = 4;
+constexpr int kSPDown = 8;
 
 // Stream table step: {expert, row0, nrows, block group}, the 16 token ids,
 // then {first batch, batches, tail item or -1, 0}.
@@ -561,9 +546,6 @@ __device__ __forceinline__ SSched s_sched(int total, int nwg, int base, int BPI)
     // finishing cost more than the shorter round saves.
     sc.split = BPI > 1 && sc.R > 0 && sc.rem > 0 && sc.rem <= kMaxTail && parts <= kMaxTailParts &&
                (parts + nwg - 1) / nwg < BPI;
-#ifdef GLMMOE_NO_TAIL_SPLIT
-    sc.split = 0;
-#endif
     if (sc.split)
         sc.nunits = sc.R + (base < parts ? (parts - base + nwg - 1) / nwg : 0);
     else
@@ -935,13 +917,11 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
                 SOps& o = ops[j & 1];
                 s_wait_ops(o);
                 if constexpr (j + 1 < kSGB) s_load_ops<j + 1>(cb, ops[(j + 1) & 1]);
-#ifndef GLMMOE_EXP_NOCOMPUTE
                 s_compute<NMAT>(o, W[j % P], Sc[j % P], dqc, acc);
                 // Pin the rescale to this step (otherwise it is deferred and
                 // every step's partial products and scales stay live).
 #pragma unroll
                 for (int m = 0; m < NMAT; ++m) asm volatile("" : "+v"(acc[m]));
-#endif
                 // The slot is free again: group j + P goes into it.
                 issue_w(W[j % P], Sc[j % P]);
                 __builtin_amdgcn_sched_barrier(0);
@@ -1072,22 +1052,12 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
 
 // ---------------------------------------------------------------------------
 // Ring depth and batch size per projection (one 8-wave workgroup per CU).
-#ifndef GLMMOE_RING_GU
-#define GLMMOE_RING_GU 3
-#define GLMMOE_PF_GU 2
-#define GLMMOE_NW_GU 8
-#endif
-#ifndef GLMMOE_RING_DOWN
-#define GLMMOE_RING_DOWN 4
-#define GLMMOE_PF_DOWN 2
-#define GLMMOE_NW_DOWN 8
-#endif
-constexpr int kRingGU = GLMMOE_RING_GU;
-constexpr int kRingDown = GLMMOE_RING_DOWN;
-constexpr int kPFGU = GLMMOE_PF_GU;
-constexpr int kPFDown = GLMMOE_PF_DOWN;
-constexpr int kNWGU = GLMMOE_NW_GU;
-constexpr int kNWDown = GLMMOE_NW_DOWN;
+constexpr int kRingGU = 3;
+constexpr int kRingDown = 4;
+constexpr int kPFGU = 2;
+constexpr int kPFDown = 2;
+constexpr int kNWGU = 8;
+constexpr int kNWDown = 8;
 
 template <int NMAT, int PF, int D, int NW>
 static int launch_expert(const ExpArgs& a, long max_work, hipStream_t s) {
@@ -1123,10 +1093,8 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, co
     a.src = x; a.gsum = xsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.rows_tok = rows_tok; a.h = h; a.hsum = hsum; a.H = H; a.I = I; a.E = E;
     const long work = (long)max_tiles * (I / 16 / kNWGU);
-#ifndef GLMMOE_NO_STREAM
     if ((H / 128) % kSGB == 0)
         return launch_stream<0>(a, (long)max_tiles * (I / 128) * (H / 128 / kSGB), s);
-#endif
     if ((H / 128) % kPFGU == 0) return launch_expert<2, kPFGU, kRingGU, kNWGU>(a, work, s);
     return launch_expert<2, 1, 6, kNWGU>(a, work, s);   // odd K-group count
 }
@@ -1141,10 +1109,8 @@ int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const
     a.src = h; a.gsum = hsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.dpart = dpart; a.H = H; a.I = I; a.E = E;
     const long work = (long)max_tiles * (H / 16 / kNWDown);
-#ifndef GLMMOE_NO_STREAM
     // Two 16-row blocks per wave (the layer's hidden size is a multiple of 256).
     if ((I / 128) % kSGB == 0 && H % 256 == 0) return launch_stream<2>(a, (long)max_tiles * (H / 256), s);
-#endif
     if ((I / 128) % kPFDown == 0) return launch_expert<1, kPFDown, kRingDown, kNWDown>(a, work, s);
     return launch_expert<1, 1, 6, kNWDown>(a, work, s);   // odd K-group count
 }
