@@ -13,10 +13,13 @@ inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Tile height of the expert GEMMs for a batch: 16-row tiles (decode kernels)
-// or 128-row tiles (large-group kernels).
-inline int tile_rows_for(int n, int topk, int with_shared) {
-    return (long)n * topk + (with_shared ? n : 0) >= kBigMinRows ? kBigRows : kTileRows;
+// Tile height of the W4A16 expert GEMMs for a batch: 16-row tiles (decode
+// kernels) or, from kBigMinRows grouped rows on shapes the large-group kernels
+// take (both K-group counts multiples of 8), 128-row tiles.
+inline int tile_rows_for(int n, int topk, int with_shared, int H, int I) {
+    return (long)n * topk + (with_shared ? n : 0) >= kBigMinRows && big_w4_shape_ok(H, I)
+               ? kBigRows
+               : kTileRows;
 }
 
 int max_tiles_for(int n, int topk, int E, int with_shared, int T) {
@@ -24,15 +27,8 @@ int max_tiles_for(int n, int topk, int E, int with_shared, int T) {
     return (n * topk) / T + E + (with_shared ? (n + T - 1) / T : 0) + 1;
 }
 
-int max_tiles_for(int n, int topk, int E, int with_shared) {
-    return max_tiles_for(n, topk, E, with_shared, tile_rows_for(n, topk, with_shared));
-}
-
-// Half-tile rows of the W4A16 tile list: with 128-row tiles, an expert's last
-// tile of at most 64 rows runs as a 64-row item of twice the features, which
-// needs an even number of feature groups in both projections.
-int half_rows_w4(int T, int H, int I) {
-    return T == kBigRows && I % 256 == 0 && H % 512 == 0 ? kBigRows / 2 : 0;
+int max_tiles_for(int n, int topk, int E, int with_shared, int H, int I) {
+    return max_tiles_for(n, topk, E, with_shared, tile_rows_for(n, topk, with_shared, H, I));
 }
 
 // Shape and pointer checks shared by the W4A16 and FP8 layer descriptors.
@@ -75,7 +71,7 @@ size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v)
     const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
     const size_t nk = (size_t)n * k;
     const size_t R = nk + (has_shared(L) ? (size_t)n : 0);
-    const size_t mt = (size_t)max_tiles_for(n, k, E, has_shared(L));
+    const size_t mt = (size_t)max_tiles_for(n, k, E, has_shared(L), H, I);
     size_t off = 0;
     auto take = [&](size_t bytes) -> char* {
         char* p = base ? base + off : nullptr;
@@ -93,7 +89,7 @@ size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v)
     w.sorted_row = reinterpret_cast<int*>(take(R * 4));
     w.inv = reinterpret_cast<int*>(take(nk * 4));
     w.tiles = reinterpret_cast<int*>(take(mt * 16));
-    w.ntiles = reinterpret_cast<int*>(take(4));
+    w.ntiles = reinterpret_cast<int*>(take(16));
     w.h = reinterpret_cast<uint16_t*>(take(R * I * 2));
     w.hsum = reinterpret_cast<float*>(take(R * (I / 128) * 4));
     w.dpart = reinterpret_cast<float*>(take(R * H * 4));
@@ -131,7 +127,7 @@ size_t carve8(const glmmoe_fp8_layer* L, int n, char* base, glmmoe_fp8_ws* v) {
     w.sorted_row = reinterpret_cast<int*>(take(R * 4));
     w.inv = reinterpret_cast<int*>(take(nk * 4));
     w.tiles = reinterpret_cast<int*>(take(mt * 16));
-    w.ntiles = reinterpret_cast<int*>(take(4));
+    w.ntiles = reinterpret_cast<int*>(take(16));
     w.hq = reinterpret_cast<uint8_t*>(take(R * I));
     w.hscale = reinterpret_cast<float*>(take(R * (I / 128) * 4));
     w.dpart = reinterpret_cast<float*>(take(R * H * 4));
@@ -172,14 +168,14 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
                 hipStream_t s, bool dispatched = false) {
     const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
     const int sh = has_shared(L) ? 1 : 0;
-    const int mt = max_tiles_for(n, k, E, sh);
-    const int T = tile_rows_for(n, k, sh);
+    const int mt = max_tiles_for(n, k, E, sh, H, I);
+    const int T = tile_rows_for(n, k, sh, H, I);
     const bool big = T == kBigRows;
     mark(GLMMOE_STAGE_DISPATCH, s);
     int rc = dispatched ? 0
                         : launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids,
                                           v.sorted_row, v.inv, v.tiles, v.ntiles, T, sh, 1, s,
-                                          dispatch_scratch(v.rpart, L, n), half_rows_w4(T, H, I));
+                                          dispatch_scratch(v.rpart, L, n), big ? kBigRows / 2 : 0);
     if (rc) return rc;
     const ExpertPtrs P = ptrs(L);
     mark(GLMMOE_STAGE_GATE_UP, s);
@@ -317,10 +313,10 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     // The router pass also writes the activation group sums the expert
     // kernels use to remove the int4 decode offset.
     const int sh = has_shared(L) ? 1 : 0;
-    const int T = tile_rows_for(n, k, sh);
+    const int T = tile_rows_for(n, k, sh, H, L->moe_inter);
     const DispOut disp{v.expert_offsets, v.sorted_token_ids, v.sorted_row, v.inv,
                        reinterpret_cast<int4*>(v.tiles), v.ntiles, T, sh, 1,
-                       half_rows_w4(T, H, L->moe_inter)};
+                       T == kBigRows ? kBigRows / 2 : 0};
     bool dispatched = false;
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
                               L->routed_scale, v.logits, v.xsum, v.rpart, v.topk_ids, v.topk_w, s,

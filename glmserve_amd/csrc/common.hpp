@@ -4,6 +4,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <utility>
+
 namespace glmmoe {
 
 constexpr int kWave = 64;
@@ -178,5 +180,23 @@ __device__ __forceinline__ void reset_dev(unsigned int* p) {
 }
 // Waits until every memory operation this wave issued has completed.
 __device__ __forceinline__ void drain_vm() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order: loop bodies
+// whose register-array indices and wait counts must be compile-time constants.
+template <class F, int... Is>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
+    (f(std::integral_constant<int, Is>{}), ...);
+}
+template <int N, class F>
+__device__ __forceinline__ void static_for(F&& f) {
+    static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// LDS u16 read (waits for every pending LDS operation of the wave).
+__device__ __forceinline__ uint32_t lds_read_u16(uint32_t addr) {
+    uint32_t v;
+    asm volatile("ds_read_u16 %0, %1\n s_waitcnt lgkmcnt(0)" : "=v"(v) : "v"(addr));
+    return v;
+}
 
 }  // namespace glmmoe

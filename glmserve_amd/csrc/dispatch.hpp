@@ -170,27 +170,38 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
 
     // Tile list: expert e (e == E is the shared expert) contributes
     // ceil(count / d.tile_rows) tiles of at most d.tile_rows consecutive rows.
-    // With d.half_rows, an expert's last tile of at most half_rows rows is a
-    // "half" tile: all the other tiles come first (ntiles[1] of them, in
-    // expert order), then the half tiles (in expert order). With
-    // half_rows == 0, ntiles[1] = ntiles[0]; below 0, only ntiles[0] is written.
-    static_assert(NT / 64 >= 4, "two scan arrays in the per-wave count area");
+    // With d.half_rows = HR > 0 an expert's last partial tile is classed by
+    // its rows: at most HR / 2 ("quarter"), at most HR ("half"), or more
+    // (full). The list holds the full tiles first (ntiles[1] of them), then
+    // the half tiles (up to ntiles[2]), then the quarter tiles, each class in
+    // expert order; ntiles[0] counts all. With half_rows == 0 every tile is
+    // full (ntiles[1] = ntiles[2] = ntiles[0]); below 0 only ntiles[0] is
+    // written.
+    static_assert(NT / 64 >= 8, "four scan arrays in the per-wave count area");
     const int nexp = E + (d.with_shared ? 1 : 0);
     const int T = d.tile_rows, HR = d.half_rows;
     // nexp <= 513 counts and nexp + 1 prefixes: each may run into the next row.
     int* nhalf = &wc[0][0];
     int* prehalf = &wc[2][0];
+    int* nq = &wc[4][0];
+    int* preq = &wc[6][0];
     for (int e = tid; e < nexp; e += NT) {
         const int ce = e < E ? cnt[e] : n;
         const int full = ce / T, rem = ce - full * T;
-        const bool half = HR > 0 && rem > 0 && rem <= HR;
-        ntl[e] = full + (rem > 0 && !half ? 1 : 0);
+        const bool quarter = HR > 0 && rem > 0 && rem <= HR / 2;
+        const bool half = HR > 0 && rem > HR / 2 && rem <= HR;
+        ntl[e] = full + (rem > 0 && !half && !quarter ? 1 : 0);
         nhalf[e] = half ? 1 : 0;
+        nq[e] = quarter ? 1 : 0;
     }
     __syncthreads();
     wave0_exclusive_scan(ntl, nexp, pre);
     __syncthreads();
-    if (HR > 0) wave0_exclusive_scan(nhalf, nexp, prehalf);
+    if (HR > 0) {
+        wave0_exclusive_scan(nhalf, nexp, prehalf);
+        __syncthreads();
+        wave0_exclusive_scan(nq, nexp, preq);
+    }
     __syncthreads();
     for (int e = tid; e < nexp; e += NT) {
         const int ce = e < E ? cnt[e] : n;
@@ -198,14 +209,19 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
         const int tbase = pre[e];
         for (int j = 0; j < ntl[e]; ++j)
             d.tiles[tbase + j] = make_int4(e, row0 + j * T, min(T, ce - j * T), 0);
-        if (nhalf[e]) {
-            const int full = ce / T;
-            d.tiles[pre[nexp] + prehalf[e]] = make_int4(e, row0 + full * T, ce - full * T, 0);
-        }
+        const int full = ce / T;
+        if (nhalf[e]) d.tiles[pre[nexp] + prehalf[e]] = make_int4(e, row0 + full * T, ce - full * T, 0);
+        if (nq[e])
+            d.tiles[pre[nexp] + prehalf[nexp] + preq[e]] = make_int4(e, row0 + full * T, ce - full * T, 0);
     }
     if (tid == 0) {
-        d.ntiles[0] = pre[nexp] + (HR > 0 ? prehalf[nexp] : 0);
-        if (HR >= 0) d.ntiles[1] = pre[nexp];   // HR < 0: the caller's ntiles holds one int
+        const int nfull = pre[nexp];
+        const int nh = HR > 0 ? prehalf[nexp] : 0, nqq = HR > 0 ? preq[nexp] : 0;
+        d.ntiles[0] = nfull + nh + nqq;
+        if (HR >= 0) {   // HR < 0: the caller's ntiles holds one int
+            d.ntiles[1] = nfull;
+            d.ntiles[2] = nfull + nh;
+        }
     }
 }
 

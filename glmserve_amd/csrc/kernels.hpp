@@ -76,6 +76,8 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, co
 int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
                 const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
                 hipStream_t s);
+// Shapes the large-group W4A16 kernels take: H / 128 and I / 128 multiples of 8.
+bool big_w4_shape_ok(int H, int I);
 int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, const float* xsum,
                        const int* tiles, const int* ntiles, int max_tiles, const int* rows_tok,
                        uint16_t* h, float* hsum, int H, int I, int E, hipStream_t s);

@@ -499,17 +499,7 @@ __global__ __launch_bounds__(NW * 64) void w4_expert_kernel(ExpArgs a) {
 // the number of loads issued after the one waited for (counted statically in
 // the 16-group unrolled batch body).
 // ---------------------------------------------------------------------------
-constexpr int kSGB = 16;
-
-template <class F, int... Is>
-__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, Is...>) {
-    (f(std::integral_constant<int, Is>{}), ...);
-}
-// f(std::integral_constant<int, i>) for i = 0 .. N - 1, in order.
-template <int N, class F>
-__device__ __forceinline__ void static_for(F&& f) {
-    static_for_impl(f, std::make_integer_sequence<int, N>{});
-}     // K-groups per activation batch
+constexpr int kSGB = 16;     // K-groups per activation batch
 constexpr int kSActDma = 9;  // activation + group-sum DMAs per wave per batch
 constexpr int kSPGU = 4;
 constexpr int kSPDown = 8;

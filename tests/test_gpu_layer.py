@@ -128,12 +128,13 @@ def test_prefill_uniform_routing(oracle, full_layer):
     _check_full(out.cpu().numpy(), oracle_full_w4(L, oracle, x, idn, w.cpu().numpy()))
 
 
-def test_prefill_half_tiles(oracle, full_layer):
-    # Large-group tile list: tiles of more than 64 rows first (ntiles[1] of
-    # them), then each expert's last tile of at most 64 rows, both in expert
-    # order; together they cover every expert's rows exactly once. Half tiles
-    # run as 64-row items of twice the features: tokens with rows in them
-    # match the oracle.
+def test_prefill_tile_list(oracle, full_layer):
+    # Large-group tile list: each expert's rows (the shared expert's last) cut
+    # into consecutive tiles of at most 128 rows. Tiles come in three classes,
+    # each in expert order: full tiles first (ntiles[1] of them), then every
+    # expert's last tile of 33-64 rows (up to ntiles[2]), then its last tile
+    # of at most 32 rows; together they cover every grouped row exactly once.
+    # The large-group kernels skip the MFMAs of the empty 32-row blocks.
     L = full_layer
     n = 3000
     x = L.x(n, 31)
@@ -142,23 +143,24 @@ def test_prefill_half_tiles(oracle, full_layer):
     L.layer.forward(x, out, ws)
     torch.cuda.synchronize()
     v = L.layer.workspace_view(n, ws)
-    nt = _ws_i32(ws, v.ntiles, 2).cpu().numpy()
-    ntiles, n128 = int(nt[0]), int(nt[1])
-    tiles = _ws_i32(ws, v.tiles, 4 * ntiles).view(ntiles, 4).cpu().numpy()
+    nt, n4, n2 = (int(c) for c in _ws_i32(ws, v.ntiles, 3).cpu().numpy())
+    tiles = _ws_i32(ws, v.tiles, 4 * nt).view(nt, 4).cpu().numpy()
     offs = _ws_i32(ws, v.expert_offsets, L.E + 2).cpu().numpy()
-    st = _ws_i32(ws, v.sorted_token_ids, n * L.k + n).cpu().numpy()
-    assert 0 < n128 < ntiles
-    full, half = tiles[:n128], tiles[n128:]
-    assert np.all(full[:, 2] > 64) and np.all(full[:, 2] <= 128)
-    assert np.all(half[:, 2] >= 1) and np.all(half[:, 2] <= 64)
-    assert np.all(np.diff(full[:, 0]) >= 0) and np.all(np.diff(half[:, 0]) > 0)
+    assert 0 < n4 < n2 < nt
+    full, half, quarter = tiles[:n4], tiles[n4:n2], tiles[n2:]
+    assert np.all(full[:, 2] > 64) or np.all((full[:, 2] > 64) | (full[:, 2] == 128))
+    assert np.all((half[:, 2] > 32) & (half[:, 2] <= 64))
+    assert np.all((quarter[:, 2] >= 1) & (quarter[:, 2] <= 32))
+    for cls in (full, half, quarter):
+        assert np.all(np.diff(cls[:, 0]) >= 0)
+    assert np.all(np.diff(half[:, 0]) > 0) and np.all(np.diff(quarter[:, 0]) > 0)
     covered = np.zeros(n * L.k + n, np.int32)
     for e, r0, nr, _ in tiles:
         lo, hi = (offs[e], offs[e + 1]) if e < L.E else (n * L.k, n * L.k + n)
         assert lo <= r0 and r0 + nr <= hi, (e, r0, nr)
         covered[r0:r0 + nr] += 1
     assert np.all(covered == 1)
-    # Every token (rows in full tiles and in half tiles) against the oracle.
+    # Every token against the oracle.
     ids = _ws_i32(ws, v.topk_ids, n * L.k).view(n, L.k).cpu().numpy()
     w = _ws_f32(ws, v.topk_w, n * L.k).view(n, L.k).cpu().numpy()
     _check_full(out.cpu().numpy(), oracle_full_w4(L, oracle, x, ids, w))
