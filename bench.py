@@ -169,6 +169,8 @@ def main():
     ap.add_argument("--head-batch", type=int, default=64,
                     help="batch of the headline line (64 = configs[1]'s largest); for profiling")
     ap.add_argument("--no-fp8", action="store_true", help="skip the configs[4] FP8 sweep line")
+    ap.add_argument("--prefill-only", action="store_true",
+                    help="only time the 4096-token prefill of configs[2] (uniform routing; for profiling)")
     ap.add_argument("--fp8-only", action="store_true",
                     help="only time the FP8 8192-token prefill (for profiling)")
     ap.add_argument("--gguf-only", action="store_true",
@@ -381,6 +383,11 @@ def main():
         r = summarize(n, ms, U, st)
         r["routing"] = "uniform-random expert ids (k distinct per token); router timed on the real logits"
         return r
+
+    if args.prefill_only:
+        r = measure_uniform(4096, args.steps, args.warmup)
+        print(json.dumps({"prefill_4096": r}), flush=True)
+        return
 
     log(f"bench: headline B={args.head_batch}")
     head = measure(args.head_batch, args.steps, args.warmup)

@@ -179,13 +179,13 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     if (rc) return rc;
     const ExpertPtrs P = ptrs(L);
     mark(GLMMOE_STAGE_GATE_UP, s);
-    rc = big ? launch_gate_up_big(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h,
-                                  v.hsum, H, I, E, s)
+    rc = big ? launch_gate_up_big(P, x, n, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.dpart,
+                                  H, I, E, s)
              : launch_gate_up(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.hsum,
                               H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_DOWN, s);
-    rc = big ? launch_down_big(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
+    rc = big ? launch_down_big(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
              : launch_down(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_COMBINE, s);

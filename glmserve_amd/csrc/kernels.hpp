@@ -78,12 +78,13 @@ int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const
                 hipStream_t s);
 // Shapes the large-group W4A16 kernels take: H / 128 and I / 128 multiples of 8.
 bool big_w4_shape_ok(int H, int I);
-int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, const float* xsum,
-                       const int* tiles, const int* ntiles, int max_tiles, const int* rows_tok,
-                       uint16_t* h, float* hsum, int H, int I, int E, hipStream_t s);
-int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
-                    const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
-                    hipStream_t s);
+// Large-group kernels (fp16 MFMA). gate/up converts x to fp16 rows in scratch
+// (at least n * H * 2 + n * 4 bytes, free until down) and writes h as fp16.
+int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int* tiles,
+                       const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
+                       void* scratch, int H, int I, int E, hipStream_t s);
+int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
+                    int max_tiles, float* dpart, int H, int I, int E, hipStream_t s);
 // bf16: the partial rows are bf16 (written by the large-group kernels).
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
                    int with_shared, float* out, hipStream_t s, bool bf16 = false);

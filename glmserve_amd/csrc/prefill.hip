@@ -1,5 +1,5 @@
 // W4A16 experts, large-group regime (prefill and wide verify batches):
-// grouped GEMM tiles of up to 128 grouped rows x 256 weight rows on bf16
+// grouped GEMM tiles of up to 128 grouped rows x 512 weight rows on fp16
 // MFMA 32x32x16.
 //
 // Reference: the expert-major tensor-core path of the reference's GGUF MoE
@@ -8,94 +8,111 @@
 // (cuda/moe_expert.cu:143-222).
 //
 // Work item = (row tile, feature group). A workgroup of 8 waves computes
-// 128 rows x 256 weight rows: for gate/up 128 features (the gate rows and the
-// up rows of the same features, one 128-feature group of h), for down 256
-// features. Wave w owns ALL 128 rows (4 row blocks of 32, the MFMA A operand)
-// and 32 weight rows (the B operand): for gate/up 16 gate + the same 16 up
-// features, for down 32 features. So every weight element is decoded once
-// per workgroup, and a lane's output column is one weight row with one scale
-// per 128-K group.
+// 128 rows x 512 weight rows: for gate/up 256 features (their gate rows and
+// their up rows), for down 512 features. Wave w owns ALL 128 rows (4 row
+// blocks of 32: the MFMA A operand, read from LDS) and 64 weight rows (2
+// column blocks of 32: the B operand, decoded in registers): for gate/up 32
+// gate rows and the 32 up rows of the same features, so SiLU(g) * u pairs
+// in one lane; for down 64 features. Every A fragment feeds 2 MFMAs and
+// every decoded B fragment 4.
+//
+// Operands are fp16. The weights decode straight to their dequantized value
+// (c - 8) * s rounded once to fp16: with the int4 code c placed in mantissa
+// bits 6-9 of 0x4800 (the fp16 of 8 + c / 2, exact), one packed fma
+//   (8 + c / 2) * 2s - 24s = (c - 8) * s
+// whose inputs 2s and 24s are exact in fp16 (s is a bf16 scale: 8
+// significant bits) rounds only the result. So the accumulators need no
+// per-group rescale and no offset correction: acc += A . B directly, fp32.
+// Activations: gate/up reads x converted to fp16 with a per-row power-of-2
+// scale (f16_rows_kernel below; exact for any finite bf16 row) and undoes the
+// scale on its outputs; down reads the fp16 h this gate/up wrote. fp16 keeps
+// 11 significant bits (bf16 keeps 8); the intermediate h must stay within
+// fp16's range (|h| <= 65504; beyond it h becomes inf and so does the output).
 //
 // Streams, per 128-K group g:
-// - activations: the 128 rows (gathered by token for gate/up) x 256 B go
-//   global -> LDS by LDS-DMA (buffer loads: the per-group step is a scalar
-//   offset, so issuing costs no VALU) into a 4-slot ring, issued three groups
-//   ahead. A row occupies 272 B of its slot (16 B of padding), so the 16 rows
-//   of a fragment read fall on 16 distinct bank groups and every fragment
-//   address is the lane's base plus an immediate offset;
-// - weights: each lane loads its own 32 B of int4 (two dwordx4) straight into
-//   registers, four groups ahead (a 4-deep register ring);
-// - per batch of 8 groups: the scales of the workgroup's 16 weight tiles and
-//   the 8 group sums of each row, one DMA per wave into double buffers.
-// One s_barrier per group, in the middle of the group, publishes slot g + 1
-// (every wave waited for its own DMAs of g + 1) and frees slot g - 1 for
-// group g + 3.
+// - activations: 128 rows x 256 B (gathered by token for gate/up) global ->
+//   LDS by buffer-load DMA into a 4-slot ring, issued 3 groups ahead. A row
+//   occupies 272 B of its slot (16 B of padding), so the 16 rows of a
+//   fragment read fall on 16 distinct bank groups and every fragment address
+//   is the lane's base plus an immediate offset;
+// - weights: each lane loads its own 2 x 32 B of int4 straight into
+//   registers (a 2-deep ring; each half refilled as soon as its last step is
+//   decoded, 1.5 groups ahead);
+// - per batch of 8 groups: the bf16 scales of the workgroup's 32 tiles, one
+//   DMA per wave into double buffers.
+// One s_barrier per group, at its start, publishes slot g + 1 (every wave
+// waited for its own DMAs of g + 1) and frees slot g - 1 for group g + 3.
+// The DMAs and loads are issued one per K-step, so they overlap the MFMAs.
 //
-// Arithmetic. The int4 code c decodes exactly to the bf16 of 128 + c
-// (dq_w4), so a group's MFMAs give P = sum_k (128 + c) x = sum_k (c - 8) x
-// + 136 X with X the row's group sum. acc += s * P per group (one fma per
-// element, s the column's bf16 scale), and once per 8 groups one MFMA adds
-// sum_g s_g * (-136 X_g) for all 8 groups: its A operand holds -136 X_g split
-// into bf16 hi + lo parts (exact to 2^-16 relative), its B operand s_g twice.
-//
-// Schedule of a group's 32 MFMAs (4 row blocks x 8 K-steps): quarters
-// Q1 = blocks 0,1 steps 0-3, Q2 = blocks 2,3 steps 0-3, Q3 = blocks 0,1
-// steps 4-7, Q4 = blocks 2,3 steps 4-7. The VALU work spreads evenly: Q1
-// rescales blocks 2,3 of the previous group, Q2 decodes steps 4-7 of this
-// group's weights, Q3 decodes steps 0-3 of the next group's, Q4 rescales
-// blocks 0,1. LDS fragments are read one step ahead. Row blocks past the
-// tile's last row skip their MFMAs and fragment reads (an expert's last tile
-// is often short), and keep the VALU work.
+// Row blocks past a tile's last row skip their MFMAs and fragment reads: the
+// dispatch lists full tiles first, then every expert's last tile of 33-64
+// rows, then of at most 32 rows; a workgroup's items run class by class, each
+// chunk through a pipeline specialized to its live row blocks (a run-time
+// branch around an MFMA would make the compiler copy whole accumulators).
 #include "common.hpp"
 #include "bigtile.hpp"
 #include "kernels.hpp"
 
 namespace glmmoe {
 
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
 struct MmArgs {
-    const uint8_t* wq[2];     // packed int4 tiles of the routed experts (gate, up) or (down, -)
+    const uint8_t* wq[2];     // packed int4 tiles of the routed experts (gate, up) or (down, down)
     const uint16_t* ws[2];    // bf16 scales [rows/16][K/128][16]
     const uint8_t* swq[2];    // the shared expert's
     const uint16_t* sws[2];
-    const uint16_t* src;      // x [n, H] (gate/up, rows gathered by token) or h [R, I] (down)
-    const float* gsum;        // xsum [n, H/128] or hsum [R, I/128]
+    const uint16_t* src;      // fp16: xh [n, H] (gate/up, rows gathered by token) or h [R, I] (down)
+    const float* rho;         // gate/up: per-token factor undoing xh's row scale
     const int4* tiles; const int* ntiles; const int* rows_tok;
-    uint16_t* h; float* hsum;   // gate/up outputs
-    uint16_t* dout;             // down output: bf16 [R, H]
+    uint16_t* h;              // gate/up output: fp16 [R, I]
+    uint16_t* dout;           // down output: bf16 [R, H]
     int H, I, E;
 };
 
 namespace mm {
 constexpr int kRowB = 272;                     // LDS bytes per activation row (256 + 16 padding)
 constexpr int kSlot = 128 * kRowB;             // 34 KiB: 34 DMAs of 1 KiB
-constexpr int kDmas = kSlot / 1024;
 constexpr int kRing = 4;
-constexpr int kXBuf = kRing * kSlot;           // 2 x 4 KiB: [row][8 groups] fp32
-constexpr int kSBuf = kXBuf + 2 * 4096;        // 2 x 4 KiB: [tile 16][group 8][row 16] bf16
-constexpr int kTab = kSBuf + 2 * 4096;
-constexpr int kTabItems = 8;
-constexpr int kTotal = kTab + kTabItems * kBigTabInts * 4;
+constexpr int kSBuf = kRing * kSlot;           // 2 x 8 KiB: [tile 32][group 8][row 16] bf16
+constexpr int kTab = kSBuf + 2 * 8192;
+constexpr int kTabItems = 6;
+constexpr int kRho = kTab + kTabItems * kBigTabInts * 4;   // [item][128] fp32 row factors
+constexpr int kTotal = kRho + kTabItems * kBigRows * 4;
 static_assert(kTotal <= 160 * 1024, "one workgroup's LDS");
 constexpr int kBlk = 32 * kRowB;               // one 32-row block
 }  // namespace mm
 
-// Weight tile of lane column col for wave w, feature group g.
-//   gate/up: matrix col >> 4 (0 gate, 1 up), 16-row block 8 g + w;
-//   down:    matrix 0, block 16 g + 2 w + (col >> 4).
+// 16-row weight tile of lane column col (0..31) in column block cb of wave w,
+// feature group g.
+//   gate/up: matrix cb (0 gate, 1 up), tile 16 g + 2 w + col / 16;
+//   down:    matrix 0, tile 32 g + 4 w + 2 cb + col / 16.
 template <int NMAT>
-__device__ __forceinline__ void mm_lane_tile(int g, int wave, int col, int& m, int& fb) {
+__device__ __forceinline__ void mm_lane_tile(int g, int wave, int cb, int col, int& m, int& fb) {
     if (NMAT == 2) {
-        m = col >> 4;
-        fb = 8 * g + wave;
+        m = cb;
+        fb = 16 * g + 2 * wave + (col >> 4);
     } else {
         m = 0;
-        fb = 16 * g + 2 * wave + (col >> 4);
+        fb = 32 * g + 4 * wave + 2 * cb + (col >> 4);
     }
 }
-// Index of lane column col's tile in the scale buffer (gate tiles 0-7, up 8-15).
+// The workgroup's tile t (0..31) in the scale buffer: gate/up tiles 0-15 are
+// gate, 16-31 up; down tiles are consecutive.
 template <int NMAT>
-__device__ __forceinline__ int mm_sbuf_tile(int wave, int col) {
-    return NMAT == 2 ? 8 * (col >> 4) + wave : 2 * wave + (col >> 4);
+__device__ __forceinline__ void mm_wg_tile(int g, int t, int& m, int& fb) {
+    if (NMAT == 2) {
+        m = t >> 4;
+        fb = 16 * g + (t & 15);
+    } else {
+        m = 0;
+        fb = 32 * g + t;
+    }
+}
+template <int NMAT>
+__device__ __forceinline__ int mm_sbuf_tile(int wave, int cb, int col) {
+    return NMAT == 2 ? 16 * cb + 2 * wave + (col >> 4) : 4 * wave + 2 * cb + (col >> 4);
 }
 
 template <int NMAT>
@@ -117,27 +134,24 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t mm_rsrc(const void* base) {
 
 // Per-lane stream state of one item.
 //   act[i]: byte offset (in src) of this lane's 16 B of activation DMA i at
-//     group 0; DMA d = wave + 8 i (and d = 32 + wave for waves 0, 1) fills
-//     slot bytes 1024 d + 16 lane = row p / 17, 16-B chunk p % 17 (p = 64 d +
-//     lane); chunk 16 is padding (loads chunk 0 again);
-//   w: the lane's 32 B of int4 at group 0 (K positions 64 h .. 64 h + 63 of
-//     weight row col % 16 of its tile);
-//   bt: byte offset of the lane's 16 B of the batch DMA at batch 0 (waves 0-3:
-//     group sums of row 32 w + lane / 2, groups 4 (lane & 1) + [0, 4); waves
-//     4-7: 16 B of scales of tile 4 (w - 4) + lane / 16).
+//     group 0; DMA d = wave + 8 i (i < 4) or 32 + (wave & 1) (i = 4; waves
+//     2-7 repeat DMAs 32 and 33 of waves 0, 1: same source, same LDS bytes,
+//     so every wave waits for the same counts) fills slot bytes 1024 d +
+//     16 lane = row p / 17, 16-B chunk p % 17 (p = 64 d + lane); chunk 16 is
+//     padding (loads chunk 0 again);
+//   w[cb]: the lane's 32 B of int4 of column block cb at group 0 (K positions
+//     64 h .. 64 h + 63 of weight row col % 16 of its tile);
+//   st: byte offset of the lane's 16 B of the scale DMA at batch 0 (tile
+//     4 w + lane / 16 of the workgroup).
 struct MmPtrs {
     uint32_t act[5];
-    const uint4* w;
-    uint32_t bt;
-};
-struct MmUni {            // the same, wave-uniform parts
-    const uint16_t* sbt;  // waves 4-7: the scale matrix the batch DMA reads
-    int nrb;              // live 32-row blocks of the item
+    const uint4* w[2];
+    uint32_t st;
 };
 
 template <int NMAT>
 __device__ __forceinline__ MmPtrs mm_ptrs(const MmArgs& a, const BigItem& it, int K, int KG, int wave,
-                                          int lane, MmUni& u) {
+                                          int lane, const uint16_t*& sbase) {
     MmPtrs p;
 #pragma unroll
     for (int i = 0; i < 5; ++i) {
@@ -148,43 +162,59 @@ __device__ __forceinline__ MmPtrs mm_ptrs(const MmArgs& a, const BigItem& it, in
     }
     const int col = lane & 31, h = lane >> 5;
     const int frows = NMAT == 2 ? a.I : a.H;
+#pragma unroll
+    for (int cb = 0; cb < 2; ++cb) {
+        int m, fb;
+        mm_lane_tile<NMAT>(it.g, wave, cb, col, m, fb);
+        const uint4* base = reinterpret_cast<const uint4*>(mm_wbase<NMAT>(a, it.e, m, frows, KG));
+        p.w[cb] = base + (size_t)fb * KG * 64 + (col & 15) + 32 * h;
+    }
     {
         int m, fb;
-        mm_lane_tile<NMAT>(it.g, wave, col, m, fb);
-        const uint4* base = reinterpret_cast<const uint4*>(mm_wbase<NMAT>(a, it.e, m, frows, KG));
-        p.w = base + (size_t)fb * KG * 64 + (col & 15) + 32 * h;
+        mm_wg_tile<NMAT>(it.g, 4 * wave + (lane >> 4), m, fb);
+        sbase = mm_sbase<NMAT>(a, it.e, m, frows, KG);   // uniform: a wave's 4 tiles share the matrix
+        p.st = ((uint32_t)fb * KG * 16 + (lane & 15) * 8) * 2u;
     }
-    if (wave < 4) {
-        const int row = wave * 32 + (lane >> 1);
-        p.bt = (lds_read32(it.tab + 16 + row * 4) * (uint32_t)KG + 4u * (lane & 1)) * 4u;
-        u.sbt = nullptr;
-    } else {
-        const int t = 4 * (wave - 4) + (lane >> 4);
-        const int m = NMAT == 2 ? (t >> 3) : 0;
-        const int fb = NMAT == 2 ? 8 * it.g + (t & 7) : 16 * it.g + t;
-        u.sbt = mm_sbase<NMAT>(a, it.e, m, frows, KG);
-        p.bt = ((uint32_t)fb * KG * 16 + (lane & 15) * 8) * 2u;
-    }
-    u.nrb = (it.nr + 31) >> 5;
     return p;
 }
 
-// bf16 pair {hi(v), bf16(v - hi(v))} as one dword (hi in the low half).
-__device__ __forceinline__ uint32_t split_bf16(float v) {
-    const float hi = __uint_as_float(__float_as_uint(v) & 0xffff0000u);
-    return pack_bf16x2(hi, v - hi);
+// Fragments of NB row blocks, OFF past addr, block b at OFF + b * kBlk.
+template <int NB, int OFF>
+__device__ __forceinline__ void lds_frags(uint32_t addr, u32x4 (&a)[4]) {
+    if constexpr (NB == 1) {
+        asm volatile("ds_read_b128 %0, %1 offset:%2" : "=&v"(a[0]) : "v"(addr), "n"(OFF));
+    } else if constexpr (NB == 2) {
+        asm volatile("ds_read_b128 %0, %2 offset:%3\n ds_read_b128 %1, %2 offset:%4"
+                     : "=&v"(a[0]), "=&v"(a[1])
+                     : "v"(addr), "n"(OFF), "n"(OFF + mm::kBlk));
+    } else {
+        asm volatile("ds_read_b128 %0, %4 offset:%5\n ds_read_b128 %1, %4 offset:%6\n"
+                     " ds_read_b128 %2, %4 offset:%7\n ds_read_b128 %3, %4 offset:%8"
+                     : "=&v"(a[0]), "=&v"(a[1]), "=&v"(a[2]), "=&v"(a[3])
+                     : "v"(addr), "n"(OFF), "n"(OFF + mm::kBlk), "n"(OFF + 2 * mm::kBlk),
+                       "n"(OFF + 3 * mm::kBlk));
+    }
 }
-
-// Fragments of two row blocks: OFF and OFF + one block past addr.
-template <int OFF>
-__device__ __forceinline__ void lds_read2(uint32_t addr, u32x4& a, u32x4& b) {
-    asm volatile("ds_read_b128 %0, %2 offset:%3\n ds_read_b128 %1, %2 offset:%4"
-                 : "=&v"(a), "=&v"(b)
-                 : "v"(addr), "n"(OFF), "n"(OFF + mm::kBlk));
+// Waits until at most N LDS operations are pending; the fragment registers
+// (and extra registers written by pending reads) are operands, so nothing
+// reads them before the data has arrived.
+template <int N, int NB>
+__device__ __forceinline__ void lgkm_frags(u32x4 (&a)[4]) {
+    if constexpr (NB == 1) asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(a[0]) : "n"(N));
+    else if constexpr (NB == 2) asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a[0]), "+v"(a[1]) : "n"(N));
+    else
+        asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]) : "n"(N));
 }
-template <int N>
-__device__ __forceinline__ void lgkm_wait(u32x4& a, u32x4& b) {
-    asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "n"(N));
+template <int N, int NB>
+__device__ __forceinline__ void lgkm_frags2(u32x4 (&a)[4], uint32_t& x, uint32_t& y) {
+    if constexpr (NB == 1)
+        asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(a[0]), "+v"(x), "+v"(y) : "n"(N));
+    else if constexpr (NB == 2)
+        asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(x), "+v"(y) : "n"(N));
+    else
+        asm volatile("s_waitcnt lgkmcnt(%6)"
+                     : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(x), "+v"(y)
+                     : "n"(N));
 }
 
 __device__ __forceinline__ void dma_buf16(__amdgpu_buffer_rsrc_t r, uint32_t lds_dst, uint32_t voff,
@@ -193,93 +223,91 @@ __device__ __forceinline__ void dma_buf16(__amdgpu_buffer_rsrc_t r, uint32_t lds
         r, (__attribute__((address_space(3))) void*)(uintptr_t)lds_dst, 16, voff, soff, 0, 0);
 }
 
-// Stores an item's outputs. red: 4 KiB of LDS free for the call (the hsum
-// partials of gate/up).
+__device__ __forceinline__ f32x16 mfma16(u32x4 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b),
+                                                  c, 0, 0, 0);
+}
+
+// The fp16 decode constants as opaque registers (mask of mantissa bits 6-9
+// of both halves, the fp16 pattern of 8.0 in both halves): with literal
+// operands the compiler splits v_and_or_b32.
+struct DqF16 {
+    uint32_t mask, bias;
+};
+__device__ __forceinline__ DqF16 dq_f16_const() {
+    DqF16 c;
+    asm volatile("v_mov_b32 %0, 0x03c003c0\n v_mov_b32 %1, 0x48004800" : "=v"(c.mask), "=v"(c.bias));
+    return c;
+}
+
+// Dequantized fp16 weights of one packed dword (8 K positions; position 2j
+// in nibble j, 2j + 1 in nibble j + 4): fp16x2 j = ((c - 8) * s) of positions
+// 2j, 2j + 1. s2 = {2s, 2s}, s24 = {-24s, -24s}.
+__device__ __forceinline__ bf16x8 dq_f16(uint32_t w, const DqF16& k, f16x2 s2, f16x2 s24) {
+    const uint32_t v0 = ((w << 6) & k.mask) | k.bias;
+    const uint32_t v1 = ((w << 2) & k.mask) | k.bias;
+    const uint32_t v2 = ((w >> 2) & k.mask) | k.bias;
+    const uint32_t v3 = ((w >> 6) & k.mask) | k.bias;
+    u32x4 r;
+    r.x = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, v0), s2, s24));
+    r.y = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, v1), s2, s24));
+    r.z = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, v2), s2, s24));
+    r.w = __builtin_bit_cast(uint32_t, __builtin_elementwise_fma(__builtin_bit_cast(f16x2, v3), s2, s24));
+    return __builtin_bit_cast(bf16x8, r);
+}
+
+// {2s, 2s} and {-24s, -24s} in fp16 from a bf16 scale pattern (exact).
+__device__ __forceinline__ void scale_pair(uint32_t sbits, f16x2& s2, f16x2& s24) {
+    const float s = bf16_to_f32(sbits & 0xffffu);
+    const _Float16 a = (_Float16)(2.0f * s), b = (_Float16)(-24.0f * s);
+    s2 = f16x2{a, a};
+    s24 = f16x2{b, b};
+}
+
+// Stores an item's outputs.
 template <int NMAT>
-__device__ __forceinline__ void mm_epilogue(const MmArgs& a, const BigItem& cur, uint32_t red, int wave,
-                                            int lane, f32x16 (&acc)[4]) {
+__device__ __forceinline__ void mm_epilogue(const MmArgs& a, const BigItem& cur, uint32_t rho, int wave,
+                                            int lane, f32x16 (&acc)[4][2]) {
     // Laundered lane index: keeps the per-row addresses below from being
     // hoisted out of the streaming loop (they would stay live and spill).
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const int col = ln & 31, h = ln >> 5;
     if constexpr (NMAT == 2) {
-        // Lanes col < 16 hold gate features, col >= 16 the same up features.
-        // Each lane of a pair forms h for half of the values: col < 16 the
-        // values i < 8 of every row block, col >= 16 the values i >= 8.
-        const bool lo = col < 16;
-        const int f = cur.g * 128 + wave * 16 + (col & 15);
-        uint16_t* hcol = a.h + (size_t)cur.r0 * a.I + f;
-        float v[32];
-#pragma unroll
-        for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-            for (int i = 0; i < 8; ++i) {
-                const float send = lo ? acc[rb][i + 8] : acc[rb][i];
-                const float recv = __shfl_xor(send, 16);
-                const float gt = lo ? acc[rb][i] : recv;
-                const float up = lo ? recv : acc[rb][i + 8];
-                const uint32_t hb = pack_bf16x2(silu_fast(gt) * up, 0.0f) & 0xffffu;
-                const int ii = lo ? i : i + 8;
-                const int row = rb * 32 + 8 * (ii >> 2) + 4 * h + (ii & 3);
-                if (row < cur.nr) hcol[(size_t)row * a.I] = (uint16_t)hb;
-                v[rb * 8 + i] = bf16_to_f32(hb);
-            }
-        // Row sums over the 16 features of the lane's 16-lane row group
-        // (fixed recursive halving: lane c ends with the sums of values
-        // 2 (c % 16) and 2 (c % 16) + 1), then over the 8 waves in order.
-        const int c = col & 15;
-        auto halve = [&](auto N_) {
-            constexpr int N = decltype(N_)::value;
-            const bool upper = (c & N) != 0;
-#pragma unroll
-            for (int j = 0; j < 2 * N; ++j) {
-                const float send = upper ? v[j] : v[j + 2 * N];
-                const float keep = upper ? v[j + 2 * N] : v[j];
-                v[j] = keep + __shfl_xor(send, N);
-            }
-        };
-        halve(std::integral_constant<int, 8>{});
-        halve(std::integral_constant<int, 4>{});
-        halve(std::integral_constant<int, 2>{});
-        halve(std::integral_constant<int, 1>{});
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const int idx = 2 * c + q;                       // value index rb * 8 + i
-            const int rb = idx >> 3, i = idx & 7;
-            const int ii = lo ? i : i + 8;
-            const int row = rb * 32 + 8 * (ii >> 2) + 4 * h + (ii & 3);
-            lds_write32(red + (uint32_t)((wave * 128 + row) * 4), v[q]);
-        }
-        __builtin_amdgcn_s_barrier();
-        if (wave == 0) {
-#pragma unroll
-            for (int half = 0; half < 2; ++half) {
-                const int row = half * 64 + ln;
-                float s = 0.0f;
-#pragma unroll
-                for (int w = 0; w < 8; ++w) s += __uint_as_float(lds_read32(red + (uint32_t)((w * 128 + row) * 4)));
-                if (row < cur.nr) a.hsum[((size_t)cur.r0 + row) * (a.I / 128) + cur.g] = s;
-            }
-        }
-        __builtin_amdgcn_s_barrier();   // partials read before the next item reuses them
-    } else {
-        // Per-row expert outputs as bf16 (the combine adds them in fp32).
-        uint16_t* dcol = a.dout + (size_t)cur.r0 * a.H + cur.g * 256 + wave * 32 + col;
+        // h = silu(g) * u of this lane's feature, rows' scale undone first.
+        uint16_t* hcol = a.h + (size_t)cur.r0 * a.I + cur.g * 256 + wave * 32 + col;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
             for (int i = 0; i < 16; ++i) {
                 const int row = rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-                if (row < cur.nr) dcol[(size_t)row * a.H] = (uint16_t)(pack_bf16x2(acc[rb][i], 0.0f) & 0xffffu);
+                if (row < cur.nr) {
+                    const float r = __uint_as_float(lds_read32(rho + (uint32_t)row * 4));
+                    const float gt = acc[rb][0][i] * r, up = acc[rb][1][i] * r;
+                    hcol[(size_t)row * a.I] = __builtin_bit_cast(uint16_t, (_Float16)(silu_fast(gt) * up));
+                }
             }
+    } else {
+        // Per-row expert outputs as bf16 (the combine adds them in fp32).
+        uint16_t* dcol = a.dout + (size_t)cur.r0 * a.H + cur.g * 512 + wave * 64 + col;
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) {
+                    const int row = rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
+                    if (row < cur.nr)
+                        dcol[(size_t)row * a.H + cb * 32] =
+                            (uint16_t)(pack_bf16x2(acc[rb][cb][i], 0.0f) & 0xffffu);
+                }
     }
 }
 
 template <int NMAT>
 __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
     extern __shared__ __align__(16) char lds[];
-    const DqConst dqc = dq_const();
+    const DqF16 dqc = dq_f16_const();
     int* table = reinterpret_cast<int*>(lds + mm::kTab);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -287,7 +315,7 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
     const int K = NMAT == 2 ? a.H : a.I;
     const int KG = K / 128;          // a multiple of 8 (checked by the launcher)
     const int NB = KG / 8;           // batches per item
-    const int nfg = NMAT == 2 ? a.I / 128 : a.H / 256;
+    const int nfg = NMAT == 2 ? a.I / 256 : a.H / 512;
     // Tile classes (dispatch order): full tiles [0, nt4), then each expert's
     // last tile of 33-64 rows [nt4, nt2), then of at most 32 rows [nt2, nt):
     // 4, 2 and 1 live 32-row blocks.
@@ -297,144 +325,105 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
     // Lane's fragment address at step 0 of row block 0 in slot 0: row col,
     // 16-B chunk 8 h; step s adds 16 s, row block rb 8704 rb, slot q 34 KiB q.
     const uint32_t xa0 = ring + (uint32_t)(col * mm::kRowB + h * 128);
-    const int stile = mm_sbuf_tile<NMAT>(wave, col);
+    const uint32_t sa0 = lds_addr(lds + mm::kSBuf) + (uint32_t)((col & 15) * 2);
+    const int st0 = mm_sbuf_tile<NMAT>(wave, 0, col), st1 = mm_sbuf_tile<NMAT>(wave, 1, col);
     const __amdgpu_buffer_rsrc_t rsrc_src = mm_rsrc(a.src);
-    const __amdgpu_buffer_rsrc_t rsrc_x = mm_rsrc(a.gsum);
 
-    // A workgroup's items come in increasing id order, so class by class.
-    // Each chunk of at most kTabItems items of one class runs one pipeline
-    // (prologue, stream, drain) specialized to its live row blocks: the
-    // accumulators never cross from one specialization to another.
     auto cls_of = [&](long k) {
         const long t = big_item_id(k) / nfg;
         return t < nt4 ? 4 : t < nt2 ? 2 : 1;
     };
+    // One chunk (at most kTabItems items of one class): table, prologue,
+    // stream, drain. The accumulators live only inside it.
     auto run_chunk = [&](auto NRB_, long k0, int cnt) {
         constexpr int NRB = decltype(NRB_)::value;
-        constexpr bool live1 = NRB > 1, live23 = NRB > 2, live3 = NRB > 3;
         big_fill_table<NMAT == 2>(a.tiles, a.rows_tok, table, k0, cnt, nfg);
         __syncthreads();
+        if constexpr (NMAT == 2) {
+            float* rho = reinterpret_cast<float*>(lds + mm::kRho);
+            for (int i = threadIdx.x; i < cnt * kBigRows; i += blockDim.x)
+                rho[i] = a.rho[table[(i / kBigRows) * kBigTabInts + 4 + (i % kBigRows)]];
+            __syncthreads();
+        }
         const int NBt = cnt * NB;        // batches of this chunk
         auto item = [&](int k) { return big_item(lds + mm::kTab, k < cnt ? k : cnt - 1); };
 
         // Stream state of the item of the current batch (pc) and of the next
         // item (pn; past the chunk's end the last item again: those loads
         // land in buffers nobody reads). In the last batch of an item the
-        // activation stream (3 groups ahead) and the weight stream (4 ahead)
+        // activation stream (3 groups ahead) and the weight stream (2 ahead)
         // cross into the next item at fixed group positions.
-        MmUni uc, un;
-        MmPtrs pc = mm_ptrs<NMAT>(a, item(0), K, KG, wave, lane, uc);
-        MmPtrs pn = mm_ptrs<NMAT>(a, item(1), K, KG, wave, lane, un);
-        // Five activation DMAs per wave per group, so every wave waits for
-        // the same counts: DMAs 32 and 33 (waves 0, 1) are repeated by waves
-        // 2-7 (same source, same LDS bytes). No branch may sit in the
-        // unrolled group body: the compiler then spills the accumulators.
-        auto issue_act = [&](const MmPtrs& p, int k, int gslot) {
-            const uint32_t dst = ring + (uint32_t)((gslot & 3) * mm::kSlot);
-            const uint32_t soff = (uint32_t)k * 256u;
+        const uint16_t *sbc, *sbn;
+        MmPtrs pc = mm_ptrs<NMAT>(a, item(0), K, KG, wave, lane, sbc);
+        MmPtrs pn = mm_ptrs<NMAT>(a, item(1), K, KG, wave, lane, sbn);
+        u32x4 W[2][2][2];   // [ring][column block][lo / hi 16 B]
+        auto issue_w = [&](const MmPtrs& p, int k, int r, int half) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) dma_buf16(rsrc_src, dst + (uint32_t)((wave + 8 * i) * 1024), p.act[i], soff);
-            dma_buf16(rsrc_src, dst + (uint32_t)((32 + (wave & 1)) * 1024), p.act[4], soff);
+            for (int cb = 0; cb < 2; ++cb)
+                W[r][cb][half] = __builtin_bit_cast(u32x4, p.w[cb][(size_t)k * 64 + half * 16]);
         };
-        u32x4 W[4][2];
-        auto issue_w = [&](const uint4* pw, int k, int r) {
-            const uint4* q = pw + (size_t)k * 64;
-            W[r][0] = __builtin_bit_cast(u32x4, q[0]);
-            W[r][1] = __builtin_bit_cast(u32x4, q[16]);
+        auto issue_act = [&](const MmPtrs& p, int k, int gslot, int i) {
+            const uint32_t dst = ring + (uint32_t)((gslot & 3) * mm::kSlot);
+            const int d = i < 4 ? wave + 8 * i : 32 + (wave & 1);
+            dma_buf16(rsrc_src, dst + (uint32_t)(d * 1024), p.act[i], (uint32_t)k * 256u);
         };
-        auto issue_batch = [&](uint32_t bt, const uint16_t* sbt, int kb, int parity) {
-            // Waves 0-3: group sums; waves 4-7: scales (selects, no branch).
-            const bool xw = wave < 4;
-            const __amdgpu_buffer_rsrc_t r = xw ? rsrc_x : mm_rsrc(sbt);
-            const uint32_t dst = xw ? lds_addr(lds + mm::kXBuf + parity * 4096 + wave * 1024)
-                                    : lds_addr(lds + mm::kSBuf + parity * 4096 + (wave - 4) * 1024);
-            dma_buf16(r, dst, bt, (uint32_t)kb * (xw ? 32u : 256u));
+        auto issue_scales = [&](uint32_t st, const uint16_t* sb, int kb, int parity) {
+            dma_buf16(mm_rsrc(sb), lds_addr(lds + mm::kSBuf + parity * 8192 + wave * 1024), st,
+                      (uint32_t)kb * 256u);
         };
 
-        // Prologue: batch 0, activation groups 0-2, weight groups 0-3.
-        issue_batch(pc.bt, uc.sbt, 0, 0);
-        issue_act(pc, 0, 0);
-        issue_act(pc, 1, 1);
-        issue_act(pc, 2, 2);
+        // Prologue: scales of batch 0, activation groups 0-2, weights 0-1.
+        issue_scales(pc.st, sbc, 0, 0);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) issue_w(pc.w, r, r);
+        for (int g0 = 0; g0 < 3; ++g0)
+#pragma unroll
+            for (int i = 0; i < 5; ++i) issue_act(pc, g0, g0, i);
+#pragma unroll
+        for (int r = 0; r < 2; ++r) {
+            issue_w(pc, r, r, 0);
+            issue_w(pc, r, r, 1);
+        }
         wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
 
-        f32x16 acc[4], P[4];
+        f32x16 acc[4][2];
 #pragma unroll
-        for (int rb = 0; rb < 4; ++rb) acc[rb] = f32x16{};
-        bf16x8 Bd[8];
-#pragma unroll
-        for (int s = 0; s < 8; ++s) Bd[s] = dq_w4(W[0][s >> 2][s & 3], dqc);
-        // Fragments of Q1 step 0 (row blocks 0, 1 of slot 0).
-        u32x4 A[2][2];
-        lds_read2<0>(xa0, A[0][0], A[0][1]);
-        float sc_prev = 0.0f;
+        for (int rb = 0; rb < 4; ++rb) acc[rb][0] = acc[rb][1] = f32x16{};
+        // Scales of group 0 and the decoded B of its step 0.
+        f16x2 s2[2], s24[2];
+        scale_pair(lds_read_u16(sa0 + (uint32_t)(st0 * 256)), s2[0], s24[0]);
+        scale_pair(lds_read_u16(sa0 + (uint32_t)(st1 * 256)), s2[1], s24[1]);
+        bf16x8 Bd[2][2];   // [parity][column block]
+        Bd[0][0] = dq_f16(W[0][0][0][0], dqc, s2[0], s24[0]);
+        Bd[0][1] = dq_f16(W[0][1][0][0], dqc, s2[1], s24[1]);
+        // Fragments of step 0 of group 0.
+        u32x4 A[2][4];
+        lds_frags<NRB, 0>(xa0, A[0]);
         int ib = 0, kb = 0;   // item and batch-in-item of the current batch
 
         for (int b = 0; b < NBt; ++b) {
             const bool last = kb == NB - 1;
-            // Liveness is a compile-time constant of the chunk: an MFMA under
-            // a run-time branch makes the compiler copy whole accumulators.
             static_for<8>([&](auto J) {
                 constexpr int j = decltype(J)::value;
-                // Fragment base of slot g and g + 1 (an opaque scalar offset,
-                // so the per-slot bases are formed here, not precomputed).
-                uint32_t so = (uint32_t)((j & 3) * mm::kSlot), nso = (uint32_t)(((j + 1) & 3) * mm::kSlot);
-                asm volatile("" : "+s"(so), "+s"(nso));
-                const uint32_t xg = xa0 + so;
-                // ---- Q1: row blocks 0, 1, steps 0-3; rescale blocks 2, 3 of g - 1.
-                static_for<4>([&](auto S_) {
-                    constexpr int s = 0 + decltype(S_)::value;
-                    constexpr int cb = s & 1, nb = cb ^ 1;
-                    if constexpr (s < 3) lds_read2<16 * (s + 1)>(xg, A[nb][0], A[nb][1]);
-                    else if constexpr (live23) lds_read2<2 * mm::kBlk>(xg, A[nb][0], A[nb][1]);
-                    else lds_read2<16 * 4>(xg, A[nb][0], A[nb][1]);
-                    lgkm_wait<2>(A[cb][0], A[cb][1]);
-                    P[0] = mfma32x32x16(as_bf16x8(A[cb][0]), Bd[s], s == 0 ? f32x16{} : P[0]);
-                    if constexpr (live1) P[1] = mfma32x32x16(as_bf16x8(A[cb][1]), Bd[s], s == 0 ? f32x16{} : P[1]);
-                    if constexpr (j > 0) {
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const int blk = 2 + (e >> 2), idx = s * 4 + (e & 3);
-                            acc[blk][idx] = __builtin_fmaf(sc_prev, P[blk][idx], acc[blk][idx]);
-                        }
-                    }
-                });
-                // ---- Q2: row blocks 2, 3, steps 0-3; decode steps 4-7 of g's weights.
-                if constexpr (live23) {
-                static_for<4>([&](auto S_) {
-                        constexpr int s = 0 + decltype(S_)::value;
-                        constexpr int cb = (s + 4) & 1, nb = cb ^ 1;
-                        if constexpr (s < 3) lds_read2<2 * mm::kBlk + 16 * (s + 1)>(xg, A[nb][0], A[nb][1]);
-                        else lds_read2<16 * 4>(xg, A[nb][0], A[nb][1]);
-                        lgkm_wait<2>(A[cb][0], A[cb][1]);
-                        P[2] = mfma32x32x16(as_bf16x8(A[cb][0]), Bd[s], s == 0 ? f32x16{} : P[2]);
-                        if constexpr (live3) P[3] = mfma32x32x16(as_bf16x8(A[cb][1]), Bd[s], s == 0 ? f32x16{} : P[3]);
-                        Bd[4 + s] = dq_w4(W[j & 3][1][s], dqc);
-                    });
-                } else {
-#pragma unroll
-                    for (int s = 0; s < 4; ++s) Bd[4 + s] = dq_w4(W[j & 3][1][s], dqc);
-                }
-                // ---- mid-group: publish slot g + 1, free slot g - 1, issue.
-                // Pending before the wait: this wave's DMAs of g + 1 (issued at
-                // g - 2) and everything after them: the weights of g + 2 (+ the
-                // batch DMA if g - 2 opened a batch) and the whole issue of g - 1
-                // (5 activation DMAs, 2 weight loads, maybe the batch DMA).
+                // ---- group start: publish slot g + 1, free slot g - 1. Pending
+                // before the wait: this wave's DMAs of g + 1 (issued in g - 2,
+                // the last at step 4) and what followed them in g - 2: the
+                // scale DMA if it opened a batch (step 5) and the high weights
+                // (step 6, 2 loads); then all of g - 1's issue (5 DMAs, 4 weight
+                // loads, maybe the scale DMA).
                 {
-                    constexpr int n2 = 2 + (((j + 6) & 7) == 0 ? 1 : 0);
-                    constexpr int n1 = 7 + (((j + 7) & 7) == 0 ? 1 : 0);
+                    constexpr int n2 = (((j + 6) & 7) == 0 ? 1 : 0) + 2;
+                    constexpr int n1 = 9 + (((j + 7) & 7) == 0 ? 1 : 0);
                     wait_vmcnt<n2 + n1>();
                 }
                 __builtin_amdgcn_s_barrier();
+                // Fragment base of slot g and g + 1 (opaque scalar offsets).
+                uint32_t so = (uint32_t)((j & 3) * mm::kSlot), nso = (uint32_t)(((j + 1) & 3) * mm::kSlot);
+                asm volatile("" : "+s"(so), "+s"(nso));
+                const uint32_t xg = xa0 + so;
                 // Stream sources: activations of group g + 3, weights of group
-                // g + 4 (this item's or, late in its last batch, the next
-                // item's: selects, no branches). The 5 activation DMAs, the
-                // weight loads and the batch DMA are spread over Q3 and Q4, one
-                // per step, so their issue overlaps the MFMAs instead of
-                // stalling all waves together after the barrier.
+                // g + 2 (this item's or, late in the item's last batch, the next
+                // item's: selects, no branches).
                 MmPtrs pa = pc;
                 int ka = 8 * kb + j + 3;
                 if constexpr (j >= 5) {
@@ -442,120 +431,71 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
                     for (int q = 0; q < 5; ++q) pa.act[q] = last ? pn.act[q] : pc.act[q];
                     ka = last ? j - 5 : ka;
                 }
-                const uint4* pw = pc.w;
-                int kw = 8 * kb + j + 4;
-                if constexpr (j >= 4) {
-                    pw = last ? pn.w : pc.w;
-                    kw = last ? j - 4 : kw;
+                MmPtrs pw = pc;
+                int kw = 8 * kb + j + 2;
+                if constexpr (j >= 6) {
+                    pw.w[0] = last ? pn.w[0] : pc.w[0];
+                    pw.w[1] = last ? pn.w[1] : pc.w[1];
+                    kw = last ? j - 6 : kw;
                 }
-                const uint32_t adst = ring + (uint32_t)(((j + 3) & 3) * mm::kSlot);
-                const uint32_t asoff = (uint32_t)ka * 256u;
-                auto issue_part = [&](auto IP_) {
-                    constexpr int ip = decltype(IP_)::value;
-                    if constexpr (ip < 4) {
-                        dma_buf16(rsrc_src, adst + (uint32_t)((wave + 8 * ip) * 1024), pa.act[ip], asoff);
-                    } else if constexpr (ip == 4) {
-                        dma_buf16(rsrc_src, adst + (uint32_t)((32 + (wave & 1)) * 1024), pa.act[4], asoff);
-                    } else if constexpr (ip == 5) {
-                        issue_w(pw, kw, (j + 4) & 3);
-                    } else if constexpr (ip == 6 && j == 0) {
-                        issue_batch(last ? pn.bt : pc.bt, last ? un.sbt : uc.sbt, last ? 0 : kb + 1, (b + 1) & 1);
+                uint32_t nsr0 = 0, nsr1 = 0;   // scales of g + 1
+                static_for<8>([&](auto S_) {
+                    constexpr int s = decltype(S_)::value;
+                    constexpr int cbuf = s & 1, nbuf = cbuf ^ 1;
+                    // Fragments of step s + 1 (or step 0 of g + 1).
+                    if constexpr (s < 7) lds_frags<NRB, 16 * (s + 1)>(xg, A[nbuf]);
+                    else lds_frags<NRB, 0>(xa0 + nso, A[nbuf]);
+                    if constexpr (s == 4) {
+                        // Scales of g + 1 (after a batch's last group: the next
+                        // batch's buffer, written in this batch's first group).
+                        const uint32_t sb = sa0 + (uint32_t)((j == 7 ? ((b + 1) & 1) : (b & 1)) * 8192 +
+                                                             ((j + 1) & 7) * 32);
+                        asm volatile("ds_read_u16 %0, %2\n ds_read_u16 %1, %3"
+                                     : "=&v"(nsr0), "=&v"(nsr1)
+                                     : "v"(sb + (uint32_t)(st0 * 256)), "v"(sb + (uint32_t)(st1 * 256)));
+                        lgkm_frags<NRB + 2, NRB>(A[cbuf]);
+                    } else if constexpr (s == 5) {
+                        lgkm_frags2<NRB, NRB>(A[cbuf], nsr0, nsr1);
+                    } else {
+                        lgkm_frags<NRB, NRB>(A[cbuf]);
                     }
-                };
-                // The scale of this lane's column for group g (waited for with
-                // Q3's first fragments).
-                uint32_t scr;
-                asm volatile("ds_read_u16 %0, %1"
-                             : "=v"(scr)
-                             : "v"(lds_addr(lds + mm::kSBuf + (b & 1) * 4096 + stile * 256 + j * 32) +
-                                   (uint32_t)((col & 15) * 2)));
-                // ---- Q3: row blocks 0, 1, steps 4-7; decode steps 0-3 of g + 1.
-                static_for<4>([&](auto S_) {
-                    constexpr int s = 4 + decltype(S_)::value;
-                    constexpr int cb = s & 1, nb = cb ^ 1;
-                    if constexpr (s < 7) lds_read2<16 * (s + 1)>(xg, A[nb][0], A[nb][1]);
-                    else if constexpr (live23) lds_read2<2 * mm::kBlk + 16 * 4>(xg, A[nb][0], A[nb][1]);
-                    else lds_read2<0>(xa0 + nso, A[nb][0], A[nb][1]);
-                    if constexpr (s == 4) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(A[cb][0]), "+v"(A[cb][1]), "+v"(scr));
-                    else lgkm_wait<2>(A[cb][0], A[cb][1]);
-                    P[0] = mfma32x32x16(as_bf16x8(A[cb][0]), Bd[s], P[0]);
-                    if constexpr (live1) P[1] = mfma32x32x16(as_bf16x8(A[cb][1]), Bd[s], P[1]);
-                    Bd[s - 4] = dq_w4(W[(j + 1) & 3][0][s - 4], dqc);
-                    issue_part(std::integral_constant<int, s - 4>{});
+#pragma unroll
+                    for (int rb = 0; rb < NRB; ++rb) {
+                        acc[rb][0] = mfma16(A[cbuf][rb], Bd[cbuf][0], acc[rb][0]);
+                        acc[rb][1] = mfma16(A[cbuf][rb], Bd[cbuf][1], acc[rb][1]);
+                    }
+                    // Decode step s + 1 (or step 0 of g + 1 with its scales).
+                    if constexpr (s < 7) {
+#pragma unroll
+                        for (int cb = 0; cb < 2; ++cb)
+                            Bd[nbuf][cb] = dq_f16(W[j & 1][cb][(s + 1) >> 2][(s + 1) & 3], dqc, s2[cb], s24[cb]);
+                    } else {
+                        scale_pair(nsr0, s2[0], s24[0]);
+                        scale_pair(nsr1, s2[1], s24[1]);
+#pragma unroll
+                        for (int cb = 0; cb < 2; ++cb)
+                            Bd[nbuf][cb] = dq_f16(W[(j + 1) & 1][cb][0][0], dqc, s2[cb], s24[cb]);
+                    }
+                    // Issue one stream piece per step.
+                    if constexpr (s <= 4) issue_act(pa, ka, j + 3, s);
+                    if constexpr (s == 2) issue_w(pw, kw, j & 1, 0);    // low halves of g decoded
+                    if constexpr (s == 5 && j == 0)
+                        issue_scales(last ? pn.st : pc.st, last ? sbn : sbc, last ? 0 : kb + 1, (b + 1) & 1);
+                    if constexpr (s == 6) issue_w(pw, kw, j & 1, 1);    // high halves of g decoded
                 });
-                const float sc = bf16_to_f32(scr);
-                // ---- Q4: row blocks 2, 3, steps 4-7; rescale blocks 0, 1 of g.
-                if constexpr (live23) {
-                static_for<4>([&](auto S_) {
-                        constexpr int s = 4 + decltype(S_)::value;
-                        constexpr int cb = (s + 4) & 1, nb = cb ^ 1;
-                        // next: Q4 step s + 1, or Q1 step 0 of g + 1 (next slot)
-                        if constexpr (s < 7) lds_read2<2 * mm::kBlk + 16 * (s + 1)>(xg, A[nb][0], A[nb][1]);
-                        else lds_read2<0>(xa0 + nso, A[nb][0], A[nb][1]);
-                        lgkm_wait<2>(A[cb][0], A[cb][1]);
-                        P[2] = mfma32x32x16(as_bf16x8(A[cb][0]), Bd[s], P[2]);
-                        if constexpr (live3) P[3] = mfma32x32x16(as_bf16x8(A[cb][1]), Bd[s], P[3]);
-                        issue_part(std::integral_constant<int, s>{});
-#pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const int blk = e >> 2, idx = (s - 4) * 4 + (e & 3);
-                            acc[blk][idx] = __builtin_fmaf(sc, P[blk][idx], acc[blk][idx]);
-                        }
-                    });
-                } else {
-                    issue_part(std::integral_constant<int, 4>{});
-                    issue_part(std::integral_constant<int, 5>{});
-                    issue_part(std::integral_constant<int, 6>{});
-#pragma unroll
-                    for (int blk = 0; blk < 2; ++blk)
-#pragma unroll
-                        for (int i = 0; i < 16; ++i) acc[blk][i] = __builtin_fmaf(sc, P[blk][i], acc[blk][i]);
-                }
-                sc_prev = sc;
             });
-
-            // ---- end of batch: rescale blocks 2, 3 of the last group, then
-            // the batch's offset correction.
-#pragma unroll
-            for (int blk = 2; blk < 4; ++blk)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) acc[blk][i] = __builtin_fmaf(sc_prev, P[blk][i], acc[blk][i]);
-            {
-                const uint32_t xb = lds_addr(lds + mm::kXBuf + (b & 1) * 4096);
-                const uint32_t sb = lds_addr(lds + mm::kSBuf + (b & 1) * 4096 + stile * 256) +
-                                    (uint32_t)((col & 15) * 2);
-                uint32_t sv[4];
-#pragma unroll
-                for (int q = 0; q < 4; ++q) sv[q] = lds_read_u16(sb + (uint32_t)((4 * h + q) * 32));
-                const bf16x8 sop = __builtin_bit_cast(
-                    bf16x8, u32x4{sv[0] | (sv[0] << 16), sv[1] | (sv[1] << 16), sv[2] | (sv[2] << 16),
-                                  sv[3] | (sv[3] << 16)});
-#pragma unroll
-                for (int rb = 0; rb < 4; ++rb) {
-                    const uint4 xv = lds_bcast16(xb + (uint32_t)((rb * 32 + col) * 32 + h * 16));
-                    const bf16x8 xop = __builtin_bit_cast(
-                        bf16x8, u32x4{split_bf16(-136.0f * __uint_as_float(xv.x)),
-                                      split_bf16(-136.0f * __uint_as_float(xv.y)),
-                                      split_bf16(-136.0f * __uint_as_float(xv.z)),
-                                      split_bf16(-136.0f * __uint_as_float(xv.w))});
-                    acc[rb] = mfma32x32x16(xop, sop, acc[rb]);
-                }
-            }
             if (last) {
-                // Item done: store it (the fragments of the next group's Q1
-                // step 0 are in flight in A[0]; wait for them first). The
-                // epilogue's LDS scratch is this batch's scale buffer, consumed
-                // above and next written by the batch DMA of the next batch.
-                lgkm_wait<0>(A[0][0], A[0][1]);
-                __builtin_amdgcn_s_barrier();   // every wave has read this batch's scales
-                mm_epilogue<NMAT>(a, item(ib), lds_addr(lds + mm::kSBuf + (b & 1) * 4096), wave, lane, acc);
+                // Item done: store it. The next group's first fragments are in
+                // flight in A[0]; wait for them first.
+                lgkm_frags<0, NRB>(A[0]);
+                mm_epilogue<NMAT>(a, item(ib), lds_addr(lds + mm::kRho + ib * kBigRows * 4), wave, lane, acc);
 #pragma unroll
-                for (int rb = 0; rb < 4; ++rb) acc[rb] = f32x16{};
+                for (int rb = 0; rb < 4; ++rb) acc[rb][0] = acc[rb][1] = f32x16{};
                 ++ib;
                 kb = 0;
                 pc = pn;
-                uc = un;
-                pn = mm_ptrs<NMAT>(a, item(ib + 1), K, KG, wave, lane, un);
+                sbc = sbn;
+                pn = mm_ptrs<NMAT>(a, item(ib + 1), K, KG, wave, lane, sbn);
             } else {
                 ++kb;
             }
@@ -593,30 +533,78 @@ static int launch_mm(const MmArgs& a, long max_items, hipStream_t s) {
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
+// x (bf16) -> fp16 with a power-of-2 scale per row so the row's largest
+// magnitude lies in [2^14, 2^15): exact for every finite bf16 row down to
+// 2^-10 of the row maximum (bf16's 8 significant bits fit fp16's 11; smaller
+// elements round to fp16's subnormal steps). rho[t] = the inverse factor,
+// applied to the row's outputs. One wave per row.
+__global__ __launch_bounds__(256) void f16_rows_kernel(const uint16_t* __restrict__ x, int n, int H,
+                                                      uint16_t* __restrict__ xh, float* __restrict__ rho) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= n) return;
+    const uint16_t* xr = x + (size_t)t * H;
+    uint32_t amax = 0;   // bf16 magnitudes compare as integers
+    for (int i = lane * 8; i < H; i += 512) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xr + i);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            amax = max(amax, w[q] & 0x7fffu);
+            amax = max(amax, (w[q] >> 16) & 0x7fffu);
+        }
+    }
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off));
+    // Exponent of the row maximum (bf16 exponent field); all-zero rows use 0.
+    const int e = amax >= 0x0080u ? (int)(amax >> 7) - 127 : 0;
+    int k = 14 - e;                       // max * 2^k in [2^14, 2^15)
+    k = k > 100 ? 100 : (k < -100 ? -100 : k);
+    const float scale = __builtin_ldexpf(1.0f, k);
+    if (lane == 0) rho[t] = __builtin_ldexpf(1.0f, -k);
+    uint16_t* yr = xh + (size_t)t * H;
+    for (int i = lane * 8; i < H; i += 512) {
+        const uint4 v = *reinterpret_cast<const uint4*>(xr + i);
+        const uint32_t w[4] = {v.x, v.y, v.z, v.w};
+        uint32_t o[4];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const _Float16 lo = (_Float16)(bf16_to_f32(w[q] & 0xffffu) * scale);
+            const _Float16 hi = (_Float16)(bf16_to_f32(w[q] >> 16) * scale);
+            o[q] = (uint32_t)__builtin_bit_cast(uint16_t, lo) | ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+        }
+        *reinterpret_cast<uint4*>(yr + i) = make_uint4(o[0], o[1], o[2], o[3]);
+    }
+}
+
 bool big_w4_shape_ok(int H, int I) { return H % 1024 == 0 && I % 1024 == 0; }
 
-int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, const float* xsum,
-                       const int* tiles, const int* ntiles, int max_tiles, const int* rows_tok,
-                       uint16_t* h, float* hsum, int H, int I, int E, hipStream_t s) {
+// scratch: the dpart region (free until the down projection): xh [n, H] fp16
+// then rho [n] fp32.
+int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int* tiles,
+                       const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
+                       void* scratch, int H, int I, int E, hipStream_t s) {
     if (!big_w4_shape_ok(H, I)) return -2;
+    uint16_t* xh = reinterpret_cast<uint16_t*>(scratch);
+    float* rho = reinterpret_cast<float*>(xh + (size_t)n * H);
+    hipLaunchKernelGGL(f16_rows_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, x, n, H, xh, rho);
+    if (hipGetLastError() != hipSuccess) return -4;
     MmArgs a{};
     a.wq[0] = P.gate_q; a.ws[0] = P.gate_s; a.wq[1] = P.up_q; a.ws[1] = P.up_s;
     a.swq[0] = P.sh_gate_q; a.sws[0] = P.sh_gate_s; a.swq[1] = P.sh_up_q; a.sws[1] = P.sh_up_s;
-    a.src = x; a.gsum = xsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
-    a.rows_tok = rows_tok; a.h = h; a.hsum = hsum; a.H = H; a.I = I; a.E = E;
-    return launch_mm<2>(a, (long)max_tiles * (I / 128), s);
+    a.src = xh; a.rho = rho; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
+    a.rows_tok = rows_tok; a.h = h; a.H = H; a.I = I; a.E = E;
+    return launch_mm<2>(a, (long)max_tiles * (I / 256), s);
 }
 
-int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
-                    const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
-                    hipStream_t s) {
+int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
+                    int max_tiles, float* dpart, int H, int I, int E, hipStream_t s) {
     if (!big_w4_shape_ok(H, I)) return -2;
     MmArgs a{};
     a.wq[0] = P.down_q; a.ws[0] = P.down_s; a.wq[1] = P.down_q; a.ws[1] = P.down_s;
     a.swq[0] = P.sh_down_q; a.sws[0] = P.sh_down_s; a.swq[1] = P.sh_down_q; a.sws[1] = P.sh_down_s;
-    a.src = h; a.gsum = hsum; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
+    a.src = h; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.dout = reinterpret_cast<uint16_t*>(dpart); a.H = H; a.I = I; a.E = E;
-    return launch_mm<1>(a, (long)max_tiles * (H / 256), s);
+    return launch_mm<1>(a, (long)max_tiles * (H / 512), s);
 }
 
 }  // namespace glmmoe
