@@ -84,32 +84,11 @@ static_assert(kTotal <= 160 * 1024, "one workgroup's LDS");
 constexpr int kBlk = 32 * kRowB;               // one 32-row block
 }  // namespace mm
 
-// 16-row weight tile of lane column col (0..31) in column block cb of wave w,
-// feature group g.
-//   gate/up: matrix cb (0 gate, 1 up), tile 16 g + 2 w + col / 16;
-//   down:    matrix 0, tile 32 g + 4 w + 2 cb + col / 16.
-template <int NMAT>
-__device__ __forceinline__ void mm_lane_tile(int g, int wave, int cb, int col, int& m, int& fb) {
-    if (NMAT == 2) {
-        m = cb;
-        fb = 16 * g + 2 * wave + (col >> 4);
-    } else {
-        m = 0;
-        fb = 32 * g + 4 * wave + 2 * cb + (col >> 4);
-    }
-}
-// The workgroup's tile t (0..31) in the scale buffer: gate/up tiles 0-15 are
-// gate, 16-31 up; down tiles are consecutive.
-template <int NMAT>
-__device__ __forceinline__ void mm_wg_tile(int g, int t, int& m, int& fb) {
-    if (NMAT == 2) {
-        m = t >> 4;
-        fb = 16 * g + (t & 15);
-    } else {
-        m = 0;
-        fb = 32 * g + t;
-    }
-}
+// Scale-buffer tile of lane column col in column block cb of wave w: the
+// workgroup's 32 tiles per group are, for gate/up, gate tiles 16 g + 0..15
+// then up tiles 16 g + 0..15; for down tiles 32 g + 0..31. Column block cb of
+// wave w holds, for gate/up, matrix cb's tile 16 g + 2 w + col / 16; for down
+// tile 32 g + 4 w + 2 cb + col / 16.
 template <int NMAT>
 __device__ __forceinline__ int mm_sbuf_tile(int wave, int cb, int col) {
     return NMAT == 2 ? 16 * cb + 2 * wave + (col >> 4) : 4 * wave + 2 * cb + (col >> 4);
@@ -132,26 +111,46 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t mm_rsrc(const void* base) {
                                              0x00020000);
 }
 
-// Per-lane stream state of one item.
-//   act[i]: byte offset (in src) of this lane's 16 B of activation DMA i at
-//     group 0; DMA d = wave + 8 i (i < 4) or 32 + (wave & 1) (i = 4; waves
-//     2-7 repeat DMAs 32 and 33 of waves 0, 1: same source, same LDS bytes,
-//     so every wave waits for the same counts) fills slot bytes 1024 d +
-//     16 lane = row p / 17, 16-B chunk p % 17 (p = 64 d + lane); chunk 16 is
-//     padding (loads chunk 0 again);
-//   w[cb]: the lane's 32 B of int4 of column block cb at group 0 (K positions
+// Stream state of one item.
+//   act[i] (per lane): byte offset (in src) of this lane's 16 B of activation
+//     DMA i at group 0; DMA d = wave + 8 i (i < 4) or 32 + (wave & 1) (i = 4;
+//     waves 2-7 repeat DMAs 32 and 33 of waves 0, 1: same source, same LDS
+//     bytes, so every wave waits for the same counts) fills slot bytes
+//     1024 d + 16 lane = row p / 17, 16-B chunk p % 17 (p = 64 d + lane);
+//     chunk 16 is padding (loads chunk 0 again);
+//   wb[cb] (uniform): base of the wave's weight tiles of column block cb; a
+//     lane adds the item-invariant MmLane::w (its 32 B of int4: K positions
 //     64 h .. 64 h + 63 of weight row col % 16 of its tile);
-//   st: byte offset of the lane's 16 B of the scale DMA at batch 0 (tile
-//     4 w + lane / 16 of the workgroup).
+//   sb (uniform): base of the scales of the workgroup's 32 tiles (as the
+//     wave sees them: the wave's 4 tiles share one matrix); a lane adds
+//     MmLane::s.
+// Only act needs vector registers: the item's other addresses are scalar.
 struct MmPtrs {
     uint32_t act[5];
-    const uint4* w[2];
-    uint32_t st;
+    const uint8_t* wb[2];
+    const uint16_t* sb;
 };
+struct MmLane {
+    uint32_t w, s;
+};
+
+// The item-invariant lane offsets:
+//   gate/up: weight tile 16 g + (2 w + col / 16), scale tile 16 g + (4 w + lane / 16) % 16;
+//   down:    weight tile 32 g + 2 cb + (4 w + col / 16), scale tile 32 g + (4 w + lane / 16).
+template <int NMAT>
+__device__ __forceinline__ MmLane mm_lane(int KG, int wave, int lane) {
+    const int col = lane & 31, h = lane >> 5;
+    const int tl = NMAT == 2 ? 2 * wave + (col >> 4) : 4 * wave + (col >> 4);
+    const int ts = NMAT == 2 ? (4 * wave + (lane >> 4)) & 15 : 4 * wave + (lane >> 4);
+    MmLane l;
+    l.w = (uint32_t)tl * KG * 1024 + (col & 15) * 16 + h * 512;
+    l.s = ((uint32_t)ts * KG * 16 + (lane & 15) * 8) * 2u;
+    return l;
+}
 
 template <int NMAT>
 __device__ __forceinline__ MmPtrs mm_ptrs(const MmArgs& a, const BigItem& it, int K, int KG, int wave,
-                                          int lane, const uint16_t*& sbase) {
+                                          int lane) {
     MmPtrs p;
 #pragma unroll
     for (int i = 0; i < 5; ++i) {
@@ -160,20 +159,17 @@ __device__ __forceinline__ MmPtrs mm_ptrs(const MmArgs& a, const BigItem& it, in
         const int row = pos / 17, c = pos % 17;
         p.act[i] = lds_read32(it.tab + 16 + row * 4) * (uint32_t)(K * 2) + (uint32_t)((c & 15) * 16);
     }
-    const int col = lane & 31, h = lane >> 5;
     const int frows = NMAT == 2 ? a.I : a.H;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
-        int m, fb;
-        mm_lane_tile<NMAT>(it.g, wave, cb, col, m, fb);
-        const uint4* base = reinterpret_cast<const uint4*>(mm_wbase<NMAT>(a, it.e, m, frows, KG));
-        p.w[cb] = base + (size_t)fb * KG * 64 + (col & 15) + 32 * h;
+        const int m = NMAT == 2 ? cb : 0;
+        const int fb = NMAT == 2 ? 16 * it.g : 32 * it.g + 2 * cb;
+        p.wb[cb] = mm_wbase<NMAT>(a, it.e, m, frows, KG) + (size_t)fb * KG * 1024;
     }
     {
-        int m, fb;
-        mm_wg_tile<NMAT>(it.g, 4 * wave + (lane >> 4), m, fb);
-        sbase = mm_sbase<NMAT>(a, it.e, m, frows, KG);   // uniform: a wave's 4 tiles share the matrix
-        p.st = ((uint32_t)fb * KG * 16 + (lane & 15) * 8) * 2u;
+        const int m = NMAT == 2 ? (wave >> 2) : 0;
+        const int fb = NMAT == 2 ? 16 * it.g : 32 * it.g;
+        p.sb = mm_sbase<NMAT>(a, it.e, m, frows, KG) + (size_t)fb * KG * 16;
     }
     return p;
 }
@@ -264,43 +260,73 @@ __device__ __forceinline__ void scale_pair(uint32_t sbits, f16x2& s2, f16x2& s24
     s24 = f16x2{b, b};
 }
 
-// Stores an item's outputs.
+// Stores an item's outputs through stg, 1 KiB of LDS private to the wave: the
+// accumulator layout gives a lane one feature of 4 consecutive rows, so each
+// round writes a block of rows x features to stg (2-byte writes) and reads it
+// back as 16 contiguous bytes of one row per lane, stored with one 16-B
+// global store (8x fewer stores than element-wise: stores count in the same
+// vmcnt as the stream's prefetches, so fewer of them means a shorter drain).
+// rho (gate/up): the item's row factors in LDS.
 template <int NMAT>
-__device__ __forceinline__ void mm_epilogue(const MmArgs& a, const BigItem& cur, uint32_t rho, int wave,
-                                            int lane, f32x16 (&acc)[4][2]) {
+__device__ __forceinline__ void mm_epilogue(const MmArgs& a, const BigItem& cur, uint32_t rho, uint32_t stg,
+                                            int wave, int lane, f32x16 (&acc)[4][2]) {
     // Laundered lane index: keeps the per-row addresses below from being
     // hoisted out of the streaming loop (they would stay live and spill).
     int ln = lane;
     asm volatile("" : "+v"(ln));
     const int col = ln & 31, h = ln >> 5;
     if constexpr (NMAT == 2) {
-        // h = silu(g) * u of this lane's feature, rows' scale undone first.
-        uint16_t* hcol = a.h + (size_t)cur.r0 * a.I + cur.g * 256 + wave * 32 + col;
+        // h = silu(g) * u of this lane's feature (rows' scale undone first);
+        // a round is 16 rows x this wave's 32 features of fp16.
+        uint16_t* hbase = a.h + (size_t)cur.r0 * a.I + cur.g * 256 + wave * 32 + (ln & 3) * 8;
+#pragma unroll
+        for (int rb = 0; rb < 4; ++rb) {
+            float rr[16];   // row factors of the lane's 16 rows of block rb
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = lds_bcast16(rho + (uint32_t)((rb * 32 + 8 * q + 4 * h) * 4));
+                rr[4 * q] = __uint_as_float(v.x);
+                rr[4 * q + 1] = __uint_as_float(v.y);
+                rr[4 * q + 2] = __uint_as_float(v.z);
+                rr[4 * q + 3] = __uint_as_float(v.w);
+            }
+#pragma unroll
+            for (int half = 0; half < 2; ++half) {
+#pragma unroll
+                for (int ii = 0; ii < 8; ++ii) {
+                    const int i = half * 8 + ii;
+                    const float gt = acc[rb][0][i] * rr[i], up = acc[rb][1][i] * rr[i];
+                    const uint16_t hv = __builtin_bit_cast(uint16_t, (_Float16)(silu_fast(gt) * up));
+                    const int rl = 8 * (ii >> 2) + 4 * h + (ii & 3);   // row within the round
+                    asm volatile("ds_write_b16 %0, %1" : : "v"(stg + (uint32_t)(rl * 64 + col * 2)), "v"((uint32_t)hv)
+                                 : "memory");
+                }
+                const uint4 v = lds_bcast16(stg + (uint32_t)(ln * 16));
+                const int row = rb * 32 + half * 16 + (ln >> 2);
+                if (row < cur.nr) *reinterpret_cast<uint4*>(hbase + (size_t)row * a.I) = v;
+            }
+        }
+    } else {
+        // Per-row expert outputs as bf16 (the combine adds them in fp32); a
+        // round is 8 rows x this wave's 64 features.
+        uint16_t* dbase = a.dout + (size_t)cur.r0 * a.H + cur.g * 512 + wave * 64 + (ln & 7) * 8;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
-            for (int i = 0; i < 16; ++i) {
-                const int row = rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-                if (row < cur.nr) {
-                    const float r = __uint_as_float(lds_read32(rho + (uint32_t)row * 4));
-                    const float gt = acc[rb][0][i] * r, up = acc[rb][1][i] * r;
-                    hcol[(size_t)row * a.I] = __builtin_bit_cast(uint16_t, (_Float16)(silu_fast(gt) * up));
-                }
+            for (int q = 0; q < 4; ++q) {
+#pragma unroll
+                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const uint32_t bv = pack_bf16x2(acc[rb][cb][4 * q + e], 0.0f) & 0xffffu;
+                        asm volatile("ds_write_b16 %0, %1"
+                                     : : "v"(stg + (uint32_t)((4 * h + e) * 128 + (32 * cb + col) * 2)), "v"(bv)
+                                     : "memory");
+                    }
+                const uint4 v = lds_bcast16(stg + (uint32_t)(ln * 16));
+                const int row = rb * 32 + 8 * q + (ln >> 3);
+                if (row < cur.nr) *reinterpret_cast<uint4*>(dbase + (size_t)row * a.H) = v;
             }
-    } else {
-        // Per-row expert outputs as bf16 (the combine adds them in fp32).
-        uint16_t* dcol = a.dout + (size_t)cur.r0 * a.H + cur.g * 512 + wave * 64 + col;
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb)
-#pragma unroll
-            for (int rb = 0; rb < 4; ++rb)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int row = rb * 32 + 8 * (i >> 2) + 4 * h + (i & 3);
-                    if (row < cur.nr)
-                        dcol[(size_t)row * a.H + cb * 32] =
-                            (uint16_t)(pack_bf16x2(acc[rb][cb][i], 0.0f) & 0xffffu);
-                }
     }
 }
 
@@ -328,6 +354,7 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
     const uint32_t sa0 = lds_addr(lds + mm::kSBuf) + (uint32_t)((col & 15) * 2);
     const int st0 = mm_sbuf_tile<NMAT>(wave, 0, col), st1 = mm_sbuf_tile<NMAT>(wave, 1, col);
     const __amdgpu_buffer_rsrc_t rsrc_src = mm_rsrc(a.src);
+    const MmLane ml = mm_lane<NMAT>(KG, wave, lane);
 
     auto cls_of = [&](long k) {
         const long t = big_item_id(k) / nfg;
@@ -353,27 +380,27 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
         // land in buffers nobody reads). In the last batch of an item the
         // activation stream (3 groups ahead) and the weight stream (2 ahead)
         // cross into the next item at fixed group positions.
-        const uint16_t *sbc, *sbn;
-        MmPtrs pc = mm_ptrs<NMAT>(a, item(0), K, KG, wave, lane, sbc);
-        MmPtrs pn = mm_ptrs<NMAT>(a, item(1), K, KG, wave, lane, sbn);
+        MmPtrs pc = mm_ptrs<NMAT>(a, item(0), K, KG, wave, lane);
+        MmPtrs pn = mm_ptrs<NMAT>(a, item(1), K, KG, wave, lane);
         u32x4 W[2][2][2];   // [ring][column block][lo / hi 16 B]
         auto issue_w = [&](const MmPtrs& p, int k, int r, int half) {
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb)
-                W[r][cb][half] = __builtin_bit_cast(u32x4, p.w[cb][(size_t)k * 64 + half * 16]);
+                W[r][cb][half] = __builtin_bit_cast(
+                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(mm_rsrc(p.wb[cb]), ml.w, k * 1024 + half * 256, 0));
         };
         auto issue_act = [&](const MmPtrs& p, int k, int gslot, int i) {
             const uint32_t dst = ring + (uint32_t)((gslot & 3) * mm::kSlot);
             const int d = i < 4 ? wave + 8 * i : 32 + (wave & 1);
             dma_buf16(rsrc_src, dst + (uint32_t)(d * 1024), p.act[i], (uint32_t)k * 256u);
         };
-        auto issue_scales = [&](uint32_t st, const uint16_t* sb, int kb, int parity) {
-            dma_buf16(mm_rsrc(sb), lds_addr(lds + mm::kSBuf + parity * 8192 + wave * 1024), st,
+        auto issue_scales = [&](const uint16_t* sb, int kb, int parity) {
+            dma_buf16(mm_rsrc(sb), lds_addr(lds + mm::kSBuf + parity * 8192 + wave * 1024), ml.s,
                       (uint32_t)kb * 256u);
         };
 
         // Prologue: scales of batch 0, activation groups 0-2, weights 0-1.
-        issue_scales(pc.st, sbc, 0, 0);
+        issue_scales(pc.sb, 0, 0);
 #pragma unroll
         for (int g0 = 0; g0 < 3; ++g0)
 #pragma unroll
@@ -434,8 +461,8 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
                 MmPtrs pw = pc;
                 int kw = 8 * kb + j + 2;
                 if constexpr (j >= 6) {
-                    pw.w[0] = last ? pn.w[0] : pc.w[0];
-                    pw.w[1] = last ? pn.w[1] : pc.w[1];
+                    pw.wb[0] = last ? pn.wb[0] : pc.wb[0];
+                    pw.wb[1] = last ? pn.wb[1] : pc.wb[1];
                     kw = last ? j - 6 : kw;
                 }
                 uint32_t nsr0 = 0, nsr1 = 0;   // scales of g + 1
@@ -480,7 +507,7 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
                     if constexpr (s <= 4) issue_act(pa, ka, j + 3, s);
                     if constexpr (s == 2) issue_w(pw, kw, j & 1, 0);    // low halves of g decoded
                     if constexpr (s == 5 && j == 0)
-                        issue_scales(last ? pn.st : pc.st, last ? sbn : sbc, last ? 0 : kb + 1, (b + 1) & 1);
+                        issue_scales(last ? pn.sb : pc.sb, last ? 0 : kb + 1, (b + 1) & 1);
                     if constexpr (s == 6) issue_w(pw, kw, j & 1, 1);    // high halves of g decoded
                 });
             });
@@ -488,14 +515,17 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
                 // Item done: store it. The next group's first fragments are in
                 // flight in A[0]; wait for them first.
                 lgkm_frags<0, NRB>(A[0]);
-                mm_epilogue<NMAT>(a, item(ib), lds_addr(lds + mm::kRho + ib * kBigRows * 4), wave, lane, acc);
+                // Staging for the stores: this batch's scale buffer, read for
+                // the last time in this batch's group 6 (the next batch's scale
+                // DMA into it is issued after the next group-start barrier).
+                mm_epilogue<NMAT>(a, item(ib), lds_addr(lds + mm::kRho + ib * kBigRows * 4),
+                                  lds_addr(lds + mm::kSBuf + (b & 1) * 8192 + wave * 1024), wave, lane, acc);
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb) acc[rb][0] = acc[rb][1] = f32x16{};
                 ++ib;
                 kb = 0;
                 pc = pn;
-                sbc = sbn;
-                pn = mm_ptrs<NMAT>(a, item(ib + 1), K, KG, wave, lane, sbn);
+                pn = mm_ptrs<NMAT>(a, item(ib + 1), K, KG, wave, lane);
             } else {
                 ++kb;
             }
