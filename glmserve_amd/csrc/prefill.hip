@@ -148,17 +148,21 @@ __device__ __forceinline__ MmLane mm_lane(int KG, int wave, int lane) {
     return l;
 }
 
-template <int NMAT>
+// act[i] of the item whose table entry is at LDS address tab.
+__device__ __forceinline__ uint32_t mm_act(uint32_t tab, int K, int wave, int lane, int i) {
+    const int d = i < 4 ? wave + 8 * i : 32 + (wave & 1);
+    const int pos = 64 * d + lane;
+    const int row = pos / 17, c = pos % 17;
+    return lds_read32(tab + 16 + row * 4) * (uint32_t)(K * 2) + (uint32_t)((c & 15) * 16);
+}
+
+// ACT false: the scalar addresses only (act left zero).
+template <int NMAT, bool ACT = true>
 __device__ __forceinline__ MmPtrs mm_ptrs(const MmArgs& a, const BigItem& it, int K, int KG, int wave,
                                           int lane) {
     MmPtrs p;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) {
-        const int d = i < 4 ? wave + 8 * i : 32 + (wave & 1);
-        const int pos = 64 * d + lane;
-        const int row = pos / 17, c = pos % 17;
-        p.act[i] = lds_read32(it.tab + 16 + row * 4) * (uint32_t)(K * 2) + (uint32_t)((c & 15) * 16);
-    }
+    for (int i = 0; i < 5; ++i) p.act[i] = ACT ? mm_act(it.tab, K, wave, lane, i) : 0u;
     const int frows = NMAT == 2 ? a.I : a.H;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
@@ -201,22 +205,18 @@ __device__ __forceinline__ void lgkm_frags(u32x4 (&a)[4]) {
     else
         asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]) : "n"(N));
 }
-template <int N, int NB>
-__device__ __forceinline__ void lgkm_frags2(u32x4 (&a)[4], uint32_t& x, uint32_t& y) {
-    if constexpr (NB == 1)
-        asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(a[0]), "+v"(x), "+v"(y) : "n"(N));
-    else if constexpr (NB == 2)
-        asm volatile("s_waitcnt lgkmcnt(%4)" : "+v"(a[0]), "+v"(a[1]), "+v"(x), "+v"(y) : "n"(N));
-    else
-        asm volatile("s_waitcnt lgkmcnt(%6)"
-                     : "+v"(a[0]), "+v"(a[1]), "+v"(a[2]), "+v"(a[3]), "+v"(x), "+v"(y)
-                     : "n"(N));
-}
 
 __device__ __forceinline__ void dma_buf16(__amdgpu_buffer_rsrc_t r, uint32_t lds_dst, uint32_t voff,
                                           uint32_t soff) {
     __builtin_amdgcn_raw_ptr_buffer_load_lds(
         r, (__attribute__((address_space(3))) void*)(uintptr_t)lds_dst, 16, voff, soff, 0, 0);
+}
+
+// One lane's 16 B of weights: buffer load at base + voff + soff (compiler
+// visible: the compiler waits for it before any use or copy of dst). The
+// weights are read once: streaming (non-temporal) cache policy.
+__device__ __forceinline__ void w_load(u32x4& dst, const uint8_t* base, uint32_t voff, uint32_t soff) {
+    dst = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(mm_rsrc(base), voff, soff, 2));
 }
 
 __device__ __forceinline__ f32x16 mfma16(u32x4 a, bf16x8 b, f32x16 c) {
@@ -351,8 +351,11 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
     // Lane's fragment address at step 0 of row block 0 in slot 0: row col,
     // 16-B chunk 8 h; step s adds 16 s, row block rb 8704 rb, slot q 34 KiB q.
     const uint32_t xa0 = ring + (uint32_t)(col * mm::kRowB + h * 128);
-    const uint32_t sa0 = lds_addr(lds + mm::kSBuf) + (uint32_t)((col & 15) * 2);
-    const int st0 = mm_sbuf_tile<NMAT>(wave, 0, col), st1 = mm_sbuf_tile<NMAT>(wave, 1, col);
+    // Lane's scale of column block 0 in scale buffer 0 at group 0; column
+    // block 1's is kSt1 bytes further.
+    const uint32_t sa0 = lds_addr(lds + mm::kSBuf) +
+                         (uint32_t)(mm_sbuf_tile<NMAT>(wave, 0, col) * 256 + (col & 15) * 2);
+    constexpr int kSt1 = NMAT == 2 ? 16 * 256 : 2 * 256;
     const __amdgpu_buffer_rsrc_t rsrc_src = mm_rsrc(a.src);
     const MmLane ml = mm_lane<NMAT>(KG, wave, lane);
 
@@ -380,19 +383,23 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
         // land in buffers nobody reads). In the last batch of an item the
         // activation stream (3 groups ahead) and the weight stream (2 ahead)
         // cross into the next item at fixed group positions.
+        // The next item's act offsets are read from its table entry when
+        // needed (5 fewer registers held through the stream).
         MmPtrs pc = mm_ptrs<NMAT>(a, item(0), K, KG, wave, lane);
-        MmPtrs pn = mm_ptrs<NMAT>(a, item(1), K, KG, wave, lane);
+        MmPtrs pn = mm_ptrs<NMAT, false>(a, item(1), K, KG, wave, lane);
+        auto next_tab = [&](int k) {
+            return lds_addr(lds + mm::kTab) + (uint32_t)((k + 1 < cnt ? k + 1 : cnt - 1) * kBigTabInts * 4);
+        };
         u32x4 W[2][2][2];   // [ring][column block][lo / hi 16 B]
         auto issue_w = [&](const MmPtrs& p, int k, int r, int half) {
 #pragma unroll
             for (int cb = 0; cb < 2; ++cb)
-                W[r][cb][half] = __builtin_bit_cast(
-                    u32x4, __builtin_amdgcn_raw_buffer_load_b128(mm_rsrc(p.wb[cb]), ml.w, k * 1024 + half * 256, 0));
+                w_load(W[r][cb][half], p.wb[cb], ml.w, (uint32_t)(k * 1024 + half * 256));
         };
-        auto issue_act = [&](const MmPtrs& p, int k, int gslot, int i) {
+        auto issue_act = [&](uint32_t act, int k, int gslot, int i) {
             const uint32_t dst = ring + (uint32_t)((gslot & 3) * mm::kSlot);
             const int d = i < 4 ? wave + 8 * i : 32 + (wave & 1);
-            dma_buf16(rsrc_src, dst + (uint32_t)(d * 1024), p.act[i], (uint32_t)k * 256u);
+            dma_buf16(rsrc_src, dst + (uint32_t)(d * 1024), act, (uint32_t)k * 256u);
         };
         auto issue_scales = [&](const uint16_t* sb, int kb, int parity) {
             dma_buf16(mm_rsrc(sb), lds_addr(lds + mm::kSBuf + parity * 8192 + wave * 1024), ml.s,
@@ -404,7 +411,7 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
 #pragma unroll
         for (int g0 = 0; g0 < 3; ++g0)
 #pragma unroll
-            for (int i = 0; i < 5; ++i) issue_act(pc, g0, g0, i);
+            for (int i = 0; i < 5; ++i) issue_act(pc.act[i], g0, g0, i);
 #pragma unroll
         for (int r = 0; r < 2; ++r) {
             issue_w(pc, r, r, 0);
@@ -418,8 +425,8 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
         for (int rb = 0; rb < 4; ++rb) acc[rb][0] = acc[rb][1] = f32x16{};
         // Scales of group 0 and the decoded B of its step 0.
         f16x2 s2[2], s24[2];
-        scale_pair(lds_read_u16(sa0 + (uint32_t)(st0 * 256)), s2[0], s24[0]);
-        scale_pair(lds_read_u16(sa0 + (uint32_t)(st1 * 256)), s2[1], s24[1]);
+        scale_pair(lds_read_u16(sa0), s2[0], s24[0]);
+        scale_pair(lds_read_u16(sa0 + kSt1), s2[1], s24[1]);
         bf16x8 Bd[2][2];   // [parity][column block]
         Bd[0][0] = dq_f16(W[0][0][0][0], dqc, s2[0], s24[0]);
         Bd[0][1] = dq_f16(W[0][1][0][0], dqc, s2[1], s24[1]);
@@ -451,13 +458,8 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
                 // Stream sources: activations of group g + 3, weights of group
                 // g + 2 (this item's or, late in the item's last batch, the next
                 // item's: selects, no branches).
-                MmPtrs pa = pc;
                 int ka = 8 * kb + j + 3;
-                if constexpr (j >= 5) {
-#pragma unroll
-                    for (int q = 0; q < 5; ++q) pa.act[q] = last ? pn.act[q] : pc.act[q];
-                    ka = last ? j - 5 : ka;
-                }
+                if constexpr (j >= 5) ka = last ? j - 5 : ka;
                 MmPtrs pw = pc;
                 int kw = 8 * kb + j + 2;
                 if constexpr (j >= 6) {
@@ -477,20 +479,24 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
                         // batch's buffer, written in this batch's first group).
                         const uint32_t sb = sa0 + (uint32_t)((j == 7 ? ((b + 1) & 1) : (b & 1)) * 8192 +
                                                              ((j + 1) & 7) * 32);
-                        asm volatile("ds_read_u16 %0, %2\n ds_read_u16 %1, %3"
+                        asm volatile("ds_read_u16 %0, %2\n ds_read_u16 %1, %2 offset:%3"
                                      : "=&v"(nsr0), "=&v"(nsr1)
-                                     : "v"(sb + (uint32_t)(st0 * 256)), "v"(sb + (uint32_t)(st1 * 256)));
-                        lgkm_frags<NRB + 2, NRB>(A[cbuf]);
-                    } else if constexpr (s == 5) {
-                        lgkm_frags2<NRB, NRB>(A[cbuf], nsr0, nsr1);
-                    } else {
-                        lgkm_frags<NRB, NRB>(A[cbuf]);
+                                     : "v"(sb), "n"(kSt1));
                     }
-#pragma unroll
-                    for (int rb = 0; rb < NRB; ++rb) {
+                    // Each row block's MFMAs start as soon as its fragment is
+                    // in (LDS reads complete in order; pending behind it: the
+                    // step's later fragments, step s + 1's and, at step 4,
+                    // the 2 scale reads).
+                    static_for<NRB>([&](auto R_) {
+                        constexpr int rb = decltype(R_)::value;
+                        constexpr int n = (s == 4 ? 2 : 0) + NRB + (NRB - 1 - rb);
+                        if constexpr (s == 5 && rb == NRB - 1)
+                            asm volatile("s_waitcnt lgkmcnt(%3)" : "+v"(A[cbuf][rb]), "+v"(nsr0), "+v"(nsr1) : "n"(n));
+                        else
+                            asm volatile("s_waitcnt lgkmcnt(%1)" : "+v"(A[cbuf][rb]) : "n"(n));
                         acc[rb][0] = mfma16(A[cbuf][rb], Bd[cbuf][0], acc[rb][0]);
                         acc[rb][1] = mfma16(A[cbuf][rb], Bd[cbuf][1], acc[rb][1]);
-                    }
+                    });
                     // Decode step s + 1 (or step 0 of g + 1 with its scales).
                     if constexpr (s < 7) {
 #pragma unroll
@@ -504,7 +510,11 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
                             Bd[nbuf][cb] = dq_f16(W[(j + 1) & 1][cb][0][0], dqc, s2[cb], s24[cb]);
                     }
                     // Issue one stream piece per step.
-                    if constexpr (s <= 4) issue_act(pa, ka, j + 3, s);
+                    if constexpr (s <= 4) {
+                        uint32_t act = pc.act[s];
+                        if constexpr (j >= 5) act = last ? mm_act(next_tab(ib), K, wave, lane, s) : act;
+                        issue_act(act, ka, j + 3, s);
+                    }
                     if constexpr (s == 2) issue_w(pw, kw, j & 1, 0);    // low halves of g decoded
                     if constexpr (s == 5 && j == 0)
                         issue_scales(last ? pn.sb : pc.sb, last ? 0 : kb + 1, (b + 1) & 1);
@@ -524,8 +534,8 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
                 for (int rb = 0; rb < 4; ++rb) acc[rb][0] = acc[rb][1] = f32x16{};
                 ++ib;
                 kb = 0;
-                pc = pn;
-                pn = mm_ptrs<NMAT>(a, item(ib + 1), K, KG, wave, lane);
+                pc = mm_ptrs<NMAT>(a, item(ib), K, KG, wave, lane);
+                pn = mm_ptrs<NMAT, false>(a, item(ib + 1), K, KG, wave, lane);
             } else {
                 ++kb;
             }
