@@ -88,7 +88,7 @@ class LayerWs(C.Structure):
     _fields_ = [("logits", _vp), ("rpart", _vp), ("xsum", _vp), ("topk_ids", _vp), ("topk_w", _vp),
                 ("expert_offsets", _vp), ("sorted_token_ids", _vp), ("sorted_row", _vp),
                 ("inv", _vp), ("tiles", _vp), ("ntiles", _vp), ("h", _vp), ("hsum", _vp),
-                ("dpart", _vp), ("bytes", _sz)]
+                ("dpart", _vp), ("sync", _vp), ("bytes", _sz)]
 
 
 class Fp8Ws(C.Structure):

@@ -93,6 +93,7 @@ size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v)
     w.h = reinterpret_cast<uint16_t*>(take(R * I * 2));
     w.hsum = reinterpret_cast<float*>(take(R * (I / 128) * 4));
     w.dpart = reinterpret_cast<float*>(take(R * H * 4));
+    w.sync = reinterpret_cast<unsigned int*>(take(kTailTicks * 4));
     w.bytes = off;
     if (v) *v = w;
     return off;
@@ -162,6 +163,13 @@ inline void end_call(hipStream_t s) {
     ++g_prof.calls;
 }
 
+// Bytes of the dpart region: free while the gate/up kernel runs, which keeps
+// the partials of its split items there.
+size_t dpart_bytes(const glmmoe_w4a16_layer* L, int n) {
+    const size_t R = (size_t)n * L->topk + (has_shared(L) ? (size_t)n : 0);
+    return R * L->hidden * 4;
+}
+
 // Dispatch onward, given ids/weights/xsum in the workspace view.
 int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int* ids,
                 const float* w, const float* xsum, float* out, const glmmoe_layer_ws& v,
@@ -175,14 +183,15 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     int rc = dispatched ? 0
                         : launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids,
                                           v.sorted_row, v.inv, v.tiles, v.ntiles, T, sh, 1, s,
-                                          dispatch_scratch(v.rpart, L, n), big ? kBigRows / 2 : 0);
+                                          dispatch_scratch(v.rpart, L, n), big ? kBigRows / 2 : 0,
+                                          v.sync, kTailTicks);
     if (rc) return rc;
     const ExpertPtrs P = ptrs(L);
     mark(GLMMOE_STAGE_GATE_UP, s);
     rc = big ? launch_gate_up_big(P, x, n, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.dpart,
                                   H, I, E, s)
              : launch_gate_up(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.hsum,
-                              H, I, E, s);
+                              v.sync, v.dpart, dpart_bytes(L, n), H, I, E, s);
     if (rc) return rc;
     mark(GLMMOE_STAGE_DOWN, s);
     rc = big ? launch_down_big(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
@@ -316,7 +325,7 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     const int T = tile_rows_for(n, k, sh, H, L->moe_inter);
     const DispOut disp{v.expert_offsets, v.sorted_token_ids, v.sorted_row, v.inv,
                        reinterpret_cast<int4*>(v.tiles), v.ntiles, T, sh, 1,
-                       T == kBigRows ? kBigRows / 2 : 0};
+                       T == kBigRows ? kBigRows / 2 : 0, v.sync, kTailTicks};
     bool dispatched = false;
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
                               L->routed_scale, v.logits, v.xsum, v.rpart, v.topk_ids, v.topk_w, s,

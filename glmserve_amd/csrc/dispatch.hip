@@ -55,10 +55,11 @@ size_t dispatch_scratch_bytes(int n, int topk, int E) {
 
 int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,
                     int* sorted_slot, int* inv, int* tiles, int* ntiles, int tile_rows,
-                    int with_shared, int mode, hipStream_t s, int* scratch, int half_rows) {
+                    int with_shared, int mode, hipStream_t s, int* scratch, int half_rows,
+                    unsigned int* zero, int nzero) {
     if (E > kDispMaxE || E < 1) return -2;
     const DispOut d{offsets, sorted_tok, sorted_slot, inv, reinterpret_cast<int4*>(tiles),
-                    ntiles, tile_rows, with_shared, mode, half_rows};
+                    ntiles, tile_rows, with_shared, mode, half_rows, zero, nzero};
     const long total = (long)n * topk;
     const long nblk = (total + kDispChunk - 1) / kDispChunk;
     if (scratch && total >= kDispMultiMin && nblk <= kDispMaxChunks) {

@@ -85,6 +85,8 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
     while ((1 << nbits) < E) ++nbits;
 
     if (i1 < 0) i1 = total;
+    if (blk == 0 && d.zero)
+        for (int i = tid; i < d.nzero; i += NT) d.zero[i] = 0u;
     for (int e = tid; e <= kDispMaxE; e += NT) cnt[e] = 0;
     for (int i = tid; i < (NT / 64) * kDispMaxE; i += NT) (&wc[0][0])[i] = 0;
     __syncthreads();

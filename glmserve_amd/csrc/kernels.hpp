@@ -45,6 +45,8 @@ struct DispOut {
     int with_shared;
     int mode;
     int half_rows;   // > 0: tail tiles of at most this many rows listed last; < 0: ntiles has one int
+    unsigned int* zero;   // nzero words the dispatch sets to 0 (the expert kernels' tickets), or null
+    int nzero;
 };
 
 // Scratch (bytes) the router-logit launch needs for n tokens; 0 for large n.
@@ -67,12 +69,16 @@ size_t dispatch_scratch_bytes(int n, int topk, int E);
 int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* sorted_tok,
                     int* sorted_slot, int* inv, int* tiles, int* ntiles, int tile_rows,
                     int with_shared, int mode, hipStream_t s, int* scratch = nullptr,
-                    int half_rows = -1);
+                    int half_rows = -1, unsigned int* zero = nullptr, int nzero = 0);
 int launch_pack_w4(const uint8_t* q, const void* sc, int sc_bf16, int n_mats, int rows, int K,
                    uint8_t* pq, uint16_t* ps, hipStream_t s);
+// tick: kTailTicks words, zero at launch (the dispatch clears them); tpart:
+// tpart_bytes of scratch for split items' partials (no split without them).
+constexpr int kTailTicks = 256;
 int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
                    const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
-                   float* hsum, int H, int I, int E, hipStream_t s);
+                   float* hsum, unsigned int* tick, float* tpart, size_t tpart_bytes, int H, int I,
+                   int E, hipStream_t s);
 int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
                 const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
                 hipStream_t s);

@@ -672,32 +672,25 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
 }
 
 // ---------------------------------------------------------------------------
-// Small batches inside the layer (n < kTiledMinTokens): logits, selection and
-// (optionally) the dispatch in one launch.
+// Small batches inside the layer (n < kTiledMinTokens): router_small_kernel
+// computes the logits and the selection's inputs (order codes, scores), then
+// router_finish_kernel selects and (n <= kFinishDispMax) dispatches.
 // Grid (ceil(E / epw), ceil(n / 8)) of 512 threads. The group's activations
 // are staged in LDS; thread (expert eb * epw + el, chunk c, token slice ts)
 // keeps the chunk's 128 router weights in registers and, for each token of
 // its slice, accumulates the chunk partial from zero in ascending K (the
 // fixed order of router_partials_kernel). Threads (expert, token) then add
 // the chunk partials in ascending chunk order: the logit, bit-identical to
-// the two-pass path.
-// Tickets: after its logits are stored, each workgroup takes a ticket of its
-// token group; the one that takes the last ticket (all the group's logits
-// are then stored) runs the top-k of the group's tokens, one wave per token.
-// With a dispatch, those selecting workgroups then take a ticket of the
-// launch, and the last one runs the whole dispatch. A ticket counter is reset
-// by the workgroup that took its last ticket, so every launch starts from
-// zero; launches that overlap in time on one GPU (different streams) must not
-// use this path together.
+// the two-pass path. No state outlives a launch: two launches may overlap on
+// different streams.
 // ---------------------------------------------------------------------------
 constexpr int kSmallThreads = 512;
 constexpr int kSmallMaxChunks = 64;
+constexpr int kFinishDispMax = 64;   // tokens up to which one workgroup selects and dispatches
 // Staged activation bytes: 8 tokens x nchunks rows of 256 B, whole 1 KiB DMAs.
 __host__ __device__ constexpr int small_x_bytes(int nchunks) {
     return (kRouterTG * nchunks * 256 + 1023) / 1024 * 1024;
 }
-constexpr int kSmallMaxTG = (kTiledMinTokens + kRouterTG - 1) / kRouterTG;
-static __device__ unsigned int g_small_tick[kSmallMaxTG + 1];
 
 // NT independent token chains over one 128-K chunk c: the ascending-K sum
 // from zero of x[t] * w, for tokens tb + t, t < nt (rows past nt repeat the
@@ -757,12 +750,9 @@ __device__ __forceinline__ void small_chunk_dots(const char* xl, const uint4 (&w
 
 __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
-    const float* __restrict__ e_bias, int n, int H, int E, int epw, int topk, int norm_topk,
-    float routed_scale, float* __restrict__ logits, float* __restrict__ xsum,
-    int* __restrict__ ids, float* __restrict__ w, DispOut d, int do_disp, int slices,
-    uint32_t* __restrict__ cs) {
+    const float* __restrict__ e_bias, int n, int H, int E, int epw, float* __restrict__ logits,
+    float* __restrict__ xsum, int slices, uint32_t* __restrict__ cs) {
     extern __shared__ __align__(16) char small_lds[];
-    __shared__ int last;
     const int nchunks = H / kRouterKC;
     const int tid = threadIdx.x;
     const int eb = blockIdx.x, tg = blockIdx.y;
@@ -847,31 +837,27 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
             st_dev(reinterpret_cast<float*>(cs) + (size_t)n * E + o, sc);
         }
     }
-    // This workgroup's logits are complete in memory; take the group ticket.
-    drain_vm();
-    __syncthreads();
-    if (tid == 0) {
-        last = ticket_dev(&g_small_tick[tg]) == gridDim.x - 1;
-        if (last) reset_dev(&g_small_tick[tg]);
-    }
-    __syncthreads();
-    if (!last) return;
+}
+
+// The selection and, for a small batch, the dispatch after router_small_kernel:
+// wave w of workgroup b selects tokens 8 b + w, 8 b + w + 8 * gridDim.x, ...
+// from the order codes and scores; with do_disp the grid is one workgroup,
+// which then runs the whole dispatch on the ids its waves stored.
+__global__ __launch_bounds__(kSmallThreads) void router_finish_kernel(
+    const float* __restrict__ logits, const float* __restrict__ e_bias, int n, int E, int topk,
+    int norm_topk, float routed_scale, int* __restrict__ ids, float* __restrict__ w,
+    const uint32_t* __restrict__ cs, DispOut d, int do_disp) {
+    __shared__ int lds[dispatch_lds_ints<kSmallThreads>()];
     __shared__ uint32_t tscratch[kSmallThreads / 64][kTopkScratch];
-    for (int t = tid >> 6; t < nt; t += kSmallThreads / 64)
-        topk_wave<true>(logits + (size_t)(t0 + t) * E, e_bias, E, topk, norm_topk, routed_scale,
-                        ids + (size_t)(t0 + t) * topk, w + (size_t)(t0 + t) * topk,
-                        tscratch[tid >> 6], cs + (size_t)(t0 + t) * E,
-                        reinterpret_cast<const float*>(cs) + (size_t)n * E + (size_t)(t0 + t) * E);
-    if (do_disp <= 0) return;
+    const int wave = threadIdx.x >> 6;
+    for (int t = blockIdx.x * (kSmallThreads / 64) + wave; t < n; t += gridDim.x * (kSmallThreads / 64))
+        topk_wave<true>(logits + (size_t)t * E, e_bias, E, topk, norm_topk, routed_scale,
+                        ids + (size_t)t * topk, w + (size_t)t * topk, tscratch[wave],
+                        cs + (size_t)t * E, reinterpret_cast<const float*>(cs) + (size_t)n * E + (size_t)t * E);
+    if (!do_disp) return;
     drain_vm();
     __syncthreads();
-    if (tid == 0) {
-        last = ticket_dev(&g_small_tick[kSmallMaxTG]) == gridDim.y - 1;
-        if (last) reset_dev(&g_small_tick[kSmallMaxTG]);
-    }
-    __syncthreads();
-    if (!last) return;
-    dispatch_block<kSmallThreads, true>(ids, n, topk, E, d, reinterpret_cast<int*>(small_lds));
+    dispatch_block<kSmallThreads, true>(ids, n, topk, E, d, lds);
 }
 
 size_t router_select_scratch_bytes(int n, int H, int E) {
@@ -910,11 +896,7 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         while (slices < kRouterTG && 2 * slices * epw * nchunks <= kSmallThreads) slices *= 2;
         const bool dd = disp && E <= kDispMaxE;
         dim3 grid((unsigned)((E + epw - 1) / epw), (unsigned)((n + kRouterTG - 1) / kRouterTG));
-        // mode: 0 logits and top-k, 1 logits, top-k and dispatch.
-        const int mode = dd ? 1 : 0;
-        // The dispatch reuses the staging area.
-        size_t lds = (size_t)small_x_bytes(nchunks) + (size_t)epw * nchunks * kRouterTG * 4;
-        if (lds < (size_t)dispatch_lds_ints<kSmallThreads>() * 4) lds = dispatch_lds_ints<kSmallThreads>() * 4;
+        const size_t lds = (size_t)small_x_bytes(nchunks) + (size_t)epw * nchunks * kRouterTG * 4;
         static bool attr_set = false;
         if (!attr_set) {
             if (hipFuncSetAttribute(reinterpret_cast<const void*>(&router_small_kernel),
@@ -925,10 +907,18 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
             attr_set = true;
         }
         hipLaunchKernelGGL(router_small_kernel, grid, dim3(kSmallThreads), lds, s, x, wr, e_bias, n,
-                           H, E, epw, topk, norm_topk, routed_scale, logits, xsum, ids, w,
-                           dd ? *disp : DispOut{}, mode, slices, reinterpret_cast<uint32_t*>(scratch));
+                           H, E, epw, logits, xsum, slices, reinterpret_cast<uint32_t*>(scratch));
         if (hipGetLastError() != hipSuccess) return -4;
-        if (dispatched) *dispatched = mode == 1;
+        // Selection: one workgroup (and then the dispatch too) up to
+        // kFinishDispMax tokens, else one wave per token.
+        const bool one = n <= kFinishDispMax;
+        const unsigned fg = one ? 1u : (unsigned)((n + kSmallThreads / 64 - 1) / (kSmallThreads / 64));
+        hipLaunchKernelGGL(router_finish_kernel, dim3(fg), dim3(kSmallThreads), 0, s, logits, e_bias,
+                           n, E, topk, norm_topk, routed_scale, ids, w,
+                           reinterpret_cast<const uint32_t*>(scratch), dd && one ? *disp : DispOut{},
+                           dd && one ? 1 : 0);
+        if (hipGetLastError() != hipSuccess) return -4;
+        if (dispatched) *dispatched = dd && one;
         return 0;
     }
     if (n >= kTiledMinTokens && H % kMfmaK == 0 && H % kRouterKC == 0 && nchunks <= 64 &&

@@ -118,6 +118,7 @@ struct ExpArgs {
     const float* gsum;       // group sums of src rows: xsum [n, H/128] or hsum [R, I/128]
     const int4* tiles; const int* ntiles; const int* rows_tok;
     uint16_t* h; float* hsum; float* dpart;
+    unsigned int* tick; float* tpart; int tcap;   // tail split state (gate/up stream kernel)
     int H, I, E;
 };
 
@@ -518,23 +519,24 @@ constexpr int kSTabInts = 24;
 // that holds an item's last part (by ticket) adds the stored t_b in batch
 // order and finishes the item. Whole or split, an item's arithmetic is the
 // same, so results do not depend on how a batch's work was spread.
-constexpr int kMaxTail = 256;          // split items per launch
-constexpr int kMaxTailParts = 1024;    // their parts
-static __device__ unsigned int g_tail_tick[kMaxTail];
-static __device__ float g_tail_part[kMaxTailParts * 8 * 512];   // [part][value][thread] t_b
+// The tickets (kTailTicks, zero at launch: the dispatch clears them) and the
+// stored t_b ([part][value][thread], 16 KiB per part, room for a.tcap parts)
+// are in the caller's workspace; a split needs rem <= kTailTicks items and
+// rem * BPI <= a.tcap parts.
+constexpr int kTailPartBytes = 8 * 512 * 4;
 
 struct SSched {
     int R, rem, split, nunits;
 };
 
-__device__ __forceinline__ SSched s_sched(int total, int nwg, int base, int BPI) {
+__device__ __forceinline__ SSched s_sched(int total, int nwg, int base, int BPI, int tcap) {
     SSched sc;
     sc.R = total / nwg;
     sc.rem = total - sc.R * nwg;
     const int parts = sc.rem * BPI;
     // With no full round (a handful of items) the split's ticket and
     // finishing cost more than the shorter round saves.
-    sc.split = BPI > 1 && sc.R > 0 && sc.rem > 0 && sc.rem <= kMaxTail && parts <= kMaxTailParts &&
+    sc.split = BPI > 1 && sc.R > 0 && sc.rem > 0 && sc.rem <= kTailTicks && parts <= tcap &&
                (parts + nwg - 1) / nwg < BPI;
     if (sc.split)
         sc.nunits = sc.R + (base < parts ? (parts - base + nwg - 1) / nwg : 0);
@@ -788,7 +790,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
     const int total = *a.ntiles * ngrp;
     const int nwg = (int)gridDim.x;
     const int base = (int)blockIdx.x;
-    const SSched sch = s_sched(total, nwg, base, GU ? BPI : 1);
+    const SSched sch = s_sched(total, nwg, base, GU ? BPI : 1, a.tcap);
     const int nitems = sch.nunits;
     int* table = reinterpret_cast<int*>(lds + LY::kTab);
     char* junk = lds + LY::kJunk;
@@ -929,7 +931,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
                     // A part: store t_b; the item is finished after the ticket.
                     // [value][thread]: each store instruction covers 256
                     // contiguous bytes (whole lines).
-                    float* dst = g_tail_part + (size_t)(ctail * BPI + ckb) * 4096 + threadIdx.x;
+                    float* dst = a.tpart + (size_t)(ctail * BPI + ckb) * 4096 + threadIdx.x;
 #pragma unroll
                     for (int m = 0; m < NMAT; ++m)
 #pragma unroll
@@ -957,8 +959,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
         for (int u = sch.split ? sch.R : nitems; u < nitems; ++u) {
             const int4 un = s_unit(sch, base, nwg, BPI, u);
             if (threadIdx.x == 0) {
-                const bool last = ticket_dev(&g_tail_tick[un.w]) == (unsigned)(BPI - 1);
-                if (last) reset_dev(&g_tail_tick[un.w]);
+                const bool last = ticket_dev(&a.tick[un.w]) == (unsigned)(BPI - 1);
                 *flag = last ? 1 : 0;
             }
             __syncthreads();
@@ -967,7 +968,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
             if (!last) continue;
             f32x4 T[NMAT];
             for (int b = 0; b < BPI; ++b) {
-                const float* src = g_tail_part + (size_t)(un.w * BPI + b) * 4096 + threadIdx.x;
+                const float* src = a.tpart + (size_t)(un.w * BPI + b) * 4096 + threadIdx.x;
 #pragma unroll
                 for (int m = 0; m < NMAT; ++m) {
                     const f32x4 t{ld_dev(src + (m * 4) * 512), ld_dev(src + (m * 4 + 1) * 512),
@@ -1074,8 +1075,11 @@ static int launch_expert(const ExpArgs& a, long max_work, hipStream_t s) {
 
 int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
                    const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
-                   float* hsum, int H, int I, int E, hipStream_t s) {
+                   float* hsum, unsigned int* tick, float* tpart, size_t tpart_bytes, int H, int I,
+                   int E, hipStream_t s) {
     ExpArgs a{};
+    a.tick = tick; a.tpart = tpart;
+    a.tcap = tick && tpart ? (int)(tpart_bytes / kTailPartBytes) : 0;
     a.wq[0] = reinterpret_cast<const uint4*>(P.gate_q); a.ws[0] = P.gate_s;
     a.wq[1] = reinterpret_cast<const uint4*>(P.up_q); a.ws[1] = P.up_s;
     a.swq[0] = reinterpret_cast<const uint4*>(P.sh_gate_q); a.sws[0] = P.sh_gate_s;

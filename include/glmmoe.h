@@ -139,6 +139,7 @@ typedef struct glmmoe_layer_ws {
     float* hsum;          /* [R, I/128] group sums of h (large-group path) */
     float* dpart;         /* [R, H] per-row expert outputs (unweighted): fp32 below 1024 grouped
                              rows (n*topk + n), bf16 (first half of the region) from there */
+    unsigned int* sync;   /* [256] expert-kernel tickets (cleared by each call's dispatch) */
     size_t bytes;         /* total workspace bytes */
 } glmmoe_layer_ws;
 
