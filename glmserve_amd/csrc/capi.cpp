@@ -66,6 +66,16 @@ int* dispatch_scratch(float* rpart, const Layer* L, int n) {
     return reinterpret_cast<int*>(rpart);
 }
 
+// Bytes of the dpart region: the per-row expert outputs, and before them (it
+// is free while the gate/up kernel runs) the partials of the gate/up stream
+// kernel's split items: up to kTailTicks items of H / 2048 parts of 16 KiB.
+size_t dpart_bytes(const glmmoe_w4a16_layer* L, int n) {
+    const size_t R = (size_t)n * L->topk + (has_shared(L) ? (size_t)n : 0);
+    const size_t rows = R * L->hidden * 4;
+    const size_t tail = (size_t)kTailTicks * (L->hidden / 2048) * 16384;
+    return rows > tail ? rows : tail;
+}
+
 // Carves the workspace; with base == nullptr only computes the size.
 size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v) {
     const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
@@ -92,7 +102,7 @@ size_t carve(const glmmoe_w4a16_layer* L, int n, char* base, glmmoe_layer_ws* v)
     w.ntiles = reinterpret_cast<int*>(take(16));
     w.h = reinterpret_cast<uint16_t*>(take(R * I * 2));
     w.hsum = reinterpret_cast<float*>(take(R * (I / 128) * 4));
-    w.dpart = reinterpret_cast<float*>(take(R * H * 4));
+    w.dpart = reinterpret_cast<float*>(take(dpart_bytes(L, n)));
     w.sync = reinterpret_cast<unsigned int*>(take(kTailTicks * 4));
     w.bytes = off;
     if (v) *v = w;
@@ -161,13 +171,6 @@ inline void end_call(hipStream_t s) {
     if (!g_prof.on || g_prof.calls >= GLMMOE_PROF_MAX_CALLS) return;
     mark(GLMMOE_N_STAGES, s);
     ++g_prof.calls;
-}
-
-// Bytes of the dpart region: free while the gate/up kernel runs, which keeps
-// the partials of its split items there.
-size_t dpart_bytes(const glmmoe_w4a16_layer* L, int n) {
-    const size_t R = (size_t)n * L->topk + (has_shared(L) ? (size_t)n : 0);
-    return R * L->hidden * 4;
 }
 
 // Dispatch onward, given ids/weights/xsum in the workspace view.

@@ -306,7 +306,7 @@ __device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
                                           int norm_topk, float routed_scale,
                                           int* __restrict__ ids_out, float* __restrict__ w_out,
                                           uint32_t* scratch, const uint32_t* pcode,
-                                          const float* pscore) {
+                                          const float* pscore, int* ids_copy = nullptr) {
     const int lane = threadIdx.x & 63;
     float score[NJ];
     uint32_t ch[NJ];   // order codes, 0 = no candidate
@@ -349,12 +349,14 @@ __device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
     // 2. k rounds, as cuda/moe_router.cu:48-53 does them: the largest lane
     //    head over the wave (a max over each 16-lane row with DPP row
     //    rotations, then the 4 row maxima); the owner lane drops its head.
-    float wsel[8];
-    int idsel[8];
+    //    Lane k keeps round k's pick. (A rolled loop: these kernels run
+    //    once per call, where fetching unrolled code costs more than the
+    //    loop.)
+    float wsel = 0.0f;
+    int idsel = 0;
     float wsum = 0.0f;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        if (k >= topk) break;
+#pragma unroll 1
+    for (int k = 0; k < topk; ++k) {
         uint32_t h = ch[0], l = kl[0];
         kmax_dpp<0x121>(h, l);
         kmax_dpp<0x122>(h, l);
@@ -379,26 +381,23 @@ __device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
             ch[NJ - 1] = 0u;
             kl[NJ - 1] = 0u;
         }
-        idsel[k] = e;
-        wsel[k] = sw;
+        idsel = lane == k ? e : idsel;
+        wsel = lane == k ? sw : wsel;
         wsum = wsum + sw;
     }
     // 3. Weights in selection order, normalized by their sum in that order.
     (void)scratch;
-#pragma unroll
-    for (int k = 0; k < 8; ++k) {
-        if (k >= topk) break;
-        if (lane == k) {
-            float v = wsel[k];
-            if (norm_topk && wsum > 0.0f) v = v / wsum;
-            if (COH) {
-                st_dev(ids_out + k, idsel[k]);
-                st_dev(w_out + k, v * routed_scale);
-            } else {
-                ids_out[k] = idsel[k];
-                w_out[k] = v * routed_scale;
-            }
+    if (lane < topk) {
+        float v = wsel;
+        if (norm_topk && wsum > 0.0f) v = v / wsum;
+        if (COH) {
+            st_dev(ids_out + lane, idsel);
+            st_dev(w_out + lane, v * routed_scale);
+        } else {
+            ids_out[lane] = idsel;
+            w_out[lane] = v * routed_scale;
         }
+        if (ids_copy) ids_copy[lane] = idsel;
     }
 }
 
@@ -686,7 +685,7 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
 // ---------------------------------------------------------------------------
 constexpr int kSmallThreads = 512;
 constexpr int kSmallMaxChunks = 64;
-constexpr int kFinishDispMax = 64;   // tokens up to which one workgroup selects and dispatches
+constexpr int kFinishDispMax = 8;   // tokens up to which one workgroup selects and dispatches
 // Staged activation bytes: 8 tokens x nchunks rows of 256 B, whole 1 KiB DMAs.
 __host__ __device__ constexpr int small_x_bytes(int nchunks) {
     return (kRouterTG * nchunks * 256 + 1023) / 1024 * 1024;
@@ -843,21 +842,24 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
 // wave w of workgroup b selects tokens 8 b + w, 8 b + w + 8 * gridDim.x, ...
 // from the order codes and scores; with do_disp the grid is one workgroup,
 // which then runs the whole dispatch on the ids its waves stored.
+template <int NJ>
 __global__ __launch_bounds__(kSmallThreads) void router_finish_kernel(
     const float* __restrict__ logits, const float* __restrict__ e_bias, int n, int E, int topk,
     int norm_topk, float routed_scale, int* __restrict__ ids, float* __restrict__ w,
     const uint32_t* __restrict__ cs, DispOut d, int do_disp) {
     __shared__ int lds[dispatch_lds_ints<kSmallThreads>()];
     __shared__ uint32_t tscratch[kSmallThreads / 64][kTopkScratch];
+    __shared__ int sids[kFinishDispMax * 8];   // the dispatch's copy of the ids
     const int wave = threadIdx.x >> 6;
     for (int t = blockIdx.x * (kSmallThreads / 64) + wave; t < n; t += gridDim.x * (kSmallThreads / 64))
-        topk_wave<true>(logits + (size_t)t * E, e_bias, E, topk, norm_topk, routed_scale,
-                        ids + (size_t)t * topk, w + (size_t)t * topk, tscratch[wave],
-                        cs + (size_t)t * E, reinterpret_cast<const float*>(cs) + (size_t)n * E + (size_t)t * E);
+        topk_wave_nj<false, NJ>(logits + (size_t)t * E, e_bias, E, topk, norm_topk, routed_scale,
+                                ids + (size_t)t * topk, w + (size_t)t * topk, tscratch[wave],
+                                cs + (size_t)t * E,
+                                reinterpret_cast<const float*>(cs) + (size_t)n * E + (size_t)t * E,
+                                do_disp ? sids + t * topk : nullptr);
     if (!do_disp) return;
-    drain_vm();
     __syncthreads();
-    dispatch_block<kSmallThreads, true>(ids, n, topk, E, d, lds);
+    dispatch_block<kSmallThreads>(sids, n, topk, E, d, lds);
 }
 
 size_t router_select_scratch_bytes(int n, int H, int E) {
@@ -913,10 +915,11 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         // kFinishDispMax tokens, else one wave per token.
         const bool one = n <= kFinishDispMax;
         const unsigned fg = one ? 1u : (unsigned)((n + kSmallThreads / 64 - 1) / (kSmallThreads / 64));
-        hipLaunchKernelGGL(router_finish_kernel, dim3(fg), dim3(kSmallThreads), 0, s, logits, e_bias,
-                           n, E, topk, norm_topk, routed_scale, ids, w,
-                           reinterpret_cast<const uint32_t*>(scratch), dd && one ? *disp : DispOut{},
-                           dd && one ? 1 : 0);
+        auto fin = E <= 64 ? router_finish_kernel<1> : E <= 128 ? router_finish_kernel<2>
+                                     : E <= 256 ? router_finish_kernel<4> : router_finish_kernel<8>;
+        hipLaunchKernelGGL(fin, dim3(fg), dim3(kSmallThreads), 0, s, logits, e_bias, n, E, topk,
+                           norm_topk, routed_scale, ids, w, reinterpret_cast<const uint32_t*>(scratch),
+                           dd && one ? *disp : DispOut{}, dd && one ? 1 : 0);
         if (hipGetLastError() != hipSuccess) return -4;
         if (dispatched) *dispatched = dd && one;
         return 0;

@@ -138,7 +138,9 @@ typedef struct glmmoe_layer_ws {
     uint16_t* h;          /* [R, I] bf16 SiLU(gate) * up */
     float* hsum;          /* [R, I/128] group sums of h (large-group path) */
     float* dpart;         /* [R, H] per-row expert outputs (unweighted): fp32 below 1024 grouped
-                             rows (n*topk + n), bf16 (first half of the region) from there */
+                             rows (n*topk + n), bf16 (first half of the region) from there;
+                             at least 256 * (H / 2048) * 16 KiB: before the down projection
+                             it holds the gate/up kernel's split-item partials */
     unsigned int* sync;   /* [256] expert-kernel tickets (cleared by each call's dispatch) */
     size_t bytes;         /* total workspace bytes */
 } glmmoe_layer_ws;
