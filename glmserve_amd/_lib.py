@@ -23,6 +23,8 @@ SIGNATURES = {
     "glmmoe_layer_workspace_bytes": (_sz, [_vp, _i]),
     "glmmoe_layer_workspace_view": (_i, [_vp, _i, _vp, _vp]),
     "glmmoe_moe_layer_w4a16": (_i, [_vp, _vp, _i, _vp, _vp, _sz, _vp]),
+    "glmmoe_noalloc_scratch_bytes": (_sz, []),
+    "glmmoe_moe_layer_w4a16_noalloc": (_i, [_vp, _vp, _i, _vp, _vp]),
     "glmmoe_moe_route_w4a16": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _sz, _vp]),
     "glmmoe_expert_ffn_w4a16": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "glmmoe_fp8_packed_bytes": (_sz, [_i, _i]),

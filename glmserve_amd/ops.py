@@ -165,6 +165,14 @@ class _MoELayer:
 class W4A16MoELayer(_MoELayer):
     """W4A16 experts: (packed_q, packed bf16 scales) from pack_w4a16."""
 
+    def forward_noalloc(self, x, out, stream=None):
+        """forward on the library's per-GPU scratch (glmmoe_moe_layer_w4a16_noalloc)."""
+        n = x.shape[0]
+        _need(x, torch.bfloat16, n * self.hidden, "x")
+        _need(out, torch.float32, n * self.hidden, "out")
+        check(lib().glmmoe_moe_layer_w4a16_noalloc(self._ref(), _p(x), n, _p(out), _s(stream)),
+              "glmmoe_moe_layer_w4a16_noalloc")
+
 
 class FP8MoELayer(_MoELayer):
     """FP8 experts: (packed e4m3 from pack_fp8, fp32 [.., rows/128, K/128] block scales)."""

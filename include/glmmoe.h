@@ -154,6 +154,19 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
                            float* out, void* workspace, size_t workspace_bytes,
                            void* stream);
 
+/* glmmoe_moe_layer_w4a16 with no workspace argument and no device allocation.
+ * No counterpart in the reference: for callers that cannot allocate (code
+ * under HIP graph capture, serving loops that forbid hipMalloc). The
+ * workspace is a device array of glmmoe_noalloc_scratch_bytes() (32 MiB) in
+ * the library, one per GPU, kept until the process ends; a batch whose
+ * glmmoe_layer_workspace_bytes exceeds it returns GLMMOE_ERR_WORKSPACE
+ * (decode batches fit: 19 MiB at n = 64 on the GLM-5 layer). Every call on a
+ * GPU uses that GPU's array: calls that overlap in time on one GPU (other
+ * streams, other threads) race and must not be made. */
+size_t glmmoe_noalloc_scratch_bytes(void);
+int glmmoe_moe_layer_w4a16_noalloc(const glmmoe_w4a16_layer* L, const uint16_t* x, int n,
+                                   float* out, void* stream);
+
 /* The layer's routing alone: router logits and sigmoid top-k, as the layer
  * runs them (replaces gemm_linear on the router and moe_router,
  * src/model_gpu.cpp:1448-1450). topk_ids/topk_w: [n, topk], bit-identical to

@@ -152,6 +152,22 @@ def test_workspace_sizing_and_view():
                                     C.c_void_p(16), 16, None) == -3
 
 
+def test_noalloc_entry_host_checks():
+    # The no-allocation entry sizes the batch before any device call: a batch
+    # whose workspace exceeds the library's scratch, or a bad layer, is
+    # refused here (no GPU needed).
+    L = _lib.lib()
+    cap = L.glmmoe_noalloc_scratch_bytes()
+    assert cap == 32 << 20
+    assert L.glmmoe_layer_workspace_bytes(C.byref(_layer()), 64) <= cap   # decode fits
+    big = 256
+    assert L.glmmoe_layer_workspace_bytes(C.byref(_layer()), big) > cap
+    assert L.glmmoe_moe_layer_w4a16_noalloc(C.byref(_layer()), C.c_void_p(16), big, C.c_void_p(16),
+                                            None) == -3
+    assert L.glmmoe_moe_layer_w4a16_noalloc(C.byref(_layer(k=9)), C.c_void_p(16), 4, C.c_void_p(16),
+                                            None) == -1
+
+
 def test_cpp_header_compiles_against_the_library(tmp_path):
     src = tmp_path / "use.cpp"
     src.write_text(
