@@ -15,6 +15,7 @@ SIGNATURES = {
     "glmmoe_version": (C.c_char_p, []),
     "glmmoe_router_logits_workspace_bytes": (_sz, [_i, _i, _i]),
     "glmmoe_router_logits": (_i, [_vp, _vp, _i, _i, _i, _vp, _vp, _vp, _sz, _vp]),
+    "glmmoe_router_logits_f32": (_i, [_vp, _vp, _vp, _vp, _i64, _i64, _i64, _vp]),
     "glmmoe_moe_router": (_i, [_vp, _vp, _i, _i, _i, _i, _f, _vp, _vp, _vp]),
     "glmmoe_moe_dispatch": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp]),
     "glmmoe_w4_packed_bytes": (_sz, [_i, _i]),

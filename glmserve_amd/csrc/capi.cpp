@@ -261,6 +261,14 @@ int glmmoe_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, in
                                 S(stream));
 }
 
+int glmmoe_router_logits_f32(const float* x, const float* W, const float* bias, float* y,
+                             int64_t n, int64_t in, int64_t out, void* stream) {
+    if (!x || !W || !y || n <= 0 || in <= 0 || out <= 0) return GLMMOE_ERR_ARG;
+    if (in % 128 || in > 8192 || n > (1 << 30) || out > (1 << 20)) return GLMMOE_ERR_SHAPE;
+    return launch_router_logits_f32(x, W, bias, y, (int)n, (int)in, (int)out, S(stream)) ? GLMMOE_ERR_LAUNCH
+                                                                                         : GLMMOE_OK;
+}
+
 int glmmoe_moe_router(const float* logits, const float* e_bias, int n, int E, int topk,
                       int norm_topk, float routed_scale, int* topk_ids, float* topk_weights,
                       void* stream) {

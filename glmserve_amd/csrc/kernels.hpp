@@ -53,6 +53,10 @@ struct DispOut {
 size_t router_logits_scratch_bytes(int n, int H, int E);
 int launch_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
                          float* logits, float* xsum, float* scratch, hipStream_t s);
+// fp32 x [n, H] and W [E, H] rounded to bf16 on load, the bf16 path's fixed
+// order, + bias (nullable). H % 128 == 0, H <= 8192; no workspace.
+int launch_router_logits_f32(const float* x, const float* W, const float* bias, float* y, int n,
+                             int H, int E, hipStream_t s);
 int launch_xsum(const uint16_t* x, int n, int H, float* xsum, hipStream_t s);
 // Router logits + top-k for the layer (logits hold only what the selection
 // reads; ids and weights are those of the fixed-order logits). Scratch of

@@ -942,6 +942,115 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
     return launch_router_topk(logits, e_bias, n, E, topk, norm_topk, routed_scale, ids, w, s);
 }
 
+// ---------------------------------------------------------------------------
+// fp32 activations and router weights (gemm_fp32's arguments, the
+// reference's router call gemm_linear(s.normed, d.router, ...),
+// src/model_gpu.cpp:1448, cuda/kernels.cuh:37-38): both are rounded to bf16
+// (round-to-nearest-even, as the bf16 entry's callers round them) on load,
+// then the same fixed order as the bf16 path: per 128-K chunk an ascending-K
+// fma chain from zero, chunk partials added in chunk order; then + bias[e]
+// (nullable). No workspace: grid (ceil(E / epw), ceil(n / 8)) of 512
+// threads, thread (expert el, chunk c) for every token of its group of 8.
+// LDS: the group's activations as bf16 rows R = t * nchunks + c of 256 B,
+// 16-B piece o at slot o ^ (R & 15) (threads of consecutive chunks reading
+// the same piece hit distinct banks), then the partials [pair][token].
+constexpr int kF32Threads = 512;
+
+__host__ __device__ constexpr size_t f32_router_lds(int H, int epw) {
+    return (size_t)kRouterTG * H * 2 + (size_t)epw * (H / kRouterKC) * kRouterTG * 4;
+}
+
+__global__ __launch_bounds__(kF32Threads) void router_logits_f32_kernel(
+    const float* __restrict__ x, const float* __restrict__ W, const float* __restrict__ bias,
+    float* __restrict__ y, int n, int H, int E, int epw) {
+    extern __shared__ __align__(16) char f32_lds[];
+    const int nchunks = H / kRouterKC;
+    const int tid = threadIdx.x;
+    const int t0 = blockIdx.y * kRouterTG, nt = min(kRouterTG, n - t0);
+    char* xl = f32_lds;
+    float* part = reinterpret_cast<float*>(f32_lds + (size_t)kRouterTG * H * 2);
+    // Stage: 8 consecutive K of one row per thread step (one 16-B piece).
+    const int pieces = nt * (H / 8);
+    for (int i = tid; i < pieces; i += kF32Threads) {
+        const int t = i / (H / 8), kp = i - t * (H / 8);
+        const int c = kp / (kRouterKC / 8), o = kp % (kRouterKC / 8);
+        const float4* src = reinterpret_cast<const float4*>(x + (size_t)(t0 + t) * H + kp * 8);
+        const float4 a = src[0], b = src[1];
+        uint4 v;
+        v.x = f32_to_bf16(a.x) | (f32_to_bf16(a.y) << 16);
+        v.y = f32_to_bf16(a.z) | (f32_to_bf16(a.w) << 16);
+        v.z = f32_to_bf16(b.x) | (f32_to_bf16(b.y) << 16);
+        v.w = f32_to_bf16(b.z) | (f32_to_bf16(b.w) << 16);
+        const int R = t * nchunks + c;
+        *reinterpret_cast<uint4*>(xl + R * 256 + ((o ^ (R & 15)) << 4)) = v;
+    }
+    const int pair = tid, el = pair / nchunks, c = pair - el * nchunks;
+    const int e = blockIdx.x * epw + el;
+    const bool active = pair < epw * nchunks && e < E;
+    uint4 wv[kRouterKC / 8];
+    if (active) {
+        const float4* wp = reinterpret_cast<const float4*>(W + (size_t)e * H + c * kRouterKC);
+#pragma unroll
+        for (int j = 0; j < kRouterKC / 8; ++j) {
+            const float4 a = wp[2 * j], b = wp[2 * j + 1];
+            wv[j].x = f32_to_bf16(a.x) | (f32_to_bf16(a.y) << 16);
+            wv[j].y = f32_to_bf16(a.z) | (f32_to_bf16(a.w) << 16);
+            wv[j].z = f32_to_bf16(b.x) | (f32_to_bf16(b.y) << 16);
+            wv[j].w = f32_to_bf16(b.z) | (f32_to_bf16(b.w) << 16);
+        }
+    }
+    __syncthreads();
+    if (active) {
+        for (int t = 0; t < nt; ++t) {
+            const int R = t * nchunks + c;
+            const char* row = xl + R * 256;
+            float acc = 0.0f;
+#pragma unroll
+            for (int j = 0; j < kRouterKC / 8; ++j) {
+                const uint4 xv = *reinterpret_cast<const uint4*>(row + ((j ^ (R & 15)) << 4));
+                const uint32_t xd[4] = {xv.x, xv.y, xv.z, xv.w};
+                const uint32_t wd[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    acc = __builtin_fmaf(bf16_to_f32(xd[q] & 0xffffu), bf16_to_f32(wd[q] & 0xffffu), acc);
+                    acc = __builtin_fmaf(__uint_as_float(xd[q] & 0xffff0000u),
+                                         __uint_as_float(wd[q] & 0xffff0000u), acc);
+                }
+            }
+            part[pair * kRouterTG + t] = acc;
+        }
+    }
+    __syncthreads();
+    if (tid < epw * kRouterTG) {
+        const int el2 = tid / kRouterTG, t = tid % kRouterTG;
+        const int e2 = blockIdx.x * epw + el2;
+        if (e2 < E && t < nt) {
+            float total = 0.0f;
+            for (int cc = 0; cc < nchunks; ++cc) total = total + part[(el2 * nchunks + cc) * kRouterTG + t];
+            y[(size_t)(t0 + t) * E + e2] = bias ? total + bias[e2] : total;
+        }
+    }
+}
+
+int launch_router_logits_f32(const float* x, const float* W, const float* bias, float* y, int n,
+                             int H, int E, hipStream_t s) {
+    if (H % kRouterKC || H / kRouterKC > kF32Threads || H > 8192) return -2;
+    const int nchunks = H / kRouterKC;
+    const int epw = kF32Threads / nchunks;
+    static bool attr_set = false;
+    if (!attr_set) {
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&router_logits_f32_kernel),
+                                hipFuncAttributeMaxDynamicSharedMemorySize,
+                                (int)f32_router_lds(8192, kF32Threads / (8192 / kRouterKC))) != hipSuccess)
+            return -4;
+        attr_set = true;
+    }
+    dim3 grid((unsigned)((E + epw - 1) / epw), (unsigned)((n + kRouterTG - 1) / kRouterTG));
+    hipLaunchKernelGGL(router_logits_f32_kernel, grid, dim3(kF32Threads), f32_router_lds(H, epw), s, x, W,
+                       bias, y, n, H, E, epw);
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 size_t router_logits_scratch_bytes(int n, int H, int E) {
     if (n >= kTiledMinTokens && H % kRouterKC == 0) return 0;
     return (size_t)n * ((H + kRouterKC - 1) / kRouterKC) * E * 4;

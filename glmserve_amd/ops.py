@@ -41,6 +41,20 @@ def router_logits(x, wr, logits, xsum=None, stream=None):
                                      _s(stream)), "router_logits")
 
 
+def router_logits_f32(x, W, bias, y, stream=None):
+    """y[n,E] = bf16(x)[n,H] . bf16(W)[E,H]^T (+ bias): gemm_fp32's arguments
+    (cuda/kernels.cuh:37-38) for the router call of src/model_gpu.cpp:1448."""
+    n, H = x.shape
+    E = W.shape[0]
+    _need(x, torch.float32, n * H, "x")
+    _need(W, torch.float32, E * H, "W")
+    _need(y, torch.float32, n * E, "y")
+    if bias is not None:
+        _need(bias, torch.float32, E, "bias")
+    check(lib().glmmoe_router_logits_f32(_p(x), _p(W), _p(bias), _p(y), n, H, E, _s(stream)),
+          "router_logits_f32")
+
+
 def moe_router(logits, e_bias, n, E, topk, norm_topk, routed_scale, topk_ids, topk_weights,
                stream=None):
     """cuda/kernels.cuh:243-245."""

@@ -50,6 +50,17 @@ int glmmoe_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, in
                          float* logits, float* xsum, void* workspace, size_t workspace_bytes,
                          void* stream);
 
+/* Router logits from fp32 activations and fp32 router weights, with
+ * gemm_fp32's argument list (cuda/kernels.cuh:37-38; the router call
+ * gemm_linear(s.normed, d.router, nullptr, s.rlogits, n) of
+ * src/model_gpu.cpp:1448): y[n, out] = bf16(x)[n, in] . bf16(W)[out, in]^T
+ * (+ bias[out], nullable). x and W are rounded to bf16 (nearest-even) inside
+ * the kernel; the sum is glmmoe_router_logits' fixed order, so y is
+ * bit-identical to glmmoe_router_logits on the rounded inputs. No workspace.
+ * Limits: in % 128 == 0, in <= 8192. */
+int glmmoe_router_logits_f32(const float* x, const float* W, const float* bias, float* y,
+                             int64_t n, int64_t in, int64_t out, void* stream);
+
 /* Sigmoid top-k routing with score-correction bias.
  * Replaces moe_router (cuda/kernels.cuh:243-245, cuda/moe_router.cu:17-79):
  * same arguments and meaning. e_bias is nullable. Ties choose the lower

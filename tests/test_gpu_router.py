@@ -116,6 +116,29 @@ def test_router_logits_bit_exact(oracle):
             assert np.array_equal(xs.cpu().numpy().view(np.uint32), rx.view(np.uint32)), (n, H)
 
 
+def test_router_logits_f32_bit_exact(oracle):
+    # gemm_fp32-shaped entry: fp32 x and W rounded to bf16 in the kernel, then
+    # the fixed order; bit-exact vs the oracle's bf16 logits of the rounded
+    # inputs, and + bias exactly as one fp32 add.
+    rng = np.random.default_rng(11)
+    for n, H, E in [(1, 6144, 256), (8, 6144, 256), (64, 6144, 256), (300, 6144, 256),
+                    (5, 256, 16), (17, 8192, 300), (3, 128, 1)]:
+        x = rng.standard_normal((n, H)).astype(np.float32)
+        w = (0.02 * rng.standard_normal((E, H))).astype(np.float32)
+        x[0, :3] = [1.0 + 2.0 ** -8, -(1.0 + 3 * 2.0 ** -9), 3.4e38]   # ties to even; rounds up to inf
+        bias = rng.uniform(-0.1, 0.1, E).astype(np.float32)
+        dx, dw = torch.from_numpy(x).cuda(), torch.from_numpy(w).cuda()
+        y = torch.full((n, E), float("nan"), dtype=torch.float32, device="cuda")
+        yb = torch.full((n, E), float("nan"), dtype=torch.float32, device="cuda")
+        G.router_logits_f32(dx, dw, None, y)
+        G.router_logits_f32(dx, dw, torch.from_numpy(bias).cuda(), yb)
+        torch.cuda.synchronize()
+        ref = oracle.router_logits_bf16(oracle.f32_to_bf16(x), oracle.f32_to_bf16(w))
+        got = y.cpu().numpy()
+        assert np.array_equal(got.view(np.uint32), ref.view(np.uint32)), (n, H, E)
+        assert np.array_equal(yb.cpu().numpy().view(np.uint32), (ref + bias[None, :]).view(np.uint32)), (n, H, E)
+
+
 @pytest.mark.parametrize("n", [256, 1000, 4096])
 def test_layer_routing_bit_exact_large_batches(oracle, n):
     """From 256 tokens the layer routes with MFMA logits plus an exact
