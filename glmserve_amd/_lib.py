@@ -37,8 +37,8 @@ SIGNATURES = {
     "glmmoe_expert_ffn_fp8": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp, _sz, _vp]),
     "glmmoe_profile_enable": (_i, [_i]),
     "glmmoe_profile_read": (_i, [_vp, _vp]),
-    "glmmoe_ref_register_w4a16": (_i, [_vp, _vp, _vp, _vp]),
-    "glmmoe_ref_unregister_w4a16": (_i, [_vp, _vp, _vp]),
+    "glmmoe_ref_register_w4a16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp]),
+    "glmmoe_ref_unregister_w4a16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp]),
     "glmmoe_ref_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
     "glmmoe_ref_set_workspace": (_i, [_vp, _sz]),
     "glmmoe_ref_moe_expert_ffn_w4a16": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp,

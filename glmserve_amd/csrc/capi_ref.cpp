@@ -18,10 +18,19 @@ inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Packed copies of reference-layout weight sets, keyed by the reference's
-// qweight pointers (host state; the lock covers lookups and updates).
+// qweight and scale pointers (host state; the lock covers lookups and
+// updates). A call must name exactly a registered set: weights moved or
+// replaced at other addresses are not found (GLMMOE_ERR_ARG) instead of
+// silently using the old packed copy.
 struct Registered {
     const uint8_t *gate_q, *up_q, *down_q;
+    const float *gate_sc, *up_sc, *down_sc;
     glmmoe_w4a16_layer packed;
+    bool same(const uint8_t* gq, const float* gs, const uint8_t* uq, const float* us,
+              const uint8_t* dq, const float* ds) const {
+        return gate_q == gq && up_q == uq && down_q == dq && gate_sc == gs && up_sc == us &&
+               down_sc == ds;
+    }
 };
 std::mutex g_mu;
 std::vector<Registered> g_sets;
@@ -47,13 +56,15 @@ glmmoe_w4a16_layer shape_layer(int topk, int hidden, int moe_inter, int E) {
 
 extern "C" {
 
-int glmmoe_ref_register_w4a16(const uint8_t* gate_q, const uint8_t* up_q, const uint8_t* down_q,
+int glmmoe_ref_register_w4a16(const uint8_t* gate_q, const float* gate_sc, const uint8_t* up_q,
+                              const float* up_sc, const uint8_t* down_q, const float* down_sc,
                               const glmmoe_w4a16_layer* packed) {
-    if (!gate_q || !up_q || !down_q || !packed) return GLMMOE_ERR_ARG;
+    if (!gate_q || !up_q || !down_q || !gate_sc || !up_sc || !down_sc || !packed)
+        return GLMMOE_ERR_ARG;
     if (!packed->gate_q || !packed->gate_s || !packed->up_q || !packed->up_s ||
         !packed->down_q || !packed->down_s)
         return GLMMOE_ERR_ARG;
-    Registered r{gate_q, up_q, down_q, *packed};
+    Registered r{gate_q, up_q, down_q, gate_sc, up_sc, down_sc, *packed};
     // Routed experts only: the reference's moe_expert_ffn_w4a16 has no shared
     // expert and no router.
     r.packed.sh_gate_q = r.packed.sh_up_q = r.packed.sh_down_q = nullptr;
@@ -62,7 +73,7 @@ int glmmoe_ref_register_w4a16(const uint8_t* gate_q, const uint8_t* up_q, const 
     r.packed.e_bias = nullptr;
     std::lock_guard<std::mutex> lk(g_mu);
     for (auto& e : g_sets)
-        if (e.gate_q == gate_q && e.up_q == up_q && e.down_q == down_q) {
+        if (e.same(gate_q, gate_sc, up_q, up_sc, down_q, down_sc)) {
             e = r;
             return GLMMOE_OK;
         }
@@ -70,11 +81,11 @@ int glmmoe_ref_register_w4a16(const uint8_t* gate_q, const uint8_t* up_q, const 
     return GLMMOE_OK;
 }
 
-int glmmoe_ref_unregister_w4a16(const uint8_t* gate_q, const uint8_t* up_q,
-                                const uint8_t* down_q) {
+int glmmoe_ref_unregister_w4a16(const uint8_t* gate_q, const float* gate_sc, const uint8_t* up_q,
+                                const float* up_sc, const uint8_t* down_q, const float* down_sc) {
     std::lock_guard<std::mutex> lk(g_mu);
     for (size_t i = 0; i < g_sets.size(); ++i)
-        if (g_sets[i].gate_q == gate_q && g_sets[i].up_q == up_q && g_sets[i].down_q == down_q) {
+        if (g_sets[i].same(gate_q, gate_sc, up_q, up_sc, down_q, down_sc)) {
             g_sets.erase(g_sets.begin() + (long)i);
             return GLMMOE_OK;
         }
@@ -104,9 +115,6 @@ int glmmoe_ref_moe_expert_ffn_w4a16(const float* x, const int* topk_ids, const f
                                     const uint8_t* down_q, const float* down_sc, int n, int topk,
                                     int hidden, int moe_inter, int E, int group_size, float* out,
                                     void* stream) {
-    (void)gate_sc;
-    (void)up_sc;
-    (void)down_sc;
     if (!x || !topk_ids || !topk_weights || !out || n <= 0) return GLMMOE_ERR_ARG;
     if (group_size != 128) return GLMMOE_ERR_SHAPE;
     glmmoe_w4a16_layer L;
@@ -116,7 +124,7 @@ int glmmoe_ref_moe_expert_ffn_w4a16(const float* x, const int* topk_ids, const f
         std::lock_guard<std::mutex> lk(g_mu);
         const Registered* hit = nullptr;
         for (const auto& e : g_sets)
-            if (e.gate_q == gate_q && e.up_q == up_q && e.down_q == down_q) hit = &e;
+            if (e.same(gate_q, gate_sc, up_q, up_sc, down_q, down_sc)) hit = &e;
         if (!hit) return GLMMOE_ERR_ARG;
         L = hit->packed;
         int dev = 0;

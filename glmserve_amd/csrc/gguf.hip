@@ -873,7 +873,9 @@ __device__ __forceinline__ bool gg_tile(int g, const int* __restrict__ ids,
                                         const int* __restrict__ d, int nk, int E, int topk,
                                         bool down, GgTile<TT>& tl) {
     if (!d) {
-        if (g >= nk) return false;
+        // An id outside [0, E) routes nowhere: no tile (the grouping drops it
+        // too, and the reduce skips its slot).
+        if (g >= nk || ids[g] < 0 || ids[g] >= E) return false;
         tl.e = ids[g];
         tl.nr = 1;
 #pragma unroll
@@ -997,14 +999,20 @@ __global__ __launch_bounds__(kGgThreads) void gg_moe_kernel(GgMoeArgs a) {
 }
 
 // out[t] = ((0 + w0 y0) + w1 y1) + ... over the slots (cuda/qgemm.cu:943-955).
+// Slots whose id is outside [0, E) add nothing (their dpart rows are never
+// written).
 __global__ __launch_bounds__(256) void gg_reduce_kernel(const float* __restrict__ dpart,
+                                                        const int* __restrict__ ids,
                                                         const float* __restrict__ w, int n,
-                                                        int topk, int H, float* __restrict__ out) {
+                                                        int topk, int H, int E, float* __restrict__ out) {
     const long i = (long)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= (long)n * H) return;
     const long t = i / H, o = i % H;
     float acc = 0.0f;
-    for (int s = 0; s < topk; ++s) acc = acc + w[t * topk + s] * dpart[(t * topk + s) * H + o];
+    for (int s = 0; s < topk; ++s) {
+        const int e = ids[t * topk + s];
+        if (e >= 0 && e < E) acc = acc + w[t * topk + s] * dpart[(t * topk + s) * H + o];
+    }
     out[i] = acc;
 }
 
@@ -1223,7 +1231,7 @@ static int gg_moe(GgMoeArgs a, float* out, int* dispatch, hipStream_t s) {
     if (rc) return rc;
     const long total = (long)n * H;
     hipLaunchKernelGGL(gg_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
-                       dpart, ids_w, n, topk, H, out);
+                       dpart, ids, ids_w, n, topk, H, E, out);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 

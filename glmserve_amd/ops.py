@@ -289,12 +289,14 @@ class RefW4Experts:
         st.up_q, st.up_s = _p(self.packed[1][0]), _p(self.packed[1][1])
         st.down_q, st.down_s = _p(self.packed[2][0]), _p(self.packed[2][1])
         self.struct = st
-        check(lib().glmmoe_ref_register_w4a16(_p(gate_q), _p(up_q), _p(down_q),
-                                              ctypes.byref(st)), "ref_register_w4a16")
+        check(lib().glmmoe_ref_register_w4a16(_p(gate_q), _p(gate_s), _p(up_q), _p(up_s),
+                                              _p(down_q), _p(down_s), ctypes.byref(st)),
+              "ref_register_w4a16")
 
     def release(self):
-        gq, _, uq, _, dq, _ = self.raw
-        check(lib().glmmoe_ref_unregister_w4a16(_p(gq), _p(uq), _p(dq)), "ref_unregister_w4a16")
+        gq, gs, uq, us, dq, ds = self.raw
+        check(lib().glmmoe_ref_unregister_w4a16(_p(gq), _p(gs), _p(uq), _p(us), _p(dq), _p(ds)),
+              "ref_unregister_w4a16")
 
     def workspace_bytes(self, n, topk):
         return lib().glmmoe_ref_workspace_bytes(n, topk, self.hidden, self.moe_inter, self.E)

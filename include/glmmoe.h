@@ -305,22 +305,27 @@ int glmmoe_profile_read(float* stage_ms, int* n_calls);
  * order (no shared expert, as in the reference).
  * The work runs the grouped kernels of glmmoe_expert_ffn_w4a16 on the native
  * packed copy of those weights (glmmoe_pack_w4a16, once at load time) that
- * glmmoe_ref_register_w4a16 associated with (gate_q, up_q, down_q), in the
+ * glmmoe_ref_register_w4a16 associated with (gate_q, gate_sc, up_q, up_sc,
+ * down_q, down_sc), in the
  * workspace glmmoe_ref_set_workspace registered for the current device, so
  * the call allocates nothing. x is rounded to bf16 (RNE) for those kernels and
  * the scales were rounded to bf16 when packed: results are within the W4A16
- * tolerance of the reference, not bit-identical. The scale pointers are not
- * read. Errors: GLMMOE_ERR_ARG when the weights are not registered,
+ * tolerance of the reference, not bit-identical. The scale arrays are not
+ * read, only matched with the registration: weights updated in place, or
+ * freed and reallocated, must be packed and registered again (registering
+ * the same six pointers replaces the entry). Errors: GLMMOE_ERR_ARG when
+ * these six pointers are not a registered set,
  * GLMMOE_ERR_WORKSPACE when no workspace of glmmoe_ref_workspace_bytes is
  * registered, GLMMOE_ERR_SHAPE for a shape other than the registered one.
  * Limits: group_size 128, hidden % 256 == 0, moe_inter % 128 == 0,
  * topk <= 8, E <= 512. The registry is a host-side table behind a lock;
  * registering or releasing while a call of the same weights is being
  * enqueued on another thread is the caller's race. */
-int glmmoe_ref_register_w4a16(const uint8_t* gate_q, const uint8_t* up_q, const uint8_t* down_q,
+int glmmoe_ref_register_w4a16(const uint8_t* gate_q, const float* gate_sc, const uint8_t* up_q,
+                              const float* up_sc, const uint8_t* down_q, const float* down_sc,
                               const glmmoe_w4a16_layer* packed);
-int glmmoe_ref_unregister_w4a16(const uint8_t* gate_q, const uint8_t* up_q,
-                                const uint8_t* down_q);
+int glmmoe_ref_unregister_w4a16(const uint8_t* gate_q, const float* gate_sc, const uint8_t* up_q,
+                                const float* up_sc, const uint8_t* down_q, const float* down_sc);
 size_t glmmoe_ref_workspace_bytes(int n, int topk, int hidden, int moe_inter, int E);
 int glmmoe_ref_set_workspace(void* workspace, size_t bytes);
 int glmmoe_ref_moe_expert_ffn_w4a16(const float* x, const int* topk_ids, const float* topk_weights,

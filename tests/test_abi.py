@@ -75,13 +75,20 @@ def test_reference_signature_host_checks():
     lw = L.glmmoe_layer_workspace_bytes(C.byref(_layer(shared=False)), 64)
     assert L.glmmoe_ref_workspace_bytes(64, 8, 6144, 2048, 256) == 64 * 6144 * 2 + lw
     assert L.glmmoe_ref_workspace_bytes(0, 8, 6144, 2048, 256) == 0
-    # registry: host-side table keyed by the reference's qweight pointers
+    # registry: host-side table keyed by the reference's qweight and scale pointers
     packed = _layer(shared=False)
     a, b, c = C.c_void_p(0x1000), C.c_void_p(0x2000), C.c_void_p(0x3000)
-    assert L.glmmoe_ref_register_w4a16(None, b, c, C.byref(packed)) == -1
-    assert L.glmmoe_ref_register_w4a16(a, b, c, C.byref(packed)) == 0
-    assert L.glmmoe_ref_unregister_w4a16(a, b, c) == 0
-    assert L.glmmoe_ref_unregister_w4a16(a, b, c) == -1
+    sa, sb, sc = C.c_void_p(0x4000), C.c_void_p(0x5000), C.c_void_p(0x6000)
+    assert L.glmmoe_ref_register_w4a16(None, sa, b, sb, c, sc, C.byref(packed)) == -1
+    assert L.glmmoe_ref_register_w4a16(a, None, b, sb, c, sc, C.byref(packed)) == -1
+    assert L.glmmoe_ref_register_w4a16(a, sa, b, sb, c, sc, C.byref(packed)) == 0
+    # a call naming the same qweights with other scale arrays finds no set
+    dummy2 = C.c_void_p(16)
+    assert L.glmmoe_ref_moe_expert_ffn_w4a16(dummy2, dummy2, dummy2, a, sa, b, C.c_void_p(0x7000), c, sc,
+                                             4, 8, 6144, 2048, 256, 128, dummy2, None) == -1
+    assert L.glmmoe_ref_unregister_w4a16(a, sa, b, C.c_void_p(0x7000), c, sc) == -1
+    assert L.glmmoe_ref_unregister_w4a16(a, sa, b, sb, c, sc) == 0
+    assert L.glmmoe_ref_unregister_w4a16(a, sa, b, sb, c, sc) == -1
     # GGUF: supported types, row lengths a multiple of the block, row_bytes large enough
     assert L.glmmoe_ref_gemm_q(18, None, dummy, None, dummy, 1, 6144, 64, 2352, None) == -1
     assert L.glmmoe_ref_gemm_q(99, dummy, dummy, None, dummy, 1, 6144, 64, 2352, None) == -2

@@ -89,6 +89,41 @@ def test_moe_expert_ffn_q(oracle, types, grouped):
     assert rel_err(out.cpu().numpy(), ref) < 1e-4
 
 
+@pytest.mark.parametrize("grouped", [False, True])
+def test_moe_expert_ffn_q_out_of_range_ids(oracle, grouped):
+    # Slots routed to an id outside [0, E) add nothing, in the ungrouped path
+    # (one tile per routed row) as in the grouped one: the output equals the
+    # oracle's with those slots' weights set to zero.
+    types = (18, 18, 23)
+    H, I, E, k, n = 512, 256, 8, 4, 40
+    rng = np.random.default_rng(77 + grouped)
+    gq = random_gguf_rows(types[0], E * I, H, rng)
+    uq = random_gguf_rows(types[1], E * I, H, rng)
+    dq = random_gguf_rows(types[2], E * H, I, rng)
+    deq = lambda t, q, rows, K: [oracle.gguf_dequant_rows(t, q[e * rows:(e + 1) * rows], rows, K)
+                                 for e in range(E)]
+    G, U, D = deq(types[0], gq, I, H), deq(types[1], uq, I, H), deq(types[2], dq, H, I)
+    x = rng.standard_normal((n, H)).astype(np.float32)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(n)]).astype(np.int32)
+    w = rng.uniform(0.1, 1.0, (n, k)).astype(np.float32)
+    bad = rng.random((n, k)) < 0.2
+    ids_bad = np.where(bad, np.where(rng.random((n, k)) < 0.5, -1, E), ids).astype(np.int32)
+    ref = oracle.moe_forward_streamed(x, ids, np.where(bad, 0.0, w).astype(np.float32),
+                                      lambda e: (G[e], U[e], D[e]))
+    dev = lambda a: torch.from_numpy(np.ascontiguousarray(a)).cuda()
+    h_act = torch.empty(n * k * I, device="cuda")
+    dpart = torch.empty(n * k * H, device="cuda")
+    out = torch.full((n, H), float("nan"), device="cuda")
+    disp = torch.full((3 * E + 1 + n * k,), -7, dtype=torch.int32, device="cuda") if grouped else None
+    ops.ref_moe_expert_ffn_q(types, dev(x), dev(ids_bad), dev(w), dev(gq), dev(uq), dev(dq), I, E,
+                             (_row_bytes(types[0], H), _row_bytes(types[1], H),
+                              _row_bytes(types[2], I)), h_act, dpart, out, disp)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    assert np.isfinite(got).all()
+    assert rel_err(got, ref) < 1e-4
+
+
 def test_gemm_q_unaligned_rows(oracle):
     # Q8_0 rows of 3 blocks (102 B) are not 4-byte aligned: the byte-load decode
     # serves them (the streamed kernels need dword-aligned rows).
