@@ -53,6 +53,11 @@ def build(verbose=False, out_lib=None, defines=()):
     os.replace(tmp, lib_path)
     for o in objs:
         os.remove(o)
+    if out_lib is None:
+        # The peak-rate probe (a stand-alone program next to the library).
+        probe = os.path.join(out_dir, "glmmoe_peaks")
+        subprocess.run([HIPCC] + HIP_FLAGS + [os.path.join(HERE, "microbench", "peaks.hip"), "-o", probe],
+                       check=True)
     return lib_path
 
 
