@@ -641,32 +641,43 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
     // Exact fixed-order logits of the candidates: lane c sums chunk c in
     // ascending K, then the chunk sums are added in ascending c. Occupancy
     // (few registers per wave) hides the weight loads.
-    for (int i = 0; i < ncand; ++i) {
-        const int ec = list[i];
-        const uint4* wp = reinterpret_cast<const uint4*>(wr + (size_t)ec * H + lane * kRouterKC);
-        float part = 0.0f;
+    // Two candidates at a time: their loads in flight together and their
+    // chains interleaved (each chain is still the ascending-K sum from zero).
+    for (int i = 0; i < ncand; i += 2) {
+        const bool two = i + 1 < ncand;
+        const int ec0 = list[i], ec1 = two ? list[i + 1] : ec0;
+        const uint4* wp0 = reinterpret_cast<const uint4*>(wr + (size_t)ec0 * H + lane * kRouterKC);
+        const uint4* wp1 = reinterpret_cast<const uint4*>(wr + (size_t)ec1 * H + lane * kRouterKC);
+        float p0 = 0.0f, p1 = 0.0f;
         if (lane < nchunks) {
-            uint4 wv[kRouterKC / 8];   // all loads in flight together
+            uint4 w0[kRouterKC / 8], w1[kRouterKC / 8];
 #pragma unroll
-            for (int q = 0; q < kRouterKC / 8; ++q) wv[q] = wp[q];
+            for (int q = 0; q < kRouterKC / 8; ++q) { w0[q] = wp0[q]; w1[q] = wp1[q]; }
 #pragma unroll
             for (int q = 0; q < kRouterKC / 8; ++q) {
-                const uint4 w4 = wv[q];
                 const uint4 xv = xw[q][lane];
-                const uint32_t wd[4] = {w4.x, w4.y, w4.z, w4.w};
                 const uint32_t xd[4] = {xv.x, xv.y, xv.z, xv.w};
+                const uint32_t a[4] = {w0[q].x, w0[q].y, w0[q].z, w0[q].w};
+                const uint32_t b[4] = {w1[q].x, w1[q].y, w1[q].z, w1[q].w};
 #pragma unroll
                 for (int d = 0; d < 4; ++d) {
-                    part = __builtin_fmaf(bf16_to_f32(xd[d] & 0xffffu), bf16_to_f32(wd[d] & 0xffffu), part);
-                    part = __builtin_fmaf(__uint_as_float(xd[d] & 0xffff0000u),
-                                          __uint_as_float(wd[d] & 0xffff0000u), part);
+                    const float xlo = bf16_to_f32(xd[d] & 0xffffu), xhi = __uint_as_float(xd[d] & 0xffff0000u);
+                    p0 = __builtin_fmaf(xlo, bf16_to_f32(a[d] & 0xffffu), p0);
+                    p1 = __builtin_fmaf(xlo, bf16_to_f32(b[d] & 0xffffu), p1);
+                    p0 = __builtin_fmaf(xhi, __uint_as_float(a[d] & 0xffff0000u), p0);
+                    p1 = __builtin_fmaf(xhi, __uint_as_float(b[d] & 0xffff0000u), p1);
                 }
             }
         }
-        float total = 0.0f;
-        for (int c = 0; c < nchunks; ++c)
-            total = total + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(part), c));
-        if (lane == 0) lrow[ec] = total;
+        float t0 = 0.0f, t1 = 0.0f;
+        for (int c = 0; c < nchunks; ++c) {
+            t0 = t0 + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p0), c));
+            t1 = t1 + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p1), c));
+        }
+        if (lane == 0) {
+            lrow[ec0] = t0;
+            if (two) lrow[ec1] = t1;
+        }
     }
 }
 
