@@ -421,7 +421,7 @@ int glmmoe_moe_layer_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, fl
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
     const int sh = has_shared(L) ? 1 : 0;
     const DispOut disp{v.expert_offsets, v.sorted_token_ids, v.sorted_row, v.inv,
-                       reinterpret_cast<int4*>(v.tiles), v.ntiles, kBigRows, sh, 1, 0};
+                       reinterpret_cast<int4*>(v.tiles), v.ntiles, kBigRows, sh, 1, 0, nullptr, 0};
     bool dispatched = false;
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
                               L->routed_scale, v.logits, nullptr, v.rpart, v.topk_ids, v.topk_w, s,
