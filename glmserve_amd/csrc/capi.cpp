@@ -176,14 +176,14 @@ inline void end_call(hipStream_t s) {
 // Dispatch onward, given ids/weights/xsum in the workspace view.
 int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int* ids,
                 const float* w, const float* xsum, float* out, const glmmoe_layer_ws& v,
-                hipStream_t s, bool dispatched = false) {
+                hipStream_t s, bool dispatched = false, const FusedRoute* fr = nullptr) {
     const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
     const int sh = has_shared(L) ? 1 : 0;
     const int mt = max_tiles_for(n, k, E, sh, H, I);
     const int T = tile_rows_for(n, k, sh, H, I);
     const bool big = T == kBigRows;
     mark(GLMMOE_STAGE_DISPATCH, s);
-    int rc = dispatched ? 0
+    int rc = dispatched || fr ? 0
                         : launch_dispatch(ids, n, k, E, v.expert_offsets, v.sorted_token_ids,
                                           v.sorted_row, v.inv, v.tiles, v.ntiles, T, sh, 1, s,
                                           dispatch_scratch(v.rpart, L, n), big ? kBigRows / 2 : 0,
@@ -194,7 +194,7 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     rc = big ? launch_gate_up_big(P, x, n, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.dpart,
                                   H, I, E, s)
              : launch_gate_up(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.hsum,
-                              v.sync, v.dpart, dpart_bytes(L, n), H, I, E, s);
+                              v.sync, v.dpart, dpart_bytes(L, n), H, I, E, s, fr);
     if (rc) return rc;
     mark(GLMMOE_STAGE_DOWN, s);
     rc = big ? launch_down_big(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
@@ -337,6 +337,18 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     const DispOut disp{v.expert_offsets, v.sorted_token_ids, v.sorted_row, v.inv,
                        reinterpret_cast<int4*>(v.tiles), v.ntiles, T, sh, 1,
                        T == kBigRows ? kBigRows / 2 : 0, v.sync, kTailTicks};
+    // Small batches: the router kernel writes the order codes and scores,
+    // and the gate/up kernel selects and dispatches (one launch fewer).
+    if (T == kTileRows && router_small_path(n, H, E, k) && fused_route_ok(n, k, E, H)) {
+        rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
+                                  L->routed_scale, v.logits, v.xsum, v.rpart, v.topk_ids, v.topk_w,
+                                  s, &disp, nullptr, false);
+        if (rc) return rc;
+        mark(GLMMOE_STAGE_ROUTER_TOPK, s);
+        const FusedRoute fr{reinterpret_cast<const uint32_t*>(v.rpart), n, k, L->norm_topk,
+                            L->routed_scale, v.topk_ids, v.topk_w, disp};
+        return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s, true, &fr);
+    }
     bool dispatched = false;
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
                               L->routed_scale, v.logits, v.xsum, v.rpart, v.topk_ids, v.topk_w, s,

@@ -227,4 +227,87 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
     }
 }
 
+// Small-batch dispatch: the outputs dispatch_block gives (mode 1,
+// half_rows 0) for total = n * topk <= 64 ids of n <= tile_rows tokens, so
+// that every expert, and the shared expert, has a single tile. One wave holds
+// the ids (lane j: id j) and finds equal ids with one ballot per id bit;
+// a packed LDS histogram (count + 65536 per distinct expert) scanned once
+// gives every expert both the number of valid ids below it (its offset) and
+// the number of distinct experts below it (its tile's index). Id j lands at
+// offset(e_j) + #{k < j : e_k == e_j}: the stable token-then-slot order.
+// ids: in LDS, visible to every thread; hist: E + 2 ints and pre: E + 2
+// ints of LDS scratch. Every output goes to ltiles / lnt / ltok (LDS) and,
+// when lead, to every pointer of gd. All NT threads call it.
+constexpr int kSmallDispIds = 64;
+
+template <int NT>
+__device__ void dispatch_small(const int* ids, int n, int topk, int E, int with_shared,
+                               int4* ltiles, int* lnt, int* ltok, const DispOut& gd, bool lead,
+                               int* hist, int* pre) {
+    static_assert(NT >= kSmallDispIds, "one wave holds every id");
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int total = n * topk;
+    for (int e = tid; e <= E; e += NT) hist[e] = 0;
+    int e = -1, before = 0;
+    bool valid = false;
+    if (tid < 64) {
+        e = lane < total ? ids[lane] : -1;
+        valid = e >= 0 && e < E;
+        int nbits = 0;
+        while ((1 << nbits) < E) ++nbits;
+        uint64_t m = __ballot(valid);
+        for (int b = 0; b < nbits; ++b) {
+            const bool bit = valid && ((e >> b) & 1);
+            const uint64_t bal = __ballot(bit);
+            m &= bit ? bal : ~bal;
+        }
+        const uint64_t below = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+        before = __popcll(m & below);
+    }
+    __syncthreads();
+    if (valid) atomicAdd(&hist[e], before == 0 ? 0x10001 : 1);
+    __syncthreads();
+    wave0_exclusive_scan(hist, E + 1, pre);
+    __syncthreads();
+    if (valid) {
+        const int pos = (pre[e] & 0xffff) + before;
+        ltok[pos] = tid / topk;
+        if (lead) {
+            gd.sorted_tok[pos] = tid / topk;
+            gd.sorted_slot[pos] = tid % topk;
+            gd.inv[tid] = pos;
+        }
+    }
+    if (with_shared && tid < n) {
+        ltok[total + tid] = tid;
+        if (lead) {
+            gd.sorted_tok[total + tid] = tid;
+            gd.sorted_slot[total + tid] = -1;
+        }
+    }
+    for (int x = tid; x <= E; x += NT) {
+        const int p = pre[x], below = p & 0xffff, dbelow = p >> 16;
+        const int cnt = x < E ? hist[x] & 0xffff : 0;
+        if (lead) gd.offsets[x] = below;
+        if (cnt > 0) {
+            const int4 t = make_int4(x, below, cnt, 0);
+            ltiles[dbelow] = t;
+            if (lead) gd.tiles[dbelow] = t;
+        }
+        if (x == E) {
+            if (with_shared) {
+                const int4 t = make_int4(E, total, n, 0);
+                ltiles[dbelow] = t;
+                if (lead) gd.tiles[dbelow] = t;
+            }
+            const int nt = dbelow + (with_shared ? 1 : 0);
+            lnt[0] = lnt[1] = lnt[2] = nt;
+            if (lead) {
+                gd.offsets[E + 1] = total + (with_shared ? n : 0);
+                gd.ntiles[0] = gd.ntiles[1] = gd.ntiles[2] = nt;
+            }
+        }
+    }
+}
+
 }  // namespace glmmoe

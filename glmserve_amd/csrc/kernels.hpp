@@ -65,7 +65,13 @@ size_t router_select_scratch_bytes(int n, int H, int E);
 int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_bias, int n, int H,
                          int E, int topk, int norm_topk, float routed_scale, float* logits,
                          float* xsum, float* scratch, int* ids, float* w, hipStream_t s,
-                         const DispOut* disp = nullptr, bool* dispatched = nullptr);
+                         const DispOut* disp = nullptr, bool* dispatched = nullptr,
+                         bool select = true);
+// The small-batch router path (router_small_kernel) applies to this shape.
+// With select == false launch_router_select then only writes the logits, the
+// order codes and scores ([2][n][E] in scratch) and xsum, and zeroes
+// disp->zero (the tickets): the selection and dispatch run inside gate/up.
+bool router_small_path(int n, int H, int E, int topk);
 int launch_router_topk(const float* logits, const float* e_bias, int n, int E, int topk,
                        int norm_topk, float routed_scale, int* ids, float* w, hipStream_t s);
 // Scratch (bytes) the multi-workgroup dispatch of a large batch uses (0 below it).
@@ -79,10 +85,26 @@ int launch_pack_w4(const uint8_t* q, const void* sc, int sc_bf16, int n_mats, in
 // tick: kTailTicks words, zero at launch (the dispatch clears them); tpart:
 // tpart_bytes of scratch for split items' partials (no split without them).
 constexpr int kTailTicks = 256;
+// Selection and dispatch of a small batch (n <= kFusedRouteMax) inside the
+// gate/up stream kernel: each workgroup selects the tokens' experts from
+// router_small_kernel's order codes and scores (the router's top-k, one wave
+// per token) and dispatches them into its LDS; workgroup 0 also stores the
+// ids, weights and dispatch outputs the later kernels read.
+constexpr int kFusedRouteMax = 8;
+struct FusedRoute {
+    const uint32_t* cs;   // order codes [n][E], then scores [n][E]
+    int n, topk, norm_topk;
+    float routed_scale;
+    int* ids;             // [n][topk]
+    float* w;
+    DispOut disp;         // global outputs (tile_rows kTileRows, mode 1, half_rows 0)
+};
+// Whether gate/up can take the fused selection for this shape.
+bool fused_route_ok(int n, int topk, int E, int H);
 int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
                    const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
                    float* hsum, unsigned int* tick, float* tpart, size_t tpart_bytes, int H, int I,
-                   int E, hipStream_t s);
+                   int E, hipStream_t s, const FusedRoute* route = nullptr);
 int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
                 const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
                 hipStream_t s);

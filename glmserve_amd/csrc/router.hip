@@ -6,6 +6,7 @@
 #include "common.hpp"
 #include "dispatch.hpp"
 #include "kernels.hpp"
+#include "topk.hpp"
 
 namespace glmmoe {
 
@@ -261,145 +262,6 @@ __global__ __launch_bounds__(256) void xsum_kernel(const uint16_t* __restrict__ 
     xsum[i] = s;
 }
 
-// ---------------------------------------------------------------------------
-// Top-k. One wave per token; lane l owns experts l, l+64, ... (E <= 512).
-// Each candidate is one 64-bit key whose unsigned order is the selection
-// order of cuda/moe_router.cu:48-53: high word = choose mapped to a
-// monotone unsigned code (NaN just above "no candidate", below every number),
-// low word = ~expert, so equal choose values prefer the lower expert index.
-// kmax / kmax_dpp: a max over keys (each 16-lane row with DPP row rotations,
-// then the 4 row maxima via readlane), used where one key per wave is wanted.
-// ---------------------------------------------------------------------------
-constexpr int kMaxPerLane = 8;  // E <= 512
-
-__device__ __forceinline__ uint32_t order_code(float f) {
-    if (f != f) return 1u;
-    if (f == 0.0f) f = 0.0f;   // -0 == +0: equal values fall through to the index
-    const uint32_t u = __float_as_uint(f);
-    return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
-}
-
-__device__ __forceinline__ void kmax(uint32_t& h, uint32_t& l, uint32_t oh, uint32_t ol) {
-    const bool take = oh > h || (oh == h && ol > l);
-    h = take ? oh : h;
-    l = take ? ol : l;
-}
-
-template <int CTRL>
-__device__ __forceinline__ void kmax_dpp(uint32_t& h, uint32_t& l) {
-    const uint32_t oh = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)h, CTRL, 0xf, 0xf, false);
-    const uint32_t ol = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)l, CTRL, 0xf, 0xf, false);
-    kmax(h, l, oh, ol);
-}
-
-constexpr int kTopkScratch = 40;   // LDS words per wave for topk_wave
-
-// Selection for token row lt (one wave; every lane calls it): the k rounds of
-// cuda/moe_router.cu:48-53 over keys (order code of choose, ~expert), each
-// lane's keys pre-sorted so a round looks at one head per lane. scratch is
-// unused (kept for the callers' LDS layout). COH: read the logits (or codes
-// and scores) with device-coherent loads and store ids/weights with
-// device-coherent stores.
-template <bool COH, int NJ>
-__device__ __forceinline__ void topk_wave_nj(const float* __restrict__ lt,
-                                          const float* __restrict__ e_bias, int E, int topk,
-                                          int norm_topk, float routed_scale,
-                                          int* __restrict__ ids_out, float* __restrict__ w_out,
-                                          uint32_t* scratch, const uint32_t* pcode,
-                                          const float* pscore, int* ids_copy = nullptr) {
-    const int lane = threadIdx.x & 63;
-    float score[NJ];
-    uint32_t ch[NJ];   // order codes, 0 = no candidate
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) {
-        const int e = lane + 64 * j;
-        score[j] = 0.0f;
-        ch[j] = 0u;
-        if (e < E) {
-            if (pcode) {   // codes and scores already computed by the caller
-                ch[j] = COH ? ld_dev(pcode + e) : pcode[e];
-                score[j] = COH ? ld_dev(pscore + e) : pscore[e];
-            } else {
-                const float sc = sigmoid_fixed(COH ? ld_dev(lt + e) : lt[e]);
-                score[j] = sc;
-                ch[j] = order_code(sc + (e_bias ? e_bias[e] : 0.0f));
-            }
-        }
-    }
-    // 1. Keys (order code, ~expert): a larger key is chosen first; equal
-    //    codes prefer the lower expert. Each lane sorts its NJ keys, largest
-    //    first, scores alongside (a fixed compare-exchange network).
-    uint32_t kl[NJ];
-#pragma unroll
-    for (int j = 0; j < NJ; ++j) kl[j] = ch[j] ? ~(uint32_t)(lane + 64 * j) : 0u;
-#pragma unroll
-    for (int i = 0; i < NJ; ++i)
-#pragma unroll
-        for (int j = 0; j + 1 < NJ - i; ++j) {
-            const bool up = ch[j + 1] > ch[j] || (ch[j + 1] == ch[j] && kl[j + 1] > kl[j]);
-            const uint32_t h0 = ch[j], l0 = kl[j];
-            const float s0 = score[j];
-            ch[j] = up ? ch[j + 1] : ch[j];
-            kl[j] = up ? kl[j + 1] : kl[j];
-            score[j] = up ? score[j + 1] : score[j];
-            ch[j + 1] = up ? h0 : ch[j + 1];
-            kl[j + 1] = up ? l0 : kl[j + 1];
-            score[j + 1] = up ? s0 : score[j + 1];
-        }
-    // 2. k rounds, as cuda/moe_router.cu:48-53 does them: the largest lane
-    //    head over the wave (a max over each 16-lane row with DPP row
-    //    rotations, then the 4 row maxima); the owner lane drops its head.
-    //    Lane k keeps round k's pick. (A rolled loop: these kernels run
-    //    once per call, where fetching unrolled code costs more than the
-    //    loop.)
-    float wsel = 0.0f;
-    int idsel = 0;
-    float wsum = 0.0f;
-#pragma unroll 1
-    for (int k = 0; k < topk; ++k) {
-        uint32_t h = ch[0], l = kl[0];
-        kmax_dpp<0x121>(h, l);
-        kmax_dpp<0x122>(h, l);
-        kmax_dpp<0x124>(h, l);
-        kmax_dpp<0x128>(h, l);
-        uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)h, 0);
-        uint32_t bl = (uint32_t)__builtin_amdgcn_readlane((int)l, 0);
-#pragma unroll
-        for (int r = 1; r < 4; ++r)
-            kmax(bh, bl, (uint32_t)__builtin_amdgcn_readlane((int)h, 16 * r),
-                 (uint32_t)__builtin_amdgcn_readlane((int)l, 16 * r));
-        const int e = (int)~bl;               // uniform winner
-        const int owner = e & 63;
-        const float sw = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(score[0]), owner));
-        if (lane == owner) {
-#pragma unroll
-            for (int j = 0; j + 1 < NJ; ++j) {
-                ch[j] = ch[j + 1];
-                kl[j] = kl[j + 1];
-                score[j] = score[j + 1];
-            }
-            ch[NJ - 1] = 0u;
-            kl[NJ - 1] = 0u;
-        }
-        idsel = lane == k ? e : idsel;
-        wsel = lane == k ? sw : wsel;
-        wsum = wsum + sw;
-    }
-    // 3. Weights in selection order, normalized by their sum in that order.
-    (void)scratch;
-    if (lane < topk) {
-        float v = wsel;
-        if (norm_topk && wsum > 0.0f) v = v / wsum;
-        if (COH) {
-            st_dev(ids_out + lane, idsel);
-            st_dev(w_out + lane, v * routed_scale);
-        } else {
-            ids_out[lane] = idsel;
-            w_out[lane] = v * routed_scale;
-        }
-        if (ids_copy) ids_copy[lane] = idsel;
-    }
-}
 
 // Dispatch on the experts per lane (E <= 64 * NJ). pcode / pscore: the
 // token's order codes and scores when the caller computed them (else null).
@@ -761,11 +623,15 @@ __device__ __forceinline__ void small_chunk_dots(const char* xl, const uint4 (&w
 __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const float* __restrict__ e_bias, int n, int H, int E, int epw, float* __restrict__ logits,
-    float* __restrict__ xsum, int slices, uint32_t* __restrict__ cs) {
+    float* __restrict__ xsum, int slices, uint32_t* __restrict__ cs, unsigned int* __restrict__ zero,
+    int nzero) {
     extern __shared__ __align__(16) char small_lds[];
     const int nchunks = H / kRouterKC;
     const int tid = threadIdx.x;
     const int eb = blockIdx.x, tg = blockIdx.y;
+    // The expert kernels' tickets, when the selection runs inside gate/up.
+    if (zero && eb == 0 && tg == 0)
+        for (int i = tid; i < nzero; i += kSmallThreads) zero[i] = 0u;
     const int t0 = tg * kRouterTG, nt = min(kRouterTG, n - t0);
     // LDS: the group's activations as 256-byte rows R = t * nchunks + c
     // (token t, chunk c), 16-byte piece o of row R at slot o ^ (R & 15) (the
@@ -873,6 +739,11 @@ __global__ __launch_bounds__(kSmallThreads) void router_finish_kernel(
     dispatch_block<kSmallThreads>(sids, n, topk, E, d, lds);
 }
 
+bool router_small_path(int n, int H, int E, int topk) {
+    return n < kTiledMinTokens && H % kRouterKC == 0 && H / kRouterKC <= kSmallMaxChunks &&
+           E <= 64 * kMaxPerLane && topk <= 8;
+}
+
 size_t router_select_scratch_bytes(int n, int H, int E) {
     const size_t a = router_logits_scratch_bytes(n, H, E);
     const size_t b = (size_t)n * E * 4;
@@ -882,11 +753,10 @@ size_t router_select_scratch_bytes(int n, int H, int E) {
 int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_bias, int n, int H,
                          int E, int topk, int norm_topk, float routed_scale, float* logits,
                          float* xsum, float* scratch, int* ids, float* w, hipStream_t s,
-                         const DispOut* disp, bool* dispatched) {
+                         const DispOut* disp, bool* dispatched, bool select) {
     const int nchunks = H / kRouterKC;
     if (dispatched) *dispatched = false;
-    if (n < kTiledMinTokens && H % kRouterKC == 0 && nchunks <= kSmallMaxChunks &&
-        E <= 64 * kMaxPerLane && topk <= 8) {
+    if (router_small_path(n, H, E, topk)) {
         // scratch: the order codes and scores [2][n][E] handed to the top-k.
         if (!scratch || router_select_scratch_bytes(n, H, E) < (size_t)2 * n * E * 4) return -3;
         // Experts per workgroup: as few as fill every CU once (one round of
@@ -920,8 +790,10 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
             attr_set = true;
         }
         hipLaunchKernelGGL(router_small_kernel, grid, dim3(kSmallThreads), lds, s, x, wr, e_bias, n,
-                           H, E, epw, logits, xsum, slices, reinterpret_cast<uint32_t*>(scratch));
+                           H, E, epw, logits, xsum, slices, reinterpret_cast<uint32_t*>(scratch),
+                           select ? nullptr : disp->zero, select ? 0 : disp->nzero);
         if (hipGetLastError() != hipSuccess) return -4;
+        if (!select) return 0;   // codes and scores only: the gate/up kernel selects
         // Selection: one workgroup (and then the dispatch too) up to
         // kFinishDispMax tokens, else one wave per token.
         const bool one = n <= kFinishDispMax;

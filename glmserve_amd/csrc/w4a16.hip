@@ -16,7 +16,9 @@
 // operand (16 output features) and tokens as the B operand (16 tokens).
 #include <utility>
 #include "common.hpp"
+#include "dispatch.hpp"
 #include "kernels.hpp"
+#include "topk.hpp"
 
 namespace glmmoe {
 
@@ -120,6 +122,7 @@ struct ExpArgs {
     uint16_t* h; float* hsum; float* dpart;
     unsigned int* tick; float* tpart; int tcap;   // tail split state (gate/up stream kernel)
     int H, I, E;
+    FusedRoute route;        // route.cs != null: select and dispatch first (gate/up stream kernel)
 };
 
 
@@ -556,13 +559,14 @@ __device__ __forceinline__ int4 s_unit(const SSched& sc, int base, int nwg, int 
 
 // Fills stream-table steps [k0, k0 + cnt) (whole workgroup; the caller
 // synchronizes afterwards).
-__device__ __forceinline__ void fill_stream_table(const ExpArgs& a, int* table, const SSched& sc,
+__device__ __forceinline__ void fill_stream_table(const int4* tiles, const int* rows_tok, int* table,
+                                                  const SSched& sc,
                                                   int base, int nwg, int ngrp, int BPI, int k0,
                                                   int cnt) {
     for (int i = threadIdx.x; i < cnt * kSTabInts; i += blockDim.x) {
         const int k = i / kSTabInts, f = i % kSTabInts;
         const int4 un = s_unit(sc, base, nwg, BPI, k0 + k);
-        const int4 tile = a.tiles[un.x / ngrp];
+        const int4 tile = tiles[un.x / ngrp];
         int v;
         if (f == 0) v = tile.x;
         else if (f == 1) v = tile.y;
@@ -570,13 +574,46 @@ __device__ __forceinline__ void fill_stream_table(const ExpArgs& a, int* table, 
         else if (f == 3) v = un.x % ngrp;
         else if (f < 20) {
             const int row = f - 4;
-            v = a.rows_tok ? a.rows_tok[tile.y + (row < tile.z ? row : 0)] : 0;
+            v = rows_tok ? rows_tok[tile.y + (row < tile.z ? row : 0)] : 0;
         } else if (f == 20) v = un.y;
         else if (f == 21) v = un.z;
         else if (f == 22) v = un.w;
         else v = 0;
         table[i] = v;
     }
+}
+
+// Fused routing bounds: n <= kFusedRouteMax tokens of topk <= 8 slots plus a
+// shared row each; with kTileRows-row tiles every expert then has one tile.
+constexpr int kRtMaxRows = kFusedRouteMax * 8 + kFusedRouteMax;
+constexpr int kRtMaxTiles = kFusedRouteMax * 8 + 1;
+static_assert(kFusedRouteMax <= kTileRows, "one tile per expert");
+
+// Selection and dispatch of a small batch by one 512-thread workgroup (all
+// threads call it): wave t selects token t (topk_wave_nj, the router's own
+// selection) into sids; dispatch_small then writes the tile list, tile
+// counts and sorted token ids to tiles / nt / tok (LDS). The lead workgroup
+// also stores the ids, weights and every dispatch output to the global
+// buffers of r.disp. scratch: kSmallDispIds + 2 * (kDispMaxE + 2) ints of LDS.
+template <int NJ>
+__device__ __forceinline__ void fused_route(const FusedRoute r, int E, bool lead, int4* tiles, int* nt,
+                                            int* tok, int* scratch) {
+    int* sids = scratch;                       // n * topk ids
+    int* hist = sids + kSmallDispIds;
+    int* pre = hist + kDispMaxE + 2;
+    const int wave = threadIdx.x >> 6;
+    if (wave < r.n) {
+        const int t = wave;
+        topk_wave_nj<false, NJ>(nullptr, nullptr, E, r.topk, r.norm_topk, r.routed_scale,
+                                lead ? r.ids + t * r.topk : nullptr,
+                                lead ? r.w + t * r.topk : nullptr, nullptr,
+                                r.cs + (size_t)t * E,
+                                reinterpret_cast<const float*>(r.cs) + (size_t)r.n * E + (size_t)t * E,
+                                sids + t * r.topk);
+    }
+    __syncthreads();
+    dispatch_small<512>(sids, r.n, r.topk, E, r.disp.with_shared, tiles, nt, tok, r.disp, lead, hist,
+                        pre);
 }
 
 template <int NMAT>
@@ -588,7 +625,12 @@ struct SLay {
     static constexpr int kJunk = 2 * kBuf;                   // placeholder DMA target
     static constexpr int kRed = kJunk + 256;                 // [8][16] h group-sum partials
     static constexpr int kTab = kRed + 8 * 16 * 4;
-    static constexpr int kTotal = kTab + kTable * kSTabInts * 4;
+    // Fused routing: the tile list, tile counts and sorted token ids the
+    // kernel then reads in place of the global ones.
+    static constexpr int kRtTiles = kTab + kTable * kSTabInts * 4;
+    static constexpr int kRtNt = kRtTiles + kRtMaxTiles * 16;
+    static constexpr int kRtTok = kRtNt + 16;
+    static constexpr int kTotal = kRtTok + kRtMaxRows * 4;
     static_assert(kTotal <= 160 * 1024, "one workgroup's LDS");
     static constexpr int P = NMAT == 2 ? kSPGU : kSPDown;    // weight groups in flight per wave
     static_assert(kSGB % P == 0, "ring slots stay static across batches");
@@ -778,6 +820,34 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
     using LY = SLay<NMAT>;
     constexpr int P = LY::P;
     extern __shared__ __align__(16) char lds[];
+    const int4* tiles = a.tiles;
+    const int* ntiles = a.ntiles;
+    const int* rows_tok = a.rows_tok;
+    static_assert((kSmallDispIds + 2 * (kDispMaxE + 2)) * 4 <= LY::kBuf, "fused routing scratch inside activation buffer 1");
+    static_assert(kFusedRouteMax * 8 <= kSmallDispIds, "the small dispatch holds every id");
+    if constexpr (GU) {
+        if (a.route.cs) {
+            // Select and dispatch here; the tile list then lives in LDS. The
+            // dispatch scratch sits in activation buffer 1, unused until the
+            // first batch is under way.
+            int4* tl = reinterpret_cast<int4*>(lds + LY::kRtTiles);
+            int* nt = reinterpret_cast<int*>(lds + LY::kRtNt);
+            int* tok = reinterpret_cast<int*>(lds + LY::kRtTok);
+            int* scr = reinterpret_cast<int*>(lds + LY::kBuf);
+            // The lead is the last workgroup: the one with the least expert
+            // work, which hides the wait for its global stores.
+            const bool lead = blockIdx.x == gridDim.x - 1;
+            const int E = a.E;
+            if (E <= 64) fused_route<1>(a.route, E, lead, tl, nt, tok, scr);
+            else if (E <= 128) fused_route<2>(a.route, E, lead, tl, nt, tok, scr);
+            else if (E <= 256) fused_route<4>(a.route, E, lead, tl, nt, tok, scr);
+            else fused_route<8>(a.route, E, lead, tl, nt, tok, scr);
+            tiles = tl;
+            ntiles = nt;
+            rows_tok = tok;
+            __syncthreads();
+        }
+    }
     const DqConst dqc = dq_const();
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -787,7 +857,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
     const int BPI = KG / kSGB;                 // activation batches per item
     const int nfb = (GU ? a.I : a.H) / 16;
     const int ngrp = nfb / (PAIR ? 16 : 8);
-    const int total = *a.ntiles * ngrp;
+    const int total = sgpr(*ntiles) * ngrp;   // uniform (ntiles may point into LDS)
     const int nwg = (int)gridDim.x;
     const int base = (int)blockIdx.x;
     const SSched sch = s_sched(total, nwg, base, GU ? BPI : 1, a.tcap);
@@ -834,7 +904,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
 
     for (int k0 = 0; k0 < nitems; k0 += kTable) {
         const int cnt = min(kTable, nitems - k0);
-        fill_stream_table(a, table, sch, base, nwg, ngrp, GU ? BPI : 1, k0, cnt);
+        fill_stream_table(tiles, rows_tok, table, sch, base, nwg, ngrp, GU ? BPI : 1, k0, cnt);
         __syncthreads();
         // Activation batches of the chunk: whole items BPI each, parts 1.
         const int nwhole = sch.split ? max(0, min(cnt, sch.R - k0)) : cnt;
@@ -976,7 +1046,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
                     T[m] = b == 0 ? t : T[m] + t;
                 }
             }
-            const int4 tile = a.tiles[un.x / ngrp];
+            const int4 tile = tiles[un.x / ngrp];
             finish(T, tile.y, tile.z, (un.x % ngrp) * 8 + wave);
         }
     }
@@ -1073,11 +1143,20 @@ static int launch_expert(const ExpArgs& a, long max_work, hipStream_t s) {
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
+bool fused_route_ok(int n, int topk, int E, int H) {
+    return n >= 1 && n <= kFusedRouteMax && topk >= 1 && topk <= 8 && topk <= E && E <= kDispMaxE &&
+           (H / 128) % kSGB == 0 && H % 128 == 0;
+}
+
 int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
                    const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
                    float* hsum, unsigned int* tick, float* tpart, size_t tpart_bytes, int H, int I,
-                   int E, hipStream_t s) {
+                   int E, hipStream_t s, const FusedRoute* route) {
     ExpArgs a{};
+    if (route) {
+        if (!fused_route_ok(route->n, route->topk, E, H)) return -1;
+        a.route = *route;
+    }
     a.tick = tick; a.tpart = tpart;
     a.tcap = tick && tpart ? (int)(tpart_bytes / kTailPartBytes) : 0;
     a.wq[0] = reinterpret_cast<const uint4*>(P.gate_q); a.ws[0] = P.gate_s;
@@ -1089,6 +1168,7 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, co
     const long work = (long)max_tiles * (I / 16 / kNWGU);
     if ((H / 128) % kSGB == 0)
         return launch_stream<0>(a, (long)max_tiles * (I / 128) * (H / 128 / kSGB), s);
+    if (route) return -1;
     if ((H / 128) % kPFGU == 0) return launch_expert<2, kPFGU, kRingGU, kNWGU>(a, work, s);
     return launch_expert<2, 1, 6, kNWGU>(a, work, s);   // odd K-group count
 }

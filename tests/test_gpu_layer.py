@@ -87,7 +87,7 @@ def test_tiny_config(oracle, n):
     _check_full(out, ref)
 
 
-@pytest.mark.parametrize("n", [1, 8, 32, 64])
+@pytest.mark.parametrize("n", [1, 3, 8, 32, 64])
 def test_decode_full_shape(oracle, full_layer, n):
     # configs[1] geometry: H 6144, 256 experts, top-8, I = S = 2048; every
     # token's output against the oracle.
@@ -95,6 +95,20 @@ def test_decode_full_shape(oracle, full_layer, n):
     x, out, logits, ids, w, offs, st, sr = _run(L, n, seed=2)
     _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
     _check_full(out, oracle_full_w4(L, oracle, x, ids, w))
+
+
+@pytest.mark.parametrize("n,shared", [(1, True), (2, False), (5, True), (8, True)])
+def test_fused_small_batch_routing(oracle, n, shared):
+    # Small batches on a K-group count the decode stream kernels take
+    # (H / 128 a multiple of 16) select and dispatch inside the gate/up
+    # kernel: 64 experts (one candidate per lane), top-6, so n * topk runs
+    # from 6 to 48 ids, with and without the shared expert. Routing and
+    # dispatch bit-exact, every output row within tolerance.
+    L = SynthLayer(2048, 64, 6, 256, seed=7, shared=shared)
+    x, out, logits, ids, w, offs, st, sr = _run(L, n, seed=13 + n)
+    ref_logits = _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
+    ref, _, _ = L.oracle_forward(oracle, x, np.arange(n), ref_logits)
+    _check_full(out, ref)
 
 
 def test_prefill_full_shape(oracle, full_layer):
