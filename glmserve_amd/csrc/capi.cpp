@@ -13,6 +13,8 @@ inline hipStream_t S(void* s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
+constexpr int kStreamWeightsMinTokens = 2;   // non-temporal expert-weight loads from this batch
+
 // Tile height of the W4A16 expert GEMMs for a batch: 16-row tiles (decode
 // kernels) or, from kBigMinRows grouped rows on shapes the large-group kernels
 // take (both K-group counts multiples of 8), 128-row tiles.
@@ -190,15 +192,18 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
                                           v.sync, kTailTicks);
     if (rc) return rc;
     const ExpertPtrs P = ptrs(L);
+    // From two tokens the routed experts' weights (up to 2 * topk + 1 of
+    // them) outgrow the 256 MiB Infinity Cache: stream them past L2.
+    const bool nt = n >= kStreamWeightsMinTokens;
     mark(GLMMOE_STAGE_GATE_UP, s);
     rc = big ? launch_gate_up_big(P, x, n, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.dpart,
                                   H, I, E, s)
              : launch_gate_up(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.hsum,
-                              v.sync, v.dpart, dpart_bytes(L, n), H, I, E, s, fr);
+                              v.sync, v.dpart, dpart_bytes(L, n), H, I, E, s, fr, nt);
     if (rc) return rc;
     mark(GLMMOE_STAGE_DOWN, s);
     rc = big ? launch_down_big(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
-             : launch_down(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s);
+             : launch_down(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s, nt);
     if (rc) return rc;
     mark(GLMMOE_STAGE_COMBINE, s);
     rc = launch_combine(v.dpart, v.inv, w, n, k, H, sh, out, s, big);

@@ -104,10 +104,14 @@ bool fused_route_ok(int n, int topk, int E, int H);
 int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
                    const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
                    float* hsum, unsigned int* tick, float* tpart, size_t tpart_bytes, int H, int I,
-                   int E, hipStream_t s, const FusedRoute* route = nullptr);
+                   int E, hipStream_t s, const FusedRoute* route = nullptr,
+                   bool stream_weights = false);
+// stream_weights: the decode kernels read the expert weights with
+// non-temporal loads (a batch whose routed weights exceed the last-level
+// cache: they are read once, and the activation rows stay in L2).
 int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
                 const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
-                hipStream_t s);
+                hipStream_t s, bool stream_weights = false);
 // Shapes the large-group W4A16 kernels take: H / 128 and I / 128 multiples of 8.
 bool big_w4_shape_ok(int H, int I);
 // Large-group kernels (fp16 MFMA). gate/up converts x to fp16 rows in scratch

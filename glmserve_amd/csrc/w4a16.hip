@@ -637,8 +637,14 @@ struct SLay {
     static constexpr int kWL = 2 * NMAT;                     // loads per weight group
 };
 
+// NT: a non-temporal load (data read once: it does not displace the
+// activation rows the workgroups re-read from L2).
+template <bool NT>
 __device__ __forceinline__ void gload16(u32x4& d, const void* base, uint32_t voff) {
-    asm volatile("global_load_dwordx4 %0, %1, %2" : "=&v"(d) : "v"(voff), "s"(base));
+    if constexpr (NT)
+        asm volatile("global_load_dwordx4 %0, %1, %2 nt" : "=&v"(d) : "v"(voff), "s"(base));
+    else
+        asm volatile("global_load_dwordx4 %0, %1, %2" : "=&v"(d) : "v"(voff), "s"(base));
 }
 __device__ __forceinline__ void gload8(u32x2& d, const void* base, uint32_t voff) {
     asm volatile("global_load_dwordx2 %0, %1, %2" : "=&v"(d) : "v"(voff), "s"(base));
@@ -732,12 +738,12 @@ __device__ __forceinline__ void s_issue_act(const ExpArgs& a, const SAItem& it, 
     dma4(a.gsum + (size_t)it.gtok * KG + grp, wave < 4 ? buf + LY::kGOff + wave * 256 : junk);
 }
 
-template <int NMAT>
+template <int NMAT, bool NT>
 __device__ __forceinline__ void s_issue_w(const SWItem& it, int kg, int lane, u32x4 (&w)[2],
                                           u32x2 (&sc)[2]) {
 #pragma unroll
     for (int m = 0; m < NMAT; ++m) {
-        gload16(w[m], reinterpret_cast<const char*>(it.wq[m]) + kg * 1024, (uint32_t)(lane * 16));
+        gload16<NT>(w[m], reinterpret_cast<const char*>(it.wq[m]) + kg * 1024, (uint32_t)(lane * 16));
         gload8(sc[m], reinterpret_cast<const char*>(it.ws[m]) + kg * 32, (uint32_t)((lane >> 4) * 8));
     }
 }
@@ -813,7 +819,7 @@ __device__ __forceinline__ void s_compute(const SOps& o, const u32x4 (&w)[2], co
 // which halves the batches, barriers and item switches per weight byte
 // against one block per wave (MODE 1, kept for shapes the layer does not
 // pass).
-template <int MODE>
+template <int MODE, bool NTW>
 __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
     constexpr int NMAT = MODE == 1 ? 1 : 2;
     constexpr bool GU = MODE == 0, PAIR = MODE == 2;
@@ -919,7 +925,7 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
         // loads, so every step issues the same loads and all waits stay
         // static; the surplus data is never read.
         auto issue_w = [&](u32x4 (&w)[2], u32x2 (&sc)[2]) {
-            s_issue_w<NMAT>(wit, wkg, lane, w, sc);
+            s_issue_w<NMAT, NTW>(wit, wkg, lane, w, sc);
             if (wkg + 1 < wit.ng) {
                 ++wkg;
             } else if (wk + 1 < cnt) {
@@ -1053,11 +1059,13 @@ __global__ __launch_bounds__(512) void w4_stream_kernel(ExpArgs a) {
 }
 
 template <int MODE>
-static int launch_stream(const ExpArgs& a, long max_work, hipStream_t s) {
+static int launch_stream(const ExpArgs& a, long max_work, hipStream_t s, bool nt) {
     using LY = SLay<MODE == 1 ? 1 : 2>;
     static bool attr_set = false;
     if (!attr_set) {
-        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4_stream_kernel<MODE>),
+        if (hipFuncSetAttribute(reinterpret_cast<const void*>(&w4_stream_kernel<MODE, false>),
+                                hipFuncAttributeMaxDynamicSharedMemorySize, LY::kTotal) != hipSuccess ||
+            hipFuncSetAttribute(reinterpret_cast<const void*>(&w4_stream_kernel<MODE, true>),
                                 hipFuncAttributeMaxDynamicSharedMemorySize, LY::kTotal) != hipSuccess)
             return -4;
         attr_set = true;
@@ -1068,7 +1076,11 @@ static int launch_stream(const ExpArgs& a, long max_work, hipStream_t s) {
     long blocks = max_work;
     if (blocks > (long)cus) blocks = cus;
     if (blocks < 1) blocks = 1;
-    hipLaunchKernelGGL((w4_stream_kernel<MODE>), dim3((unsigned)blocks), dim3(512), LY::kTotal, s, a);
+    if (nt)
+        hipLaunchKernelGGL((w4_stream_kernel<MODE, true>), dim3((unsigned)blocks), dim3(512), LY::kTotal, s, a);
+    else
+        hipLaunchKernelGGL((w4_stream_kernel<MODE, false>), dim3((unsigned)blocks), dim3(512), LY::kTotal, s,
+                           a);
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
@@ -1151,7 +1163,7 @@ bool fused_route_ok(int n, int topk, int E, int H) {
 int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, const int* tiles,
                    const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
                    float* hsum, unsigned int* tick, float* tpart, size_t tpart_bytes, int H, int I,
-                   int E, hipStream_t s, const FusedRoute* route) {
+                   int E, hipStream_t s, const FusedRoute* route, bool stream_weights) {
     ExpArgs a{};
     if (route) {
         if (!fused_route_ok(route->n, route->topk, E, H)) return -1;
@@ -1167,7 +1179,7 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, co
     a.rows_tok = rows_tok; a.h = h; a.hsum = hsum; a.H = H; a.I = I; a.E = E;
     const long work = (long)max_tiles * (I / 16 / kNWGU);
     if ((H / 128) % kSGB == 0)
-        return launch_stream<0>(a, (long)max_tiles * (I / 128) * (H / 128 / kSGB), s);
+        return launch_stream<0>(a, (long)max_tiles * (I / 128) * (H / 128 / kSGB), s, stream_weights);
     if (route) return -1;
     if ((H / 128) % kPFGU == 0) return launch_expert<2, kPFGU, kRingGU, kNWGU>(a, work, s);
     return launch_expert<2, 1, 6, kNWGU>(a, work, s);   // odd K-group count
@@ -1175,7 +1187,7 @@ int launch_gate_up(const ExpertPtrs& P, const uint16_t* x, const float* xsum, co
 
 int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const int* tiles,
                 const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
-                hipStream_t s) {
+                hipStream_t s, bool stream_weights) {
     ExpArgs a{};
     a.wq[0] = reinterpret_cast<const uint4*>(P.down_q); a.ws[0] = P.down_s;
     a.swq[0] = reinterpret_cast<const uint4*>(P.sh_down_q); a.sws[0] = P.sh_down_s;
@@ -1184,7 +1196,7 @@ int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const
     a.dpart = dpart; a.H = H; a.I = I; a.E = E;
     const long work = (long)max_tiles * (H / 16 / kNWDown);
     // Two 16-row blocks per wave (the layer's hidden size is a multiple of 256).
-    if ((I / 128) % kSGB == 0 && H % 256 == 0) return launch_stream<2>(a, (long)max_tiles * (H / 256), s);
+    if ((I / 128) % kSGB == 0 && H % 256 == 0) return launch_stream<2>(a, (long)max_tiles * (H / 256), s, stream_weights);
     if ((I / 128) % kPFDown == 0) return launch_expert<1, kPFDown, kRingDown, kNWDown>(a, work, s);
     return launch_expert<1, 1, 6, kNWDown>(a, work, s);   // odd K-group count
 }
