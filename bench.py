@@ -434,6 +434,10 @@ def main():
         for n in (1, 8, 32):
             log(f"bench: sweep B={n}")
             sweep[f"decode_B{n}"] = measure(n, args.steps, args.warmup)
+        # The headline's synthetic router hits ~143 distinct experts at B=64;
+        # uniform routing (~222) is the expert count throughput targets assume.
+        log("bench: sweep B=64 with uniform-random routing")
+        sweep["decode_B64_uniform"] = measure_uniform(64, args.steps, args.warmup)
         log("bench: sweep prefill 4096 (configs[2], uniform routing)")
         sweep["prefill_4096"] = measure_uniform(4096, max(3, args.steps // 10), 2)
         log("bench: sweep prefill 4096 (router-chosen routing)")

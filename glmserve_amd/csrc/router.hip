@@ -620,6 +620,22 @@ __device__ __forceinline__ void small_chunk_dots(const char* xl, const uint4 (&w
         if (t < nt) out[tb + t] = acc[t];
 }
 
+// ((0 + p[0]) + p[stride]) + ... over count partials, in that order; the
+// loads go out 8 at a time ahead of the dependent adds.
+__device__ __forceinline__ float chunk_sum(const float* p, int stride, int count) {
+    float total = 0.0f;
+    int c = 0;
+    for (; c + 8 <= count; c += 8) {
+        float v[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) v[u] = p[(c + u) * stride];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) total = total + v[u];
+    }
+    for (; c < count; ++c) total = total + p[c * stride];
+    return total;
+}
+
 __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const float* __restrict__ e_bias, int n, int H, int E, int epw, float* __restrict__ logits,
@@ -701,9 +717,7 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
         const int el2 = tid / kRouterTG, t = tid % kRouterTG;
         const int e2 = eb * epw + el2;
         if (e2 < E && t < nt) {
-            float total = 0.0f;
-            for (int cc = 0; cc < nchunks; ++cc)
-                total = total + part[(el2 * nchunks + cc) * kRouterTG + t];
+            const float total = chunk_sum(part + el2 * nchunks * kRouterTG + t, kRouterTG, nchunks);
             st_dev(logits + (size_t)(t0 + t) * E + e2, total);
             // The selection's inputs, computed here in parallel: the score
             // and the order code of choose = score + bias.
@@ -908,8 +922,7 @@ __global__ __launch_bounds__(kF32Threads) void router_logits_f32_kernel(
         const int el2 = tid / kRouterTG, t = tid % kRouterTG;
         const int e2 = blockIdx.x * epw + el2;
         if (e2 < E && t < nt) {
-            float total = 0.0f;
-            for (int cc = 0; cc < nchunks; ++cc) total = total + part[(el2 * nchunks + cc) * kRouterTG + t];
+            const float total = chunk_sum(part + el2 * nchunks * kRouterTG + t, kRouterTG, nchunks);
             y[(size_t)(t0 + t) * E + e2] = bias ? total + bias[e2] : total;
         }
     }
