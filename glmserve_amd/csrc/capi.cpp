@@ -389,8 +389,13 @@ int glmmoe_expert_ffn_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int 
     hipStream_t s = S(stream);
     begin_call();
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
-    rc = launch_xsum(x, n, L->hidden, v.xsum, s);
-    if (rc) return rc;
+    // The activation group sums are read only by the decode kernels (the
+    // large-group kernels decode the int4 weights exactly instead).
+    const int sh = has_shared(L) ? 1 : 0;
+    if (tile_rows_for(n, L->topk, sh, L->hidden, L->moe_inter) != kBigRows) {
+        rc = launch_xsum(x, n, L->hidden, v.xsum, s);
+        if (rc) return rc;
+    }
     return run_experts(L, x, n, topk_ids, topk_w, v.xsum, out, v, s);
 }
 
