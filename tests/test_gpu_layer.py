@@ -97,14 +97,17 @@ def test_decode_full_shape(oracle, full_layer, n):
     _check_full(out, oracle_full_w4(L, oracle, x, ids, w))
 
 
-@pytest.mark.parametrize("n,shared", [(1, True), (2, False), (5, True), (8, True)])
-def test_fused_small_batch_routing(oracle, n, shared):
+@pytest.mark.parametrize("n,shared,E,k", [(1, True, 64, 6), (2, False, 64, 6), (5, True, 64, 6),
+                                          (8, True, 64, 6), (3, True, 100, 8), (8, True, 100, 8),
+                                          (1, True, 512, 8), (7, False, 512, 8)])
+def test_fused_small_batch_routing(oracle, n, shared, E, k):
     # Small batches on a K-group count the decode stream kernels take
     # (H / 128 a multiple of 16) select and dispatch inside the gate/up
-    # kernel: 64 experts (one candidate per lane), top-6, so n * topk runs
-    # from 6 to 48 ids, with and without the shared expert. Routing and
-    # dispatch bit-exact, every output row within tolerance.
-    L = SynthLayer(2048, 64, 6, 256, seed=7, shared=shared)
+    # kernel. 64, 100 and 512 experts (1, 2 and 8 candidates per lane of the
+    # selection), top-6 or top-8, so n * topk runs from 6 to 64 ids, with and
+    # without the shared expert. Routing and dispatch bit-exact, every output
+    # row within tolerance.
+    L = SynthLayer(2048, E, k, 256, seed=7, shared=shared)
     x, out, logits, ids, w, offs, st, sr = _run(L, n, seed=13 + n)
     ref_logits = _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
     ref, _, _ = L.oracle_forward(oracle, x, np.arange(n), ref_logits)
