@@ -82,7 +82,7 @@ int launch_dispatch(const int* ids, int n, int topk, int E, int* offsets, int* s
                     int half_rows = -1, unsigned int* zero = nullptr, int nzero = 0);
 int launch_pack_w4(const uint8_t* q, const void* sc, int sc_bf16, int n_mats, int rows, int K,
                    uint8_t* pq, uint16_t* ps, hipStream_t s);
-// tick: kTailTicks words, zero at launch (the dispatch clears them); tpart:
+// tick: kTailTicks words, zero at launch (the router or dispatch kernel clears them); tpart:
 // tpart_bytes of scratch for split items' partials (no split without them).
 constexpr int kTailTicks = 256;
 // Selection and dispatch of a small batch (n <= kFusedRouteMax) inside the

@@ -522,7 +522,7 @@ constexpr int kSTabInts = 24;
 // that holds an item's last part (by ticket) adds the stored t_b in batch
 // order and finishes the item. Whole or split, an item's arithmetic is the
 // same, so results do not depend on how a batch's work was spread.
-// The tickets (kTailTicks, zero at launch: the dispatch clears them) and the
+// The tickets (kTailTicks, zero at launch: the call's router or dispatch kernel clears them) and the
 // stored t_b ([part][value][thread], 16 KiB per part, room for a.tcap parts)
 // are in the caller's workspace; a split needs rem <= kTailTicks items and
 // rem * BPI <= a.tcap parts.

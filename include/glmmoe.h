@@ -152,7 +152,7 @@ typedef struct glmmoe_layer_ws {
                              rows (n*topk + n), bf16 (first half of the region) from there;
                              at least 256 * (H / 2048) * 16 KiB: before the down projection
                              it holds the gate/up kernel's split-item partials */
-    unsigned int* sync;   /* [256] expert-kernel tickets (cleared by each call's dispatch) */
+    unsigned int* sync;   /* [256] expert-kernel tickets (cleared by each call's router or dispatch kernel) */
     size_t bytes;         /* total workspace bytes */
 } glmmoe_layer_ws;
 
