@@ -531,12 +531,16 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
                 }
             }
         }
-        float t0 = 0.0f, t1 = 0.0f;
-        for (int c = 0; c < nchunks; ++c) {
-            t0 = t0 + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p0), c));
-            t1 = t1 + __int_as_float(__builtin_amdgcn_readlane(__float_as_int(p1), c));
+        // ((0 + p_0) + p_1) + ... in chunk order, as a ripple across lanes:
+        // each step every lane adds its own partial to its left neighbour's
+        // running sum (wave shift right by one; lane 0 reads 0). After
+        // nchunks - 1 steps lane nchunks - 1 holds the whole ordered sum.
+        float t0 = 0.0f + p0, t1 = 0.0f + p1;
+        for (int c = 1; c < nchunks; ++c) {
+            t0 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t0), 0x138, 0xf, 0xf, true)) + p0;
+            t1 = __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(t1), 0x138, 0xf, 0xf, true)) + p1;
         }
-        if (lane == 0) {
+        if (lane == nchunks - 1) {
             lrow[ec0] = t0;
             if (two) lrow[ec1] = t1;
         }
