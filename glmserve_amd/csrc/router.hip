@@ -397,28 +397,13 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __rest
     }
 }
 
-// Float -> 64-bit selection key helpers of the top-k kernel above.
-__device__ __forceinline__ void kmax_wave(uint32_t& h, uint32_t& l) {
-    kmax_dpp<0x121>(h, l);
-    kmax_dpp<0x122>(h, l);
-    kmax_dpp<0x124>(h, l);
-    kmax_dpp<0x128>(h, l);
-    uint32_t bh = (uint32_t)__builtin_amdgcn_readlane((int)h, 0);
-    uint32_t bl = (uint32_t)__builtin_amdgcn_readlane((int)l, 0);
-#pragma unroll
-    for (int r = 1; r < 4; ++r)
-        kmax(bh, bl, (uint32_t)__builtin_amdgcn_readlane((int)h, 16 * r),
-             (uint32_t)__builtin_amdgcn_readlane((int)l, 16 * r));
-    h = bh;
-    l = bl;
-}
-
 __device__ __forceinline__ float code_to_float(uint32_t c) {
     return __uint_as_float((c & 0x80000000u) ? (c & 0x7fffffffu) : ~c);
 }
 
 constexpr int kRefineWaves = 2;   // tokens (waves) per workgroup: small LDS, high occupancy
 
+template <int NJ>   // keys per lane: E <= 64 * NJ
 __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const float* __restrict__ e_bias, const float* __restrict__ sb, int n, int H, int E, int topk,
@@ -449,10 +434,10 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
     }
     float* lrow = logits + (size_t)t * E;
     const float* srow = sb + (size_t)t * E;
-    uint32_t lo[kMaxPerLane];   // order codes of the lower bounds (0 = none / taken)
-    float up[kMaxPerLane];
+    uint32_t lo[NJ];   // order codes of the lower bounds (0 = none / taken)
+    float up[NJ];
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         const int e = lane + 64 * j;
         lo[j] = 0u;
         up[j] = -INFINITY;
@@ -469,27 +454,34 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
             }
         }
     }
-    // T = k-th largest lower bound.
+    // T = k-th largest lower bound (counted with multiplicity): each round
+    // takes the largest remaining code and drops all its copies, until k
+    // codes are covered.
     uint32_t tcode = 0u;
-    for (int k = 0; k < topk; ++k) {
-        uint32_t h = 0u, l = 0u;
+    int remaining = topk;
+    for (int k = 0; k < topk && remaining > 0; ++k) {
+        uint32_t m = lo[0];
 #pragma unroll
-        for (int j = 0; j < kMaxPerLane; ++j) kmax(h, l, lo[j], lo[j] ? ~(uint32_t)(lane + 64 * j) : 0u);
-        kmax_wave(h, l);
-        tcode = h;
-        const int e = (int)~l;
+        for (int j = 1; j < NJ; ++j) m = lo[j] > m ? lo[j] : m;
+        const uint32_t bh = wave_umax(m);
+        int c = 0;
 #pragma unroll
-        for (int j = 0; j < kMaxPerLane; ++j)
-            if (lane + 64 * j == e) lo[j] = 0u;
+        for (int j = 0; j < NJ; ++j) {
+            const bool hit = lo[j] == bh;
+            c += __builtin_popcountll(__ballot(hit));
+            lo[j] = hit ? 0u : lo[j];
+        }
+        tcode = bh;
+        remaining -= c;
     }
     const float T = tcode > 1u ? code_to_float(tcode) : -INFINITY;
     // Candidates in ascending expert order into this wave's LDS list; the rest
     // get -inf.
-    __shared__ int cl[kRefineWaves][64 * kMaxPerLane];
+    __shared__ int cl[kRefineWaves][64 * NJ];
     int* list = cl[threadIdx.x >> 6];
     int ncand = 0;
 #pragma unroll
-    for (int j = 0; j < kMaxPerLane; ++j) {
+    for (int j = 0; j < NJ; ++j) {
         const int e = lane + 64 * j;
         const bool cand = e < E && up[j] >= T;
         if (e < E && !cand) lrow[e] = -INFINITY;
@@ -832,7 +824,9 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(256), kMfmaD * 2 * kMfmaTok * 128, s, x,
                            wr, n, H, E, logits, scratch);
         if (hipGetLastError() != hipSuccess) return -4;
-        hipLaunchKernelGGL(router_refine_kernel, dim3((unsigned)((n + kRefineWaves - 1) / kRefineWaves)),
+        auto refine = E <= 64 ? router_refine_kernel<1> : E <= 128 ? router_refine_kernel<2>
+                                      : E <= 256 ? router_refine_kernel<4> : router_refine_kernel<8>;
+        hipLaunchKernelGGL(refine, dim3((unsigned)((n + kRefineWaves - 1) / kRefineWaves)),
                            dim3(kRefineWaves * 64), 0, s, x,
                            wr, e_bias, scratch, n, H, E, topk, logits, xsum);
         if (hipGetLastError() != hipSuccess) return -4;
