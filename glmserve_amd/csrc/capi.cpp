@@ -355,9 +355,10 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
         return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s, true, &fr);
     }
     bool dispatched = false;
+    // The large-group kernels do not read the activation group sums.
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
-                              L->routed_scale, v.logits, v.xsum, v.rpart, v.topk_ids, v.topk_w, s,
-                              &disp, &dispatched);
+                              L->routed_scale, v.logits, T == kBigRows ? nullptr : v.xsum, v.rpart,
+                              v.topk_ids, v.topk_w, s, &disp, &dispatched);
     if (rc) return rc;
     mark(GLMMOE_STAGE_ROUTER_TOPK, s);
     return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s, dispatched);
