@@ -780,9 +780,9 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
                 (void)hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev);
         }
         const int ntg = (n + kRouterTG - 1) / kRouterTG;
-        // (One token group: two experts per workgroup, half as many copies
-        // of the staged activations as one would take.)
-        int epw = ntg == 1 ? E / 128 : (E * ntg + cus - 1) / cus;
+        // (One token group included: one expert per workgroup at E = 256 on
+        // 256 CUs measured faster than two, 4.9 against 5.3 us at one token.)
+        int epw = (E * ntg + cus - 1) / cus;
         if (epw > kSmallThreads / nchunks) epw = kSmallThreads / nchunks;
         if (epw < 1) epw = 1;
         int slices = 1;
