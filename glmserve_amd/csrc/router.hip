@@ -328,10 +328,14 @@ __device__ __forceinline__ uint32_t mfma_tile_off(int r, int c) {
 // Stages (64 K of 64 token rows and 64 expert rows, 16 KiB) stream into a
 // kMfmaD-slot LDS ring by LDS-DMA: 4 DMAs per wave per stage, each 8 whole
 // 128-B rows (lane l: row l / 8, slot l % 8 holding chunk (l % 8) ^ swz(row)).
+// K split z of nsplit (blockIdx.z) covers stages [z nk / nsplit, (z + 1) nk
+// / nsplit) and writes its partial L~ to lt (z = 0) or lp + (z - 1) n E, its
+// partial S to sb + z n E.
 __global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __restrict__ x,
                                                           const uint16_t* __restrict__ wr, int n,
                                                           int H, int E, float* __restrict__ lt,
-                                                          float* __restrict__ sb) {
+                                                          float* __restrict__ sb, float* __restrict__ lp,
+                                                          int nsplit) {
     extern __shared__ __align__(16) char tl[];   // [kMfmaD][x | w][64 rows x 128 B]
     constexpr int kStage = 2 * kMfmaTok * 128;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -357,10 +361,11 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __rest
     };
     f32x16 accl = {}, accs = {};
     const int ar = tb * 32 + (lane & 31), br = eb * 32 + (lane & 31), hh = lane >> 5;
-    const int nk = H / kMfmaK;
+    const int nkt = H / kMfmaK, z = blockIdx.z;
+    const int k0 = (int)((long)nkt * z / nsplit), nk = (int)((long)nkt * (z + 1) / nsplit);
     for (int j = 0; j < kMfmaD - 1; ++j)
-        if (j < nk) issue(j);
-    for (int ks = 0; ks < nk; ++ks) {
+        if (k0 + j < nk) issue(k0 + j);
+    for (int ks = k0; ks < nk; ++ks) {
         if (ks + kMfmaD - 2 < nk) wait_vmcnt<4 * (kMfmaD - 2)>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();   // stage ks visible; stage ks - 1 free
@@ -387,12 +392,14 @@ __global__ __launch_bounds__(256) void router_mfma_kernel(const uint16_t* __rest
     }
     // D: lane -> expert column br, rows (tokens) 8 (i / 4) + 4 hh + i % 4 of the block.
     const int e = e0 + br;
+    float* lo = z == 0 ? lt : lp + (size_t)(z - 1) * n * E;
+    float* so = sb + (size_t)z * n * E;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int t = t0 + tb * 32 + 8 * (i >> 2) + 4 * hh + (i & 3);
         if (t < n && e < E) {
-            lt[(size_t)t * E + e] = accl[i];
-            sb[(size_t)t * E + e] = accs[i];
+            lo[(size_t)t * E + e] = accl[i];
+            so[(size_t)t * E + e] = accs[i];
         }
     }
 }
@@ -407,7 +414,7 @@ template <int NJ>   // keys per lane: E <= 64 * NJ
 __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const float* __restrict__ e_bias, const float* __restrict__ sb, int n, int H, int E, int topk,
-    float* __restrict__ logits, float* __restrict__ xsum) {
+    float* __restrict__ logits, float* __restrict__ xsum, int nsplit) {
     const int lane = threadIdx.x & 63;
     const int t = blockIdx.x * kRefineWaves + (threadIdx.x >> 6);
     if (t >= n) return;   // whole wave
@@ -442,8 +449,14 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
         lo[j] = 0u;
         up[j] = -INFINITY;
         if (e < E) {
-            const float l = lrow[e];
-            const float eps = srow[e] * 0x1p-11f;
+            // The K splits' partials, added in split order (any order keeps
+            // L~ a sum of the same exact products: the bound below holds).
+            float l = lrow[e], sabs = srow[e];
+            for (int z = 1; z < nsplit; ++z) {
+                l = l + sb[(size_t)nsplit * n * E + (size_t)(z - 1) * n * E + (size_t)t * E + e];
+                sabs = sabs + sb[(size_t)z * n * E + (size_t)t * E + e];
+            }
+            const float eps = sabs * 0x1p-11f;
             const float b = e_bias ? e_bias[e] : 0.0f;
             if (l != l || eps != eps) {
                 up[j] = INFINITY;    // always a candidate; never sets the threshold
@@ -754,10 +767,23 @@ bool router_small_path(int n, int H, int E, int topk) {
            E <= 64 * kMaxPerLane && topk <= 8;
 }
 
+// K splits of the MFMA router pass: enough (up to 8) that a batch of a few
+// hundred tokens still launches about 256 workgroups.
+int router_mfma_splits(int n, int E) {
+    const long tiles = (long)((E + kMfmaExp - 1) / kMfmaExp) * ((n + kMfmaTok - 1) / kMfmaTok);
+    int z = 1;
+    while (z < 8 && tiles * z * 2 <= 256) z *= 2;
+    return z;
+}
+
 size_t router_select_scratch_bytes(int n, int H, int E) {
     const size_t a = router_logits_scratch_bytes(n, H, E);
-    const size_t b = (size_t)n * E * 4;
-    return a > b ? a : b;
+    // The MFMA pass: S partials [nsplit][n][E], L~ partials of splits 1.. .
+    const int z = n >= kTiledMinTokens ? router_mfma_splits(n, E) : 1;
+    const size_t b = (size_t)(2 * z - 1) * n * E * 4;
+    const size_t c = (size_t)n * E * 4 * 2;   // small batches: order codes and scores
+    const size_t m = a > b ? a : b;
+    return m > c ? m : c;
 }
 
 int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_bias, int n, int H,
@@ -820,15 +846,17 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
     if (n >= kTiledMinTokens && H % kMfmaK == 0 && H % kRouterKC == 0 && nchunks <= 64 &&
         E <= 64 * kMaxPerLane) {
         if (!scratch) return -3;
-        dim3 grid((unsigned)((E + kMfmaExp - 1) / kMfmaExp), (unsigned)((n + kMfmaTok - 1) / kMfmaTok));
+        const int nsplit = router_mfma_splits(n, E);
+        dim3 grid((unsigned)((E + kMfmaExp - 1) / kMfmaExp), (unsigned)((n + kMfmaTok - 1) / kMfmaTok),
+                  (unsigned)nsplit);
         hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(256), kMfmaD * 2 * kMfmaTok * 128, s, x,
-                           wr, n, H, E, logits, scratch);
+                           wr, n, H, E, logits, scratch, scratch + (size_t)nsplit * n * E, nsplit);
         if (hipGetLastError() != hipSuccess) return -4;
         auto refine = E <= 64 ? router_refine_kernel<1> : E <= 128 ? router_refine_kernel<2>
                                       : E <= 256 ? router_refine_kernel<4> : router_refine_kernel<8>;
         hipLaunchKernelGGL(refine, dim3((unsigned)((n + kRefineWaves - 1) / kRefineWaves)),
                            dim3(kRefineWaves * 64), 0, s, x,
-                           wr, e_bias, scratch, n, H, E, topk, logits, xsum);
+                           wr, e_bias, scratch, n, H, E, topk, logits, xsum, nsplit);
         if (hipGetLastError() != hipSuccess) return -4;
     } else {
         const int rc = launch_router_logits(x, wr, n, H, E, logits, xsum, scratch, s);
