@@ -767,12 +767,14 @@ bool router_small_path(int n, int H, int E, int topk) {
            E <= 64 * kMaxPerLane && topk <= 8;
 }
 
-// K splits of the MFMA router pass: enough (up to 8) that a batch of a few
-// hundred tokens still launches about 256 workgroups.
+// K splits of the MFMA router pass: enough (up to 8) for about 512
+// workgroups, two per CU (a batch of a few hundred tokens has only a few
+// dozen 64 x 64 tiles; at 4096 tokens two splits measured 61 -> 46 us for
+// this pass, +4 us for the refinement's extra reads).
 int router_mfma_splits(int n, int E) {
     const long tiles = (long)((E + kMfmaExp - 1) / kMfmaExp) * ((n + kMfmaTok - 1) / kMfmaTok);
     int z = 1;
-    while (z < 8 && tiles * z * 2 <= 256) z *= 2;
+    while (z < 8 && tiles * z * 2 <= 512) z *= 2;
     return z;
 }
 
