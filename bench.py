@@ -60,10 +60,13 @@ def time_layer(L, n, steps, warmup, seed, torch):
     return ms, U, (x, ws, out)
 
 
-def time_layer_cold(L, n, reps, seed, torch):
+def time_layer_cold(L, n, reps, seed, torch, dirty=True):
     """Per-call time with the caches cold: before each timed call a 512 MiB
-    scrub buffer is rewritten (more than the 256 MiB of L2 + Infinity Cache),
-    so the weights come from HBM. Only the layer call is inside the events."""
+    scrub buffer (more than the 256 MiB of L2 + Infinity Cache) is rewritten
+    (dirty: the caches then hold modified lines, whose write-back competes
+    with the layer's reads) or read (clean: only evicted, as when the layers
+    before this one read their own weights), so the weights come from HBM.
+    Only the layer call is inside the events."""
     x = L.x(n, seed)
     ws = L.layer.alloc_workspace(n)
     out = torch.empty(n, H, dtype=torch.float32, device="cuda")
@@ -71,7 +74,10 @@ def time_layer_cold(L, n, reps, seed, torch):
     L.layer.forward(x, out, ws)
     total = 0.0
     for i in range(reps):
-        scrub.fill_(i & 0xFF)
+        if dirty:
+            scrub.fill_(i & 0xFF)
+        else:
+            scrub.view(torch.int64).sum()
         t0 = torch.cuda.Event(enable_timing=True)
         t1 = torch.cuda.Event(enable_timing=True)
         t0.record()
@@ -446,12 +452,17 @@ def main():
     if not args.no_sweep:
         for n in (1, 64):
             log(f"bench: sweep cold-cache B={n}")
-            ms = time_layer_cold(L, n, 10, 100 + n, torch)
             hot = sweep[f"decode_B{n}"]
-            sweep[f"decode_B{n}_cold"] = {
-                "n": n, "ms": ms, "tokens_per_s": n / (ms * 1e-3),
-                "hbm_frac_layer": hot["alg_bytes"] / (ms * 1e-3) / HBM_PEAK,
-                "note": "512 MiB scrub rewritten before each timed call (L2 and Infinity Cache cold)"}
+            for dirty in (False, True):
+                ms = time_layer_cold(L, n, 10, 100 + n, torch, dirty=dirty)
+                sweep[f"decode_B{n}_cold" + ("_dirty" if dirty else "")] = {
+                    "n": n, "ms": ms, "tokens_per_s": n / (ms * 1e-3),
+                    "hbm_frac_layer": hot["alg_bytes"] / (ms * 1e-3) / HBM_PEAK,
+                    "note": ("512 MiB scrub rewritten before each timed call: L2 and Infinity Cache "
+                             "cold and full of modified lines, whose write-back competes with the "
+                             "layer's reads") if dirty else
+                            ("512 MiB scrub read before each timed call: L2 and Infinity Cache cold "
+                             "(evicted, clean), as after layers that read their own weights")}
     if not args.no_sweep:
         log("bench: sweep spec-verify 520 (configs[3], Zipf s=1.1 skew)")
         LZ = SynthLayer(H, E, K, I, seed=2, zipf_s=1.1)
