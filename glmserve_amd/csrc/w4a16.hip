@@ -612,6 +612,48 @@ __device__ __forceinline__ void fused_route(const FusedRoute r, int E, bool lead
                                 sids + t * r.topk);
     }
     __syncthreads();
+    if (r.n == 1) {
+        // One token: its topk ids are distinct experts, one row each, so an
+        // expert's offset and tile index are its rank among the ids (the
+        // outputs dispatch_small gives, without its histogram and scan).
+        const int K = r.topk, sh = r.disp.with_shared;
+        const int t = threadIdx.x;
+        if (t < K) {
+            const int e = sids[t];
+            int rank = 0;
+            for (int k = 0; k < K; ++k) rank += sids[k] < e ? 1 : 0;
+            tiles[rank] = make_int4(e, rank, 1, 0);
+            tok[rank] = 0;
+            if (lead) {
+                r.disp.tiles[rank] = make_int4(e, rank, 1, 0);
+                r.disp.sorted_tok[rank] = 0;
+                r.disp.sorted_slot[rank] = t;
+                r.disp.inv[t] = rank;
+            }
+        } else if (t == K) {
+            if (sh) {
+                tiles[K] = make_int4(E, K, 1, 0);
+                tok[K] = 0;
+            }
+            nt[0] = nt[1] = nt[2] = K + sh;
+            if (lead) {
+                if (sh) {
+                    r.disp.tiles[K] = make_int4(E, K, 1, 0);
+                    r.disp.sorted_tok[K] = 0;
+                    r.disp.sorted_slot[K] = -1;
+                }
+                r.disp.ntiles[0] = r.disp.ntiles[1] = r.disp.ntiles[2] = K + sh;
+                r.disp.offsets[E + 1] = K + sh;
+            }
+        }
+        if (lead)
+            for (int e = t; e <= E; e += 512) {
+                int below = 0;
+                for (int k = 0; k < K; ++k) below += sids[k] < e ? 1 : 0;
+                r.disp.offsets[e] = below;
+            }
+        return;
+    }
     dispatch_small<512>(sids, r.n, r.topk, E, r.disp.with_shared, tiles, nt, tok, r.disp, lead, hist,
                         pre);
 }
