@@ -49,7 +49,7 @@ int glmmoe_moe_layer_w4a16_noalloc(const glmmoe_w4a16_layer* L, const uint16_t* 
     const int rc = scratch_ptr(&ws);
     if (rc) return rc;
     // Every field of the workspace is written by the call before it is read
-    // (the expert kernels' tickets are cleared by its dispatch kernel), so
-    // the previous call's contents do not matter.
+    // (the expert kernels' tickets are cleared by its router or dispatch
+    // kernel), so the previous call's contents do not matter.
     return glmmoe_moe_layer_w4a16(L, x, n, out, ws, kScratchBytes, stream);
 }
