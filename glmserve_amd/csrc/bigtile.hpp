@@ -89,6 +89,38 @@ __device__ __forceinline__ void big_fill_table(const int4* tiles, const int* row
     }
 }
 
+// Expert-major item order (tile lists in expert order, every tile full-class):
+// the items of expert e are ids [f nfg, (f + m) nfg) for its m tiles from tile
+// f, and id f nfg + i is feature group i / m of tile f + i % m. So the m tiles
+// of one (expert, feature group) are neighbours in the id order, run at the
+// same time on one XCD and read the group's weights into its L2 once; the
+// tile's nfg feature groups stay within m nfg neighbouring ids.
+template <bool GATHER>
+__device__ __forceinline__ void big_fill_table_em(const int4* tiles, const int* rows_tok, int* table,
+                                                  long k0, int cnt, int nfg) {
+    for (int i = threadIdx.x; i < cnt * kBigTabInts; i += blockDim.x) {
+        const int k = i / kBigTabInts, f = i % kBigTabInts;
+        const long item = big_item_id(k0 + k);
+        const long t0 = item / nfg;
+        const int w = tiles[t0].w;
+        const int j = w & 0xffff, m = max(w >> 16, 1);
+        const long first = t0 - j;
+        const long local = item - first * nfg;
+        const int4 tile = tiles[first + local % m];
+        int v;
+        if (f == 0) v = tile.x;
+        else if (f == 1) v = tile.y;
+        else if (f == 2) v = tile.z;
+        else if (f == 3) v = (int)(local / m);
+        else {
+            const int row = f - 4;
+            const int rr = row < tile.z ? row : 0;
+            v = GATHER ? rows_tok[tile.y + rr] : tile.y + rr;
+        }
+        table[i] = v;
+    }
+}
+
 // Items of a tile list with half tiles (W4A16 kernels): the first n128 tiles
 // take nfg 128-row items each, the half tiles after them nfg / 2 64-row items
 // (each twice as many features wide).

@@ -171,7 +171,9 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
         }
 
     // Tile list: expert e (e == E is the shared expert) contributes
-    // ceil(count / d.tile_rows) tiles of at most d.tile_rows consecutive rows.
+    // ceil(count / d.tile_rows) tiles of at most d.tile_rows consecutive rows,
+    // {e, first row, rows, j | m << 16}: tile j of the expert's m consecutive
+    // (full-class) tiles; the half and quarter tiles carry 0 there.
     // With d.half_rows = HR > 0 an expert's last partial tile is classed by
     // its rows: at most HR / 2 ("quarter"), at most HR ("half"), or more
     // (full). The list holds the full tiles first (ntiles[1] of them), then
@@ -210,7 +212,7 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
         const int row0 = e < E ? cursor[e] - ce : total;  // cursor ended at offset + count
         const int tbase = pre[e];
         for (int j = 0; j < ntl[e]; ++j)
-            d.tiles[tbase + j] = make_int4(e, row0 + j * T, min(T, ce - j * T), 0);
+            d.tiles[tbase + j] = make_int4(e, row0 + j * T, min(T, ce - j * T), j | (ntl[e] << 16));
         const int full = ce / T;
         if (nhalf[e]) d.tiles[pre[nexp] + prehalf[e]] = make_int4(e, row0 + full * T, ce - full * T, 0);
         if (nq[e])

@@ -252,74 +252,77 @@ __device__ __forceinline__ void f8_issue(const F8Args& a, const F8Issue& p, int 
     dma4(wave < 3 ? p.sc + kg : p.sc, sdst);
 }
 
-// Operands a wave reads from one ring slot: its two weight blocks (4 chunk
-// rows each), its two 32-row activation blocks (4 chunks each: K step s,
-// half h, 16-B piece q at chunk 4 s + 2 h + q), the activation scales of its
-// rows and the weight block scales.
-struct F8Ops {
-    u32x4 aw[2][4];
-    u32x4 bx[2][4];
-    float xs[2], ws[2];
+// Operands a wave reads from one ring slot for one 64-K half (K step s) of a
+// group: chunk rows 2 s, 2 s + 1 of its two weight blocks and, of its two
+// 32-row activation blocks, chunks 4 s + 2 h + {0, 1} (K step s, half h,
+// 16-B piece q at chunk 4 s + 2 h + q). Row R = wm * 64 + tb * 32 + col
+// (tb = 1 is 32 rows = 4 KiB further, same swizzle); chunk c at slot
+// c ^ swz(R).
+struct F8Half {
+    u32x4 aw[2][2];
+    u32x4 bx[2][2];
 };
 
-__device__ __forceinline__ void f8_load_ops(const char* slot, int wave, int lane, int nmat,
-                                            F8Ops& o) {
+template <int S>
+__device__ __forceinline__ void f8_load_half(const char* slot, int wave, int lane, F8Half& o) {
     using RG = F8Ring;
     const int wn = wave >> 1, wm = wave & 1;
     const int col = lane & 31, h = lane >> 5;
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
         const uint32_t wa = lds_addr(slot + (wn * 2 + jb) * 4096) + (uint32_t)(lane * 16);
-        asm volatile(
-            "ds_read_b128 %0, %4\n ds_read_b128 %1, %4 offset:1024\n"
-            " ds_read_b128 %2, %4 offset:2048\n ds_read_b128 %3, %4 offset:3072"
-            : "=&v"(o.aw[jb][0]), "=&v"(o.aw[jb][1]), "=&v"(o.aw[jb][2]), "=&v"(o.aw[jb][3])
-            : "v"(wa));
+        asm volatile("ds_read_b128 %0, %2 offset:%3\n ds_read_b128 %1, %2 offset:%4"
+                     : "=&v"(o.aw[jb][0]), "=&v"(o.aw[jb][1])
+                     : "v"(wa), "n"(2048 * S), "n"(2048 * S + 1024));
     }
-    // Row R = wm*64 + tb*32 + col (tb = 1 is 32 rows = 4 KiB further, same
-    // swizzle); chunk c = 4 s + 2 h + q at slot c ^ swz(R).
     const int R = wm * 64 + col;
     const uint32_t xr = lds_addr(slot + RG::kXOff) + (uint32_t)(R * 128);
     const int f = RG::swz(R);
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
-#pragma unroll
-        for (int q = 0; q < 2; ++q) {
-            const uint32_t xa = xr + (uint32_t)((((4 * s + 2 * h + q) ^ f)) * 16);
-            asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:4096"
-                         : "=&v"(o.bx[0][2 * s + q]), "=&v"(o.bx[1][2 * s + q]) : "v"(xa));
-        }
+    for (int q = 0; q < 2; ++q) {
+        const uint32_t xa = xr + (uint32_t)((((4 * S + 2 * h + q) ^ f)) * 16);
+        asm volatile("ds_read_b128 %0, %2\n ds_read_b128 %1, %2 offset:4096"
+                     : "=&v"(o.bx[0][q]), "=&v"(o.bx[1][q]) : "v"(xa));
+    }
+}
+
+// The activation scales of the wave's rows and the weight block scales.
+__device__ __forceinline__ void f8_load_scales(const char* slot, int wave, int lane, int nmat, float (&xs)[2],
+                                               float (&ws)[2]) {
+    using RG = F8Ring;
+    const int wn = wave >> 1, wm = wave & 1;
+    const int R = wm * 64 + (lane & 31);
     const uint32_t sa = lds_addr(slot + RG::kSOff) + (uint32_t)(R * 4);
-    asm volatile("ds_read_b32 %0, %2\n ds_read_b32 %1, %2 offset:128"
-                 : "=&v"(o.xs[0]), "=&v"(o.xs[1]) : "v"(sa));
+    asm volatile("ds_read_b32 %0, %2\n ds_read_b32 %1, %2 offset:128" : "=&v"(xs[0]), "=&v"(xs[1]) : "v"(sa));
 #pragma unroll
     for (int jb = 0; jb < 2; ++jb) {
         const int idx = nmat == 2 ? jb : (wn >> 1);
         const uint32_t wa = lds_addr(slot + RG::kWSOff) + (uint32_t)(idx * 4);
-        asm volatile("ds_read_b32 %0, %1" : "=&v"(o.ws[jb]) : "v"(wa));
+        asm volatile("ds_read_b32 %0, %1" : "=&v"(ws[jb]) : "v"(wa));
     }
 }
 
-__device__ __forceinline__ void f8_wait_ops(F8Ops& o) {
+__device__ __forceinline__ void f8_wait_half(F8Half& o) {
     asm volatile("s_waitcnt lgkmcnt(0)"
-                 : "+v"(o.aw[0][0]), "+v"(o.aw[0][1]), "+v"(o.aw[0][2]), "+v"(o.aw[0][3]),
-                   "+v"(o.aw[1][0]), "+v"(o.aw[1][1]), "+v"(o.aw[1][2]), "+v"(o.aw[1][3]),
-                   "+v"(o.bx[0][0]), "+v"(o.bx[0][1]), "+v"(o.bx[0][2]), "+v"(o.bx[0][3]),
-                   "+v"(o.bx[1][0]), "+v"(o.bx[1][1]), "+v"(o.bx[1][2]), "+v"(o.bx[1][3]),
-                   "+v"(o.xs[0]), "+v"(o.xs[1]), "+v"(o.ws[0]), "+v"(o.ws[1]));
+                 : "+v"(o.aw[0][0]), "+v"(o.aw[0][1]), "+v"(o.aw[1][0]), "+v"(o.aw[1][1]),
+                   "+v"(o.bx[0][0]), "+v"(o.bx[0][1]), "+v"(o.bx[1][0]), "+v"(o.bx[1][1]));
+}
+__device__ __forceinline__ void f8_wait_half(F8Half& o, float (&xs)[2], float (&ws)[2]) {
+    asm volatile("s_waitcnt lgkmcnt(0)"
+                 : "+v"(o.aw[0][0]), "+v"(o.aw[0][1]), "+v"(o.aw[1][0]), "+v"(o.aw[1][1]),
+                   "+v"(o.bx[0][0]), "+v"(o.bx[0][1]), "+v"(o.bx[1][0]), "+v"(o.bx[1][1]),
+                   "+v"(xs[0]), "+v"(xs[1]), "+v"(ws[0]), "+v"(ws[1]));
 }
 
-// One 128-K group: p = the two 64-K MFMA products per 32 x 32 block.
-__device__ __forceinline__ void f8_compute(const F8Ops& o, f32x16 (&p)[2][2]) {
+// K step S of a group: p = A . B over the half's 64 K (S = 0 from zero).
+template <int S>
+__device__ __forceinline__ void f8_mfma_half(const F8Half& o, f32x16 (&p)[2][2]) {
 #pragma unroll
-    for (int s = 0; s < 2; ++s)
+    for (int jb = 0; jb < 2; ++jb)
 #pragma unroll
-        for (int jb = 0; jb < 2; ++jb)
-#pragma unroll
-            for (int tb = 0; tb < 2; ++tb)
-                p[jb][tb] = mfma_f8_32x32x64(cat8(o.aw[jb][2 * s], o.aw[jb][2 * s + 1]),
-                                             cat8(o.bx[tb][2 * s], o.bx[tb][2 * s + 1]),
-                                             s == 0 ? f32x16{} : p[jb][tb]);
+        for (int tb = 0; tb < 2; ++tb)
+            p[jb][tb] = mfma_f8_32x32x64(cat8(o.aw[jb][0], o.aw[jb][1]), cat8(o.bx[tb][0], o.bx[tb][1]),
+                                         S == 0 ? f32x16{} : p[jb][tb]);
 }
 
 // acc += (w_scale * x_scale) * p.
@@ -420,7 +423,7 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
 
     for (int k0 = 0; k0 < nitems; k0 += kBigTable) {
         const int cnt = min(kBigTable, nitems - k0);
-        big_fill_table<NMAT == 2>(a.tiles, a.rows_tok, table, k0, cnt, nfg);
+        big_fill_table_em<NMAT == 2>(a.tiles, a.rows_tok, table, k0, cnt, nfg);
         __syncthreads();
         const int nsteps = cnt * KG;
 
@@ -444,9 +447,13 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
         else if (nsteps == 2) wait_vmcnt<RG::kDma>();
         else wait_vmcnt<0>();
         __builtin_amdgcn_s_barrier();
-        F8Ops ops;
-        f8_load_ops(lds, wave, lane, NMAT, ops);
-        f8_wait_ops(ops);
+        // Operands by 64-K half: h0 (K step 0) of the current group, h1 (K
+        // step 1); its scales in xs / ws, the next group's in nxs / nws.
+        F8Half h0, h1;
+        float xs[2], ws[2], nxs[2], nws[2];
+        f8_load_half<0>(lds, wave, lane, h0);
+        f8_load_scales(lds, wave, lane, NMAT, xs, ws);
+        f8_wait_half(h0, xs, ws);
 
         int cur_k = 0, cur_g = 0;
         BigItem cur = big_item(lds + RG::kTab, 0);
@@ -459,16 +466,28 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
             for (int tb = 0; tb < 2; ++tb) acc[jb][tb] = f32x16{};
 
         for (int step = 0; step < nsteps; ++step) {
+            // Half 1's reads go out under half 0's MFMAs; after the barrier
+            // the next group's half 0 (and scales) under half 1's MFMAs and
+            // this group's rescale. Every wave has its reads of slot g in
+            // (waited before the barrier) when slot g is refilled.
+            const char* slot = lds + (step % kF8D) * RG::kSlot;
             f32x16 p[2][2];
-            if (live) f8_compute(ops, p);
+            f8_load_half<1>(slot, wave, lane, h1);
+            if (live) f8_mfma_half<0>(h0, p);
+            f8_wait_half(h1);
             if (step + 2 < nsteps) wait_vmcnt<RG::kDma>();
             else wait_vmcnt<0>();
             __builtin_amdgcn_s_barrier();
             if (step + kF8D < nsteps) issue_next(step + kF8D);
-            const float xs[2] = {ops.xs[0], ops.xs[1]};
-            const float ws[2] = {ops.ws[0], ops.ws[1]};
-            if (step + 1 < nsteps) f8_load_ops(lds + ((step + 1) % kF8D) * RG::kSlot, wave, lane, NMAT, ops);
-            if (live) f8_rescale(xs, ws, p, acc);
+            if (step + 1 < nsteps) {
+                const char* nslot = lds + ((step + 1) % kF8D) * RG::kSlot;
+                f8_load_half<0>(nslot, wave, lane, h0);
+                f8_load_scales(nslot, wave, lane, NMAT, nxs, nws);
+            }
+            if (live) {
+                f8_mfma_half<1>(h1, p);
+                f8_rescale(xs, ws, p, acc);
+            }
             if (++cur_g == KG) {
                 f8_epilogue<NMAT>(a, cur, lds, wave, lane, acc);
 #pragma unroll
@@ -481,10 +500,15 @@ __global__ __launch_bounds__(512) void fp8_big_kernel(F8Args a) {
                     live = cur.nr > wm * 64;
                 }
             }
-            // Last in the iteration: the next step's operands have arrived before
-            // anything (including copies the compiler makes for the loop) reads
-            // their registers.
-            f8_wait_ops(ops);
+            // Last in the iteration: the next group's operands have arrived
+            // before anything (including copies the compiler makes for the
+            // loop) reads their registers.
+            f8_wait_half(h0, nxs, nws);
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                xs[i] = nxs[i];
+                ws[i] = nws[i];
+            }
         }
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         __syncthreads();

@@ -144,7 +144,8 @@ typedef struct glmmoe_layer_ws {
     int* sorted_token_ids;/* [R] */
     int* sorted_row;      /* [R] slot, -1 for shared rows */
     int* inv;             /* [n*topk]: grouped row of (t, s) */
-    int* tiles;           /* [max_tiles * 4]: {expert, row0, nrows, 0} */
+    int* tiles;           /* [max_tiles * 4]: {expert, row0, nrows, j | m << 16} (tile j of
+                             the expert's m full tiles; 0 for the half tiles) */
     int* ntiles;          /* [2]: tiles; tiles before the half tiles (128-row layout) */
     uint16_t* h;          /* [R, I] bf16 SiLU(gate) * up */
     float* hsum;          /* [R, I/128] group sums of h (large-group path) */
