@@ -197,7 +197,7 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     const bool nt = n >= kStreamWeightsMinTokens;
     mark(GLMMOE_STAGE_GATE_UP, s);
     rc = big ? launch_gate_up_big(P, x, n, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.dpart,
-                                  H, I, E, s)
+                                  dpart_bytes(L, n), v.sync, H, I, E, s)
              : launch_gate_up(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.hsum,
                               v.sync, v.dpart, dpart_bytes(L, n), H, I, E, s, fr, nt);
     if (rc) return rc;

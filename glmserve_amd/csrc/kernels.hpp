@@ -118,7 +118,8 @@ bool big_w4_shape_ok(int H, int I);
 // (at least n * H * 2 + n * 4 bytes, free until down) and writes h as fp16.
 int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int* tiles,
                        const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
-                       void* scratch, int H, int I, int E, hipStream_t s);
+                       void* scratch, size_t scratch_bytes, unsigned int* tick, int H, int I, int E,
+                       hipStream_t s);
 int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
                     int max_tiles, float* dpart, int H, int I, int E, hipStream_t s);
 // bf16: the partial rows are bf16 (written by the large-group kernels).

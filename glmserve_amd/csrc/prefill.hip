@@ -68,8 +68,14 @@ struct MmArgs {
     const int4* tiles; const int* ntiles; const int* rows_tok;
     uint16_t* h;              // gate/up output: fp16 [R, I]
     uint16_t* dout;           // down output: bf16 [R, H]
+    // Split last round (gate/up): the items of a short last round run as two
+    // K halves each; partials [item][half][wave][128][64] fp32, a ticket per
+    // item (zero at launch). part null: no split.
+    unsigned int* tick; float* part; int pcap;
     int H, I, E;
 };
+
+constexpr int kMmPartFloats = 8 * 128 * 64;   // one half item's accumulators
 
 namespace mm {
 constexpr int kRowB = 272;                     // LDS bytes per activation row (256 + 16 padding)
@@ -161,19 +167,22 @@ template <int NMAT, bool ACT = true>
 __device__ __forceinline__ MmPtrs mm_ptrs(const MmArgs& a, const BigItem& it, int K, int KG, int wave,
                                           int lane) {
     MmPtrs p;
+    // A half item (hs 1 or 2: the first or second half of K) starts its
+    // streams at batch kb0.
+    const int kb0 = (it.hs & 3) == 2 ? K / 2048 : 0;
 #pragma unroll
-    for (int i = 0; i < 5; ++i) p.act[i] = ACT ? mm_act(it.tab, K, wave, lane, i) : 0u;
+    for (int i = 0; i < 5; ++i) p.act[i] = ACT ? mm_act(it.tab, K, wave, lane, i) + (uint32_t)kb0 * 2048u : 0u;
     const int frows = NMAT == 2 ? a.I : a.H;
 #pragma unroll
     for (int cb = 0; cb < 2; ++cb) {
         const int m = NMAT == 2 ? cb : 0;
         const int fb = NMAT == 2 ? 16 * it.g : 32 * it.g + 2 * cb;
-        p.wb[cb] = mm_wbase<NMAT>(a, it.e, m, frows, KG) + (size_t)fb * KG * 1024;
+        p.wb[cb] = mm_wbase<NMAT>(a, it.e, m, frows, KG) + (size_t)fb * KG * 1024 + (size_t)kb0 * 8192;
     }
     {
         const int m = NMAT == 2 ? (wave >> 2) : 0;
         const int fb = NMAT == 2 ? 16 * it.g : 32 * it.g;
-        p.sb = mm_sbase<NMAT>(a, it.e, m, frows, KG) + (size_t)fb * KG * 16;
+        p.sb = mm_sbase<NMAT>(a, it.e, m, frows, KG) + (size_t)fb * KG * 16 + (size_t)kb0 * 128;
     }
     return p;
 }
@@ -346,7 +355,27 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
     // last tile of 33-64 rows [nt4, nt2), then of at most 32 rows [nt2, nt):
     // 4, 2 and 1 live 32-row blocks.
     const int nt = a.ntiles[0], nt4 = a.ntiles[1], nt2 = a.ntiles[2];
-    const long nitems = big_rounds((long)nt * nfg);
+    // Items round-robin over the workgroups; a short last round (at most
+    // half the workgroups busy) runs as two K halves per item on two
+    // neighbouring workgroups, so it takes half as long.
+    const long total = (long)nt * nfg;
+    const int nb = gridDim.x;
+    const long R = (total + nb - 1) / nb;
+    const long rem = total - (R - 1) * nb;
+    const bool split = NMAT == 2 && a.part != nullptr && R >= 1 && 2 * rem <= nb && rem <= a.pcap &&
+                       rem <= kTailTicks && NB % 2 == 0;
+    const int lir = (nb % 8 == 0) ? (blockIdx.x % 8) * (nb / 8) + blockIdx.x / 8 : blockIdx.x;   // big_item_id's slot
+    const long nitems = split ? (R - 1) + (lir < 2 * rem ? 1 : 0) : big_rounds(total);
+    // Item id of round k and its table tag: 0 whole, 1 / 2 first / second
+    // half, with the half item's index (for its ticket and partials) above.
+    auto ident = [&](long k, int& tag) -> long {
+        if (split && k == R - 1) {
+            tag = (1 + (lir & 1)) | ((lir >> 1) << 2);
+            return (R - 1) * nb + (lir >> 1);
+        }
+        tag = 0;
+        return big_item_id(k);
+    };
     const uint32_t ring = lds_addr(lds);
     // Lane's fragment address at step 0 of row block 0 in slot 0: row col,
     // 16-B chunk 8 h; step s adds 16 s, row block rb 8704 rb, slot q 34 KiB q.
@@ -360,14 +389,33 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
     const MmLane ml = mm_lane<NMAT>(KG, wave, lane);
 
     auto cls_of = [&](long k) {
-        const long t = big_item_id(k) / nfg;
-        return t < nt4 ? 4 : t < nt2 ? 2 : 1;
+        int tag;
+        const long t = ident(k, tag) / nfg;
+        return (t < nt4 ? 4 : t < nt2 ? 2 : 1) + (tag ? 8 : 0);
     };
     // One chunk (at most kTabItems items of one class): table, prologue,
     // stream, drain. The accumulators live only inside it.
-    auto run_chunk = [&](auto NRB_, long k0, int cnt) {
+    auto run_chunk = [&](auto NRB_, long k0, int cnt, bool halves) {
         constexpr int NRB = decltype(NRB_)::value;
-        big_fill_table<NMAT == 2>(a.tiles, a.rows_tok, table, k0, cnt, nfg);
+        // Table rows (big_fill_table's layout; the tag in the high bits of
+        // the feature-group word).
+        for (int i = threadIdx.x; i < cnt * kBigTabInts; i += blockDim.x) {
+            const int k = i / kBigTabInts, f = i % kBigTabInts;
+            int tag;
+            const long id = ident(k0 + k, tag);
+            const int4 tile = a.tiles[id / nfg];
+            int v;
+            if (f == 0) v = tile.x;
+            else if (f == 1) v = tile.y;
+            else if (f == 2) v = tile.z;
+            else if (f == 3) v = (int)(id % nfg) | (tag << 16);
+            else {
+                const int row = f - 4;
+                const int rr = row < tile.z ? row : 0;
+                v = NMAT == 2 ? a.rows_tok[tile.y + rr] : tile.y + rr;
+            }
+            table[i] = v;
+        }
         __syncthreads();
         if constexpr (NMAT == 2) {
             float* rho = reinterpret_cast<float*>(lds + mm::kRho);
@@ -375,7 +423,8 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
                 rho[i] = a.rho[table[(i / kBigRows) * kBigTabInts + 4 + (i % kBigRows)]];
             __syncthreads();
         }
-        const int NBt = cnt * NB;        // batches of this chunk
+        const int NBi = halves ? NB / 2 : NB;   // batches per item
+        const int NBt = cnt * NBi;              // batches of this chunk
         auto item = [&](int k) { return big_item(lds + mm::kTab, k < cnt ? k : cnt - 1); };
 
         // Stream state of the item of the current batch (pc) and of the next
@@ -436,7 +485,7 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
         int ib = 0, kb = 0;   // item and batch-in-item of the current batch
 
         for (int b = 0; b < NBt; ++b) {
-            const bool last = kb == NB - 1;
+            const bool last = kb == NBi - 1;
             static_for<8>([&](auto J) {
                 constexpr int j = decltype(J)::value;
                 // ---- group start: publish slot g + 1, free slot g - 1. Pending
@@ -528,8 +577,42 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
                 // Staging for the stores: this batch's scale buffer, read for
                 // the last time in this batch's group 6 (the next batch's scale
                 // DMA into it is issued after the next group-start barrier).
-                mm_epilogue<NMAT>(a, item(ib), lds_addr(lds + mm::kRho + ib * kBigRows * 4),
-                                  lds_addr(lds + mm::kSBuf + (b & 1) * 8192 + wave * 1024), wave, lane, acc);
+                bool store = true;
+                if constexpr (NMAT == 2) {
+                    if (halves) {
+                        // Half item: store the partials, take the item's
+                        // ticket; the second to arrive adds the other half
+                        // (a + b, the same sum either way) and stores.
+                        const int tag = item(ib).hs, half = (tag & 3) - 1, pi = tag >> 2;
+                        float* dst = a.part + ((size_t)(pi * 2 + half) * 8 + wave) * 8192 + lane;
+#pragma unroll
+                        for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                            for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                                for (int i = 0; i < 16; ++i) st_dev(dst + ((rb * 2 + cb) * 16 + i) * 64, acc[rb][cb][i]);
+                        drain_vm();
+                        __syncthreads();
+                        int* flag = table + (mm::kTabItems - 1) * kBigTabInts;
+                        if (threadIdx.x == 0) *flag = ticket_dev(&a.tick[pi]) == 1u ? 1 : 0;
+                        __syncthreads();
+                        store = *flag != 0;
+                        __syncthreads();
+                        if (store) {
+                            const float* src = a.part + ((size_t)(pi * 2 + (1 - half)) * 8 + wave) * 8192 + lane;
+#pragma unroll
+                            for (int rb = 0; rb < 4; ++rb)
+#pragma unroll
+                                for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+                                    for (int i = 0; i < 16; ++i)
+                                        acc[rb][cb][i] = acc[rb][cb][i] + ld_dev(src + ((rb * 2 + cb) * 16 + i) * 64);
+                        }
+                    }
+                }
+                if (store)
+                    mm_epilogue<NMAT>(a, item(ib), lds_addr(lds + mm::kRho + ib * kBigRows * 4),
+                                      lds_addr(lds + mm::kSBuf + (b & 1) * 8192 + wave * 1024), wave, lane, acc);
 #pragma unroll
                 for (int rb = 0; rb < 4; ++rb) acc[rb][0] = acc[rb][1] = f32x16{};
                 ++ib;
@@ -547,10 +630,11 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
     for (long k0 = 0; k0 < nitems;) {
         const int cls = cls_of(k0);
         int cnt = 1;
-        while (cnt < mm::kTabItems && k0 + cnt < nitems && cls_of(k0 + cnt) == cls) ++cnt;
-        if (cls == 4) run_chunk(std::integral_constant<int, 4>{}, k0, cnt);
-        else if (cls == 2) run_chunk(std::integral_constant<int, 2>{}, k0, cnt);
-        else run_chunk(std::integral_constant<int, 1>{}, k0, cnt);
+        while (cnt < mm::kTabItems - 1 && k0 + cnt < nitems && cls_of(k0 + cnt) == cls) ++cnt;
+        const bool halves = cls >= 8;
+        if ((cls & 7) == 4) run_chunk(std::integral_constant<int, 4>{}, k0, cnt, halves);
+        else if ((cls & 7) == 2) run_chunk(std::integral_constant<int, 2>{}, k0, cnt, halves);
+        else run_chunk(std::integral_constant<int, 1>{}, k0, cnt, halves);
         k0 += cnt;
     }
 }
@@ -618,11 +702,13 @@ __global__ __launch_bounds__(256) void f16_rows_kernel(const uint16_t* __restric
 
 bool big_w4_shape_ok(int H, int I) { return H % 1024 == 0 && I % 1024 == 0; }
 
-// scratch: the dpart region (free until the down projection): xh [n, H] fp16
-// then rho [n] fp32.
+// scratch: the dpart region (free until the down projection, scratch_bytes):
+// xh [n, H] fp16, rho [n] fp32, then the split last round's partials; tick:
+// its tickets (kTailTicks, zero at launch).
 int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int* tiles,
                        const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
-                       void* scratch, int H, int I, int E, hipStream_t s) {
+                       void* scratch, size_t scratch_bytes, unsigned int* tick, int H, int I, int E,
+                       hipStream_t s) {
     if (!big_w4_shape_ok(H, I)) return -2;
     uint16_t* xh = reinterpret_cast<uint16_t*>(scratch);
     float* rho = reinterpret_cast<float*>(xh + (size_t)n * H);
@@ -633,6 +719,14 @@ int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int*
     a.swq[0] = P.sh_gate_q; a.sws[0] = P.sh_gate_s; a.swq[1] = P.sh_up_q; a.sws[1] = P.sh_up_s;
     a.src = xh; a.rho = rho; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.rows_tok = rows_tok; a.h = h; a.H = H; a.I = I; a.E = E;
+    // The split last round's partials after xh and rho (two halves per item).
+    const size_t off = ((size_t)n * H * 2 + (size_t)n * 4 + 255) / 256 * 256;
+    if (tick && scratch_bytes > off) {
+        const size_t cap = (scratch_bytes - off) / ((size_t)2 * kMmPartFloats * 4);
+        a.tick = tick;
+        a.part = reinterpret_cast<float*>(reinterpret_cast<char*>(scratch) + off);
+        a.pcap = (int)(cap < (size_t)kTailTicks ? cap : (size_t)kTailTicks);
+    }
     return launch_mm<2>(a, (long)max_tiles * (I / 256), s);
 }
 
