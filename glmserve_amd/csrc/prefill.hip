@@ -351,10 +351,10 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
     const int KG = K / 128;          // a multiple of 8 (checked by the launcher)
     const int NB = KG / 8;           // batches per item
     const int nfg = NMAT == 2 ? a.I / 256 : a.H / 512;
-    // Tile classes (dispatch order): full tiles [0, nt4), then each expert's
-    // last tile of 33-64 rows [nt4, nt2), then of at most 32 rows [nt2, nt):
-    // 4, 2 and 1 live 32-row blocks.
-    const int nt = a.ntiles[0], nt4 = a.ntiles[1], nt2 = a.ntiles[2];
+    // Tile classes by rows: more than 64, 33-64, at most 32 rows: 4, 2 and 1
+    // live 32-row blocks (the dispatch lists them in that order, so a
+    // workgroup's items run class by class in few chunks).
+    const int nt = a.ntiles[0];
     // Items round-robin over the workgroups; a short last round (at most
     // half the workgroups busy) runs as two K halves per item on two
     // neighbouring workgroups, so it takes half as long.
@@ -390,8 +390,8 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
 
     auto cls_of = [&](long k) {
         int tag;
-        const long t = ident(k, tag) / nfg;
-        return (t < nt4 ? 4 : t < nt2 ? 2 : 1) + (tag ? 8 : 0);
+        const int nr = a.tiles[ident(k, tag) / nfg].z;
+        return (nr > 64 ? 4 : nr > 32 ? 2 : 1) + (tag ? 8 : 0);
     };
     // One chunk (at most kTabItems items of one class): table, prologue,
     // stream, drain. The accumulators live only inside it.
