@@ -1165,6 +1165,47 @@ __global__ __launch_bounds__(256) void combine_kernel(const float* __restrict__ 
     reinterpret_cast<float4*>(out + (size_t)t * H)[f4] = acc;
 }
 
+// The bf16 partial rows of the large-group kernels, topk <= 8: 8 features
+// (16 B of each row) per thread, every row's load issued before the adds.
+// The same per-element operations in the same order as combine_kernel.
+__global__ __launch_bounds__(256) void combine_bf16x8_kernel(const uint16_t* __restrict__ dpart,
+                                                             const int* __restrict__ inv,
+                                                             const float* __restrict__ w, int n,
+                                                             int topk, int H, int with_shared,
+                                                             float* __restrict__ out) {
+    const int t = blockIdx.y;
+    const int f8 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (f8 * 8 >= H) return;
+    uint4 v[9];
+    float ws[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+        if (s < topk) {
+            ws[s] = w[(size_t)t * topk + s];
+            v[s] = reinterpret_cast<const uint4*>(dpart + (size_t)inv[(size_t)t * topk + s] * H)[f8];
+        }
+    }
+    if (with_shared) v[8] = reinterpret_cast<const uint4*>(dpart + ((size_t)n * topk + t) * H)[f8];
+    auto el = [](const uint4& r, int q) {
+        const uint32_t d = q < 2 ? r.x : q < 4 ? r.y : q < 6 ? r.z : r.w;
+        return (q & 1) ? __uint_as_float(d & 0xffff0000u) : bf16_to_f32(d & 0xffffu);
+    };
+    float acc[8];
+#pragma unroll
+    for (int q = 0; q < 8; ++q) acc[q] = 0.0f;
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+        if (s < topk)
+#pragma unroll
+            for (int q = 0; q < 8; ++q) acc[q] = acc[q] + ws[s] * el(v[s], q);
+    if (with_shared)
+#pragma unroll
+        for (int q = 0; q < 8; ++q) acc[q] = acc[q] + el(v[8], q);
+    float4* o = reinterpret_cast<float4*>(out + (size_t)t * H) + 2 * f8;
+    o[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
+    o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+}
+
 // ---------------------------------------------------------------------------
 // Ring depth and batch size per projection (one 8-wave workgroup per CU).
 constexpr int kRingGU = 3;
@@ -1245,6 +1286,12 @@ int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const
 
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
                    int with_shared, float* out, hipStream_t s, bool bf16) {
+    if (bf16 && topk <= 8 && H % 8 == 0) {
+        hipLaunchKernelGGL(combine_bf16x8_kernel, dim3((unsigned)((H / 8 + 255) / 256), (unsigned)n),
+                           dim3(256), 0, s, reinterpret_cast<const uint16_t*>(dpart), inv, w, n, topk,
+                           H, with_shared, out);
+        return hipGetLastError() == hipSuccess ? 0 : -4;
+    }
     dim3 grid((unsigned)((H / 4 + 255) / 256), (unsigned)n);
     if (bf16)
         hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, s, dpart, inv, w, n, topk, H,
