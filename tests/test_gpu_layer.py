@@ -215,6 +215,19 @@ def test_decode_poisoned_workspace_deterministic(full_layer):
         assert torch.equal(outs[0], outs[1]), n
 
 
+@pytest.mark.parametrize("n", [300, 600])
+def test_large_group_other_shape(oracle, n):
+    # The large-group kernels at a second legal shape (H and I multiples of
+    # 1024): 2048 -> 1024 with 32 experts, top-4 (n * 5 >= 1024 grouped rows).
+    # The down items are a single 8-group batch; gate/up items have two, so a
+    # short last round splits them into one-batch halves. Every token against
+    # the oracle.
+    L = SynthLayer(2048, 32, 4, 1024, seed=9)
+    x, out, logits, ids, w, offs, st, sr = _run(L, n, seed=21 + n)
+    ref_logits = _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
+    _check_full(out, oracle_full_w4(L, oracle, x, ids, w))
+
+
 def test_split_last_round_deterministic():
     # Large-group batches whose gate/up last round runs as two K halves per
     # item (partials and a ticket per item; whichever half arrives second adds
