@@ -73,9 +73,10 @@ def _run(L, n, seed):
     return x, out, ws, logits, ids, w, offs, st, sr
 
 
-@pytest.mark.parametrize("n", [1, 7, 64, 300])
+@pytest.mark.parametrize("n", [1, 7, 64, 300, 1500])
 def test_fp8_tiny(oracle, n):
-    # configs[0] geometry with FP8 experts.
+    # configs[0] geometry with FP8 experts; at 1500 tokens every expert has
+    # several 128-row tiles, which run in expert-major item order.
     L = SynthFp8Layer(256, 16, 4, 128, seed=12)
     x, out, ws, logits, ids, w, offs, st, sr = _run(L, n, seed=8)
     ref_logits = _check_routing(oracle, L, x, logits, ids, w, offs, st, sr)
