@@ -36,7 +36,7 @@ int max_tiles_for(int n, int topk, int E, int with_shared, int H, int I) {
 // Shape and pointer checks shared by the W4A16 and FP8 layer descriptors.
 template <class Layer>
 int check_layer(const Layer* L, int n) {
-    if (!L || n <= 0) return GLMMOE_ERR_ARG;
+    if (!L || n < 0) return GLMMOE_ERR_ARG;
     if (L->hidden <= 0 || L->moe_inter <= 0 || L->n_experts <= 0 || L->topk <= 0)
         return GLMMOE_ERR_ARG;
     if (L->hidden % 256 || L->moe_inter % 128 || L->hidden > 8192) return GLMMOE_ERR_SHAPE;
@@ -196,13 +196,17 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     // them) outgrow the 256 MiB Infinity Cache: stream them past L2.
     const bool nt = n >= kStreamWeightsMinTokens;
     mark(GLMMOE_STAGE_GATE_UP, s);
-    rc = big ? launch_gate_up_big(P, x, n, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.dpart,
+    // The large-group path keeps h's block exponents where the decode
+    // kernels keep h's group sums (I / 32 bytes per row either way).
+    int8_t* hexp = reinterpret_cast<int8_t*>(v.hsum);
+    const int R = n * k + sh * n;
+    rc = big ? launch_gate_up_big(P, x, n, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, hexp, v.dpart,
                                   dpart_bytes(L, n), v.sync, H, I, E, s)
              : launch_gate_up(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.hsum,
                               v.sync, v.dpart, dpart_bytes(L, n), H, I, E, s, fr, nt);
     if (rc) return rc;
     mark(GLMMOE_STAGE_DOWN, s);
-    rc = big ? launch_down_big(P, v.h, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
+    rc = big ? launch_down_big(P, v.h, hexp, R, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s)
              : launch_down(P, v.h, v.hsum, v.tiles, v.ntiles, mt, v.dpart, H, I, E, s, nt);
     if (rc) return rc;
     mark(GLMMOE_STAGE_COMBINE, s);
@@ -250,13 +254,14 @@ extern "C" {
 const char* glmmoe_version(void) { return "glmmoe 0.1 (gfx950)"; }
 
 size_t glmmoe_router_logits_workspace_bytes(int n, int H, int E) {
-    if (n <= 0 || H <= 0 || E <= 0) return 0;
+    if (n <= 0 || H <= 0 || E <= 0) return 0;   // n == 0: no workspace needed
     return router_logits_scratch_bytes(n, H, E);
 }
 
 int glmmoe_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, int E,
                          float* logits, float* xsum, void* workspace, size_t workspace_bytes,
                          void* stream) {
+    if (n == 0 && H > 0 && E > 0) return GLMMOE_OK;
     if (!x || !wr || !logits || n <= 0 || H <= 0 || E <= 0) return GLMMOE_ERR_ARG;
     if (H % 8 || H > 8192) return GLMMOE_ERR_SHAPE;
     if (xsum && H % 128) return GLMMOE_ERR_SHAPE;
@@ -268,6 +273,7 @@ int glmmoe_router_logits(const uint16_t* x, const uint16_t* wr, int n, int H, in
 
 int glmmoe_router_logits_f32(const float* x, const float* W, const float* bias, float* y,
                              int64_t n, int64_t in, int64_t out, void* stream) {
+    if (n == 0 && in > 0 && out > 0) return GLMMOE_OK;
     if (!x || !W || !y || n <= 0 || in <= 0 || out <= 0) return GLMMOE_ERR_ARG;
     if (in % 128 || in > 8192 || n > (1 << 30) || out > (1 << 20)) return GLMMOE_ERR_SHAPE;
     return launch_router_logits_f32(x, W, bias, y, (int)n, (int)in, (int)out, S(stream)) ? GLMMOE_ERR_LAUNCH
@@ -277,6 +283,7 @@ int glmmoe_router_logits_f32(const float* x, const float* W, const float* bias, 
 int glmmoe_moe_router(const float* logits, const float* e_bias, int n, int E, int topk,
                       int norm_topk, float routed_scale, int* topk_ids, float* topk_weights,
                       void* stream) {
+    if (n == 0 && E > 0 && topk > 0) return GLMMOE_OK;
     if (!logits || !topk_ids || !topk_weights || n <= 0 || E <= 0 || topk <= 0)
         return GLMMOE_ERR_ARG;
     if (topk > 8 || topk > E || E > 512) return GLMMOE_ERR_SHAPE;
@@ -286,9 +293,10 @@ int glmmoe_moe_router(const float* logits, const float* e_bias, int n, int E, in
 
 int glmmoe_moe_dispatch(const int* topk_ids, int n, int topk, int E, int* expert_offsets,
                         int* sorted_token_ids, int* sorted_row, void* stream) {
-    if (!topk_ids || !expert_offsets || !sorted_token_ids || !sorted_row || n <= 0 ||
-        topk <= 0 || E <= 0)
-        return GLMMOE_ERR_ARG;
+    // n == 0 still writes expert_offsets (all zero), as the reference's
+    // kernel does (cuda/moe_dispatch.cu:23-26).
+    if (!expert_offsets || n < 0 || topk <= 0 || E <= 0) return GLMMOE_ERR_ARG;
+    if (n > 0 && (!topk_ids || !sorted_token_ids || !sorted_row)) return GLMMOE_ERR_ARG;
     if (E > 512 || (long)n * topk > (1L << 24)) return GLMMOE_ERR_SHAPE;
     return launch_dispatch(topk_ids, n, topk, E, expert_offsets, sorted_token_ids, sorted_row,
                            nullptr, nullptr, nullptr, kTileRows, 0, 0, S(stream));
@@ -323,18 +331,28 @@ int glmmoe_layer_workspace_view(const glmmoe_w4a16_layer* L, int n, void* worksp
     return GLMMOE_OK;
 }
 
-int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, float* out,
-                           void* workspace, size_t workspace_bytes, void* stream) {
-    int rc = check_layer(L, n);
-    if (rc) return rc;
-    if (!x || !out || !workspace || !L->router_w) return GLMMOE_ERR_ARG;
-    glmmoe_layer_ws v;
-    if (carve(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)
-        return GLMMOE_ERR_WORKSPACE;
-    hipStream_t s = S(stream);
+}  // extern "C"
+
+namespace {
+
+// The MoE branch on a carved workspace. xf (fp32 activations) non-null: the
+// bf16 rows x are written to xb first -- by the router kernel of the
+// small-batch path as it stages them, otherwise by one conversion launch --
+// and x is ignored.
+int layer_w4(const glmmoe_w4a16_layer* L, const uint16_t* x, const float* xf, uint16_t* xb, int n,
+             float* out, const glmmoe_layer_ws& v, hipStream_t s) {
+    int rc = 0;
     const int H = L->hidden, E = L->n_experts, k = L->topk;
     begin_call();
     mark(GLMMOE_STAGE_ROUTER_LOGITS, s);
+    if (xf) {
+        if (!router_small_path(n, H, E, k)) {
+            rc = launch_f32_to_bf16(xf, xb, (long)n * H, s);
+            if (rc) return GLMMOE_ERR_LAUNCH;
+            xf = nullptr;
+        }
+        x = xb;
+    }
     // The router pass also writes the activation group sums the expert
     // kernels use to remove the int4 decode offset.
     const int sh = has_shared(L) ? 1 : 0;
@@ -347,7 +365,7 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     if (T == kTileRows && router_small_path(n, H, E, k) && fused_route_ok(n, k, E, H)) {
         rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
                                   L->routed_scale, v.logits, v.xsum, v.rpart, v.topk_ids, v.topk_w,
-                                  s, &disp, nullptr, false);
+                                  s, &disp, nullptr, false, xf, xb);
         if (rc) return rc;
         mark(GLMMOE_STAGE_ROUTER_TOPK, s);
         const FusedRoute fr{reinterpret_cast<const uint32_t*>(v.rpart), n, k, L->norm_topk,
@@ -358,10 +376,44 @@ int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
     // The large-group kernels do not read the activation group sums.
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
                               L->routed_scale, v.logits, T == kBigRows ? nullptr : v.xsum, v.rpart,
-                              v.topk_ids, v.topk_w, s, &disp, &dispatched);
+                              v.topk_ids, v.topk_w, s, &disp, &dispatched, true, xf, xb);
     if (rc) return rc;
     mark(GLMMOE_STAGE_ROUTER_TOPK, s);
     return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s, dispatched);
+}
+
+}  // namespace
+
+extern "C" {
+
+int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, float* out,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_layer(L, n);
+    if (rc) return rc;
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
+    if (!x || !out || !workspace || !L->router_w) return GLMMOE_ERR_ARG;
+    glmmoe_layer_ws v;
+    if (carve(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)
+        return GLMMOE_ERR_WORKSPACE;
+    return layer_w4(L, x, nullptr, nullptr, n, out, v, S(stream));
+}
+
+size_t glmmoe_layer_f32_workspace_bytes(const glmmoe_w4a16_layer* L, int n) {
+    if (check_layer(L, n)) return 0;
+    return carve(L, n, nullptr, nullptr) + align256((size_t)n * L->hidden * 2);
+}
+
+int glmmoe_moe_layer_w4a16_f32(const glmmoe_w4a16_layer* L, const float* x, int n, float* out,
+                               void* workspace, size_t workspace_bytes, void* stream) {
+    int rc = check_layer(L, n);
+    if (rc) return rc;
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
+    if (!x || !out || !workspace || !L->router_w) return GLMMOE_ERR_ARG;
+    glmmoe_layer_ws v;
+    const size_t lb = carve(L, n, static_cast<char*>(workspace), &v);
+    if (lb + align256((size_t)n * L->hidden * 2) > workspace_bytes) return GLMMOE_ERR_WORKSPACE;
+    uint16_t* xb = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + lb);
+    return layer_w4(L, nullptr, x, xb, n, out, v, S(stream));
 }
 
 int glmmoe_moe_route_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n,
@@ -369,6 +421,7 @@ int glmmoe_moe_route_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n
                            size_t workspace_bytes, void* stream) {
     int rc = check_layer(L, n);
     if (rc) return rc;
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!x || !topk_ids || !topk_w || !workspace || !L->router_w) return GLMMOE_ERR_ARG;
     glmmoe_layer_ws v;
     if (carve(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)
@@ -383,6 +436,7 @@ int glmmoe_expert_ffn_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int 
                             void* workspace, size_t workspace_bytes, void* stream) {
     int rc = check_layer(L, n);
     if (rc) return rc;
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!x || !out || !workspace || !topk_ids || !topk_w) return GLMMOE_ERR_ARG;
     glmmoe_layer_ws v;
     if (carve(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)
@@ -411,6 +465,7 @@ int glmmoe_pack_fp8(const uint8_t* w, int n_mats, int rows, int K, uint8_t* pack
 
 int glmmoe_quant_act_fp8(const uint16_t* x, int n, int K, uint8_t* q, float* scale,
                          void* stream) {
+    if (n == 0 && K > 0) return GLMMOE_OK;
     if (!x || !q || !scale || n <= 0 || K <= 0) return GLMMOE_ERR_ARG;
     if (K % 128) return GLMMOE_ERR_SHAPE;
     return launch_quant_act_fp8(x, n, K, q, scale, S(stream));
@@ -434,6 +489,7 @@ int glmmoe_moe_layer_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n, fl
                          void* workspace, size_t workspace_bytes, void* stream) {
     int rc = check_layer(L, n);
     if (rc) return rc;
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!x || !out || !workspace || !L->router_w) return GLMMOE_ERR_ARG;
     glmmoe_fp8_ws v;
     if (carve8(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)
@@ -459,6 +515,7 @@ int glmmoe_expert_ffn_fp8(const glmmoe_fp8_layer* L, const uint16_t* x, int n,
                           void* workspace, size_t workspace_bytes, void* stream) {
     int rc = check_layer(L, n);
     if (rc) return rc;
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!x || !out || !workspace || !topk_ids || !topk_w) return GLMMOE_ERR_ARG;
     glmmoe_fp8_ws v;
     if (carve8(L, n, static_cast<char*>(workspace), &v) > workspace_bytes)

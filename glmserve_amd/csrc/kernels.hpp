@@ -66,7 +66,10 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
                          int E, int topk, int norm_topk, float routed_scale, float* logits,
                          float* xsum, float* scratch, int* ids, float* w, hipStream_t s,
                          const DispOut* disp = nullptr, bool* dispatched = nullptr,
-                         bool select = true);
+                         bool select = true, const float* xf = nullptr, uint16_t* xb = nullptr);
+// xf (small-batch path only): fp32 activations [n, H], rounded to bf16 as the
+// router stages them; the rounded rows are written to xb ([n, H]) and x is
+// not read.
 // The small-batch router path (router_small_kernel) applies to this shape.
 // With select == false launch_router_select then only writes the logits, the
 // order codes and scores ([2][n][E] in scratch) and xsum, and zeroes
@@ -115,13 +118,16 @@ int launch_down(const ExpertPtrs& P, const uint16_t* h, const float* hsum, const
 // Shapes the large-group W4A16 kernels take: H / 128 and I / 128 multiples of 8.
 bool big_w4_shape_ok(int H, int I);
 // Large-group kernels (fp16 MFMA). gate/up converts x to fp16 rows in scratch
-// (at least n * H * 2 + n * 4 bytes, free until down) and writes h as fp16.
+// (at least n * H * 2 + n * 4 bytes, free until down) and writes h as fp16
+// rows with a power-of-2 exponent per 32-feature block in hexp ([R, I / 32]
+// bytes); down first brings each of the R rows to one exponent, then undoes it.
 int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int* tiles,
                        const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
-                       void* scratch, size_t scratch_bytes, unsigned int* tick, int H, int I, int E,
-                       hipStream_t s);
-int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
-                    int max_tiles, float* dpart, int H, int I, int E, hipStream_t s);
+                       int8_t* hexp, void* scratch, size_t scratch_bytes, unsigned int* tick, int H,
+                       int I, int E, hipStream_t s);
+int launch_down_big(const ExpertPtrs& P, uint16_t* h, int8_t* hexp, int R, const int* tiles,
+                    const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
+                    hipStream_t s);
 // bf16: the partial rows are bf16 (written by the large-group kernels).
 int launch_combine(const float* dpart, const int* inv, const float* w, int n, int topk, int H,
                    int with_shared, float* out, hipStream_t s, bool bf16 = false);

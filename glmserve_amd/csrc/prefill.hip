@@ -23,11 +23,19 @@
 // whose inputs 2s and 24s are exact in fp16 (s is a bf16 scale: 8
 // significant bits) rounds only the result. So the accumulators need no
 // per-group rescale and no offset correction: acc += A . B directly, fp32.
+// The scales enter the decode multiplied by 2^kWPre (exact), so scales from
+// 2^-(15 + kWPre) to 2729 * 2^-kWPre decode without fp16 subnormals or
+// overflow; the epilogues undo the factor.
 // Activations: gate/up reads x converted to fp16 with a per-row power-of-2
 // scale (f16_rows_kernel below; exact for any finite bf16 row) and undoes the
 // scale on its outputs; down reads the fp16 h this gate/up wrote. fp16 keeps
-// 11 significant bits (bf16 keeps 8); the intermediate h must stay within
-// fp16's range (|h| <= 65504; beyond it h becomes inf and so does the output).
+// 11 significant bits (bf16 keeps 8) but only 5 exponent bits, so h is stored
+// with a power-of-2 exponent per row: the gate/up epilogue picks one per
+// (row, 32 features) by a monotone rule of the block's largest |h|
+// (h_exp_rule), h_rescale_kernel brings every block of a row to the row's
+// smallest exponent (the rule of the row's largest |h|), and the down
+// epilogue undoes it per row. Any finite h then reaches down in fp16 normal
+// range: no overflow to inf, no row flushed to subnormals.
 //
 // Streams, per 128-K group g:
 // - activations: 128 rows x 256 B (gathered by token for gate/up) global ->
@@ -66,7 +74,9 @@ struct MmArgs {
     const uint16_t* src;      // fp16: xh [n, H] (gate/up, rows gathered by token) or h [R, I] (down)
     const float* rho;         // gate/up: per-token factor undoing xh's row scale
     const int4* tiles; const int* ntiles; const int* rows_tok;
-    uint16_t* h;              // gate/up output: fp16 [R, I]
+    uint16_t* h;              // gate/up output: fp16 [R, I], row r scaled by 2^e(r)
+    int8_t* hexp;             // [R, I / 32] exponents of h's 32-feature blocks (after
+                              // h_rescale_kernel: every block of a row holds e(r))
     uint16_t* dout;           // down output: bf16 [R, H]
     // Split last round (gate/up): the items of a short last round run as two
     // K halves each; partials [item][half][wave][128][64] fp32, a ticket per
@@ -76,6 +86,33 @@ struct MmArgs {
 };
 
 constexpr int kMmPartFloats = 8 * 128 * 64;   // one half item's accumulators
+constexpr int kWPre = 8;                       // log2 of the weight scales' decode factor
+constexpr int kHExpNone = 127;                 // exponent of an all-zero block: no constraint
+
+// Exponent e for a block whose largest |h| has fp32 bits m: 0 while
+// 2^-6 <= |h| < 2^15 (fp16's normal range with 11 significant bits to spare
+// below); outside that band the block's largest |h| * 2^e lands in
+// [2^14, 2^15). Non-increasing in m, so the smallest e over a row's blocks is
+// the rule of the row's largest |h|.
+__device__ __forceinline__ int h_exp_rule(uint32_t m) {
+    if (m == 0) return kHExpNone;
+    const int e2 = (int)(m >> 23) - 127;   // inf / NaN: 128
+    if (e2 >= 15 || e2 < -6) {
+        const int e = 14 - e2;
+        return e > 126 ? 126 : e;
+    }
+    return 0;
+}
+
+// Maximum of v over the 32 lanes of the wave's half that holds this lane.
+__device__ __forceinline__ uint32_t max_half_wave(uint32_t v) {
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0xB1, 0xF, 0xF, false));   // quad xor 1
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x4E, 0xF, 0xF, false));   // quad xor 2
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x124, 0xF, 0xF, false));  // row_ror 4
+    v = max(v, (uint32_t)__builtin_amdgcn_update_dpp(0, (int)v, 0x128, 0xF, 0xF, false));  // row_ror 8
+    v = max(v, (uint32_t)__builtin_amdgcn_ds_swizzle((int)v, 0x401F));                    // lane xor 16
+    return v;
+}
 
 namespace mm {
 constexpr int kRowB = 272;                     // LDS bytes per activation row (256 + 16 padding)
@@ -261,10 +298,12 @@ __device__ __forceinline__ bf16x8 dq_f16(uint32_t w, const DqF16& k, f16x2 s2, f
     return __builtin_bit_cast(bf16x8, r);
 }
 
-// {2s, 2s} and {-24s, -24s} in fp16 from a bf16 scale pattern (exact).
+// {2s, 2s} and {-24s, -24s} times 2^kWPre in fp16 from a bf16 scale pattern
+// (exact for scales in 2^-(15 + kWPre) .. 2729 * 2^-kWPre).
 __device__ __forceinline__ void scale_pair(uint32_t sbits, f16x2& s2, f16x2& s24) {
     const float s = bf16_to_f32(sbits & 0xffffu);
-    const _Float16 a = (_Float16)(2.0f * s), b = (_Float16)(-24.0f * s);
+    constexpr float kPre = (float)(1 << kWPre);
+    const _Float16 a = (_Float16)((2.0f * kPre) * s), b = (_Float16)((-24.0f * kPre) * s);
     s2 = f16x2{a, a};
     s24 = f16x2{b, b};
 }
@@ -286,8 +325,10 @@ __device__ __forceinline__ void mm_epilogue(const MmArgs& a, const BigItem& cur,
     const int col = ln & 31, h = ln >> 5;
     if constexpr (NMAT == 2) {
         // h = silu(g) * u of this lane's feature (rows' scale undone first);
-        // a round is 16 rows x this wave's 32 features of fp16.
+        // a round is 16 rows x this wave's 32 features of fp16, each row
+        // scaled by 2^e of its largest |h| among those features.
         uint16_t* hbase = a.h + (size_t)cur.r0 * a.I + cur.g * 256 + wave * 32 + (ln & 3) * 8;
+        int8_t* ebase = a.hexp + (size_t)cur.r0 * (a.I / 32) + cur.g * 8 + wave;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb) {
             float rr[16];   // row factors of the lane's 16 rows of block rb
@@ -301,14 +342,25 @@ __device__ __forceinline__ void mm_epilogue(const MmArgs& a, const BigItem& cur,
             }
 #pragma unroll
             for (int half = 0; half < 2; ++half) {
+                float hf[8];
+                uint32_t mx[8];
 #pragma unroll
                 for (int ii = 0; ii < 8; ++ii) {
                     const int i = half * 8 + ii;
                     const float gt = acc[rb][0][i] * rr[i], up = acc[rb][1][i] * rr[i];
-                    const uint16_t hv = __builtin_bit_cast(uint16_t, (_Float16)(silu_fast(gt) * up));
+                    hf[ii] = silu_fast(gt) * up;
+                    mx[ii] = max_half_wave(__float_as_uint(hf[ii]) & 0x7fffffffu);
+                }
+#pragma unroll
+                for (int ii = 0; ii < 8; ++ii) {
+                    const int e = h_exp_rule(mx[ii]);
+                    const float hs = __builtin_ldexpf(hf[ii], e == kHExpNone ? 0 : e);
+                    const uint16_t hv = __builtin_bit_cast(uint16_t, (_Float16)hs);
                     const int rl = 8 * (ii >> 2) + 4 * h + (ii & 3);   // row within the round
                     asm volatile("ds_write_b16 %0, %1" : : "v"(stg + (uint32_t)(rl * 64 + col * 2)), "v"((uint32_t)hv)
                                  : "memory");
+                    const int row = rb * 32 + half * 16 + rl;
+                    if (col == 0 && row < cur.nr) ebase[(size_t)row * (a.I / 32)] = (int8_t)e;
                 }
                 const uint4 v = lds_bcast16(stg + (uint32_t)(ln * 16));
                 const int row = rb * 32 + half * 16 + (ln >> 2);
@@ -316,18 +368,22 @@ __device__ __forceinline__ void mm_epilogue(const MmArgs& a, const BigItem& cur,
             }
         }
     } else {
-        // Per-row expert outputs as bf16 (the combine adds them in fp32); a
-        // round is 8 rows x this wave's 64 features.
+        // Per-row expert outputs as bf16 (the combine adds them in fp32), h's
+        // row exponent and the weight factor undone (rho: the rows' factors);
+        // a round is 8 rows x this wave's 64 features.
         uint16_t* dbase = a.dout + (size_t)cur.r0 * a.H + cur.g * 512 + wave * 64 + (ln & 7) * 8;
 #pragma unroll
         for (int rb = 0; rb < 4; ++rb)
 #pragma unroll
             for (int q = 0; q < 4; ++q) {
+                const uint4 fv = lds_bcast16(rho + (uint32_t)((rb * 32 + 8 * q + 4 * h) * 4));
+                const float rf[4] = {__uint_as_float(fv.x), __uint_as_float(fv.y), __uint_as_float(fv.z),
+                                     __uint_as_float(fv.w)};
 #pragma unroll
                 for (int cb = 0; cb < 2; ++cb)
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
-                        const uint32_t bv = pack_bf16x2(acc[rb][cb][4 * q + e], 0.0f) & 0xffffu;
+                        const uint32_t bv = pack_bf16x2(acc[rb][cb][4 * q + e] * rf[e], 0.0f) & 0xffffu;
                         asm volatile("ds_write_b16 %0, %1"
                                      : : "v"(stg + (uint32_t)((4 * h + e) * 128 + (32 * cb + col) * 2)), "v"(bv)
                                      : "memory");
@@ -417,10 +473,16 @@ __global__ __launch_bounds__(512) void w4_mm_kernel(MmArgs a) {
             table[i] = v;
         }
         __syncthreads();
-        if constexpr (NMAT == 2) {
+        {
+            // Row factors: gate/up x's row scale and the weight factor
+            // (f16_rows_kernel folds both into rho); down h's row exponent
+            // and the weight factor.
             float* rho = reinterpret_cast<float*>(lds + mm::kRho);
-            for (int i = threadIdx.x; i < cnt * kBigRows; i += blockDim.x)
-                rho[i] = a.rho[table[(i / kBigRows) * kBigTabInts + 4 + (i % kBigRows)]];
+            for (int i = threadIdx.x; i < cnt * kBigRows; i += blockDim.x) {
+                const int row = table[(i / kBigRows) * kBigTabInts + 4 + (i % kBigRows)];
+                if constexpr (NMAT == 2) rho[i] = a.rho[row];
+                else rho[i] = __builtin_ldexpf(1.0f, -((int)a.hexp[(size_t)row * (a.I / 32)] + kWPre));
+            }
             __syncthreads();
         }
         const int NBi = halves ? NB / 2 : NB;   // batches per item
@@ -660,8 +722,8 @@ static int launch_mm(const MmArgs& a, long max_items, hipStream_t s) {
 // x (bf16) -> fp16 with a power-of-2 scale per row so the row's largest
 // magnitude lies in [2^14, 2^15): exact for every finite bf16 row down to
 // 2^-10 of the row maximum (bf16's 8 significant bits fit fp16's 11; smaller
-// elements round to fp16's subnormal steps). rho[t] = the inverse factor,
-// applied to the row's outputs. One wave per row.
+// elements round to fp16's subnormal steps). rho[t] = the inverse factor
+// times 2^-kWPre, applied to the row's outputs. One wave per row.
 __global__ __launch_bounds__(256) void f16_rows_kernel(const uint16_t* __restrict__ x, int n, int H,
                                                       uint16_t* __restrict__ xh, float* __restrict__ rho) {
     const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
@@ -684,7 +746,7 @@ __global__ __launch_bounds__(256) void f16_rows_kernel(const uint16_t* __restric
     int k = 14 - e;                       // max * 2^k in [2^14, 2^15)
     k = k > 100 ? 100 : (k < -100 ? -100 : k);
     const float scale = __builtin_ldexpf(1.0f, k);
-    if (lane == 0) rho[t] = __builtin_ldexpf(1.0f, -k);
+    if (lane == 0) rho[t] = __builtin_ldexpf(1.0f, -k - kWPre);   // also undoes the weights' factor
     uint16_t* yr = xh + (size_t)t * H;
     for (int i = lane * 8; i < H; i += 512) {
         const uint4 v = *reinterpret_cast<const uint4*>(xr + i);
@@ -700,6 +762,46 @@ __global__ __launch_bounds__(256) void f16_rows_kernel(const uint16_t* __restric
     }
 }
 
+// Brings every 32-feature block of an h row to the row's smallest block
+// exponent (h_exp_rule is non-increasing, so that is the rule of the row's
+// largest |h|): blocks with a larger exponent are multiplied by 2^(e_row - e)
+// (exact unless the result is an fp16 subnormal, i.e. below 2^-24 of the
+// row's largest |h| once scaled). One wave per row; every block byte then
+// holds e_row. Blocks already at e_row (every block of every row whose |h|
+// stays in the band) are only read.
+__global__ __launch_bounds__(256) void h_rescale_kernel(uint16_t* __restrict__ h, int8_t* __restrict__ hexp, int R,
+                                                       int I) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= R) return;
+    const int nb = I / 32;
+    int8_t* er = hexp + (size_t)r * nb;
+    int emin = kHExpNone;
+    for (int b = lane; b < nb; b += 64) emin = min(emin, (int)er[b]);
+#pragma unroll
+    for (int off = 32; off > 0; off >>= 1) emin = min(emin, __shfl_xor(emin, off));
+    for (int b = lane; b < nb; b += 64) {
+        const int e = er[b];
+        if (e != emin) {
+            uint4* p = reinterpret_cast<uint4*>(h + (size_t)r * I + b * 32);
+            for (int q = 0; q < 4; ++q) {
+                const uint4 v = p[q];
+                uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    const float lo = __builtin_ldexpf((float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffffu)),
+                                                      emin - e);
+                    const float hi = __builtin_ldexpf((float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16)),
+                                                      emin - e);
+                    w[j] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+                }
+                p[q] = make_uint4(w[0], w[1], w[2], w[3]);
+            }
+            er[b] = (int8_t)emin;
+        }
+    }
+}
+
 bool big_w4_shape_ok(int H, int I) { return H % 1024 == 0 && I % 1024 == 0; }
 
 // scratch: the dpart region (free until the down projection, scratch_bytes):
@@ -707,8 +809,8 @@ bool big_w4_shape_ok(int H, int I) { return H % 1024 == 0 && I % 1024 == 0; }
 // its tickets (kTailTicks, zero at launch).
 int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int* tiles,
                        const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
-                       void* scratch, size_t scratch_bytes, unsigned int* tick, int H, int I, int E,
-                       hipStream_t s) {
+                       int8_t* hexp, void* scratch, size_t scratch_bytes, unsigned int* tick, int H,
+                       int I, int E, hipStream_t s) {
     if (!big_w4_shape_ok(H, I)) return -2;
     uint16_t* xh = reinterpret_cast<uint16_t*>(scratch);
     float* rho = reinterpret_cast<float*>(xh + (size_t)n * H);
@@ -718,7 +820,7 @@ int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int*
     a.wq[0] = P.gate_q; a.ws[0] = P.gate_s; a.wq[1] = P.up_q; a.ws[1] = P.up_s;
     a.swq[0] = P.sh_gate_q; a.sws[0] = P.sh_gate_s; a.swq[1] = P.sh_up_q; a.sws[1] = P.sh_up_s;
     a.src = xh; a.rho = rho; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
-    a.rows_tok = rows_tok; a.h = h; a.H = H; a.I = I; a.E = E;
+    a.rows_tok = rows_tok; a.h = h; a.hexp = hexp; a.H = H; a.I = I; a.E = E;
     // The split last round's partials after xh and rho (two halves per item).
     const size_t off = ((size_t)n * H * 2 + (size_t)n * 4 + 255) / 256 * 256;
     if (tick && scratch_bytes > off) {
@@ -730,13 +832,16 @@ int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int*
     return launch_mm<2>(a, (long)max_tiles * (I / 256), s);
 }
 
-int launch_down_big(const ExpertPtrs& P, const uint16_t* h, const int* tiles, const int* ntiles,
-                    int max_tiles, float* dpart, int H, int I, int E, hipStream_t s) {
+int launch_down_big(const ExpertPtrs& P, uint16_t* h, int8_t* hexp, int R, const int* tiles,
+                    const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
+                    hipStream_t s) {
     if (!big_w4_shape_ok(H, I)) return -2;
+    hipLaunchKernelGGL(h_rescale_kernel, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, s, h, hexp, R, I);
+    if (hipGetLastError() != hipSuccess) return -4;
     MmArgs a{};
     a.wq[0] = P.down_q; a.ws[0] = P.down_s; a.wq[1] = P.down_q; a.ws[1] = P.down_s;
     a.swq[0] = P.sh_down_q; a.sws[0] = P.sh_down_s; a.swq[1] = P.sh_down_q; a.sws[1] = P.sh_down_s;
-    a.src = h; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
+    a.src = h; a.hexp = hexp; a.tiles = reinterpret_cast<const int4*>(tiles); a.ntiles = ntiles;
     a.dout = reinterpret_cast<uint16_t*>(dpart); a.H = H; a.I = I; a.E = E;
     return launch_mm<1>(a, (long)max_tiles * (H / 512), s);
 }

@@ -145,10 +145,17 @@ typedef struct glmmoe_layer_ws {
     int* sorted_row;      /* [R] slot, -1 for shared rows */
     int* inv;             /* [n*topk]: grouped row of (t, s) */
     int* tiles;           /* [max_tiles * 4]: {expert, row0, nrows, j | m << 16} (tile j of
-                             the expert's m full tiles; 0 for the half tiles) */
-    int* ntiles;          /* [2]: tiles; tiles before the half tiles (128-row layout) */
-    uint16_t* h;          /* [R, I] bf16 SiLU(gate) * up */
-    float* hsum;          /* [R, I/128] group sums of h (large-group path) */
+                             the expert's m full tiles, every batch size; 0 in the 4th
+                             field for the 128-row layout's last tiles of 1-64 rows) */
+    int* ntiles;          /* [3]: all tiles; the full tiles; the full and the 33-64-row
+                             tiles. The 128-row layout (from 1024 grouped rows) lists the
+                             full tiles (more than 64 rows, or every tile of the 16-row
+                             layout), then each expert's last tile of 33-64 rows, then of
+                             1-32 rows; the 16-row layout has only full tiles */
+    uint16_t* h;          /* [R, I] SiLU(gate) * up: bf16 (16-row tiles) or fp16 scaled
+                             by 2^e per row (128-row tiles; e in hsum, below) */
+    float* hsum;          /* [R, I/128] group sums of h (decode kernels); from 1024 grouped rows
+                             the int8 exponents of h's 32-feature blocks, [R, I/32] bytes */
     float* dpart;         /* [R, H] per-row expert outputs (unweighted): fp32 below 1024 grouped
                              rows (n*topk + n), bf16 (first half of the region) from there;
                              at least 256 * (H / 2048) * 16 KiB: before the down projection
@@ -161,10 +168,28 @@ size_t glmmoe_layer_workspace_bytes(const glmmoe_w4a16_layer* L, int n);
 int glmmoe_layer_workspace_view(const glmmoe_w4a16_layer* L, int n, void* workspace,
                                 glmmoe_layer_ws* view);
 
-/* Runs the whole layer. x: [n, H] bf16; out: [n, H] fp32 (overwritten). */
+/* Runs the whole layer. x: [n, H] bf16; out: [n, H] fp32 (overwritten).
+ * n == 0 returns GLMMOE_OK and touches nothing (x, out, workspace may be
+ * NULL); so do the other layer, routing, dispatch (which then writes its
+ * E + 1 zero offsets, as the reference's kernel does) and glmmoe_ref_* entry
+ * points. */
 int glmmoe_moe_layer_w4a16(const glmmoe_w4a16_layer* L, const uint16_t* x, int n,
                            float* out, void* workspace, size_t workspace_bytes,
                            void* stream);
+
+/* The same layer on fp32 activations, the reference's s.normed as
+ * run_layer_step hands it to the MoE branch (src/model_gpu.cpp:1446-1494):
+ * x [n, H] fp32 is rounded to bf16 (nearest even) and the layer then runs
+ * exactly as glmmoe_moe_layer_w4a16 on the rounded rows (bit-identical
+ * output). Below 256 tokens the router kernel rounds the rows as it stages
+ * them and writes the bf16 copy for the expert kernels (no extra launch);
+ * from 256 tokens one conversion kernel runs first. The workspace is
+ * glmmoe_layer_f32_workspace_bytes(L, n): the layer's plus the n x H bf16
+ * copy at its end. */
+size_t glmmoe_layer_f32_workspace_bytes(const glmmoe_w4a16_layer* L, int n);
+int glmmoe_moe_layer_w4a16_f32(const glmmoe_w4a16_layer* L, const float* x, int n,
+                               float* out, void* workspace, size_t workspace_bytes,
+                               void* stream);
 
 /* glmmoe_moe_layer_w4a16 with no workspace argument and no device allocation.
  * No counterpart in the reference: for callers that cannot allocate (code

@@ -42,7 +42,7 @@ class SynthLayer:
     for the oracle), plus its packed device form."""
 
     def __init__(self, H, E, k, I, seed=0, shared=True, zipf_s=None, device="cuda",
-                 norm_topk=True, routed_scale=2.5):
+                 norm_topk=True, routed_scale=2.5, down_scale_mul=1.0):
         from glmserve_amd import W4A16MoELayer, pack_w4a16
         self.H, self.E, self.k, self.I = H, E, k, I
         self.norm_topk, self.routed_scale = norm_topk, routed_scale
@@ -62,10 +62,17 @@ class SynthLayer:
             s = (0.01 * torch.randn(n, rows, K // 128, generator=g, device=dev)).abs().to(torch.bfloat16)
             return q, s
 
+        def scaled(m):
+            # down_scale_mul: every down scale times a factor (rounded to bf16
+            # again), for scales outside the usual magnitude.
+            if down_scale_mul == 1.0:
+                return m
+            return m[0], (m[1].float() * down_scale_mul).to(torch.bfloat16)
+
         self.gate = mat(E, I, H)
         self.up = mat(E, I, H)
-        self.down = mat(E, H, I)
-        self.shared = (mat(1, I, H), mat(1, I, H), mat(1, H, I)) if shared else None
+        self.down = scaled(mat(E, H, I))
+        self.shared = (mat(1, I, H), mat(1, I, H), scaled(mat(1, H, I))) if shared else None
         self.has_shared_expert = shared
         pk = lambda m, rows, K: pack_w4a16(m[0], m[1], m[0].shape[0], rows, K)
         sh_packed = None
