@@ -186,9 +186,10 @@ def cpu_baseline_prefill(L, torch, n_sample=256, seed=100 + 4096):
 
 
 def profiled_traffic():
-    """HBM bytes per gate/up launch at B=64 from the committed rocprofv3 summary
-    (FETCH_SIZE / WRITE_SIZE passes scaled by a copy-kernel calibration)."""
-    path = os.path.join(ROOT, "profiles", "w4_stream_gate_up_decode_B64.md")
+    """HBM bytes per launch of the B=64 gate/up kernel the headline runs
+    (w4_stream_kernel<0, true>) from the committed rocprofv3 summary of the
+    layer (FETCH_SIZE + WRITE_SIZE passes scaled by a copy-kernel calibration)."""
+    path = os.path.join(ROOT, "profiles", "decode_B64_layer.md")
     try:
         for line in open(path):
             if line.startswith("traffic_bytes_per_launch:"):

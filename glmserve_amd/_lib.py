@@ -24,6 +24,8 @@ SIGNATURES = {
     "glmmoe_layer_workspace_bytes": (_sz, [_vp, _i]),
     "glmmoe_layer_workspace_view": (_i, [_vp, _i, _vp, _vp]),
     "glmmoe_moe_layer_w4a16": (_i, [_vp, _vp, _i, _vp, _vp, _sz, _vp]),
+    "glmmoe_layer_f32_workspace_bytes": (_sz, [_vp, _i]),
+    "glmmoe_moe_layer_w4a16_f32": (_i, [_vp, _vp, _i, _vp, _vp, _sz, _vp]),
     "glmmoe_noalloc_scratch_bytes": (_sz, []),
     "glmmoe_moe_layer_w4a16_noalloc": (_i, [_vp, _vp, _i, _vp, _vp]),
     "glmmoe_moe_route_w4a16": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _sz, _vp]),

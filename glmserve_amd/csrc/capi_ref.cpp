@@ -115,7 +115,8 @@ int glmmoe_ref_moe_expert_ffn_w4a16(const float* x, const int* topk_ids, const f
                                     const uint8_t* down_q, const float* down_sc, int n, int topk,
                                     int hidden, int moe_inter, int E, int group_size, float* out,
                                     void* stream) {
-    if (!x || !topk_ids || !topk_weights || !out || n <= 0) return GLMMOE_ERR_ARG;
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
+    if (!x || !topk_ids || !topk_weights || !out || n < 0) return GLMMOE_ERR_ARG;
     if (group_size != 128) return GLMMOE_ERR_SHAPE;
     glmmoe_w4a16_layer L;
     void* ws = nullptr;
@@ -154,6 +155,7 @@ int glmmoe_ref_moe_expert_ffn(const float* x, const int* topk_ids, const float* 
                               int topk, int hidden, int moe_inter, int E, float* out,
                               void* stream) {
     (void)E;
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!x || !topk_ids || !topk_weights || !gate_w || !up_w || !down_w || !out || n <= 0 ||
         topk <= 0 || hidden <= 0 || moe_inter <= 0)
         return GLMMOE_ERR_ARG;
@@ -165,6 +167,7 @@ int glmmoe_ref_moe_expert_ffn(const float* x, const int* topk_ids, const float* 
 int glmmoe_ref_gemm_w4a16(const float* x, const uint8_t* qW, const float* scales,
                           const float* bias, float* y, int64_t n, int64_t in, int64_t out,
                           int64_t group_size, void* stream) {
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!x || !qW || !scales || !y || n <= 0 || in <= 0 || out <= 0 || group_size <= 0)
         return GLMMOE_ERR_ARG;
     if (n > INT32_MAX || in > INT32_MAX || out > INT32_MAX) return GLMMOE_ERR_SHAPE;
@@ -177,6 +180,7 @@ int glmmoe_ref_gemm_w4a16(const float* x, const uint8_t* qW, const float* scales
 int glmmoe_ref_gemm_fp8(const float* x, const uint8_t* fp8W, const float* w_scale,
                         const float* bias, float* y, int64_t n, int64_t in, int64_t out,
                         void* stream) {
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!x || !fp8W || !y || n <= 0 || in <= 0 || out <= 0) return GLMMOE_ERR_ARG;
     if (n > INT32_MAX || in > INT32_MAX || out > INT32_MAX) return GLMMOE_ERR_SHAPE;
     return launch_ref_gemm_fp8(x, fp8W, w_scale, bias, y, (int)n, (int)in, (int)out, S(stream))
@@ -185,11 +189,13 @@ int glmmoe_ref_gemm_fp8(const float* x, const uint8_t* fp8W, const float* w_scal
 }
 
 int glmmoe_ref_silu_mul(const float* g, const float* u, float* out, int64_t n, void* stream) {
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!g || !u || !out || n <= 0) return GLMMOE_ERR_ARG;
     return launch_ref_silu_mul(g, u, out, (long)n, S(stream)) ? GLMMOE_ERR_LAUNCH : GLMMOE_OK;
 }
 
 int glmmoe_ref_add_inplace(float* y, const float* x, int64_t n, void* stream) {
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!y || !x || n <= 0) return GLMMOE_ERR_ARG;
     return launch_ref_add_inplace(y, x, (long)n, S(stream)) ? GLMMOE_ERR_LAUNCH : GLMMOE_OK;
 }
@@ -203,6 +209,7 @@ static bool gguf_rows_ok(uint32_t t, int64_t in, int64_t row_bytes) {
 int glmmoe_ref_gemm_q(uint32_t qtype, const float* x, const uint8_t* qW, const float* bias,
                       float* y, int64_t n, int64_t in, int64_t out, int64_t row_bytes,
                       void* stream) {
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!x || !qW || !y || n <= 0 || in <= 0 || out <= 0) return GLMMOE_ERR_ARG;
     if (n > INT32_MAX || in > INT32_MAX || out > INT32_MAX || !gguf_rows_ok(qtype, in, row_bytes))
         return GLMMOE_ERR_SHAPE;
@@ -220,6 +227,7 @@ int glmmoe_ref_moe_expert_ffn_q(uint32_t gate_type, uint32_t up_type, uint32_t d
                                 int64_t down_row_bytes, float* h_act, float* dpart, float* out,
                                 int* dispatch, float* gu_part, void* stream) {
     (void)gu_part;   // split-K partials of the reference's decode path; not needed here
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!x || !topk_ids || !topk_w || !gate_q || !up_q || !down_q || !h_act || !dpart || !out ||
         n <= 0 || topk <= 0 || hidden <= 0 || moe_inter <= 0 || E <= 0)
         return GLMMOE_ERR_ARG;
@@ -238,6 +246,7 @@ int glmmoe_ref_qtype_has_i8(uint32_t qtype) { return gguf_has_i8(qtype) ? 1 : 0;
 
 int glmmoe_ref_quantize_act_q8(const float* x, int64_t n, int64_t in, int8_t* xq, float* xs,
                                void* stream) {
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!x || !xq || !xs || n <= 0 || in <= 0) return GLMMOE_ERR_ARG;
     if (in % 32 || n > INT32_MAX || in > INT32_MAX) return GLMMOE_ERR_SHAPE;
     return launch_gg_quant_q8(x, (long)(n * in), xq, xs, S(stream)) ? GLMMOE_ERR_LAUNCH
@@ -252,6 +261,7 @@ static bool i8_rows_ok(const int8_t* q, int64_t in) {
 int glmmoe_ref_gemm_q_i8(uint32_t qtype, const int8_t* xq, const float* xs, const uint8_t* qW,
                          const float* bias, float* y, int64_t n, int64_t in, int64_t out,
                          int64_t row_bytes, void* stream) {
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!xq || !xs || !qW || !y || n <= 0 || in <= 0 || out <= 0) return GLMMOE_ERR_ARG;
     if (n > INT32_MAX || in > INT32_MAX || out > INT32_MAX || !gguf_has_i8(qtype) ||
         !gguf_rows_ok(qtype, in, row_bytes) || !i8_rows_ok(xq, in))
@@ -271,6 +281,7 @@ int glmmoe_ref_moe_expert_ffn_q_i8(uint32_t gate_type, uint32_t up_type, uint32_
                                    int8_t* hq, float* hs, float* dpart, float* out, int* dispatch,
                                    float* gu_part, void* stream) {
     (void)gu_part;
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     if (!xq || !xs || !topk_ids || !topk_w || !gate_q || !up_q || !down_q || !h_act || !hq ||
         !hs || !dpart || !out || n <= 0 || topk <= 0 || hidden <= 0 || moe_inter <= 0 || E <= 0)
         return GLMMOE_ERR_ARG;

@@ -292,13 +292,13 @@ __device__ void dispatch_small(const int* ids, int n, int topk, int E, int with_
         const int cnt = x < E ? hist[x] & 0xffff : 0;
         if (lead) gd.offsets[x] = below;
         if (cnt > 0) {
-            const int4 t = make_int4(x, below, cnt, 0);
+            const int4 t = make_int4(x, below, cnt, 1 << 16);
             ltiles[dbelow] = t;
             if (lead) gd.tiles[dbelow] = t;
         }
         if (x == E) {
             if (with_shared) {
-                const int4 t = make_int4(E, total, n, 0);
+                const int4 t = make_int4(E, total, n, 1 << 16);
                 ltiles[dbelow] = t;
                 if (lead) gd.tiles[dbelow] = t;
             }

@@ -45,6 +45,7 @@ int glmmoe_moe_layer_w4a16_noalloc(const glmmoe_w4a16_layer* L, const uint16_t* 
     const size_t need = glmmoe_layer_workspace_bytes(L, n);
     if (need == 0) return GLMMOE_ERR_ARG;
     if (need > kScratchBytes) return GLMMOE_ERR_WORKSPACE;
+    if (n == 0) return GLMMOE_OK;   // no tokens: nothing to compute or write
     void* ws = nullptr;
     const int rc = scratch_ptr(&ws);
     if (rc) return rc;

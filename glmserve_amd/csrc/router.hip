@@ -649,7 +649,7 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const float* __restrict__ e_bias, int n, int H, int E, int epw, float* __restrict__ logits,
     float* __restrict__ xsum, int slices, uint32_t* __restrict__ cs, unsigned int* __restrict__ zero,
-    int nzero) {
+    int nzero, const float* __restrict__ xf, uint16_t* __restrict__ xb) {
     extern __shared__ __align__(16) char small_lds[];
     const int nchunks = H / kRouterKC;
     const int tid = threadIdx.x;
@@ -667,7 +667,7 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
     const int xrows = nt * nchunks;
     const int xdma = (xrows + 3) / 4;
     float* part = reinterpret_cast<float*>(small_lds + small_x_bytes(nchunks));
-    {
+    if (!xf) {
         const int wave = tid >> 6, lane = tid & 63;
         for (int b = wave; b < xdma; b += kSmallThreads / 64) {
             int R = 4 * b + (lane >> 4);
@@ -675,6 +675,27 @@ __global__ __launch_bounds__(kSmallThreads) void router_small_kernel(
             const int t = R / nchunks, cc = R - t * nchunks;
             const int o = (lane & 15) ^ (R & 15);
             dma16(x + (size_t)(t0 + t) * H + cc * kRouterKC + o * 8, xl + b * 1024);
+        }
+    } else {
+        // fp32 activations: the same 16-B pieces, each from 8 fp32 values
+        // rounded to bf16 (nearest even) on the way into LDS; the first
+        // expert block also writes the rounded rows to xb for the expert
+        // kernels, so the layer reads fp32 x once and needs no cast launch.
+        const int wave = tid >> 6, lane = tid & 63;
+        for (int b = wave; b < xdma; b += kSmallThreads / 64) {
+            const int R = 4 * b + (lane >> 4);
+            if (R >= xrows) continue;
+            const int t = R / nchunks, cc = R - t * nchunks;
+            const int o = (lane & 15) ^ (R & 15);
+            const size_t off = (size_t)(t0 + t) * H + cc * kRouterKC + o * 8;
+            const float4 lo = *reinterpret_cast<const float4*>(xf + off);
+            const float4 hi = *reinterpret_cast<const float4*>(xf + off + 4);
+            const uint4 v = make_uint4(f32_to_bf16(lo.x) | (f32_to_bf16(lo.y) << 16),
+                                       f32_to_bf16(lo.z) | (f32_to_bf16(lo.w) << 16),
+                                       f32_to_bf16(hi.x) | (f32_to_bf16(hi.y) << 16),
+                                       f32_to_bf16(hi.z) | (f32_to_bf16(hi.w) << 16));
+            *reinterpret_cast<uint4*>(xl + b * 1024 + lane * 16) = v;
+            if (eb == 0) *reinterpret_cast<uint4*>(xb + off) = v;
         }
     }
     // Thread -> (expert el, chunk c, token slice ts): slice ts holds tokens
@@ -791,9 +812,11 @@ size_t router_select_scratch_bytes(int n, int H, int E) {
 int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_bias, int n, int H,
                          int E, int topk, int norm_topk, float routed_scale, float* logits,
                          float* xsum, float* scratch, int* ids, float* w, hipStream_t s,
-                         const DispOut* disp, bool* dispatched, bool select) {
+                         const DispOut* disp, bool* dispatched, bool select, const float* xf,
+                         uint16_t* xb) {
     const int nchunks = H / kRouterKC;
     if (dispatched) *dispatched = false;
+    if (xf && !router_small_path(n, H, E, topk)) return -2;   // the caller converts x first
     if (router_small_path(n, H, E, topk)) {
         // scratch: the order codes and scores [2][n][E] handed to the top-k.
         if (!scratch || router_select_scratch_bytes(n, H, E) < (size_t)2 * n * E * 4) return -3;
@@ -829,7 +852,7 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         }
         hipLaunchKernelGGL(router_small_kernel, grid, dim3(kSmallThreads), lds, s, x, wr, e_bias, n,
                            H, E, epw, logits, xsum, slices, reinterpret_cast<uint32_t*>(scratch),
-                           select ? nullptr : disp->zero, select ? 0 : disp->nzero);
+                           select ? nullptr : disp->zero, select ? 0 : disp->nzero, xf, xb);
         if (hipGetLastError() != hipSuccess) return -4;
         if (!select) return 0;   // codes and scores only: the gate/up kernel selects
         // Selection: one workgroup (and then the dispatch too) up to

@@ -622,23 +622,23 @@ __device__ __forceinline__ void fused_route(const FusedRoute r, int E, bool lead
             const int e = sids[t];
             int rank = 0;
             for (int k = 0; k < K; ++k) rank += sids[k] < e ? 1 : 0;
-            tiles[rank] = make_int4(e, rank, 1, 0);
+            tiles[rank] = make_int4(e, rank, 1, 1 << 16);
             tok[rank] = 0;
             if (lead) {
-                r.disp.tiles[rank] = make_int4(e, rank, 1, 0);
+                r.disp.tiles[rank] = make_int4(e, rank, 1, 1 << 16);
                 r.disp.sorted_tok[rank] = 0;
                 r.disp.sorted_slot[rank] = t;
                 r.disp.inv[t] = rank;
             }
         } else if (t == K) {
             if (sh) {
-                tiles[K] = make_int4(E, K, 1, 0);
+                tiles[K] = make_int4(E, K, 1, 1 << 16);
                 tok[K] = 0;
             }
             nt[0] = nt[1] = nt[2] = K + sh;
             if (lead) {
                 if (sh) {
-                    r.disp.tiles[K] = make_int4(E, K, 1, 0);
+                    r.disp.tiles[K] = make_int4(E, K, 1, 1 << 16);
                     r.disp.sorted_tok[K] = 0;
                     r.disp.sorted_slot[K] = -1;
                 }

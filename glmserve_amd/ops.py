@@ -187,6 +187,21 @@ class W4A16MoELayer(_MoELayer):
         check(lib().glmmoe_moe_layer_w4a16_noalloc(self._ref(), _p(x), n, _p(out), _s(stream)),
               "glmmoe_moe_layer_w4a16_noalloc")
 
+    def alloc_workspace_f32(self, n, device="cuda"):
+        """Workspace of forward_f32 (the layer's plus the bf16 copy of x)."""
+        b = lib().glmmoe_layer_f32_workspace_bytes(self._ref(), n)
+        if b == 0:
+            raise GlmMoeError("layer shape not supported")
+        return torch.empty(b, dtype=torch.uint8, device=device)
+
+    def forward_f32(self, x, out, ws, stream=None):
+        """x: [n, H] fp32 (rounded to bf16 inside); out: [n, H] fp32."""
+        n = x.shape[0]
+        _need(x, torch.float32, n * self.hidden, "x")
+        _need(out, torch.float32, n * self.hidden, "out")
+        check(lib().glmmoe_moe_layer_w4a16_f32(self._ref(), _p(x), n, _p(out), _p(ws), ws.numel(),
+                                               _s(stream)), "glmmoe_moe_layer_w4a16_f32")
+
 
 class FP8MoELayer(_MoELayer):
     """FP8 experts: (packed e4m3 from pack_fp8, fp32 [.., rows/128, K/128] block scales)."""

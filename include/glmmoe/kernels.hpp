@@ -88,6 +88,17 @@ inline size_t moe_layer_workspace_bytes(const glmmoe_w4a16_layer& layer, int n) 
     return glmmoe_layer_workspace_bytes(&layer, n);
 }
 
+// The same branch on run_layer_step's fp32 s.normed, passed unchanged
+// (src/model_gpu.cpp:1446-1494); workspace of moe_layer_f32_workspace_bytes.
+inline int moe_layer_w4a16(const glmmoe_w4a16_layer& layer, const float* x_f32, int n, float* out,
+                           void* workspace, size_t workspace_bytes, void* s = nullptr) {
+    return glmmoe_moe_layer_w4a16_f32(&layer, x_f32, n, out, workspace, workspace_bytes, s);
+}
+
+inline size_t moe_layer_f32_workspace_bytes(const glmmoe_w4a16_layer& layer, int n) {
+    return glmmoe_layer_f32_workspace_bytes(&layer, n);
+}
+
 // ---- The reference's own argument lists (fp32 activations, reference weight
 // layouts). moe_expert_ffn_w4a16 needs the weights registered once at load
 // time (glmmoe_ref_register_w4a16 with their packed copy) and a workspace

@@ -65,10 +65,10 @@ def test_reference_signature_host_checks():
                                              dummy, dummy, 1, 8, 6144, 2048, 256, 64, dummy,
                                              None) == -2
     assert L.glmmoe_ref_gemm_w4a16(None, dummy, dummy, None, dummy, 1, 6144, 2048, 128, None) == -1
-    assert L.glmmoe_ref_gemm_w4a16(dummy, dummy, dummy, None, dummy, 0, 6144, 2048, 128, None) == -1
+    assert L.glmmoe_ref_gemm_w4a16(dummy, dummy, dummy, None, dummy, -1, 6144, 2048, 128, None) == -1
     assert L.glmmoe_ref_gemm_fp8(dummy, None, None, None, dummy, 1, 64, 64, None) == -1
     assert L.glmmoe_ref_silu_mul(dummy, dummy, None, 8, None) == -1
-    assert L.glmmoe_ref_add_inplace(dummy, dummy, 0, None) == -1
+    assert L.glmmoe_ref_add_inplace(dummy, dummy, -1, None) == -1
     assert L.glmmoe_ref_moe_expert_ffn(dummy, dummy, dummy, None, dummy, dummy, 1, 8, 64, 64, 16,
                                        dummy, None) == -1
     # x in bf16 plus the routed-only layer workspace
@@ -159,6 +159,67 @@ def test_workspace_sizing_and_view():
                                     C.c_void_p(16), 16, None) == -3
 
 
+def test_zero_token_calls_are_no_ops():
+    # n == 0 returns GLMMOE_OK on every entry point without a device call (so
+    # without a GPU here), with NULL data pointers; negative n stays an
+    # argument error. (moe_dispatch at n == 0 writes its zero offsets: a GPU
+    # test covers it.)
+    L = _lib.lib()
+    st = C.byref(_layer())
+    assert L.glmmoe_moe_layer_w4a16(st, None, 0, None, None, 0, None) == 0
+    assert L.glmmoe_moe_layer_w4a16_f32(st, None, 0, None, None, 0, None) == 0
+    assert L.glmmoe_moe_layer_w4a16_noalloc(st, None, 0, None, None) == 0
+    assert L.glmmoe_moe_route_w4a16(st, None, 0, None, None, None, 0, None) == 0
+    assert L.glmmoe_expert_ffn_w4a16(st, None, 0, None, None, None, None, 0, None) == 0
+    st8 = _lib.Fp8Layer()
+    for name, _ in _lib.Layer._fields_:
+        setattr(st8, name, getattr(_layer(), name))
+    assert L.glmmoe_moe_layer_fp8(C.byref(st8), None, 0, None, None, 0, None) == 0
+    assert L.glmmoe_expert_ffn_fp8(C.byref(st8), None, 0, None, None, None, None, 0, None) == 0
+    assert L.glmmoe_quant_act_fp8(None, 0, 6144, None, None, None) == 0
+    assert L.glmmoe_router_logits(None, None, 0, 6144, 256, None, None, None, 0, None) == 0
+    assert L.glmmoe_router_logits_f32(None, None, None, None, 0, 6144, 256, None) == 0
+    assert L.glmmoe_moe_router(None, None, 0, 256, 8, 1, 2.5, None, None, None) == 0
+    assert L.glmmoe_ref_moe_expert_ffn_w4a16(None, None, None, None, None, None, None, None, None,
+                                             0, 8, 6144, 2048, 256, 128, None, None) == 0
+    assert L.glmmoe_ref_moe_expert_ffn(None, None, None, None, None, None, 0, 8, 64, 64, 16,
+                                       None, None) == 0
+    assert L.glmmoe_ref_gemm_w4a16(None, None, None, None, None, 0, 6144, 2048, 128, None) == 0
+    assert L.glmmoe_ref_gemm_fp8(None, None, None, None, None, 0, 64, 64, None) == 0
+    assert L.glmmoe_ref_silu_mul(None, None, None, 0, None) == 0
+    assert L.glmmoe_ref_add_inplace(None, None, 0, None) == 0
+    assert L.glmmoe_ref_gemm_q(18, None, None, None, None, 0, 6144, 64, 2352, None) == 0
+    assert L.glmmoe_ref_moe_expert_ffn_q(18, 18, 23, None, None, None, None, None, None, 0, 8,
+                                         6144, 2048, 256, 2352, 2352, 1088, None, None, None,
+                                         None, None, None) == 0
+    assert L.glmmoe_ref_quantize_act_q8(None, 0, 64, None, None, None) == 0
+    assert L.glmmoe_ref_gemm_q_i8(18, None, None, None, None, None, 0, 256, 8, 98, None) == 0
+    assert L.glmmoe_ref_moe_expert_ffn_q_i8(18, 18, 23, None, None, None, None, None, None, None,
+                                            0, 8, 6144, 2048, 256, 2352, 2352, 1088, None, None,
+                                            None, None, None, None, None, None) == 0
+    # negative counts are errors
+    assert L.glmmoe_moe_layer_w4a16(st, None, -1, None, None, 0, None) == -1
+    assert L.glmmoe_moe_router(None, None, -1, 256, 8, 1, 2.5, None, None, None) == -1
+    assert L.glmmoe_moe_dispatch(None, -1, 8, 256, C.c_void_p(16), None, None, None) == -1
+    # dispatch at n == 0 needs only the offsets
+    assert L.glmmoe_moe_dispatch(None, 0, 8, 256, None, None, None, None) == -1
+
+
+def test_f32_layer_workspace_and_checks():
+    # The fp32-activation layer: the layer's workspace plus the n x H bf16
+    # copy of x at its end (256-byte aligned).
+    L = _lib.lib()
+    st = C.byref(_layer())
+    for n in (1, 64, 300, 4096):
+        lw = L.glmmoe_layer_workspace_bytes(st, n)
+        assert L.glmmoe_layer_f32_workspace_bytes(st, n) == lw + (n * 6144 * 2 + 255) // 256 * 256
+    assert L.glmmoe_layer_f32_workspace_bytes(C.byref(_layer(k=9)), 4) == 0
+    d = C.c_void_p(16)
+    assert L.glmmoe_moe_layer_w4a16_f32(st, None, 4, d, d, 1 << 30, None) == -1
+    assert L.glmmoe_moe_layer_w4a16_f32(st, d, 4, d, d, L.glmmoe_layer_workspace_bytes(st, 4),
+                                        None) == -3
+
+
 def test_noalloc_entry_host_checks():
     # The no-allocation entry sizes the batch before any device call: a batch
     # whose workspace exceeds the library's scratch, or a bad layer, is
@@ -206,7 +267,9 @@ def test_cpp_header_compiles_against_the_library(tmp_path):
         '                                        y, disp);\n'
         '  }\n'
         '  glmmoe_w4a16_layer L{};\n'
-        '  return (int)glmserve::cuda::moe_layer_workspace_bytes(L, 1);\n'
+        '  glmserve::cuda::moe_layer_w4a16(L, x, 1, y, nullptr, 0);   // fp32 s.normed\n'
+        '  return (int)glmserve::cuda::moe_layer_workspace_bytes(L, 1) +\n'
+        '         (int)glmserve::cuda::moe_layer_f32_workspace_bytes(L, 1);\n'
         '}\n')
     exe = tmp_path / "use"
     r = subprocess.run(["g++", "-std=c++17", "-I", os.path.join(ROOT, "include"), str(src), "-o",
