@@ -290,8 +290,10 @@ def main():
         U = int(torch.unique(ids).numel())
         per_expert = (2 * I * rb[0] + H * rb[2])
         alg = U * per_expert + n * H * 4 * 2
+        ops = 2.0 * n * K * 3 * H * I   # routed experts' multiply-adds x 2
         return {"n": n, "ms": ms, "tokens_per_s": n / (ms * 1e-3), "distinct_experts": U,
                 "alg_bytes": alg, "GBps": alg / (ms * 1e-3) / 1e9,
+                "TOPs": ops / (ms * 1e-3) / 1e12,
                 "hbm_frac_layer": alg / (ms * 1e-3) / HBM_PEAK,
                 "expert_bytes": per_expert,
                 "note": "routed experts only (the reference's moe_expert_ffn_q has no shared "
@@ -359,6 +361,8 @@ def main():
     if args.gguf_only:
         r = {f"gguf{'_i8' if i8 else ''}_decode_B{n}": measure_gguf(n, args.steps, args.warmup, i8)
              for n in (1, 64) for i8 in (False, True)}
+        for i8 in (False, True):
+            r[f"gguf{'_i8' if i8 else ''}_prefill_1024"] = measure_gguf(1024, max(3, args.steps // 10), 1, i8)
         for name, qt, bb, be in (("q8_0", 8, 34, 32), ("iq3_xxs", 18, 98, 256)):
             for n in (1, 64):
                 r[f"gguf_gemm_q_{name}_n{n}"] = measure_gemm_q(qt, bb, be, n, args.steps, args.warmup)
@@ -476,6 +480,11 @@ def main():
             sweep[f"gguf_decode_B{n}"] = measure_gguf(n, args.steps, args.warmup)
             sweep[f"gguf_i8_decode_B{n}"] = measure_gguf(n, args.steps, args.warmup, i8=True)
             sweep[f"gguf_gemm_q_q8_0_n{n}"] = measure_gemm_q(8, 34, 32, n, args.steps, args.warmup)
+        # Prefill-sized GGUF batch: 1024 tokens = 8192 grouped rows, past the
+        # reference's tensor-core threshold (n * topk >= 2048).
+        log("bench: sweep GGUF prefill 1024")
+        sweep["gguf_prefill_1024"] = measure_gguf(1024, max(3, args.steps // 10), 1)
+        sweep["gguf_i8_prefill_1024"] = measure_gguf(1024, max(3, args.steps // 10), 1, i8=True)
         torch.cuda.empty_cache()
     if not args.no_sweep and not args.no_fp8:
         log("bench: sweep FP8 prefill 8192")

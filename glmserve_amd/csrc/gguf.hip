@@ -1171,6 +1171,213 @@ int launch_gg_quant_q8(const float* x, long total, int8_t* xq, float* xs, hipStr
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
 
+// ---- Large groups on the matrix cores: moe_expert_ffn_q_i8 from
+// kGgMmaMinRows routed rows, the reference's tensor-core policy
+// (GLMSERVE_MMA_MOE_MIN_TS = 2048, cuda/qgemm.cu:1563-1587; its kernel
+// emajor_mma_s8_kernel, :1262-1349). The arithmetic class is the reference's:
+// per 32-element block an exact int32 dot of the int8 weights and int8
+// activations, then * weight scale * activation scale added in fp32.
+//
+// Tiles: the routed rows grouped by expert (gg_group_kernel) in tiles of up
+// to kGgMmaTM rows. A workgroup (4 waves) computes one tile x kGgMmaRows
+// weight rows: phase 1 64 features (wave w: the gate rows and up rows of
+// features 16 w .. 16 w + 15, stacked as one 32-row block so that a lane
+// holds gate and up of the same feature), phase 2 128 output rows (wave w:
+// rows 32 w .. 32 w + 31). Per 256-K chunk the workgroup decodes its weight
+// rows into LDS as int8 plus a scale per 32-block (the integer-fragment
+// decode of gg_dec8i, whose per-32 scale is uniform over a block for Q8_0,
+// IQ3_XXS and IQ4_XS) and stages the tile's int8 activation rows and
+// scales; then each wave runs v_mfma_i32_32x32x32_i8 per 32-block over its
+// 32 weight rows x 4 blocks of 32 rows (A = weights, B = activations: a
+// lane's 16 outputs are one row's 16 weight rows, so their 16 weight scales
+// come as 4 broadcast LDS reads and its row's activation scale as one).
+// Rows past the tile's end repeat its last row and are not stored.
+constexpr int kGgMmaMinRows = 2048;
+constexpr int kGgMmaTM = 128;       // routed rows per tile
+constexpr int kGgMmaRows = 128;     // weight rows per workgroup
+constexpr int kGgMmaStride = 272;   // LDS bytes per int8 row of a chunk (256 + 16 padding)
+
+typedef int gg_i32x4 __attribute__((ext_vector_type(4)));
+typedef int gg_i32x16 __attribute__((ext_vector_type(16)));
+
+struct GgMmaLds {
+    int8_t wq[kGgMmaRows * kGgMmaStride];
+    int8_t xq[kGgMmaTM * kGgMmaStride];
+    float ws[8][kGgMmaRows];   // [32-block][weight row]
+    float xs[8][kGgMmaTM];     // [32-block][tile row]
+    uint32_t grid[256];        // IQ3_XXS codebook
+    uint32_t sgn[256];         // IQ3_XXS sign byte masks, two words per 7-bit pattern
+    int src[kGgMmaTM];         // activation row of each tile row
+    int row[kGgMmaTM];         // routed row of each tile row
+};
+
+// Bytes of one 256-element chunk of a row of type T.
+__host__ __device__ constexpr int gg_mma_chunk_bytes(uint32_t t) {
+    return t == 18 ? 98 : t == 23 ? 136 : t == 8 ? 8 * 34 : 0;
+}
+bool gg_mma_type_ok(uint32_t t) { return t == 8 || t == 18 || t == 23; }
+
+template <bool DOWN, uint32_t T>
+__global__ __launch_bounds__(256) void gg_mma_kernel(GgMoeArgs a) {
+    __shared__ __align__(16) GgMmaLds L;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int E = a.E;
+    const int* off = a.d;
+    const int* tp = a.d + E + 1;
+    const int* rows = a.d + 2 * (E + 1);
+    const int g = (int)blockIdx.x;
+    if (g >= tp[E]) return;   // the grid covers the largest possible tile count
+    int lo = 0, hi = E;       // the expert e with tp[e] <= g < tp[e + 1]
+    while (hi - lo > 1) {
+        const int mid = (lo + hi) / 2;
+        if (tp[mid] <= g) lo = mid;
+        else hi = mid;
+    }
+    const int e = lo;
+    const int r0 = off[e] + (g - tp[e]) * kGgMmaTM;
+    const int nr = min(kGgMmaTM, off[e + 1] - r0);
+    if (tid < kGgMmaTM) {
+        const int r = rows[r0 + min(tid, nr - 1)];
+        L.row[tid] = r;
+        L.src[tid] = DOWN ? r : r / a.topk;
+    }
+    if constexpr (T == 18) {
+        L.grid[tid] = c_iq3xxs_grid[tid];
+        const uint32_t pe = (uint32_t)tid >> 1;
+        const uint32_t sg = pe | ((uint32_t)(__builtin_popcount(pe) & 1) << 7);
+        L.sgn[tid] = gg_bytemask4(sg >> (4 * (tid & 1)));
+    }
+    const int K = DOWN ? a.I : a.H;
+    const int nch = K / 256;
+    constexpr int CB = gg_mma_chunk_bytes(T);
+    // This thread decodes weight row rr (fragments 16 fh .. 16 fh + 15 of each chunk).
+    const int rr = tid >> 1, fh = tid & 1;
+    const uint8_t* wrow;
+    if constexpr (DOWN) {
+        const size_t o = (size_t)blockIdx.y * kGgMmaRows + rr;
+        wrow = a.down_q + ((size_t)e * a.H + o) * a.down_rb;
+    } else {
+        const int j = rr & 31;
+        const size_t f = (size_t)blockIdx.y * 64 + 16 * (rr >> 5) + (j & 15);
+        wrow = j < 16 ? a.gate_q + ((size_t)e * a.I + f) * a.gate_rb : a.up_q + ((size_t)e * a.I + f) * a.up_rb;
+    }
+    __syncthreads();
+    const int8_t* X = DOWN ? a.hq : a.xq;
+    const float* XS = DOWN ? a.hs : a.xs;
+    // This thread stages half (128 B) of tile row xr's chunk, and (tid < 128)
+    // that row's 8 block scales.
+    const int xr = tid >> 1, xh = tid & 1;
+    const int8_t* xrow = X + (size_t)L.src[xr] * K + xh * 128;
+    const float* xsrow = XS + (size_t)L.src[tid & (kGgMmaTM - 1)] * (K / 32);
+
+    float acc[4][16];
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) acc[tb][i] = 0.0f;
+    const int ar = wave * 32 + (lane & 31), hh = lane >> 5;
+    for (int c = 0; c < nch; ++c) {
+        uint4 xv[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) xv[j] = reinterpret_cast<const uint4*>(xrow + (size_t)c * 256)[j];
+        float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0;
+        if (tid < kGgMmaTM) {
+            s0 = reinterpret_cast<const float4*>(xsrow + c * 8)[0];
+            s1 = reinterpret_cast<const float4*>(xsrow + c * 8)[1];
+        }
+        const uint8_t* wc = wrow + (size_t)c * CB;
+#pragma unroll 4
+        for (int j = 0; j < 16; ++j) {
+            const int f = fh * 16 + j, kk = 8 * f;
+            int w0, w1;
+            float ds, dm;
+            gg_dec8i_any<true>(T, wc, kk, L.grid, L.sgn, w0, w1, ds, dm);
+            *reinterpret_cast<int2*>(L.wq + rr * kGgMmaStride + kk) = make_int2(w0, w1);
+            if ((f & 3) == 0) L.ws[f >> 2][rr] = ds;
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j)
+            *reinterpret_cast<uint4*>(L.xq + xr * kGgMmaStride + xh * 128 + 16 * j) = xv[j];
+        if (tid < kGgMmaTM) {
+            L.xs[0][tid] = s0.x; L.xs[1][tid] = s0.y; L.xs[2][tid] = s0.z; L.xs[3][tid] = s0.w;
+            L.xs[4][tid] = s1.x; L.xs[5][tid] = s1.y; L.xs[6][tid] = s1.z; L.xs[7][tid] = s1.w;
+        }
+        __syncthreads();
+#pragma unroll 2
+        for (int kb = 0; kb < 8; ++kb) {
+            const gg_i32x4 A = *reinterpret_cast<const gg_i32x4*>(L.wq + ar * kGgMmaStride + kb * 32 + hh * 16);
+            float wsv[16];
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                const float4 v = *reinterpret_cast<const float4*>(&L.ws[kb][wave * 32 + 8 * q + 4 * hh]);
+                wsv[4 * q] = v.x; wsv[4 * q + 1] = v.y; wsv[4 * q + 2] = v.z; wsv[4 * q + 3] = v.w;
+            }
+#pragma unroll
+            for (int tb = 0; tb < 4; ++tb) {
+                const int xrow_l = tb * 32 + (lane & 31);
+                const gg_i32x4 B =
+                    *reinterpret_cast<const gg_i32x4*>(L.xq + xrow_l * kGgMmaStride + kb * 32 + hh * 16);
+                const gg_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, gg_i32x16{}, 0, 0, 0);
+                const float xsv = L.xs[kb][xrow_l];
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    acc[tb][i] = __builtin_fmaf((float)d[i] * wsv[i], xsv, acc[tb][i]);
+            }
+        }
+        __syncthreads();
+    }
+    // Lane: tile row tb * 32 + lane % 32; its 16 outputs are weight rows
+    // 8 (i / 4) + 4 hh + i % 4 of the wave's 32-row block.
+#pragma unroll
+    for (int tb = 0; tb < 4; ++tb) {
+        const int t = tb * 32 + (lane & 31);
+        if (t >= nr) continue;
+        const size_t r = (size_t)L.row[t];
+        if constexpr (DOWN) {
+            float* dst = a.dpart + r * a.H + (size_t)blockIdx.y * kGgMmaRows + wave * 32 + 4 * hh;
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+                *reinterpret_cast<float4*>(dst + 8 * q) =
+                    make_float4(acc[tb][4 * q], acc[tb][4 * q + 1], acc[tb][4 * q + 2], acc[tb][4 * q + 3]);
+        } else {
+            // i < 8: gate of feature 8 (i / 4) + 4 hh + i % 4; i + 8: its up.
+            float* dst = a.h_act + r * a.I + (size_t)blockIdx.y * 64 + wave * 16 + 4 * hh;
+#pragma unroll
+            for (int q = 0; q < 2; ++q) {
+                float hv[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u) hv[u] = gg_silu(acc[tb][4 * q + u]) * acc[tb][4 * q + u + 8];
+                *reinterpret_cast<float4*>(dst + 8 * q) = make_float4(hv[0], hv[1], hv[2], hv[3]);
+            }
+        }
+    }
+}
+
+// The matrix-core phases for a batch the caller grouped with kGgMmaTM-row
+// tiles; h_act is requantized into (hq, hs) between them.
+static int gg_mma_phases(const GgMoeArgs& a, hipStream_t s) {
+    const unsigned tiles = (unsigned)(a.n * a.topk / kGgMmaTM + a.E);
+    auto by = [&](uint32_t t, auto f) {
+        if (t == 8) f(std::integral_constant<uint32_t, 8>{});
+        else if (t == 18) f(std::integral_constant<uint32_t, 18>{});
+        else f(std::integral_constant<uint32_t, 23>{});
+    };
+    by(a.gate_type, [&](auto tc) {
+        hipLaunchKernelGGL((gg_mma_kernel<false, decltype(tc)::value>), dim3(tiles, (unsigned)(a.I / 64)),
+                           dim3(256), 0, s, a);
+    });
+    if (hipGetLastError() != hipSuccess) return -4;
+    if (launch_gg_quant_q8(a.h_act, (long)a.n * a.topk * a.I, const_cast<int8_t*>(a.hq),
+                           const_cast<float*>(a.hs), s))
+        return -4;
+    by(a.down_type, [&](auto tc) {
+        hipLaunchKernelGGL((gg_mma_kernel<true, decltype(tc)::value>),
+                           dim3(tiles, (unsigned)(a.H / kGgMmaRows)), dim3(256), 0, s, a);
+    });
+    return hipGetLastError() == hipSuccess ? 0 : -4;
+}
+
 // I8: h_act is quantized into (hq, hs) between the phases.
 template <int TT, bool I8>
 static int gg_moe_phases(uint32_t gt, uint32_t ut, uint32_t dt, const GgMoeArgs& a, unsigned tiles,
@@ -1213,6 +1420,29 @@ static int gg_moe(GgMoeArgs a, float* out, int* dispatch, hipStream_t s) {
     // Rows per tile: about the rows an expert holds (decode: one or a few). With
     // one row per tile, grouping changes nothing but the order of the tiles, so
     // the routed rows are taken as they come (an exact grid, no counting pass).
+    // int8 activations from kGgMmaMinRows routed rows, on types whose scale is
+    // uniform over each 32-block and shapes of whole 256-K chunks: the
+    // matrix-core phases (the reference's tensor-core policy).
+    if constexpr (I8) {
+        const bool al = ((uintptr_t)a.xq & 15) == 0 && ((uintptr_t)a.hq & 15) == 0 &&
+                        ((uintptr_t)a.xs & 15) == 0 && ((uintptr_t)a.hs & 15) == 0 &&
+                        ((uintptr_t)a.gate_q & 1) == 0 && ((uintptr_t)a.up_q & 1) == 0 &&
+                        ((uintptr_t)a.down_q & 1) == 0 && (a.gate_rb & 1) == 0 && (a.up_rb & 1) == 0 &&
+                        (a.down_rb & 1) == 0;
+        if (dispatch && nk >= kGgMmaMinRows && gt == ut && gg_mma_type_ok(gt) && gg_mma_type_ok(dt) &&
+            H % 256 == 0 && a.I % 256 == 0 && al) {
+            hipLaunchKernelGGL(gg_group_kernel, dim3(1), dim3(1024), (size_t)2 * E * 4, s, ids, nk, E,
+                               kGgMmaTM, dispatch);
+            if (hipGetLastError() != hipSuccess) return -4;
+            a.d = dispatch;
+            const int rc = gg_mma_phases(a, s);
+            if (rc) return rc;
+            const long total = (long)n * H;
+            hipLaunchKernelGGL(gg_reduce_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, s,
+                               dpart, ids, ids_w, n, topk, H, E, out);
+            return hipGetLastError() == hipSuccess ? 0 : -4;
+        }
+    }
     const int tt = !dispatch || nk <= E ? 1 : nk <= 4 * E ? 4 : 8;
     if (tt == 1) {
         dispatch = nullptr;

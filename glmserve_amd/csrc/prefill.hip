@@ -766,39 +766,48 @@ __global__ __launch_bounds__(256) void f16_rows_kernel(const uint16_t* __restric
 // exponent (h_exp_rule is non-increasing, so that is the rule of the row's
 // largest |h|): blocks with a larger exponent are multiplied by 2^(e_row - e)
 // (exact unless the result is an fp16 subnormal, i.e. below 2^-24 of the
-// row's largest |h| once scaled). One wave per row; every block byte then
-// holds e_row. Blocks already at e_row (every block of every row whose |h|
+// row's largest |h| once scaled); every block byte then holds e_row. One
+// thread per row reads the row's I / 32 exponent bytes (consecutive rows:
+// coalesced 16-B loads); rows whose blocks already agree (every row whose |h|
 // stays in the band) are only read.
 __global__ __launch_bounds__(256) void h_rescale_kernel(uint16_t* __restrict__ h, int8_t* __restrict__ hexp, int R,
                                                        int I) {
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    const int r = blockIdx.x * 256 + threadIdx.x;
     if (r >= R) return;
-    const int nb = I / 32;
-    int8_t* er = hexp + (size_t)r * nb;
-    int emin = kHExpNone;
-    for (int b = lane; b < nb; b += 64) emin = min(emin, (int)er[b]);
+    const int nb = I / 32;   // a multiple of 16 (I % 1024 == 0)
+    uint4* er = reinterpret_cast<uint4*>(hexp + (size_t)r * nb);
+    int emin = kHExpNone, emax = -128;
+    for (int v = 0; v < nb / 16; ++v) {
+        const uint4 q = er[v];
+        const uint32_t d[4] = {q.x, q.y, q.z, q.w};
 #pragma unroll
-    for (int off = 32; off > 0; off >>= 1) emin = min(emin, __shfl_xor(emin, off));
-    for (int b = lane; b < nb; b += 64) {
-        const int e = er[b];
-        if (e != emin) {
-            uint4* p = reinterpret_cast<uint4*>(h + (size_t)r * I + b * 32);
-            for (int q = 0; q < 4; ++q) {
-                const uint4 v = p[q];
-                uint32_t w[4] = {v.x, v.y, v.z, v.w};
-#pragma unroll
-                for (int j = 0; j < 4; ++j) {
-                    const float lo = __builtin_ldexpf((float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffffu)),
-                                                      emin - e);
-                    const float hi = __builtin_ldexpf((float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16)),
-                                                      emin - e);
-                    w[j] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
-                           ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
-                }
-                p[q] = make_uint4(w[0], w[1], w[2], w[3]);
-            }
-            er[b] = (int8_t)emin;
+        for (int j = 0; j < 16; ++j) {
+            const int e = (int)(int8_t)(d[j >> 2] >> (8 * (j & 3)));
+            emin = min(emin, e);
+            emax = max(emax, e);
         }
+    }
+    if (emin == emax) return;
+    int8_t* eb = hexp + (size_t)r * nb;
+    for (int b = 0; b < nb; ++b) {
+        const int e = eb[b];
+        if (e == emin) continue;
+        uint4* p = reinterpret_cast<uint4*>(h + (size_t)r * I + b * 32);
+        for (int q = 0; q < 4; ++q) {
+            const uint4 v = p[q];
+            uint32_t w[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const float lo = __builtin_ldexpf((float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] & 0xffffu)),
+                                                  emin - e);
+                const float hi = __builtin_ldexpf((float)__builtin_bit_cast(_Float16, (uint16_t)(w[j] >> 16)),
+                                                  emin - e);
+                w[j] = (uint32_t)__builtin_bit_cast(uint16_t, (_Float16)lo) |
+                       ((uint32_t)__builtin_bit_cast(uint16_t, (_Float16)hi) << 16);
+            }
+            p[q] = make_uint4(w[0], w[1], w[2], w[3]);
+        }
+        eb[b] = (int8_t)emin;
     }
 }
 
@@ -836,7 +845,7 @@ int launch_down_big(const ExpertPtrs& P, uint16_t* h, int8_t* hexp, int R, const
                     const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
                     hipStream_t s) {
     if (!big_w4_shape_ok(H, I)) return -2;
-    hipLaunchKernelGGL(h_rescale_kernel, dim3((unsigned)((R + 3) / 4)), dim3(256), 0, s, h, hexp, R, I);
+    hipLaunchKernelGGL(h_rescale_kernel, dim3((unsigned)((R + 255) / 256)), dim3(256), 0, s, h, hexp, R, I);
     if (hipGetLastError() != hipSuccess) return -4;
     MmArgs a{};
     a.wq[0] = P.down_q; a.ws[0] = P.down_s; a.wq[1] = P.down_q; a.ws[1] = P.down_s;

@@ -169,3 +169,72 @@ def test_gemm_q_i8_unaligned_rows(oracle):
     torch.cuda.synchronize()
     ref = oracle.gemm_q_i8(8, xq.cpu().numpy(), xs.cpu().numpy(), w, out, _row_bytes(8, in_))
     assert rel_err(y.cpu().numpy(), ref) < 1e-5
+
+
+@pytest.mark.parametrize("types", [(18, 18, 23), (8, 8, 8), (23, 23, 18)])
+def test_moe_expert_ffn_q_i8_matrix_cores(oracle, types):
+    # n * topk = 2048 routed rows with the grouping scratch: the matrix-core
+    # phases (v_mfma_i32_32x32x32_i8 per 32-block, then the fp32 rescale; the
+    # reference's tensor-core policy, cuda/qgemm.cu:1563-1587) on the types
+    # whose scale is uniform over each 32-block. Link by link as above:
+    # h_act against the oracle's fp64 sums of the same integer products
+    # (1e-5), (hq, hs) bit for bit against the oracle's quantizer of that
+    # h_act, out against the oracle's int8 down and slot-order combine (1e-5);
+    # then the fp32 layer within 3e-2, and the token-major run (no grouping:
+    # the VALU kernels): h_act within 1e-5, the output within 1e-2 (after the
+    # requantization of h, see below).
+    H, I, E, k, n = 512, 256, 8, 4, 512
+    rng = np.random.default_rng(sum(types) + 123)
+    gq = random_gguf_rows(types[0], E * I, H, rng)
+    uq = random_gguf_rows(types[1], E * I, H, rng)
+    dq = random_gguf_rows(types[2], E * H, I, rng)
+    rb = (_row_bytes(types[0], H), _row_bytes(types[1], H), _row_bytes(types[2], I))
+    x = rng.standard_normal((n, H)).astype(np.float32)
+    ids = np.stack([rng.permutation(E)[:k] for _ in range(n)]).astype(np.int32)
+    w = rng.uniform(0.1, 1.0, (n, k)).astype(np.float32)
+    deq = lambda t, q, rows, K: [oracle.gguf_dequant_rows(t, q[e * rows:(e + 1) * rows], rows, K)
+                                 for e in range(E)]
+    G, U, D = deq(types[0], gq, I, H), deq(types[1], uq, I, H), deq(types[2], dq, H, I)
+    ref32 = oracle.moe_forward_streamed(x, ids, w, lambda e: (G[e], U[e], D[e]))
+    xq, xs = _quant(_dev(x))
+    outs = []
+    for grouped in (True, False):
+        h_act = torch.full((n * k, I), float("nan"), device="cuda")
+        hq = torch.empty(n * k, I, dtype=torch.int8, device="cuda")
+        hs = torch.empty(n * k, I // 32, device="cuda")
+        dpart = torch.empty(n * k * H, device="cuda")
+        out = torch.full((n, H), float("nan"), device="cuda")
+        disp = (torch.full((3 * E + 1 + n * k,), -7, dtype=torch.int32, device="cuda")
+                if grouped else None)
+        ops.ref_moe_expert_ffn_q_i8(types, xq, xs, _dev(ids), _dev(w), _dev(gq), _dev(uq),
+                                    _dev(dq), I, E, rb, h_act, hq, hs, dpart, out, disp)
+        torch.cuda.synchronize()
+        outs.append((h_act.cpu().numpy(), hq.cpu().numpy(), hs.cpu().numpy(),
+                     out.cpu().numpy()))
+    h_g, hq_g, hs_g, out_g = outs[0]
+    assert np.isfinite(h_g).all() and np.isfinite(out_g).all()
+    xq_h, xs_h = xq.cpu().numpy(), xs.cpu().numpy()
+    flat = ids.reshape(-1)
+    h_ref = np.empty((n * k, I))
+    for e in range(E):
+        rows = np.nonzero(flat == e)[0]
+        t = rows // k
+        g = oracle.gemm_q_i8(types[0], xq_h[t], xs_h[t], gq[e * I:(e + 1) * I], I, rb[0])
+        u = oracle.gemm_q_i8(types[1], xq_h[t], xs_h[t], uq[e * I:(e + 1) * I], I, rb[1])
+        h_ref[rows] = _silu(g) * u
+    assert rel_err(h_g, h_ref) < 1e-5
+    q, s = oracle.quant_act_q8(h_g)
+    assert np.array_equal(hq_g, q) and np.array_equal(hs_g, s)
+    ref = np.zeros((n, H))
+    for e in range(E):
+        rows = np.nonzero(flat == e)[0]
+        y = oracle.gemm_q_i8(types[2], hq_g[rows], hs_g[rows], dq[e * H:(e + 1) * H], H, rb[2])
+        for j, r in enumerate(rows):
+            ref[r // k] += w.reshape(-1)[r] * y[j]
+    assert rel_err(out_g, ref) < 1e-5
+    assert rel_err(out_g, ref32) < 3e-2
+    # Across the two paths h_act differs by fp32 summation order (~1e-7), which
+    # moves a few h values across an int8 rounding boundary when h is
+    # requantized; each path is exact against the oracle given its own h.
+    assert rel_err(outs[1][0], h_g) < 1e-5
+    assert rel_err(outs[1][3], out_g) < 1e-2

@@ -11,7 +11,11 @@ index the full E = 256 weight arrays). Every token is checked: the fp32 path
 within 1e-4 of the oracle's fp32 forward on the dequantized weights (as the
 small-shape tests), the int8 path within the reference's 3e-2
 (tests/test_qgemm.cpp:351-352) of the same forward; grouped and token-major
-runs of the int8 path are bit-identical.
+runs of the int8 path are bit-identical below 2048 grouped rows, and within
+1e-2 of each other from there (the grouped run then takes the matrix-core
+kernels, whose h differs in fp32 rounding, which the int8 requantization of h
+can turn into a code step; tests/test_gpu_gguf_i8.py checks that path link by
+link against the oracle).
 """
 import numpy as np
 import pytest
@@ -110,4 +114,10 @@ def test_served_shape_int8_activations(oracle, served, n):
         outs.append(out.cpu().numpy())
     assert np.isfinite(outs[0]).all()
     assert rel_err(outs[0], ref32) < 3e-2, rel_err(outs[0], ref32)
-    assert np.array_equal(outs[0], outs[1])
+    if n * K < 2048:
+        assert np.array_equal(outs[0], outs[1])
+    else:
+        # The grouped run takes the matrix-core kernels (exact int32 dots per
+        # 32-block, fp32 sums in another order than the VALU kernels); the
+        # requantization of h turns that into int8 flips of a few h values.
+        assert rel_err(outs[1], outs[0]) < 1e-2
