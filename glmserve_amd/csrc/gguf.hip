@@ -1179,32 +1179,55 @@ int launch_gg_quant_q8(const float* x, long total, int8_t* xq, float* xs, hipStr
 // activations, then * weight scale * activation scale added in fp32.
 //
 // Tiles: the routed rows grouped by expert (gg_group_kernel) in tiles of up
-// to kGgMmaTM rows. A workgroup (4 waves) computes one tile x kGgMmaRows
-// weight rows: phase 1 64 features (wave w: the gate rows and up rows of
-// features 16 w .. 16 w + 15, stacked as one 32-row block so that a lane
-// holds gate and up of the same feature), phase 2 128 output rows (wave w:
-// rows 32 w .. 32 w + 31). Per 256-K chunk the workgroup decodes its weight
-// rows into LDS as int8 plus a scale per 32-block (the integer-fragment
-// decode of gg_dec8i, whose per-32 scale is uniform over a block for Q8_0,
-// IQ3_XXS and IQ4_XS) and stages the tile's int8 activation rows and
-// scales; then each wave runs v_mfma_i32_32x32x32_i8 per 32-block over its
-// 32 weight rows x 4 blocks of 32 rows (A = weights, B = activations: a
-// lane's 16 outputs are one row's 16 weight rows, so their 16 weight scales
-// come as 4 broadcast LDS reads and its row's activation scale as one).
-// Rows past the tile's end repeat its last row and are not stored.
+// to kGgMmaTM rows. A workgroup (8 waves) computes one tile x kGgMmaRows
+// weight rows: phase 1 128 features (wave w: the gate rows and the up rows
+// of features 16 w .. 16 w + 15, stacked as one 32-row block, so a lane
+// holds gate and up of the same feature), phase 2 256 output rows (wave w:
+// rows 32 w .. 32 w + 31). Per 256-K chunk:
+//   - the chunk's raw block bytes of the workgroup's weight rows (IQ3_XXS,
+//     IQ4_XS) and the tile's int8 activation rows and scales arrive in
+//     registers, loaded one chunk ahead (coalesced: two threads per row);
+//   - they are written to LDS; each thread decodes 4 of its row's 32-element
+//     sub-blocks to int8 plus the sub-block's scale (the decode of
+//     gg_dec8i_any per 32 elements: the scale read and computed once per
+//     sub-block; the same float operations, so the same scale values);
+//     Q8_0 sub-blocks are read from global memory directly;
+//   - each wave runs v_mfma_i32_32x32x32_i8 per 32-block over its 32 weight
+//     rows x the tile's 4 blocks of 32 rows (A = weights, B = activations:
+//     a lane's 16 outputs are one row's 16 weight rows, so their 16 weight
+//     scales come as 4 broadcast LDS reads and the row's activation scale
+//     as one), then acc += (d * w_scale) * x_scale in fp32.
+// Rows past the tile's end repeat its last row and are not stored; 32-row
+// blocks wholly past it skip their MFMAs.
 constexpr int kGgMmaMinRows = 2048;
 constexpr int kGgMmaTM = 128;       // routed rows per tile
-constexpr int kGgMmaRows = 128;     // weight rows per workgroup
+constexpr int kGgMmaRows = 256;     // weight rows per workgroup (8 waves x 32)
 constexpr int kGgMmaStride = 272;   // LDS bytes per int8 row of a chunk (256 + 16 padding)
+constexpr int kGgMmaThreads = 512;
 
 typedef int gg_i32x4 __attribute__((ext_vector_type(4)));
 typedef int gg_i32x16 __attribute__((ext_vector_type(16)));
 
+// Raw chunk bytes of one row in LDS (IQ3_XXS 98, IQ4_XS 136; Q8_0 is decoded
+// from global memory) and the per-thread register words that carry them.
+template <uint32_t T>
+struct GgMmaRaw {
+    static constexpr int kBytes = T == 18 ? 98 : T == 23 ? 136 : 0;
+    static constexpr int kStride = T == 18 ? 104 : T == 23 ? 144 : 16;
+    // IQ3_XXS rows are 2-byte aligned: 16-bit pieces, 25 per thread; IQ4_XS
+    // rows are 4-byte aligned: dwords, 17 per thread.
+    static constexpr int kPiece = T == 18 ? 2 : 4;
+    static constexpr int kPieces = kBytes / kPiece;
+    static constexpr int kPerThread = (kPieces + 1) / 2;
+};
+
+template <uint32_t T>
 struct GgMmaLds {
     int8_t wq[kGgMmaRows * kGgMmaStride];
     int8_t xq[kGgMmaTM * kGgMmaStride];
     float ws[8][kGgMmaRows];   // [32-block][weight row]
     float xs[8][kGgMmaTM];     // [32-block][tile row]
+    uint8_t raw[kGgMmaRows * GgMmaRaw<T>::kStride];
     uint32_t grid[256];        // IQ3_XXS codebook
     uint32_t sgn[256];         // IQ3_XXS sign byte masks, two words per 7-bit pattern
     int src[kGgMmaTM];         // activation row of each tile row
@@ -1217,9 +1240,51 @@ __host__ __device__ constexpr int gg_mma_chunk_bytes(uint32_t t) {
 }
 bool gg_mma_type_ok(uint32_t t) { return t == 8 || t == 18 || t == 23; }
 
+// Sub-block ib (32 elements) of a chunk as 8 int8 words plus its scale.
+// IQ3_XXS / IQ4_XS from the LDS copy of the chunk (b), Q8_0 from global (g).
+template <uint32_t T>
+__device__ __forceinline__ void gg_mma_sub(const uint8_t* b, const uint8_t* g, int ib,
+                                           const uint32_t* grid, const uint32_t* sgn, uint32_t (&w)[8],
+                                           float& ds) {
+    if constexpr (T == 18) {
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(b);
+        const uint32_t aux = (uint32_t)h[33 + 2 * ib] | ((uint32_t)h[34 + 2 * ib] << 16);
+        ds = (float)__builtin_bit_cast(_Float16, h[0]) * (0.5f + (float)(aux >> 28)) * 0.5f;
+#pragma unroll
+        for (int l = 0; l < 4; ++l) {
+            const uint32_t i7 = (aux >> (7 * l)) & 127u;
+            const uint2 m = *reinterpret_cast<const uint2*>(sgn + 2 * i7);
+            const uint32_t qs = h[1 + 4 * ib + l];
+            const uint32_t g0 = grid[qs & 255u], g1 = grid[qs >> 8];
+            w[2 * l] = (g0 ^ m.x) + (m.x & 0x01010101u);
+            w[2 * l + 1] = (g1 ^ m.y) + (m.y & 0x01010101u);
+        }
+    } else if constexpr (T == 23) {
+        const uint16_t sh = *reinterpret_cast<const uint16_t*>(b + 2);
+        const int lo = (b[4 + ib / 2] >> (4 * (ib & 1))) & 15;
+        const int hi = (sh >> (2 * ib)) & 3;
+        ds = (float)__builtin_bit_cast(_Float16, *reinterpret_cast<const uint16_t*>(b)) *
+             (float)((int)(int8_t)(uint8_t)(lo | (hi << 4)) - 32);
+        const uint2 q01 = *reinterpret_cast<const uint2*>(b + 8 + 16 * ib);
+        const uint2 q23 = *reinterpret_cast<const uint2*>(b + 16 + 16 * ib);
+        const uint32_t q[4] = {q01.x, q01.y, q23.x, q23.y};
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            w[j] = gg_iq4nl4(q[j] & 0x0f0f0f0fu);
+            w[4 + j] = gg_iq4nl4((q[j] >> 4) & 0x0f0f0f0fu);
+        }
+    } else {   // Q8_0: block ib of the chunk (34 bytes, 2-byte aligned) in global memory
+        const uint16_t* h = reinterpret_cast<const uint16_t*>(g + 34 * ib);
+        ds = (float)__builtin_bit_cast(_Float16, h[0]);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) w[j] = (uint32_t)h[1 + 2 * j] | ((uint32_t)h[2 + 2 * j] << 16);
+    }
+}
+
 template <bool DOWN, uint32_t T>
-__global__ __launch_bounds__(256) void gg_mma_kernel(GgMoeArgs a) {
-    __shared__ __align__(16) GgMmaLds L;
+__global__ __launch_bounds__(kGgMmaThreads) void gg_mma_kernel(GgMoeArgs a) {
+    using RW = GgMmaRaw<T>;
+    __shared__ __align__(16) GgMmaLds<T> L;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int E = a.E;
@@ -1243,15 +1308,18 @@ __global__ __launch_bounds__(256) void gg_mma_kernel(GgMoeArgs a) {
         L.src[tid] = DOWN ? r : r / a.topk;
     }
     if constexpr (T == 18) {
-        L.grid[tid] = c_iq3xxs_grid[tid];
-        const uint32_t pe = (uint32_t)tid >> 1;
-        const uint32_t sg = pe | ((uint32_t)(__builtin_popcount(pe) & 1) << 7);
-        L.sgn[tid] = gg_bytemask4(sg >> (4 * (tid & 1)));
+        if (tid < 256) {
+            L.grid[tid] = c_iq3xxs_grid[tid];
+            const uint32_t pe = (uint32_t)tid >> 1;
+            const uint32_t sg = pe | ((uint32_t)(__builtin_popcount(pe) & 1) << 7);
+            L.sgn[tid] = gg_bytemask4(sg >> (4 * (tid & 1)));
+        }
     }
     const int K = DOWN ? a.I : a.H;
     const int nch = K / 256;
     constexpr int CB = gg_mma_chunk_bytes(T);
-    // This thread decodes weight row rr (fragments 16 fh .. 16 fh + 15 of each chunk).
+    // This thread stages and decodes half (sub-blocks 4 fh .. 4 fh + 3) of
+    // weight row rr of the workgroup.
     const int rr = tid >> 1, fh = tid & 1;
     const uint8_t* wrow;
     if constexpr (DOWN) {
@@ -1259,17 +1327,38 @@ __global__ __launch_bounds__(256) void gg_mma_kernel(GgMoeArgs a) {
         wrow = a.down_q + ((size_t)e * a.H + o) * a.down_rb;
     } else {
         const int j = rr & 31;
-        const size_t f = (size_t)blockIdx.y * 64 + 16 * (rr >> 5) + (j & 15);
+        const size_t f = (size_t)blockIdx.y * 128 + 16 * (rr >> 5) + (j & 15);
         wrow = j < 16 ? a.gate_q + ((size_t)e * a.I + f) * a.gate_rb : a.up_q + ((size_t)e * a.I + f) * a.up_rb;
     }
     __syncthreads();
     const int8_t* X = DOWN ? a.hq : a.xq;
     const float* XS = DOWN ? a.hs : a.xs;
-    // This thread stages half (128 B) of tile row xr's chunk, and (tid < 128)
-    // that row's 8 block scales.
-    const int xr = tid >> 1, xh = tid & 1;
-    const int8_t* xrow = X + (size_t)L.src[xr] * K + xh * 128;
-    const float* xsrow = XS + (size_t)L.src[tid & (kGgMmaTM - 1)] * (K / 32);
+    // Activations: this thread stages 64 B (a quarter) of tile row xr's chunk
+    // and (tid < 256) half of row tid / 2's 8 block scales.
+    const int xr = tid >> 2, xqtr = tid & 3;
+    const int8_t* xrow = X + (size_t)L.src[xr] * K + xqtr * 64;
+    const float* xsrow = XS + (size_t)L.src[(tid >> 1) & (kGgMmaTM - 1)] * (K / 32) + 4 * (tid & 1);
+
+    // The next chunk's loads (registers).
+    uint32_t rv[RW::kPerThread > 0 ? RW::kPerThread : 1];
+    uint4 xv0, xv1, xv2, xv3;
+    float4 sv = make_float4(0.f, 0.f, 0.f, 0.f);
+#define GG_MMA_LOAD(cc)                                                                              \
+    do {                                                                                             \
+        if constexpr (RW::kBytes > 0) {                                                              \
+            const uint8_t* src_ = wrow + (size_t)(cc) * CB;                                          \
+            _Pragma("unroll") for (int i = 0; i < RW::kPerThread; ++i) {                             \
+                const int p = fh * RW::kPerThread + i;                                               \
+                if (p < RW::kPieces) {                                                               \
+                    if constexpr (RW::kPiece == 2) rv[i] = reinterpret_cast<const uint16_t*>(src_)[p]; \
+                    else rv[i] = reinterpret_cast<const uint32_t*>(src_)[p];                         \
+                }                                                                                    \
+            }                                                                                        \
+        }                                                                                            \
+        const uint4* xp_ = reinterpret_cast<const uint4*>(xrow + (size_t)(cc) * 256);                \
+        xv0 = xp_[0]; xv1 = xp_[1]; xv2 = xp_[2]; xv3 = xp_[3];                                      \
+        if (tid < 2 * kGgMmaTM) sv = *reinterpret_cast<const float4*>(xsrow + (cc) * 8);             \
+    } while (0)
 
     float acc[4][16];
 #pragma unroll
@@ -1277,31 +1366,47 @@ __global__ __launch_bounds__(256) void gg_mma_kernel(GgMoeArgs a) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) acc[tb][i] = 0.0f;
     const int ar = wave * 32 + (lane & 31), hh = lane >> 5;
+    // 32-row blocks of the tile holding rows: an expert's last tile (at
+    // prefill sizes often its only one) skips the MFMAs of the empty blocks.
+    const int ntb = __builtin_amdgcn_readfirstlane((nr + 31) / 32);
+    GG_MMA_LOAD(0);
     for (int c = 0; c < nch; ++c) {
-        uint4 xv[8];
+        // Stage chunk c.
+        if constexpr (RW::kBytes > 0) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) xv[j] = reinterpret_cast<const uint4*>(xrow + (size_t)c * 256)[j];
-        float4 s0 = make_float4(0.f, 0.f, 0.f, 0.f), s1 = s0;
-        if (tid < kGgMmaTM) {
-            s0 = reinterpret_cast<const float4*>(xsrow + c * 8)[0];
-            s1 = reinterpret_cast<const float4*>(xsrow + c * 8)[1];
+            for (int i = 0; i < RW::kPerThread; ++i) {
+                const int p = fh * RW::kPerThread + i;
+                if (p < RW::kPieces) {
+                    if constexpr (RW::kPiece == 2)
+                        reinterpret_cast<uint16_t*>(L.raw + rr * RW::kStride)[p] = (uint16_t)rv[i];
+                    else
+                        reinterpret_cast<uint32_t*>(L.raw + rr * RW::kStride)[p] = rv[i];
+                }
+            }
         }
-        const uint8_t* wc = wrow + (size_t)c * CB;
-#pragma unroll 4
-        for (int j = 0; j < 16; ++j) {
-            const int f = fh * 16 + j, kk = 8 * f;
-            int w0, w1;
-            float ds, dm;
-            gg_dec8i_any<true>(T, wc, kk, L.grid, L.sgn, w0, w1, ds, dm);
-            *reinterpret_cast<int2*>(L.wq + rr * kGgMmaStride + kk) = make_int2(w0, w1);
-            if ((f & 3) == 0) L.ws[f >> 2][rr] = ds;
+        {
+            uint4* xd = reinterpret_cast<uint4*>(L.xq + xr * kGgMmaStride + xqtr * 64);
+            xd[0] = xv0; xd[1] = xv1; xd[2] = xv2; xd[3] = xv3;
         }
+        if (tid < 2 * kGgMmaTM) {
+            const int t = tid >> 1, b0 = 4 * (tid & 1);
+            L.xs[b0][t] = sv.x; L.xs[b0 + 1][t] = sv.y; L.xs[b0 + 2][t] = sv.z; L.xs[b0 + 3][t] = sv.w;
+        }
+        __syncthreads();
+        // The next chunk (the last one again at the end: harmless reloads)
+        // in flight during the decode and the MFMAs.
+        GG_MMA_LOAD(c + 1 < nch ? c + 1 : c);
+        // Decode this thread's 4 sub-blocks.
 #pragma unroll
-        for (int j = 0; j < 8; ++j)
-            *reinterpret_cast<uint4*>(L.xq + xr * kGgMmaStride + xh * 128 + 16 * j) = xv[j];
-        if (tid < kGgMmaTM) {
-            L.xs[0][tid] = s0.x; L.xs[1][tid] = s0.y; L.xs[2][tid] = s0.z; L.xs[3][tid] = s0.w;
-            L.xs[4][tid] = s1.x; L.xs[5][tid] = s1.y; L.xs[6][tid] = s1.z; L.xs[7][tid] = s1.w;
+        for (int s = 0; s < 4; ++s) {
+            const int ib = 4 * fh + s;
+            uint32_t w[8];
+            float ds;
+            gg_mma_sub<T>(L.raw + rr * RW::kStride, wrow + (size_t)c * CB, ib, L.grid, L.sgn, w, ds);
+            uint4* dst = reinterpret_cast<uint4*>(L.wq + rr * kGgMmaStride + 32 * ib);
+            dst[0] = make_uint4(w[0], w[1], w[2], w[3]);
+            dst[1] = make_uint4(w[4], w[5], w[6], w[7]);
+            L.ws[ib][rr] = ds;
         }
         __syncthreads();
 #pragma unroll 2
@@ -1315,14 +1420,16 @@ __global__ __launch_bounds__(256) void gg_mma_kernel(GgMoeArgs a) {
             }
 #pragma unroll
             for (int tb = 0; tb < 4; ++tb) {
-                const int xrow_l = tb * 32 + (lane & 31);
-                const gg_i32x4 B =
-                    *reinterpret_cast<const gg_i32x4*>(L.xq + xrow_l * kGgMmaStride + kb * 32 + hh * 16);
-                const gg_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, gg_i32x16{}, 0, 0, 0);
-                const float xsv = L.xs[kb][xrow_l];
+                if (tb < ntb) {   // blocks past the tile's rows skip (uniform)
+                    const int xrow_l = tb * 32 + (lane & 31);
+                    const gg_i32x4 B =
+                        *reinterpret_cast<const gg_i32x4*>(L.xq + xrow_l * kGgMmaStride + kb * 32 + hh * 16);
+                    const gg_i32x16 d = __builtin_amdgcn_mfma_i32_32x32x32_i8(A, B, gg_i32x16{}, 0, 0, 0);
+                    const float xsv = L.xs[kb][xrow_l];
 #pragma unroll
-                for (int i = 0; i < 16; ++i)
-                    acc[tb][i] = __builtin_fmaf((float)d[i] * wsv[i], xsv, acc[tb][i]);
+                    for (int i = 0; i < 16; ++i)
+                        acc[tb][i] = __builtin_fmaf((float)d[i] * wsv[i], xsv, acc[tb][i]);
+                }
             }
         }
         __syncthreads();
@@ -1342,7 +1449,7 @@ __global__ __launch_bounds__(256) void gg_mma_kernel(GgMoeArgs a) {
                     make_float4(acc[tb][4 * q], acc[tb][4 * q + 1], acc[tb][4 * q + 2], acc[tb][4 * q + 3]);
         } else {
             // i < 8: gate of feature 8 (i / 4) + 4 hh + i % 4; i + 8: its up.
-            float* dst = a.h_act + r * a.I + (size_t)blockIdx.y * 64 + wave * 16 + 4 * hh;
+            float* dst = a.h_act + r * a.I + (size_t)blockIdx.y * 128 + wave * 16 + 4 * hh;
 #pragma unroll
             for (int q = 0; q < 2; ++q) {
                 float hv[4];
@@ -1354,6 +1461,8 @@ __global__ __launch_bounds__(256) void gg_mma_kernel(GgMoeArgs a) {
     }
 }
 
+#undef GG_MMA_LOAD
+
 // The matrix-core phases for a batch the caller grouped with kGgMmaTM-row
 // tiles; h_act is requantized into (hq, hs) between them.
 static int gg_mma_phases(const GgMoeArgs& a, hipStream_t s) {
@@ -1364,8 +1473,8 @@ static int gg_mma_phases(const GgMoeArgs& a, hipStream_t s) {
         else f(std::integral_constant<uint32_t, 23>{});
     };
     by(a.gate_type, [&](auto tc) {
-        hipLaunchKernelGGL((gg_mma_kernel<false, decltype(tc)::value>), dim3(tiles, (unsigned)(a.I / 64)),
-                           dim3(256), 0, s, a);
+        hipLaunchKernelGGL((gg_mma_kernel<false, decltype(tc)::value>), dim3(tiles, (unsigned)(a.I / 128)),
+                           dim3(kGgMmaThreads), 0, s, a);
     });
     if (hipGetLastError() != hipSuccess) return -4;
     if (launch_gg_quant_q8(a.h_act, (long)a.n * a.topk * a.I, const_cast<int8_t*>(a.hq),
@@ -1373,7 +1482,7 @@ static int gg_mma_phases(const GgMoeArgs& a, hipStream_t s) {
         return -4;
     by(a.down_type, [&](auto tc) {
         hipLaunchKernelGGL((gg_mma_kernel<true, decltype(tc)::value>),
-                           dim3(tiles, (unsigned)(a.H / kGgMmaRows)), dim3(256), 0, s, a);
+                           dim3(tiles, (unsigned)(a.H / kGgMmaRows)), dim3(kGgMmaThreads), 0, s, a);
     });
     return hipGetLastError() == hipSuccess ? 0 : -4;
 }
@@ -1426,9 +1535,9 @@ static int gg_moe(GgMoeArgs a, float* out, int* dispatch, hipStream_t s) {
     if constexpr (I8) {
         const bool al = ((uintptr_t)a.xq & 15) == 0 && ((uintptr_t)a.hq & 15) == 0 &&
                         ((uintptr_t)a.xs & 15) == 0 && ((uintptr_t)a.hs & 15) == 0 &&
-                        ((uintptr_t)a.gate_q & 1) == 0 && ((uintptr_t)a.up_q & 1) == 0 &&
-                        ((uintptr_t)a.down_q & 1) == 0 && (a.gate_rb & 1) == 0 && (a.up_rb & 1) == 0 &&
-                        (a.down_rb & 1) == 0;
+                        ((uintptr_t)a.gate_q & 3) == 0 && ((uintptr_t)a.up_q & 3) == 0 &&
+                        ((uintptr_t)a.down_q & 3) == 0 && (a.gate_rb & 3) == 0 && (a.up_rb & 3) == 0 &&
+                        (a.down_rb & 3) == 0;
         if (dispatch && nk >= kGgMmaMinRows && gt == ut && gg_mma_type_ok(gt) && gg_mma_type_ok(dt) &&
             H % 256 == 0 && a.I % 256 == 0 && al) {
             hipLaunchKernelGGL(gg_group_kernel, dim3(1), dim3(1024), (size_t)2 * E * 4, s, ids, nk, E,
