@@ -783,6 +783,201 @@ __global__ __launch_bounds__(kSmallThreads) void router_finish_kernel(
     dispatch_block<kSmallThreads>(sids, n, topk, E, d, lds);
 }
 
+// ---------------------------------------------------------------------------
+// Mid-size batches (kGemvMinTokens <= n < kTiledMinTokens, selection in the
+// same call): router_gemv_kernel, then router_fold_select_kernel.
+// router_gemv_kernel: grid (ceil(nchunks / 4), ceil(E / 64), ceil(n / NT)) of
+// 4 waves. Wave w of workgroup (cb, eb, tg) takes the 128-K chunk
+// c = 4 cb + w, lane l the expert e = 64 eb + l, and tokens NT tg .. + NT.
+// The lane keeps its expert's 128 chunk weights in registers (each converted
+// once for the NT tokens); the activations are wave-uniform, so they are
+// loaded and split into fp32 on the scalar unit and feed the FMAs as scalar
+// operands: about one vector instruction per product. Each lane writes the
+// ascending-K chain from zero of every token (the fixed chunk order of
+// router_partials_kernel) to part[c][t][e]. The first expert block's lanes
+// t < NT also write the chunk's activation sums xsum[t][c] (ascending K).
+// router_fold_select_kernel: one workgroup per token adds the chunk partials
+// in chunk order ((0 + p0) + p1) + ..., writes the logits, and one wave
+// selects: the logit of every expert bit-identical to the other paths.
+// ---------------------------------------------------------------------------
+constexpr int kGemvMinTokens = 9;
+constexpr int kGemvChunksPerBlock = 4;   // waves per workgroup
+
+template <int NT>
+__global__ __launch_bounds__(64 * kGemvChunksPerBlock) void router_gemv_kernel(
+    const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, int n, int H, int E,
+    float* __restrict__ part, float* __restrict__ xsum, unsigned int* __restrict__ fold_ticket) {
+    constexpr int KB = kGemvChunksPerBlock * kRouterKC;   // K of the workgroup
+    constexpr int NTH = 64 * kGemvChunksPerBlock;
+    // LDS: the group's activations over the workgroup's K range as fp32,
+    // xl[t][k], first (their reads then fit the instruction's offset field),
+    // then the weight rows.
+    __shared__ __align__(16) char glds[NT * KB * 4 + kGemvChunksPerBlock * 64 * 256];
+    float (*xl)[KB] = reinterpret_cast<float (*)[KB]>(glds);
+    char (*wl)[64 * 256] = reinterpret_cast<char (*)[64 * 256]>(glds + NT * KB * 4);
+    const int nchunks = H / kRouterKC;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
+    const int c = blockIdx.x * kGemvChunksPerBlock + wave;
+    const int e = blockIdx.y * 64 + lane;
+    const int t0 = blockIdx.z * NT, nt = min(NT, n - t0);
+    const int k0 = blockIdx.x * KB;
+    const bool live = e < E && c < nchunks;
+    // The fold kernel's ticket (nothing in this launch reads it).
+    if (fold_ticket && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
+        reset_dev(fold_ticket);
+    // The wave's 64 expert rows of its chunk, 256 B each, staged by LDS-DMA
+    // (whole cache lines per instruction): 16-byte piece o of row R at slot
+    // o ^ (R & 15), so the lanes reading their own rows hit distinct banks.
+    {
+        const int cc = c < nchunks ? c : nchunks - 1;
+#pragma unroll
+        for (int b = 0; b < 16; ++b) {
+            const int R = 4 * b + (lane >> 4);
+            const int er = min((int)blockIdx.y * 64 + R, E - 1);
+            const int o = (lane & 15) ^ (R & 15);
+            dma16(wr + (size_t)er * H + cc * kRouterKC + o * 8, &wl[wave][b * 1024]);
+        }
+    }
+    // Stage: 8 activations per thread per step, rows past nt repeat the last
+    // row (not stored), chunks past nchunks are not read.
+#pragma unroll
+    for (int i = tid; i < NT * KB / 8; i += NTH) {
+        const int t = i / (KB / 8), kk = (i - t * (KB / 8)) * 8;
+        const int tt = t < nt ? t : nt - 1;
+        uint4 v = make_uint4(0u, 0u, 0u, 0u);
+        if (k0 + kk < H) v = *reinterpret_cast<const uint4*>(x + (size_t)(t0 + tt) * H + k0 + kk);
+        const uint32_t xd[4] = {v.x, v.y, v.z, v.w};
+        float4 lo, hi;
+        lo.x = bf16_to_f32(xd[0] & 0xffffu); lo.y = __uint_as_float(xd[0] & 0xffff0000u);
+        lo.z = bf16_to_f32(xd[1] & 0xffffu); lo.w = __uint_as_float(xd[1] & 0xffff0000u);
+        hi.x = bf16_to_f32(xd[2] & 0xffffu); hi.y = __uint_as_float(xd[2] & 0xffff0000u);
+        hi.z = bf16_to_f32(xd[3] & 0xffffu); hi.w = __uint_as_float(xd[3] & 0xffff0000u);
+        *reinterpret_cast<float4*>(&xl[t][kk]) = lo;
+        *reinterpret_cast<float4*>(&xl[t][kk + 4]) = hi;
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    if (c >= nchunks) return;   // wave-uniform; no barrier follows
+    uint4 wv[kRouterKC / 8];
+#pragma unroll
+    for (int j = 0; j < kRouterKC / 8; ++j)
+        wv[j] = *reinterpret_cast<const uint4*>(&wl[wave][lane * 256 + ((j ^ (lane & 15)) << 4)]);
+    const float* xw = &xl[0][wave * kRouterKC];
+    float acc[NT];
+#pragma unroll
+    for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
+    // Step j: the 8 activations of every token (LDS broadcasts: every lane
+    // reads the same bytes), read one step ahead.
+    auto rd = [&](int j, float4 (&xv)[NT][2]) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            xv[t][0] = *reinterpret_cast<const float4*>(xw + t * KB + j * 8);
+            xv[t][1] = *reinterpret_cast<const float4*>(xw + t * KB + j * 8 + 4);
+        }
+    };
+    float4 xa[NT][2], xb[NT][2];
+    rd(0, xa);
+#pragma unroll
+    for (int j = 0; j < kRouterKC / 8; ++j) {
+        float4 (&cur)[NT][2] = (j & 1) ? xb : xa;
+        float4 (&nxt)[NT][2] = (j & 1) ? xa : xb;
+        if (j + 1 < kRouterKC / 8) rd(j + 1, nxt);
+        const uint32_t wd[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
+        float wf[8];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            wf[2 * q] = bf16_to_f32(wd[q] & 0xffffu);
+            wf[2 * q + 1] = __uint_as_float(wd[q] & 0xffff0000u);
+        }
+#pragma unroll
+        for (int t = 0; t < NT; ++t) {
+            acc[t] = __builtin_fmaf(cur[t][0].x, wf[0], acc[t]);
+            acc[t] = __builtin_fmaf(cur[t][0].y, wf[1], acc[t]);
+            acc[t] = __builtin_fmaf(cur[t][0].z, wf[2], acc[t]);
+            acc[t] = __builtin_fmaf(cur[t][0].w, wf[3], acc[t]);
+            acc[t] = __builtin_fmaf(cur[t][1].x, wf[4], acc[t]);
+            acc[t] = __builtin_fmaf(cur[t][1].y, wf[5], acc[t]);
+            acc[t] = __builtin_fmaf(cur[t][1].z, wf[6], acc[t]);
+            acc[t] = __builtin_fmaf(cur[t][1].w, wf[7], acc[t]);
+        }
+        // Pin each step's chains here (otherwise the reads of later steps
+        // are hoisted and the arithmetic sunk).
+#pragma unroll
+        for (int t = 0; t < NT; ++t) asm volatile("" : "+v"(acc[t]));
+        __builtin_amdgcn_sched_barrier(0);
+    }
+    if (live) {
+#pragma unroll
+        for (int t = 0; t < NT; ++t)
+            if (t < nt) part[((size_t)c * n + t0 + t) * E + e] = acc[t];
+    }
+    if (xsum && blockIdx.y == 0 && lane < nt) {
+        float xs = 0.0f;
+        for (int k = 0; k < kRouterKC; ++k) xs += xw[lane * KB + k];
+        xsum[(size_t)(t0 + lane) * nchunks + c] = xs;
+    }
+}
+
+constexpr int kFoldThreads = 512;   // dispatch_block needs 8 waves
+
+template <int NJ>
+__global__ __launch_bounds__(kFoldThreads) void router_fold_select_kernel(
+    const float* __restrict__ part, int nchunks, const float* __restrict__ e_bias, int n, int E,
+    int topk, int norm_topk, float routed_scale, float* __restrict__ logits, int* __restrict__ ids,
+    float* __restrict__ w, unsigned int* __restrict__ ticket, DispOut d) {
+    __shared__ float lt[64 * NJ];
+    __shared__ uint32_t tscratch[kTopkScratch];
+    __shared__ int sids[8];
+    __shared__ int last;
+    __shared__ int dlds[dispatch_lds_ints<kFoldThreads>()];
+    const int t = blockIdx.x;
+    const size_t stride = (size_t)n * E;
+    for (int e = threadIdx.x; e < E; e += kFoldThreads) {
+        const float* p = part + (size_t)t * E + e;
+        // Up to 48 partials in flight (one round trip at H = 6144), added in
+        // chunk order.
+        float total = 0.0f;
+        for (int c = 0; c < nchunks; c += 48) {
+            float v[48];
+#pragma unroll
+            for (int u = 0; u < 48; ++u) v[u] = p[min(c + u, nchunks - 1) * stride];
+            const int m = min(48, nchunks - c);
+            if (m == 48) {
+#pragma unroll
+                for (int u = 0; u < 48; ++u) total = total + v[u];
+            } else {
+#pragma unroll
+                for (int u = 0; u < 48; ++u)
+                    if (u < m) total = total + v[u];
+            }
+        }
+        logits[(size_t)t * E + e] = total;
+        lt[e] = total;
+    }
+    __syncthreads();
+    if (threadIdx.x < 64) {
+        // With a ticket the ids also go out with device-coherent stores (the
+        // same values): the last workgroup to finish reads every token's ids
+        // with coherent loads and dispatches.
+        topk_wave_nj<false, NJ>(lt, e_bias, E, topk, norm_topk, routed_scale,
+                                ids + (size_t)t * topk, w + (size_t)t * topk, tscratch, nullptr,
+                                nullptr, ticket ? sids : nullptr);
+        if (ticket) {
+            if (threadIdx.x < topk) st_dev(ids + (size_t)t * topk + threadIdx.x, sids[threadIdx.x]);
+            drain_vm();
+            if (threadIdx.x == 0) last = ticket_dev(ticket) == (unsigned int)(n - 1);
+        }
+    }
+    if (!ticket) return;
+    __syncthreads();
+    if (!last) return;   // workgroup-uniform
+    dispatch_block<kFoldThreads, true>(ids, n, topk, E, d, dlds);
+}
+
+bool router_gemv_path(int n, int H, int E, int topk) {
+    return n >= kGemvMinTokens && router_small_path(n, H, E, topk);
+}
+
 bool router_small_path(int n, int H, int E, int topk) {
     return n < kTiledMinTokens && H % kRouterKC == 0 && H / kRouterKC <= kSmallMaxChunks &&
            E <= 64 * kMaxPerLane && topk <= 8;
@@ -804,7 +999,12 @@ size_t router_select_scratch_bytes(int n, int H, int E) {
     // The MFMA pass: S partials [nsplit][n][E], L~ partials of splits 1.. .
     const int z = n >= kTiledMinTokens ? router_mfma_splits(n, E) : 1;
     const size_t b = (size_t)(2 * z - 1) * n * E * 4;
-    const size_t c = (size_t)n * E * 4 * 2;   // small batches: order codes and scores
+    // Small batches: the order codes and scores; from kGemvMinTokens the
+    // chunk partials [H / 128][n][E] instead.
+    size_t c = (size_t)n * E * 4 * 2;
+    // (+ 256 bytes: the fold kernel's ticket.)
+    if (n >= kGemvMinTokens && n < kTiledMinTokens && (size_t)(H / kRouterKC) * n * E * 4 + 256 > c)
+        c = (size_t)(H / kRouterKC) * n * E * 4 + 256;
     const size_t m = a > b ? a : b;
     return m > c ? m : c;
 }
@@ -817,6 +1017,37 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
     const int nchunks = H / kRouterKC;
     if (dispatched) *dispatched = false;
     if (xf && !router_small_path(n, H, E, topk)) return -2;   // the caller converts x first
+    if (select && !xf && router_gemv_path(n, H, E, topk)) {
+        const size_t need = (size_t)nchunks * n * E * 4 + 256;
+        if (!scratch || router_select_scratch_bytes(n, H, E) < need) return -3;
+        // With the dispatch outputs the last fold workgroup dispatches too.
+        const bool dd = disp && E <= kDispMaxE;
+        unsigned int* ticket = dd ? reinterpret_cast<unsigned int*>(scratch + (size_t)nchunks * n * E)
+                                  : nullptr;
+        // Tokens per wave: 2 up to 16 tokens (more workgroups to fill the
+        // CUs), else 4 (measured per layer at 16 / 32 / 64 / 128 tokens: 8
+        // was 1-5 us slower, its workgroups stacking two to a CU).
+#ifdef GLMMOE_GEMV_NT
+        const int NT = GLMMOE_GEMV_NT;
+#else
+        const int NT = n <= 16 ? 2 : 4;
+#endif
+        dim3 grid((unsigned)((nchunks + kGemvChunksPerBlock - 1) / kGemvChunksPerBlock),
+                  (unsigned)((E + 63) / 64), (unsigned)((n + NT - 1) / NT));
+        auto gemv = NT == 2 ? router_gemv_kernel<2> : NT == 4 ? router_gemv_kernel<4>
+                                                                : router_gemv_kernel<8>;
+        hipLaunchKernelGGL(gemv, grid, dim3(64 * kGemvChunksPerBlock), 0, s, x, wr, n, H, E,
+                           scratch, xsum, ticket);
+        if (hipGetLastError() != hipSuccess) return -4;
+        auto fold = E <= 64 ? router_fold_select_kernel<1> : E <= 128 ? router_fold_select_kernel<2>
+                                   : E <= 256 ? router_fold_select_kernel<4> : router_fold_select_kernel<8>;
+        hipLaunchKernelGGL(fold, dim3((unsigned)n), dim3(kFoldThreads), 0, s, scratch, nchunks,
+                           e_bias, n, E, topk, norm_topk, routed_scale, logits, ids, w, ticket,
+                           dd ? *disp : DispOut{});
+        if (hipGetLastError() != hipSuccess) return -4;
+        if (dispatched) *dispatched = dd;
+        return 0;
+    }
     if (router_small_path(n, H, E, topk)) {
         // scratch: the order codes and scores [2][n][E] handed to the top-k.
         if (!scratch || router_select_scratch_bytes(n, H, E) < (size_t)2 * n * E * 4) return -3;

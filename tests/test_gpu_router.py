@@ -173,13 +173,16 @@ def test_layer_routing_bit_exact_large_batches(oracle, n):
 
 
 @pytest.mark.parametrize("H,E,k,n", [(1024, 64, 8, 1), (2048, 100, 6, 37), (8192, 512, 8, 9),
-                                     (6144, 256, 8, 255), (256, 16, 4, 8)])
+                                     (6144, 256, 8, 255), (6144, 256, 8, 64), (256, 16, 4, 8),
+                                     (768, 40, 4, 17)])
 def test_layer_routing_bit_exact_small_batches(oracle, H, E, k, n):
     """Below 256 tokens the layer computes logits, top-k and dispatch in one
     launch (workgroups hand over through tickets). ids, weights, the
     activation group sums and the dispatch must equal the oracle's bit for
     bit, with duplicated router rows forcing exact ties, E not a multiple of
-    64, E = 512 and the largest hidden size."""
+    64, E = 512 and the largest hidden size. From 9 tokens the logits come
+    from per-chunk partials folded in a second kernel; they are compared
+    too."""
     from moe_cases import SynthLayer
     from glmserve_amd.ops import ws_tensor
     L = SynthLayer(H, E, k, 128, seed=12)
@@ -201,6 +204,8 @@ def test_layer_routing_bit_exact_small_batches(oracle, H, E, k, n):
     wb = L.router_w.view(torch.int16).cpu().numpy().view(np.uint16)
     logits = oracle.router_logits_bf16(xb, wb)
     rid, rw = oracle.router_topk(logits, L.e_bias.cpu().numpy(), k, True, 2.5)
+    lg = ws_tensor(None, v.logits, ws, torch.float32, n * E).cpu().numpy().reshape(n, E)
+    assert np.array_equal(lg.view(np.uint32), logits.view(np.uint32))
     assert np.array_equal(ids, rid)
     assert np.array_equal(w.view(np.uint32), rw.view(np.uint32))
     xf = (xb.astype(np.uint32) << 16).view(np.float32).reshape(n, H // 128, 128)
