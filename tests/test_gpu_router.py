@@ -139,12 +139,14 @@ def test_router_logits_f32_bit_exact(oracle):
         assert np.array_equal(yb.cpu().numpy().view(np.uint32), (ref + bias[None, :]).view(np.uint32)), (n, H, E)
 
 
-@pytest.mark.parametrize("n", [256, 1000, 4096])
+@pytest.mark.parametrize("n", [256, 520, 1000, 4096])
 def test_layer_routing_bit_exact_large_batches(oracle, n):
     """From 256 tokens the layer routes with MFMA logits plus an exact
     fixed-order recompute of every expert that can reach the top-k; ids,
     weights and the activation group sums must still equal the oracle's bit
-    for bit. Duplicate router rows force exact ties between experts."""
+    for bit. Duplicate router rows force exact ties between experts. The
+    dispatch (one workgroup below 4096 ids, chunked from there) must give
+    the stable counting sort."""
     from moe_cases import SynthLayer
     from glmserve_amd.ops import ws_tensor
     H, E, k, I = 1024, 64, 8, 128
@@ -170,14 +172,22 @@ def test_layer_routing_bit_exact_large_batches(oracle, n):
     xf = (xb.astype(np.uint32) << 16).view(np.float32).reshape(n, H // 128, 128)
     rx = np.cumsum(xf, axis=2, dtype=np.float32)[:, :, -1].reshape(-1)
     assert np.array_equal(xs.view(np.uint32), rx.view(np.uint32))
+    offs = ws_tensor(None, v.expert_offsets, ws, torch.int32, E + 1).cpu().numpy()
+    st = ws_tensor(None, v.sorted_token_ids, ws, torch.int32, n * k).cpu().numpy()
+    flat = rid.reshape(-1)
+    order = np.argsort(flat, kind="stable")
+    assert np.array_equal(st, (order // k).astype(np.int32))
+    ref_offs = np.concatenate([[0], np.cumsum(np.bincount(flat, minlength=E))]).astype(np.int32)
+    assert np.array_equal(offs, ref_offs)
 
 
 @pytest.mark.parametrize("H,E,k,n", [(1024, 64, 8, 1), (2048, 100, 6, 37), (8192, 512, 8, 9),
                                      (6144, 256, 8, 255), (6144, 256, 8, 64), (256, 16, 4, 8),
                                      (768, 40, 4, 17)])
 def test_layer_routing_bit_exact_small_batches(oracle, H, E, k, n):
-    """Below 256 tokens the layer computes logits, top-k and dispatch in one
-    launch (workgroups hand over through tickets). ids, weights, the
+    """Below 256 tokens the layer's routing kernels (up to 8 tokens the
+    router kernel plus the gate/up prologue; from 9 the chunk-partials
+    kernel plus the fold / select / dispatch kernel). ids, weights, the
     activation group sums and the dispatch must equal the oracle's bit for
     bit, with duplicated router rows forcing exact ties, E not a multiple of
     64, E = 512 and the largest hidden size. From 9 tokens the logits come
