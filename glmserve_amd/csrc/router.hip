@@ -408,27 +408,39 @@ __device__ __forceinline__ float code_to_float(uint32_t c) {
     return __uint_as_float((c & 0x80000000u) ? (c & 0x7fffffffu) : ~c);
 }
 
-constexpr int kRefineWaves = 2;   // tokens (waves) per workgroup: small LDS, high occupancy
+constexpr int kRefineWaves = 2;   // tokens (waves) per workgroup with one wave per token
+// Below this many tokens each token gets kRefineSplit waves: the token waves
+// then do not fill the SIMDs, and the kernel takes one token's serial chain
+// of candidate passes; the waves split the candidates (every wave computes
+// the same bounds and candidate list).
+constexpr int kRefineSplitMax = 1024;
+constexpr int kRefineSplit = 4;
 
-template <int NJ>   // keys per lane: E <= 64 * NJ
-__global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
+// TW: waves per token (1: kRefineWaves tokens per workgroup; else one token
+// per workgroup of TW waves).
+template <int NJ, int TW>   // keys per lane: E <= 64 * NJ
+__global__ __launch_bounds__(TW == 1 ? kRefineWaves * 64 : TW * 64) void router_refine_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const float* __restrict__ e_bias, const float* __restrict__ sb, int n, int H, int E, int topk,
     float* __restrict__ logits, float* __restrict__ xsum, int nsplit) {
+    constexpr int TPW = TW == 1 ? kRefineWaves : 1;   // tokens per workgroup
     const int lane = threadIdx.x & 63;
-    const int t = blockIdx.x * kRefineWaves + (threadIdx.x >> 6);
-    if (t >= n) return;   // whole wave
+    const int slot = TW == 1 ? (int)(threadIdx.x >> 6) : 0;    // token slot of this wave
+    const int sub = TW == 1 ? 0 : (int)(threadIdx.x >> 6);     // this wave's share of the candidates
+    const int t = blockIdx.x * TPW + slot;
+    if (t >= n) return;   // whole wave (TW > 1: whole workgroup)
     const int nchunks = H / kRouterKC;
     // This lane's 128-K chunk of x (lanes past the chunk count hold zeros),
     // kept in LDS for the exact sums (registers go to the weight buffers).
-    __shared__ uint4 xl[kRefineWaves][kRouterKC / 8][64];
-    uint4 (*xw)[64] = xl[threadIdx.x >> 6];
-    {
+    __shared__ uint4 xl[TPW][kRouterKC / 8][64];
+    uint4 (*xw)[64] = xl[slot];
+    if (sub == 0) {
         const uint4* xp = reinterpret_cast<const uint4*>(x + (size_t)t * H + lane * kRouterKC);
 #pragma unroll
         for (int j = 0; j < kRouterKC / 8; ++j) xw[j][lane] = lane < nchunks ? xp[j] : make_uint4(0, 0, 0, 0);
     }
-    if (xsum && lane < nchunks) {
+    if constexpr (TW > 1) __syncthreads();   // wave 0 staged the token's x
+    if (xsum && sub == 0 && lane < nchunks) {
         float s = 0.0f;
 #pragma unroll
         for (int j = 0; j < kRouterKC / 8; ++j) {
@@ -490,14 +502,14 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
     const float T = tcode > 1u ? code_to_float(tcode) : -INFINITY;
     // Candidates in ascending expert order into this wave's LDS list; the rest
     // get -inf.
-    __shared__ int cl[kRefineWaves][64 * NJ];
+    __shared__ int cl[TPW * TW][64 * NJ];
     int* list = cl[threadIdx.x >> 6];
     int ncand = 0;
 #pragma unroll
     for (int j = 0; j < NJ; ++j) {
         const int e = lane + 64 * j;
         const bool cand = e < E && up[j] >= T;
-        if (e < E && !cand) lrow[e] = -INFINITY;
+        if (sub == 0 && e < E && !cand) lrow[e] = -INFINITY;
         const uint64_t mask = __ballot(cand);
         const int before = __builtin_popcountll(mask & ((1ull << lane) - 1));
         if (cand) list[ncand + before] = e;
@@ -510,7 +522,7 @@ __global__ __launch_bounds__(kRefineWaves * 64) void router_refine_kernel(
     // (few registers per wave) hides the weight loads.
     // Two candidates at a time: their loads in flight together and their
     // chains interleaved (each chain is still the ascending-K sum from zero).
-    for (int i = 0; i < ncand; i += 2) {
+    for (int i = 2 * sub; i < ncand; i += 2 * TW) {
         const bool two = i + 1 < ncand;
         const int ec0 = list[i], ec1 = two ? list[i + 1] : ec0;
         const uint4* wp0 = reinterpret_cast<const uint4*>(wr + (size_t)ec0 * H + lane * kRouterKC);
@@ -1108,11 +1120,20 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         hipLaunchKernelGGL(router_mfma_kernel, grid, dim3(256), kMfmaD * 2 * kMfmaTok * 128, s, x,
                            wr, n, H, E, logits, scratch, scratch + (size_t)nsplit * n * E, nsplit);
         if (hipGetLastError() != hipSuccess) return -4;
-        auto refine = E <= 64 ? router_refine_kernel<1> : E <= 128 ? router_refine_kernel<2>
-                                      : E <= 256 ? router_refine_kernel<4> : router_refine_kernel<8>;
-        hipLaunchKernelGGL(refine, dim3((unsigned)((n + kRefineWaves - 1) / kRefineWaves)),
-                           dim3(kRefineWaves * 64), 0, s, x,
-                           wr, e_bias, scratch, n, H, E, topk, logits, xsum, nsplit);
+        if (n < kRefineSplitMax) {
+            auto refine = E <= 64 ? router_refine_kernel<1, kRefineSplit>
+                        : E <= 128 ? router_refine_kernel<2, kRefineSplit>
+                        : E <= 256 ? router_refine_kernel<4, kRefineSplit>
+                                   : router_refine_kernel<8, kRefineSplit>;
+            hipLaunchKernelGGL(refine, dim3((unsigned)n), dim3(kRefineSplit * 64), 0, s, x, wr, e_bias,
+                               scratch, n, H, E, topk, logits, xsum, nsplit);
+        } else {
+            auto refine = E <= 64 ? router_refine_kernel<1, 1> : E <= 128 ? router_refine_kernel<2, 1>
+                        : E <= 256 ? router_refine_kernel<4, 1> : router_refine_kernel<8, 1>;
+            hipLaunchKernelGGL(refine, dim3((unsigned)((n + kRefineWaves - 1) / kRefineWaves)),
+                               dim3(kRefineWaves * 64), 0, s, x, wr, e_bias, scratch, n, H, E, topk,
+                               logits, xsum, nsplit);
+        }
         if (hipGetLastError() != hipSuccess) return -4;
     } else {
         const int rc = launch_router_logits(x, wr, n, H, E, logits, xsum, scratch, s);
