@@ -818,7 +818,8 @@ constexpr int kGemvChunksPerBlock = 4;   // waves per workgroup
 template <int NT>
 __global__ __launch_bounds__(64 * kGemvChunksPerBlock) void router_gemv_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, int n, int H, int E,
-    float* __restrict__ part, float* __restrict__ xsum, unsigned int* __restrict__ fold_ticket) {
+    float* __restrict__ part, float* __restrict__ xsum, unsigned int* __restrict__ fold_ticket,
+    const float* __restrict__ xf, uint16_t* __restrict__ xb) {
     constexpr int KB = kGemvChunksPerBlock * kRouterKC;   // K of the workgroup
     constexpr int NTH = 64 * kGemvChunksPerBlock;
     // LDS: the group's activations over the workgroup's K range as fp32,
@@ -851,13 +852,28 @@ __global__ __launch_bounds__(64 * kGemvChunksPerBlock) void router_gemv_kernel(
         }
     }
     // Stage: 8 activations per thread per step, rows past nt repeat the last
-    // row (not stored), chunks past nchunks are not read.
+    // row (not stored), chunks past nchunks are not read. fp32 activations
+    // (xf) are rounded to bf16 (nearest even) first, and the first expert
+    // block writes those bf16 rows to xb for the expert kernels.
 #pragma unroll
     for (int i = tid; i < NT * KB / 8; i += NTH) {
         const int t = i / (KB / 8), kk = (i - t * (KB / 8)) * 8;
         const int tt = t < nt ? t : nt - 1;
         uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (k0 + kk < H) v = *reinterpret_cast<const uint4*>(x + (size_t)(t0 + tt) * H + k0 + kk);
+        if (k0 + kk < H) {
+            const size_t off = (size_t)(t0 + tt) * H + k0 + kk;
+            if (xf) {
+                const float4 lo = *reinterpret_cast<const float4*>(xf + off);
+                const float4 hi = *reinterpret_cast<const float4*>(xf + off + 4);
+                v = make_uint4(f32_to_bf16(lo.x) | (f32_to_bf16(lo.y) << 16),
+                               f32_to_bf16(lo.z) | (f32_to_bf16(lo.w) << 16),
+                               f32_to_bf16(hi.x) | (f32_to_bf16(hi.y) << 16),
+                               f32_to_bf16(hi.z) | (f32_to_bf16(hi.w) << 16));
+                if (blockIdx.y == 0 && t < nt) *reinterpret_cast<uint4*>(xb + off) = v;
+            } else {
+                v = *reinterpret_cast<const uint4*>(x + off);
+            }
+        }
         const uint32_t xd[4] = {v.x, v.y, v.z, v.w};
         float4 lo, hi;
         lo.x = bf16_to_f32(xd[0] & 0xffffu); lo.y = __uint_as_float(xd[0] & 0xffff0000u);
@@ -887,12 +903,12 @@ __global__ __launch_bounds__(64 * kGemvChunksPerBlock) void router_gemv_kernel(
             xv[t][1] = *reinterpret_cast<const float4*>(xw + t * KB + j * 8 + 4);
         }
     };
-    float4 xa[NT][2], xb[NT][2];
-    rd(0, xa);
+    float4 xs0[NT][2], xs1[NT][2];
+    rd(0, xs0);
 #pragma unroll
     for (int j = 0; j < kRouterKC / 8; ++j) {
-        float4 (&cur)[NT][2] = (j & 1) ? xb : xa;
-        float4 (&nxt)[NT][2] = (j & 1) ? xa : xb;
+        float4 (&cur)[NT][2] = (j & 1) ? xs1 : xs0;
+        float4 (&nxt)[NT][2] = (j & 1) ? xs0 : xs1;
         if (j + 1 < kRouterKC / 8) rd(j + 1, nxt);
         const uint32_t wd[4] = {wv[j].x, wv[j].y, wv[j].z, wv[j].w};
         float wf[8];
@@ -1029,7 +1045,7 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
     const int nchunks = H / kRouterKC;
     if (dispatched) *dispatched = false;
     if (xf && !router_small_path(n, H, E, topk)) return -2;   // the caller converts x first
-    if (select && !xf && router_gemv_path(n, H, E, topk)) {
+    if (select && router_gemv_path(n, H, E, topk)) {
         const size_t need = (size_t)nchunks * n * E * 4 + 256;
         if (!scratch || router_select_scratch_bytes(n, H, E) < need) return -3;
         // With the dispatch outputs the last fold workgroup dispatches too.
@@ -1049,7 +1065,7 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         auto gemv = NT == 2 ? router_gemv_kernel<2> : NT == 4 ? router_gemv_kernel<4>
                                                                 : router_gemv_kernel<8>;
         hipLaunchKernelGGL(gemv, grid, dim3(64 * kGemvChunksPerBlock), 0, s, x, wr, n, H, E,
-                           scratch, xsum, ticket);
+                           scratch, xsum, ticket, xf, xb);
         if (hipGetLastError() != hipSuccess) return -4;
         auto fold = E <= 64 ? router_fold_select_kernel<1> : E <= 128 ? router_fold_select_kernel<2>
                                    : E <= 256 ? router_fold_select_kernel<4> : router_fold_select_kernel<8>;
