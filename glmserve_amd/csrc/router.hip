@@ -1055,15 +1055,10 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         // Tokens per wave: 2 up to 16 tokens (more workgroups to fill the
         // CUs), else 4 (measured per layer at 16 / 32 / 64 / 128 tokens: 8
         // was 1-5 us slower, its workgroups stacking two to a CU).
-#ifdef GLMMOE_GEMV_NT
-        const int NT = GLMMOE_GEMV_NT;
-#else
         const int NT = n <= 16 ? 2 : 4;
-#endif
         dim3 grid((unsigned)((nchunks + kGemvChunksPerBlock - 1) / kGemvChunksPerBlock),
                   (unsigned)((E + 63) / 64), (unsigned)((n + NT - 1) / NT));
-        auto gemv = NT == 2 ? router_gemv_kernel<2> : NT == 4 ? router_gemv_kernel<4>
-                                                                : router_gemv_kernel<8>;
+        auto gemv = NT == 2 ? router_gemv_kernel<2> : router_gemv_kernel<4>;
         hipLaunchKernelGGL(gemv, grid, dim3(64 * kGemvChunksPerBlock), 0, s, x, wr, n, H, E,
                            scratch, xsum, ticket, xf, xb);
         if (hipGetLastError() != hipSuccess) return -4;
