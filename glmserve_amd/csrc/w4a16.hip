@@ -1206,6 +1206,44 @@ __global__ __launch_bounds__(256) void combine_bf16x8_kernel(const uint16_t* __r
     o[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
 }
 
+// The fp32 partial rows of the decode kernels, topk <= 8: 4 features (16 B
+// of each row) per thread, the slots' indices and weights loaded first, then
+// every row's 16 bytes, then the adds: combine_kernel's operations in its
+// order, with two dependent load rounds instead of two per slot.
+__global__ __launch_bounds__(256) void combine_f32x4_kernel(const float* __restrict__ dpart,
+                                                            const int* __restrict__ inv,
+                                                            const float* __restrict__ w, int n,
+                                                            int topk, int H, int with_shared,
+                                                            float* __restrict__ out) {
+    const int t = blockIdx.y;
+    const int f4 = blockIdx.x * blockDim.x + threadIdx.x;
+    if (f4 * 4 >= H) return;
+    int row[8];
+    float ws[8];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+        if (s < topk) {
+            row[s] = inv[(size_t)t * topk + s];
+            ws[s] = w[(size_t)t * topk + s];
+        }
+    float4 y[9];
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+        if (s < topk) y[s] = reinterpret_cast<const float4*>(dpart + (size_t)row[s] * H)[f4];
+    if (with_shared) y[8] = reinterpret_cast<const float4*>(dpart + ((size_t)n * topk + t) * H)[f4];
+    float4 acc = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int s = 0; s < 8; ++s)
+        if (s < topk) {
+            acc.x = acc.x + ws[s] * y[s].x; acc.y = acc.y + ws[s] * y[s].y;
+            acc.z = acc.z + ws[s] * y[s].z; acc.w = acc.w + ws[s] * y[s].w;
+        }
+    if (with_shared) {
+        acc.x = acc.x + y[8].x; acc.y = acc.y + y[8].y; acc.z = acc.z + y[8].z; acc.w = acc.w + y[8].w;
+    }
+    reinterpret_cast<float4*>(out + (size_t)t * H)[f4] = acc;
+}
+
 // ---------------------------------------------------------------------------
 // Ring depth and batch size per projection (one 8-wave workgroup per CU).
 constexpr int kRingGU = 3;
@@ -1293,6 +1331,11 @@ int launch_combine(const float* dpart, const int* inv, const float* w, int n, in
         return hipGetLastError() == hipSuccess ? 0 : -4;
     }
     dim3 grid((unsigned)((H / 4 + 255) / 256), (unsigned)n);
+    if (!bf16 && topk <= 8 && H % 4 == 0) {
+        hipLaunchKernelGGL(combine_f32x4_kernel, grid, dim3(256), 0, s, dpart, inv, w, n, topk, H,
+                           with_shared, out);
+        return hipGetLastError() == hipSuccess ? 0 : -4;
+    }
     if (bf16)
         hipLaunchKernelGGL(combine_kernel<true>, grid, dim3(256), 0, s, dpart, inv, w, n, topk, H,
                            with_shared, out);
