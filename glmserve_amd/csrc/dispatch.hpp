@@ -85,6 +85,17 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
     while ((1 << nbits) < E) ++nbits;
 
     if (i1 < 0) i1 = total;
+    // One workgroup doing the whole dispatch: the ids of its first kIdRegs
+    // passes are loaded once, up front (their latency under the clearing
+    // below), and serve both the histogram and the permutation.
+    constexpr int kIdRegs = 4;
+    const bool cached = !bcounts;
+    int idr[kIdRegs];
+#pragma unroll
+    for (int j = 0; j < kIdRegs; ++j) {
+        const int i = tid + j * NT;
+        idr[j] = cached && i < total ? id_at(i) : -1;
+    }
     if (blk == 0 && d.zero)
         for (int i = tid; i < d.nzero; i += NT) d.zero[i] = 0u;
     for (int e = tid; e <= kDispMaxE; e += NT) cnt[e] = 0;
@@ -104,7 +115,10 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
             ntl[e] = before;
         }
     } else {
-        for (int i = tid; i < total; i += NT) {
+#pragma unroll
+        for (int j = 0; j < kIdRegs; ++j)
+            if (idr[j] >= 0 && idr[j] < E) atomicAdd(&cnt[idr[j]], 1);
+        for (int i = tid + kIdRegs * NT; i < total; i += NT) {
             const int e = id_at(i);
             if (e >= 0 && e < E) atomicAdd(&cnt[e], 1);
         }
@@ -123,9 +137,13 @@ __device__ void dispatch_block(const int* __restrict__ ids, int n, int topk, int
     __syncthreads();
 
     // Stable permute.
-    for (int base = i0; base < i1; base += NT) {
+    for (int base = i0, pass = 0; base < i1; base += NT, ++pass) {
         const int i = base + tid;
-        const int e = i < i1 ? id_at(i) : -1;
+        int e;
+        if (cached && pass < kIdRegs)
+            e = pass == 0 ? idr[0] : pass == 1 ? idr[1] : pass == 2 ? idr[2] : idr[3];
+        else
+            e = i < i1 ? id_at(i) : -1;
         const bool valid = e >= 0 && e < E;
         uint64_t m = __ballot(valid);
         for (int b = 0; b < nbits; ++b) {
