@@ -798,81 +798,76 @@ __global__ __launch_bounds__(kSmallThreads) void router_finish_kernel(
 // ---------------------------------------------------------------------------
 // Mid-size batches (kGemvMinTokens <= n < kTiledMinTokens, selection in the
 // same call): router_gemv_kernel, then router_fold_select_kernel.
-// router_gemv_kernel: grid (ceil(nchunks / 4), ceil(E / 64), ceil(n / NT)) of
-// 4 waves. Wave w of workgroup (cb, eb, tg) takes the 128-K chunk
-// c = 4 cb + w, lane l the expert e = 64 eb + l, and tokens NT tg .. + NT.
-// The lane keeps its expert's 128 chunk weights in registers (each converted
-// once for the NT tokens); the activations are wave-uniform, so they are
-// loaded and split into fp32 on the scalar unit and feed the FMAs as scalar
-// operands: about one vector instruction per product. Each lane writes the
-// ascending-K chain from zero of every token (the fixed chunk order of
-// router_partials_kernel) to part[c][t][e]. The first expert block's lanes
-// t < NT also write the chunk's activation sums xsum[t][c] (ascending K).
+// router_gemv_kernel: grid (nchunks, ceil(E / 64), ceil(n / (4 NT))) of 4
+// waves. Workgroup (c, eb, tg) takes the 128-K chunk c and the 64 experts of
+// block eb: their 256-B weight rows are staged once by LDS-DMA (whole cache
+// lines per instruction, 16-B pieces XOR-swizzled by row) and lane l keeps
+// row 64 eb + l in registers. Wave w takes tokens 4 NT tg + NT w .. + NT,
+// whose chunk activations the workgroup stages into LDS as fp32 (converted
+// once); the FMAs read them as LDS broadcasts, one step (8 K) ahead, and each
+// weight is converted once for the NT tokens: about one vector instruction
+// per product. Each lane writes the ascending-K chain from zero of every
+// token (the fixed chunk order of router_partials_kernel) to part[c][t][e];
+// the first expert block's lanes t < NT also write the chunk's activation
+// sums xsum[t][c] (ascending K).
 // router_fold_select_kernel: one workgroup per token adds the chunk partials
 // in chunk order ((0 + p0) + p1) + ..., writes the logits, and one wave
 // selects: the logit of every expert bit-identical to the other paths.
 // ---------------------------------------------------------------------------
 constexpr int kGemvMinTokens = 9;
-constexpr int kGemvChunksPerBlock = 4;   // waves per workgroup
+constexpr int kGemvWaves = 4;   // token groups (waves) per workgroup
 
 template <int NT>
-__global__ __launch_bounds__(64 * kGemvChunksPerBlock) void router_gemv_kernel(
+__global__ __launch_bounds__(64 * kGemvWaves) void router_gemv_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr, int n, int H, int E,
     float* __restrict__ part, float* __restrict__ xsum, unsigned int* __restrict__ fold_ticket,
     const float* __restrict__ xf, uint16_t* __restrict__ xb) {
-    constexpr int KB = kGemvChunksPerBlock * kRouterKC;   // K of the workgroup
-    constexpr int NTH = 64 * kGemvChunksPerBlock;
-    // LDS: the group's activations over the workgroup's K range as fp32,
-    // xl[t][k], first (their reads then fit the instruction's offset field),
-    // then the weight rows.
-    __shared__ __align__(16) char glds[NT * KB * 4 + kGemvChunksPerBlock * 64 * 256];
-    float (*xl)[KB] = reinterpret_cast<float (*)[KB]>(glds);
-    char (*wl)[64 * 256] = reinterpret_cast<char (*)[64 * 256]>(glds + NT * KB * 4);
+    constexpr int TPB = kGemvWaves * NT;   // tokens of the workgroup
+    constexpr int NTH = 64 * kGemvWaves;
+    // LDS: the tokens' chunk activations as fp32, xl[t][k], first (their
+    // reads then fit the instruction's offset field), then the weight rows.
+    __shared__ __align__(16) char glds[TPB * kRouterKC * 4 + 64 * 256];
+    float (*xl)[kRouterKC] = reinterpret_cast<float (*)[kRouterKC]>(glds);
+    char* wl = glds + TPB * kRouterKC * 4;
     const int nchunks = H / kRouterKC;
     const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63;
-    const int c = blockIdx.x * kGemvChunksPerBlock + wave;
+    const int c = blockIdx.x;
     const int e = blockIdx.y * 64 + lane;
-    const int t0 = blockIdx.z * NT, nt = min(NT, n - t0);
-    const int k0 = blockIdx.x * KB;
-    const bool live = e < E && c < nchunks;
+    const int tb = blockIdx.z * TPB, nb = min(TPB, n - tb);
     // The fold kernel's ticket (nothing in this launch reads it).
     if (fold_ticket && tid == 0 && blockIdx.x == 0 && blockIdx.y == 0 && blockIdx.z == 0)
         reset_dev(fold_ticket);
-    // The wave's 64 expert rows of its chunk, 256 B each, staged by LDS-DMA
-    // (whole cache lines per instruction): 16-byte piece o of row R at slot
-    // o ^ (R & 15), so the lanes reading their own rows hit distinct banks.
-    {
-        const int cc = c < nchunks ? c : nchunks - 1;
+    // Weight rows of the 64 experts: 16 DMAs of 4 rows, 4 per wave; piece o
+    // of row R at slot o ^ (R & 15), so the lanes reading their own rows hit
+    // distinct banks.
 #pragma unroll
-        for (int b = 0; b < 16; ++b) {
-            const int R = 4 * b + (lane >> 4);
-            const int er = min((int)blockIdx.y * 64 + R, E - 1);
-            const int o = (lane & 15) ^ (R & 15);
-            dma16(wr + (size_t)er * H + cc * kRouterKC + o * 8, &wl[wave][b * 1024]);
-        }
+    for (int i = 0; i < 4; ++i) {
+        const int b = wave * 4 + i;
+        const int R = 4 * b + (lane >> 4);
+        const int er = min((int)blockIdx.y * 64 + R, E - 1);
+        const int o = (lane & 15) ^ (R & 15);
+        dma16(wr + (size_t)er * H + c * kRouterKC + o * 8, wl + b * 1024);
     }
-    // Stage: 8 activations per thread per step, rows past nt repeat the last
-    // row (not stored), chunks past nchunks are not read. fp32 activations
-    // (xf) are rounded to bf16 (nearest even) first, and the first expert
-    // block writes those bf16 rows to xb for the expert kernels.
+    // Activations: 8 per thread per step; rows past the batch repeat its last
+    // row (not stored). fp32 activations (xf) are rounded to bf16 (nearest
+    // even) first, and the first expert block writes those bf16 rows to xb
+    // for the expert kernels.
 #pragma unroll
-    for (int i = tid; i < NT * KB / 8; i += NTH) {
-        const int t = i / (KB / 8), kk = (i - t * (KB / 8)) * 8;
-        const int tt = t < nt ? t : nt - 1;
-        uint4 v = make_uint4(0u, 0u, 0u, 0u);
-        if (k0 + kk < H) {
-            const size_t off = (size_t)(t0 + tt) * H + k0 + kk;
-            if (xf) {
-                const float4 lo = *reinterpret_cast<const float4*>(xf + off);
-                const float4 hi = *reinterpret_cast<const float4*>(xf + off + 4);
-                v = make_uint4(f32_to_bf16(lo.x) | (f32_to_bf16(lo.y) << 16),
-                               f32_to_bf16(lo.z) | (f32_to_bf16(lo.w) << 16),
-                               f32_to_bf16(hi.x) | (f32_to_bf16(hi.y) << 16),
-                               f32_to_bf16(hi.z) | (f32_to_bf16(hi.w) << 16));
-                if (blockIdx.y == 0 && t < nt) *reinterpret_cast<uint4*>(xb + off) = v;
-            } else {
-                v = *reinterpret_cast<const uint4*>(x + off);
-            }
+    for (int i = tid; i < TPB * kRouterKC / 8; i += NTH) {
+        const int t = i / (kRouterKC / 8), kk = (i - t * (kRouterKC / 8)) * 8;
+        const int tt = t < nb ? t : nb - 1;
+        const size_t off = (size_t)(tb + tt) * H + c * kRouterKC + kk;
+        uint4 v;
+        if (xf) {
+            const float4 lo = *reinterpret_cast<const float4*>(xf + off);
+            const float4 hi = *reinterpret_cast<const float4*>(xf + off + 4);
+            v = make_uint4(f32_to_bf16(lo.x) | (f32_to_bf16(lo.y) << 16),
+                           f32_to_bf16(lo.z) | (f32_to_bf16(lo.w) << 16),
+                           f32_to_bf16(hi.x) | (f32_to_bf16(hi.y) << 16),
+                           f32_to_bf16(hi.z) | (f32_to_bf16(hi.w) << 16));
+            if (blockIdx.y == 0 && t < nb) *reinterpret_cast<uint4*>(xb + off) = v;
+        } else {
+            v = *reinterpret_cast<const uint4*>(x + off);
         }
         const uint32_t xd[4] = {v.x, v.y, v.z, v.w};
         float4 lo, hi;
@@ -885,22 +880,25 @@ __global__ __launch_bounds__(64 * kGemvChunksPerBlock) void router_gemv_kernel(
     }
     wait_vmcnt<0>();
     __syncthreads();
-    if (c >= nchunks) return;   // wave-uniform; no barrier follows
+    const int t0 = wave * NT, nt = min(NT, nb - t0);   // this wave's tokens
+    if (nt <= 0) return;   // wave-uniform; no barrier follows
     uint4 wv[kRouterKC / 8];
 #pragma unroll
     for (int j = 0; j < kRouterKC / 8; ++j)
-        wv[j] = *reinterpret_cast<const uint4*>(&wl[wave][lane * 256 + ((j ^ (lane & 15)) << 4)]);
-    const float* xw = &xl[0][wave * kRouterKC];
+        wv[j] = *reinterpret_cast<const uint4*>(wl + lane * 256 + ((j ^ (lane & 15)) << 4));
+    const float* xw = &xl[t0][0];
     float acc[NT];
 #pragma unroll
     for (int t = 0; t < NT; ++t) acc[t] = 0.0f;
     // Step j: the 8 activations of every token (LDS broadcasts: every lane
-    // reads the same bytes), read one step ahead.
+    // reads the same bytes), read one step ahead; rows past nt repeat the
+    // wave's last row.
     auto rd = [&](int j, float4 (&xv)[NT][2]) {
 #pragma unroll
         for (int t = 0; t < NT; ++t) {
-            xv[t][0] = *reinterpret_cast<const float4*>(xw + t * KB + j * 8);
-            xv[t][1] = *reinterpret_cast<const float4*>(xw + t * KB + j * 8 + 4);
+            const int tt = t < nt ? t : nt - 1;
+            xv[t][0] = *reinterpret_cast<const float4*>(xw + tt * kRouterKC + j * 8);
+            xv[t][1] = *reinterpret_cast<const float4*>(xw + tt * kRouterKC + j * 8 + 4);
         }
     };
     float4 xs0[NT][2], xs1[NT][2];
@@ -934,15 +932,15 @@ __global__ __launch_bounds__(64 * kGemvChunksPerBlock) void router_gemv_kernel(
         for (int t = 0; t < NT; ++t) asm volatile("" : "+v"(acc[t]));
         __builtin_amdgcn_sched_barrier(0);
     }
-    if (live) {
+    if (e < E) {
 #pragma unroll
         for (int t = 0; t < NT; ++t)
-            if (t < nt) part[((size_t)c * n + t0 + t) * E + e] = acc[t];
+            if (t < nt) part[((size_t)c * n + tb + t0 + t) * E + e] = acc[t];
     }
     if (xsum && blockIdx.y == 0 && lane < nt) {
         float xs = 0.0f;
-        for (int k = 0; k < kRouterKC; ++k) xs += xw[lane * KB + k];
-        xsum[(size_t)(t0 + lane) * nchunks + c] = xs;
+        for (int k = 0; k < kRouterKC; ++k) xs += xw[lane * kRouterKC + k];
+        xsum[(size_t)(tb + t0 + lane) * nchunks + c] = xs;
     }
 }
 
@@ -1056,11 +1054,11 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
         // CUs), else 4 (measured per layer at 16 / 32 / 64 / 128 tokens: 8
         // was 1-5 us slower, its workgroups stacking two to a CU).
         const int NT = n <= 16 ? 2 : 4;
-        dim3 grid((unsigned)((nchunks + kGemvChunksPerBlock - 1) / kGemvChunksPerBlock),
-                  (unsigned)((E + 63) / 64), (unsigned)((n + NT - 1) / NT));
+        dim3 grid((unsigned)nchunks, (unsigned)((E + 63) / 64),
+                  (unsigned)((n + kGemvWaves * NT - 1) / (kGemvWaves * NT)));
         auto gemv = NT == 2 ? router_gemv_kernel<2> : router_gemv_kernel<4>;
-        hipLaunchKernelGGL(gemv, grid, dim3(64 * kGemvChunksPerBlock), 0, s, x, wr, n, H, E,
-                           scratch, xsum, ticket, xf, xb);
+        hipLaunchKernelGGL(gemv, grid, dim3(64 * kGemvWaves), 0, s, x, wr, n, H, E, scratch, xsum,
+                           ticket, xf, xb);
         if (hipGetLastError() != hipSuccess) return -4;
         auto fold = E <= 64 ? router_fold_select_kernel<1> : E <= 128 ? router_fold_select_kernel<2>
                                    : E <= 256 ? router_fold_select_kernel<4> : router_fold_select_kernel<8>;
