@@ -227,3 +227,30 @@ def test_layer_routing_bit_exact_small_batches(oracle, H, E, k, n):
     assert np.array_equal(st, (order // k).astype(np.int32))
     ref_offs = np.concatenate([[0], np.cumsum(np.bincount(flat, minlength=E))]).astype(np.int32)
     assert np.array_equal(offs, ref_offs)
+
+
+@pytest.mark.parametrize("n", [1, 9, 64, 300])
+def test_route_entry_bit_exact(oracle, n):
+    """glmmoe_moe_route_w4a16 (the router GEMM + top-k alone, no dispatch)
+    through each routing path: the small-batch kernels (1 token), the chunk
+    GEMV and fold / select kernels (9, 64) and the MFMA pass with the exact
+    refinement (300). ids and weights equal the oracle's bit for bit, with
+    duplicated router rows forcing exact ties."""
+    from moe_cases import SynthLayer
+    H, E, k = 6144, 256, 8
+    L = SynthLayer(H, E, k, 2048, seed=21)
+    L.router_w[7] = L.router_w[2]
+    L.router_w[200] = L.router_w[2]
+    x = L.x(n, seed=5 * n + 1)
+    ws = L.layer.alloc_workspace(n)
+    ws.fill_(0xFF)
+    ids = torch.full((n, k), -1, dtype=torch.int32, device="cuda")
+    w = torch.full((n, k), float("nan"), dtype=torch.float32, device="cuda")
+    L.layer.route(x, ids, w, ws)
+    torch.cuda.synchronize()
+    xb = x.view(torch.int16).cpu().numpy().view(np.uint16)
+    wb = L.router_w.view(torch.int16).cpu().numpy().view(np.uint16)
+    logits = oracle.router_logits_bf16(xb, wb)
+    rid, rw = oracle.router_topk(logits, L.e_bias.cpu().numpy(), k, True, 2.5)
+    assert np.array_equal(ids.cpu().numpy(), rid)
+    assert np.array_equal(w.cpu().numpy().view(np.uint32), rw.view(np.uint32))
