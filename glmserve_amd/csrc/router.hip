@@ -797,7 +797,10 @@ __global__ __launch_bounds__(kSmallThreads) void router_finish_kernel(
 
 // ---------------------------------------------------------------------------
 // Mid-size batches (kGemvMinTokens <= n < kTiledMinTokens, selection in the
-// same call): router_gemv_kernel, then router_fold_select_kernel.
+// same call): router_gemv_kernel, then router_fold_select_kernel. Together
+// they replace the reference's router GEMM, top-k and dispatch launches
+// (src/model_gpu.cpp:1448-1450 -> cuda/gemm.cu:62-77, cuda/moe_router.cu:17-72,
+// cuda/moe_dispatch.cu:16-45) with the fixed summation order of this build.
 // router_gemv_kernel: grid (nchunks, ceil(E / 64), ceil(n / (4 NT))) of 4
 // waves. Workgroup (c, eb, tg) takes the 128-K chunk c and the 64 experts of
 // block eb: their 256-B weight rows are staged once by LDS-DMA (whole cache
