@@ -176,9 +176,12 @@ inline void end_call(hipStream_t s) {
 }
 
 // Dispatch onward, given ids/weights/xsum in the workspace view.
+// x16_ready: the router already wrote x's fp16 rows for the large-group
+// gate/up kernel into the start of dpart.
 int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int* ids,
                 const float* w, const float* xsum, float* out, const glmmoe_layer_ws& v,
-                hipStream_t s, bool dispatched = false, const FusedRoute* fr = nullptr) {
+                hipStream_t s, bool dispatched = false, const FusedRoute* fr = nullptr,
+                bool x16_ready = false) {
     const int H = L->hidden, I = L->moe_inter, E = L->n_experts, k = L->topk;
     const int sh = has_shared(L) ? 1 : 0;
     const int mt = max_tiles_for(n, k, E, sh, H, I);
@@ -201,7 +204,7 @@ int run_experts(const glmmoe_w4a16_layer* L, const uint16_t* x, int n, const int
     int8_t* hexp = reinterpret_cast<int8_t*>(v.hsum);
     const int R = n * k + sh * n;
     rc = big ? launch_gate_up_big(P, x, n, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, hexp, v.dpart,
-                                  dpart_bytes(L, n), v.sync, H, I, E, s)
+                                  dpart_bytes(L, n), v.sync, H, I, E, s, x16_ready)
              : launch_gate_up(P, x, xsum, v.tiles, v.ntiles, mt, v.sorted_token_ids, v.h, v.hsum,
                               v.sync, v.dpart, dpart_bytes(L, n), H, I, E, s, fr, nt);
     if (rc) return rc;
@@ -372,14 +375,20 @@ int layer_w4(const glmmoe_w4a16_layer* L, const uint16_t* x, const float* xf, ui
                             L->routed_scale, v.topk_ids, v.topk_w, disp};
         return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s, true, &fr);
     }
-    bool dispatched = false;
-    // The large-group kernels do not read the activation group sums.
+    bool dispatched = false, x16 = false;
+    // The large-group kernels do not read the activation group sums; their
+    // fp16 input rows go to the start of dpart (launch_gate_up_big's scratch,
+    // free until then) when the router stages whole rows.
+    const bool big = T == kBigRows;
+    uint16_t* xh = big ? reinterpret_cast<uint16_t*>(v.dpart) : nullptr;
+    float* xrho = big ? reinterpret_cast<float*>(xh + (size_t)n * H) : nullptr;
     rc = launch_router_select(x, L->router_w, L->e_bias, n, H, E, k, L->norm_topk,
-                              L->routed_scale, v.logits, T == kBigRows ? nullptr : v.xsum, v.rpart,
-                              v.topk_ids, v.topk_w, s, &disp, &dispatched, true, xf, xb);
+                              L->routed_scale, v.logits, big ? nullptr : v.xsum, v.rpart,
+                              v.topk_ids, v.topk_w, s, &disp, &dispatched, true, xf, xb, xh, xrho,
+                              &x16);
     if (rc) return rc;
     mark(GLMMOE_STAGE_ROUTER_TOPK, s);
-    return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s, dispatched);
+    return run_experts(L, x, n, v.topk_ids, v.topk_w, v.xsum, out, v, s, dispatched, nullptr, x16);
 }
 
 }  // namespace

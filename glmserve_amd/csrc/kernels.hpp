@@ -66,7 +66,12 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
                          int E, int topk, int norm_topk, float routed_scale, float* logits,
                          float* xsum, float* scratch, int* ids, float* w, hipStream_t s,
                          const DispOut* disp = nullptr, bool* dispatched = nullptr,
-                         bool select = true, const float* xf = nullptr, uint16_t* xb = nullptr);
+                         bool select = true, const float* xf = nullptr, uint16_t* xb = nullptr,
+                         uint16_t* xh = nullptr, float* xrho = nullptr, bool* x16_done = nullptr);
+// xh / xrho (nullable): where the large-group gate/up kernel reads x as fp16
+// rows ([n, H]) and their factors ([n]); the router writes them (the
+// conversion launch_gate_up_big otherwise runs) when it stages whole rows
+// (from kTiledMinTokens tokens) and then sets *x16_done.
 // xf (small-batch path only): fp32 activations [n, H], rounded to bf16 as the
 // router stages them; the rounded rows are written to xb ([n, H]) and x is
 // not read.
@@ -124,7 +129,10 @@ bool big_w4_shape_ok(int H, int I);
 int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int* tiles,
                        const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
                        int8_t* hexp, void* scratch, size_t scratch_bytes, unsigned int* tick, int H,
-                       int I, int E, hipStream_t s);
+                       int I, int E, hipStream_t s, bool x16_ready = false);
+// log2 of the factor the large-group kernels' weight decode applies to the
+// scales (and their epilogues undo).
+constexpr int kWPre = 8;
 int launch_down_big(const ExpertPtrs& P, uint16_t* h, int8_t* hexp, int R, const int* tiles,
                     const int* ntiles, int max_tiles, float* dpart, int H, int I, int E,
                     hipStream_t s);

@@ -86,7 +86,6 @@ struct MmArgs {
 };
 
 constexpr int kMmPartFloats = 8 * 128 * 64;   // one half item's accumulators
-constexpr int kWPre = 8;                       // log2 of the weight scales' decode factor
 constexpr int kHExpNone = 127;                 // exponent of an all-zero block: no constraint
 
 // Exponent e for a block whose largest |h| has fp32 bits m: 0 while
@@ -819,12 +818,14 @@ bool big_w4_shape_ok(int H, int I) { return H % 1024 == 0 && I % 1024 == 0; }
 int launch_gate_up_big(const ExpertPtrs& P, const uint16_t* x, int n, const int* tiles,
                        const int* ntiles, int max_tiles, const int* rows_tok, uint16_t* h,
                        int8_t* hexp, void* scratch, size_t scratch_bytes, unsigned int* tick, int H,
-                       int I, int E, hipStream_t s) {
+                       int I, int E, hipStream_t s, bool x16_ready) {
     if (!big_w4_shape_ok(H, I)) return -2;
     uint16_t* xh = reinterpret_cast<uint16_t*>(scratch);
     float* rho = reinterpret_cast<float*>(xh + (size_t)n * H);
-    hipLaunchKernelGGL(f16_rows_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, x, n, H, xh, rho);
-    if (hipGetLastError() != hipSuccess) return -4;
+    if (!x16_ready) {
+        hipLaunchKernelGGL(f16_rows_kernel, dim3((unsigned)((n + 3) / 4)), dim3(256), 0, s, x, n, H, xh, rho);
+        if (hipGetLastError() != hipSuccess) return -4;
+    }
     MmArgs a{};
     a.wq[0] = P.gate_q; a.ws[0] = P.gate_s; a.wq[1] = P.up_q; a.ws[1] = P.up_s;
     a.swq[0] = P.sh_gate_q; a.sws[0] = P.sh_gate_s; a.swq[1] = P.sh_up_q; a.sws[1] = P.sh_up_s;

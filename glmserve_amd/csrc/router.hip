@@ -422,7 +422,8 @@ template <int NJ, int TW>   // keys per lane: E <= 64 * NJ
 __global__ __launch_bounds__(TW == 1 ? kRefineWaves * 64 : TW * 64) void router_refine_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ wr,
     const float* __restrict__ e_bias, const float* __restrict__ sb, int n, int H, int E, int topk,
-    float* __restrict__ logits, float* __restrict__ xsum, int nsplit) {
+    float* __restrict__ logits, float* __restrict__ xsum, int nsplit, uint16_t* __restrict__ xh,
+    float* __restrict__ xrho) {
     constexpr int TPW = TW == 1 ? kRefineWaves : 1;   // tokens per workgroup
     const int lane = threadIdx.x & 63;
     const int slot = TW == 1 ? (int)(threadIdx.x >> 6) : 0;    // token slot of this wave
@@ -440,6 +441,49 @@ __global__ __launch_bounds__(TW == 1 ? kRefineWaves * 64 : TW * 64) void router_
         for (int j = 0; j < kRouterKC / 8; ++j) xw[j][lane] = lane < nchunks ? xp[j] : make_uint4(0, 0, 0, 0);
     }
     if constexpr (TW > 1) __syncthreads();   // wave 0 staged the token's x
+    if (xh && sub == 0) {
+        // The large-group gate/up kernel's input row: x in fp16 with a
+        // power-of-2 scale that puts the row's largest magnitude in
+        // [2^14, 2^15), and the factor undoing it (times 2^-kWPre): the rule
+        // and operations of f16_rows_kernel, from the staged row.
+        uint32_t amax = 0;   // bf16 magnitudes compare as integers
+        if (lane < nchunks) {
+#pragma unroll
+            for (int j = 0; j < kRouterKC / 8; ++j) {
+                const uint4 v = xw[j][lane];
+                const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    amax = max(amax, d[q] & 0x7fffu);
+                    amax = max(amax, (d[q] >> 16) & 0x7fffu);
+                }
+            }
+        }
+#pragma unroll
+        for (int off = 32; off > 0; off >>= 1) amax = max(amax, (uint32_t)__shfl_xor((int)amax, off));
+        const int ex = amax >= 0x0080u ? (int)(amax >> 7) - 127 : 0;
+        int kx = 14 - ex;
+        kx = kx > 100 ? 100 : (kx < -100 ? -100 : kx);
+        const float scale = __builtin_ldexpf(1.0f, kx);
+        if (lane == 0) xrho[t] = __builtin_ldexpf(1.0f, -kx - kWPre);
+        if (lane < nchunks) {
+            uint4* yr = reinterpret_cast<uint4*>(xh + (size_t)t * H + lane * kRouterKC);
+#pragma unroll
+            for (int j = 0; j < kRouterKC / 8; ++j) {
+                const uint4 v = xw[j][lane];
+                const uint32_t d[4] = {v.x, v.y, v.z, v.w};
+                uint32_t o[4];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const _Float16 lo = (_Float16)(bf16_to_f32(d[q] & 0xffffu) * scale);
+                    const _Float16 hi = (_Float16)(bf16_to_f32(d[q] >> 16) * scale);
+                    o[q] = (uint32_t)__builtin_bit_cast(uint16_t, lo) |
+                           ((uint32_t)__builtin_bit_cast(uint16_t, hi) << 16);
+                }
+                yr[j] = make_uint4(o[0], o[1], o[2], o[3]);
+            }
+        }
+    }
     if (xsum && sub == 0 && lane < nchunks) {
         float s = 0.0f;
 #pragma unroll
@@ -1042,7 +1086,7 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
                          int E, int topk, int norm_topk, float routed_scale, float* logits,
                          float* xsum, float* scratch, int* ids, float* w, hipStream_t s,
                          const DispOut* disp, bool* dispatched, bool select, const float* xf,
-                         uint16_t* xb) {
+                         uint16_t* xb, uint16_t* xh, float* xrho, bool* x16_done) {
     const int nchunks = H / kRouterKC;
     if (dispatched) *dispatched = false;
     if (xf && !router_small_path(n, H, E, topk)) return -2;   // the caller converts x first
@@ -1138,15 +1182,16 @@ int launch_router_select(const uint16_t* x, const uint16_t* wr, const float* e_b
                         : E <= 256 ? router_refine_kernel<4, kRefineSplit>
                                    : router_refine_kernel<8, kRefineSplit>;
             hipLaunchKernelGGL(refine, dim3((unsigned)n), dim3(kRefineSplit * 64), 0, s, x, wr, e_bias,
-                               scratch, n, H, E, topk, logits, xsum, nsplit);
+                               scratch, n, H, E, topk, logits, xsum, nsplit, xh, xrho);
         } else {
             auto refine = E <= 64 ? router_refine_kernel<1, 1> : E <= 128 ? router_refine_kernel<2, 1>
                         : E <= 256 ? router_refine_kernel<4, 1> : router_refine_kernel<8, 1>;
             hipLaunchKernelGGL(refine, dim3((unsigned)((n + kRefineWaves - 1) / kRefineWaves)),
                                dim3(kRefineWaves * 64), 0, s, x, wr, e_bias, scratch, n, H, E, topk,
-                               logits, xsum, nsplit);
+                               logits, xsum, nsplit, xh, xrho);
         }
         if (hipGetLastError() != hipSuccess) return -4;
+        if (x16_done) *x16_done = xh && xrho;
     } else {
         const int rc = launch_router_logits(x, wr, n, H, E, logits, xsum, scratch, s);
         if (rc) return rc;

@@ -124,6 +124,30 @@ def test_prefill_full_shape(oracle, full_layer):
     _check_full(out, oracle_full_w4(L, oracle, x, ids, w))
 
 
+@pytest.mark.parametrize("n", [300, 1200])
+def test_layer_router_rows_match_expert_ffn(full_layer, n):
+    """From 256 tokens the layer's router writes x's fp16 rows (and their
+    factors) for the large-group gate/up kernel; the expert-FFN entry
+    converts them itself (f16_rows_kernel). On the layer's own routing the
+    two must give the same output bit for bit (300: four waves per token in
+    the refinement, 1200: one)."""
+    L = full_layer
+    x = L.x(n, 31 + n)
+    ws = L.layer.alloc_workspace(n)
+    out = _nan_out(n, L.H)
+    L.layer.forward(x, out, ws)
+    torch.cuda.synchronize()
+    v = L.layer.workspace_view(n, ws)
+    ids = _ws_i32(ws, v.topk_ids, n * L.k).clone()
+    w = _ws_f32(ws, v.topk_w, n * L.k).clone()
+    ws2 = L.layer.alloc_workspace(n)
+    out2 = _nan_out(n, L.H)
+    L.layer.expert_ffn(x, ids, w, out2, ws2)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    assert torch.equal(out, out2)
+
+
 def test_prefill_uniform_routing(oracle, full_layer):
     # configs[2] as specified: 4096 tokens with uniform-random routing (k
     # distinct experts per token, ~128 rows per expert, every expert hit),
